@@ -1,0 +1,111 @@
+/*
+ * prism_amd.h -- C ABI of the MI355X (gfx950) quantized linear-layer library (libprism_amd.so).
+ *
+ * Every entry point takes device pointers, plain sizes and a HIP stream (hipStream_t passed as void*; NULL is the
+ * null stream), launches asynchronously on that stream, never synchronizes the host and never allocates.  It
+ * returns PRISM_OK (0) or one of the error codes below; prism_error_string() names them.  Argument meaning,
+ * layouts and the "live rows" convention follow StartLux-Prism's kernel ops (citations are relative to its
+ * source tree):
+ *   - n_rows: a DEVICE int32[1] holding the live row count, read inside the kernels so one captured graph serves
+ *     every batch size; rows >= *n_rows of the outputs are left untouched (kernels/w8a8.py:44-46, 77-85).
+ *   - operands are K-contiguous ("TN"): activations [M, K], weights [N, K] (csrc/w8a8_gemm.cu:3-6).
+ *   - bf16 / fp16 values are passed as uint16_t bit patterns.
+ */
+#ifndef PRISM_AMD_H
+#define PRISM_AMD_H
+
+#include <stdint.h>
+
+#if defined(__GNUC__)
+#define PRISM_API __attribute__((visibility("default")))
+#else
+#define PRISM_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    PRISM_OK = 0,
+    PRISM_ERR_SHAPE = 1,       /* a size is not supported (e.g. K not a multiple of 32) */
+    PRISM_ERR_ALIGN = 2,       /* a pointer or stride is not aligned as the kernel needs */
+    PRISM_ERR_ARG = 3,         /* a bad argument value (epilogue, group size, null pointer) */
+    PRISM_ERR_LAUNCH = 4,      /* the HIP runtime rejected the launch */
+    PRISM_ERR_DEVICE = 5,      /* the current device is not a gfx950 (MI355X / MI350X) */
+};
+
+/* Version of this ABI (major * 100 + minor). */
+PRISM_API int prism_version(void);
+
+/* Static description of an error code. */
+PRISM_API const char* prism_error_string(int code);
+
+/*
+ * Per-token int8 activation quantization.  Replaces kernels/quant.py:481-486 (rows_q8, mode 0) and its kernel
+ * _rows_q8_kernel (kernels/quant.py:287-309).
+ *   y = x * inv_s[k] (inv_s may be NULL: y = x); scale = max(max_k |y|, 1e-10) / 127 (IEEE division);
+ *   q = rint(y / scale) (IEEE division, ties to even).
+ * x bf16 [M, K] with row stride ldx (elements); q int8 [M, K] (row stride K); s fp32 [M].
+ * Needs K % 8 == 0, ldx % 8 == 0, 16-byte aligned x and q, K <= 65536.
+ */
+PRISM_API int prism_quant_rows_i8(const uint16_t* x, int64_t ldx, const float* inv_s, int8_t* q, float* s,
+                        const int32_t* n_rows, int64_t M, int64_t K, void* stream);
+
+/*
+ * Per-(row, group) int8 quantization.  Replaces kernels/w8a8.py:264-271 (quant_rows) and _quant_rows_kernel
+ * (kernels/w8a8.py:101-112): per gk inputs scale = max(amax, 1e-10) / 127, q = rint(x / scale).
+ * x bf16 [M, K] -> q int8 [M, K], s fp32 [M, K / gk].  gk in {32, 64, 128, 256, ...}, a multiple of 32 dividing K.
+ */
+PRISM_API int prism_quant_rows_groups(const uint16_t* x, int8_t* q, float* s, const int32_t* n_rows, int64_t M, int64_t K,
+                            int64_t gk, void* stream);
+
+/*
+ * W4A8 activation producer.  Replaces kernels/quant.py:409-411 (rows_g) and _store_g (kernels/quant.py:314-330);
+ * bit-identical to kernels/w4a8.py:144-155 (quantize_ref).
+ *   per `group` inputs (256 as the reference, or K for one scale per token) a = max(amax, 1e-10) / 127,
+ *   xq = rint(x / a); per 32 inputs the int32 sum S of xq stored as S & 63 and S >> 6.
+ * x bf16 [M, K] (row stride ldx); xq int8 [M, K]; a fp32 [K / group, M]; xs int8 [K / 256, M, 16].
+ * Needs K % 256 == 0, ldx % 8 == 0.
+ */
+PRISM_API int prism_quant_rows_g(const uint16_t* x, int64_t ldx, int8_t* xq, float* a, int8_t* xs, const int32_t* n_rows,
+                       int64_t M, int64_t K, int64_t group, void* stream);
+
+/*
+ * W8A8 GEMM with per-group scales along K (Q8_0 when gk == 32; per-channel when gk == K).  Replaces
+ * kernels/w8a8.py:183-231 (gemm, epilogues 0 and 1) with the arithmetic of _w8a8_kernel (kernels/w8a8.py:64-85);
+ * the native schema it stands for is startlux_prism::w8a8_gemm (csrc/w8a8_gemm.cu:737-767, 794-797).
+ *   per group g, in increasing g:  P = sum_{k in g} a[m,k] w[n,k]  (int32, exact)
+ *                                  y = RN(y + RN(RN(float(P) * sa[m,g]) * sw[n,g]))
+ *   epi 0: out bf16 [m, n] = RN_bf16(y);  epi 1: out fp32 [m, n] = RN(out[m, n] + y).
+ * a int8 [M, K]; a_s fp32, element (m, g) at a_s[m * as_sm + g * as_sg] (as_sg = 0: one scale per token);
+ * w int8 [N, K]; w_s [N, K / gk], fp16 bits (ws_fp16 = 1, Q8_0's own block scales) or fp32 (ws_fp16 = 0);
+ * out row stride ldo (elements).  kernel: -1 picks by shape; 0 the tile kernel; 1 the decode kernel (gk == 32,
+ * M <= 64).  Needs K % 32 == 0, gk % 32 == 0, K % gk == 0, N % 16 == 0, 16-byte aligned a and w.
+ */
+PRISM_API int prism_w8a8_gemm(const int8_t* a, const float* a_s, int64_t as_sm, int64_t as_sg, const int8_t* w,
+                    const void* w_s, int ws_fp16, void* out, int64_t ldo, const int32_t* n_rows, int64_t M,
+                    int64_t N, int64_t K, int64_t gk, int epi, int kernel, void* stream);
+
+/*
+ * W4A8 GEMM on Q4_K weights in the repacked W4 layout.  Replaces kernels/w4a8.py:353-366 (gemm, kind "q4k") and
+ * the native startlux_prism::w4a8_gemm (csrc/w4a8_gemm.cu:887-961, schema :963-966); arithmetic of
+ * kernels/w4a8.py:14-22 / gemm_ref (:177-199), per super-block b of 256 inputs in increasing b:
+ *   acc  = sum_g sc[b,n,g] (xq . q)_g ;  mins = sum_g mn[b,n,g] S[m, 8b+g]          (int32, exact)
+ *   t = RN(d[b,n] float(acc)); t = fma(-dm[b,n], float(mins), t); y = fma(a[b,m], t, y)
+ *   epi 0: bf16(y); epi 1: out = RN(out + y).
+ * xq int8 [M, K]; a fp32, element (b, m) at a[b * a_sb + m] (a_sb = 0: one scale per token);
+ * xs int8 [K/256, M, 16] (split per-32 sums); q uint8 [N, K/2] (per 32 inputs byte t = q[t] | q[t+16] << 4);
+ * sc, mn uint8 [K/256, N, 8]; d, dm fp32 [K/256, N].  Needs K % 256 == 0, N % 16 == 0.
+ * kernel: -1 picks by shape; 0 the tile kernel; 1 the decode kernel (M <= 64).
+ */
+PRISM_API int prism_w4a8_q4k_gemm(const int8_t* xq, const float* a, int64_t a_sb, const int8_t* xs, const uint8_t* q,
+                        const uint8_t* sc, const uint8_t* mn, const float* d, const float* dm, void* out,
+                        int64_t ldo, const int32_t* n_rows, int64_t M, int64_t N, int64_t K, int epi, int kernel,
+                        void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PRISM_AMD_H */

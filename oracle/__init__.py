@@ -1,0 +1,244 @@
+"""CPU oracle for StartLux-Prism's quantized linear-layer hot path -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this package, and only as the
+checker (or the timed CPU baseline), never as the thing measured or shipped.  The arithmetic lives in
+prism_oracle.c (built by oracle/Makefile into oracle/_build/liboracle.so); this module wraps it with numpy.
+
+Pinning (each function is checked by tests/test_oracle.py against something other than its own formula):
+  fp16/bf16 conversions      numpy's float16 / a bit-level bf16 rounding of float64, exhaustive over patterns
+  q8_0_quantize              numpy dequantisation round trip (|w - q d| <= d / 2), absmax element -> +-127,
+                             the torch restatement in the product package (gguf_formats.as_q8) bit for bit
+  quant_rows_i8 / _groups    special cases (zero row -> scale 1e-10/127, absmax -> +-127), numpy IEEE division
+  w8a8_gemm                  int32 block sums vs brute-force int64 (numpy), fp32 result vs float64 within the
+                             rounding bound, gk == K reducing to the per-channel formula, epi 1 = out + epi 0 value
+  q4k_quantize / dequant     an independent numpy decoder of the GGUF block_q4_K layout (ggml get_scale_min_k4)
+  q4k_repack                 the W4 nibble order re-derived from the dequantised values
+  quant_rows_g               per-32 sums vs numpy, split-sum reconstruction, scale special cases
+  w4a8_gemm                  int32 super-block sums vs brute force, fmaf vs exact rational arithmetic
+                             (fractions.Fraction), fp32 result vs float64 within the rounding bound
+Parity unpinned: none of the above is checked against the reference's own numbers, because the reference holds
+no numeric fixtures for this path (its GEMM tests compare GPU kernels with each other on CUDA-seeded inputs).
+"""
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "_build", "liboracle.so")
+_lib = None
+
+_i64 = ctypes.c_int64
+_p = ctypes.c_void_p
+
+
+def build():
+    import subprocess
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        sig = {
+            "orc_bf16_to_float": (ctypes.c_float, [ctypes.c_uint16]),
+            "orc_float_to_bf16": (ctypes.c_uint16, [ctypes.c_float]),
+            "orc_half_to_float": (ctypes.c_float, [ctypes.c_uint16]),
+            "orc_float_to_half": (ctypes.c_uint16, [ctypes.c_float]),
+            "orc_q8_0_quantize": (None, [_p, _i64, _i64, _p, _p, ctypes.c_int]),
+            "orc_quant_rows_i8": (None, [_p, _i64, _p, _i64, _i64, _i64, _p, _p, ctypes.c_int]),
+            "orc_quant_rows_groups": (None, [_p, _i64, _i64, _i64, _i64, _p, _p, ctypes.c_int]),
+            "orc_w8a8_block_sums": (None, [_p, _p, _i64, _i64, _i64, _i64, _p]),
+            "orc_w8a8_gemm": (None, [_p, _p, _i64, _i64, _p, _p, ctypes.c_int, _i64, _i64, _i64, _i64,
+                                     ctypes.c_int, _p, _i64, _i64, ctypes.c_int]),
+            "orc_q4k_quantize": (None, [_p, _i64, _i64, _p, ctypes.c_int]),
+            "orc_q4k_dequant": (None, [_p, _i64, _i64, _p]),
+            "orc_q4k_repack": (None, [_p, _i64, _i64, _p, _p, _p, _p, _p]),
+            "orc_quant_rows_g": (None, [_p, _i64, _i64, _i64, _i64, _p, _p, _p, ctypes.c_int]),
+            "orc_w4a8_gemm": (None, [_p, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, ctypes.c_int, _p,
+                                     _i64, _i64, _p, _p, ctypes.c_int]),
+            "orc_fmaf": (ctypes.c_double, [ctypes.c_float, ctypes.c_float, ctypes.c_float]),
+        }
+        for name, (res, args) in sig.items():
+            f = getattr(L, name)
+            f.restype, f.argtypes = res, args
+        _lib = L
+    return _lib
+
+
+def _ptr(x):
+    return None if x is None else x.ctypes.data
+
+
+def _c(x, dtype):
+    assert x.dtype == dtype, (x.dtype, dtype)
+    assert x.flags["C_CONTIGUOUS"]
+    return x
+
+
+# ------------------------------------------------------------------------------------------------ formats
+def bf16_bits(x):
+    """fp32 array -> bf16 bit patterns (uint16), round to nearest even (the C conversion, vectorised in numpy)."""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return np.where(nan, ((u >> 16) | 0x40).astype(np.uint16), r)
+
+
+def bf16_to_f32(h):
+    return (np.asarray(h, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16_c(v):
+    return lib().orc_float_to_bf16(float(v))
+
+
+def f32_to_half_c(v):
+    return lib().orc_float_to_half(float(v))
+
+
+def half_to_f32_c(h):
+    return lib().orc_half_to_float(int(h))
+
+
+def fmaf(a, b, c):
+    return lib().orc_fmaf(float(a), float(b), float(c))
+
+
+# ------------------------------------------------------------------------------------------------ Q8_0 / W8A8
+def q8_0_quantize(w, nthreads=0):
+    """fp32 [N, K] -> (qs int8 [N, K], d fp16-bits uint16 [N, K/32]) (gguf_weights.py:121-133)."""
+    w = _c(np.ascontiguousarray(w, np.float32), np.float32)
+    N, K = w.shape
+    qs = np.empty((N, K), np.int8)
+    d = np.empty((N, K // 32), np.uint16)
+    lib().orc_q8_0_quantize(_ptr(w), N, K, _ptr(qs), _ptr(d), nthreads)
+    return qs, d
+
+
+def quant_rows_i8(x_bf16, inv_s=None, live=None, nthreads=0):
+    """bf16 bits uint16 [M, K] -> (q int8 [M, K], s fp32 [M]) (kernels/quant.py:287-309)."""
+    x = _c(np.ascontiguousarray(x_bf16), np.uint16)
+    M, K = x.shape
+    live = M if live is None else live
+    q = np.zeros((M, K), np.int8)
+    s = np.zeros(M, np.float32)
+    inv = None if inv_s is None else _c(np.ascontiguousarray(inv_s, np.float32), np.float32)
+    lib().orc_quant_rows_i8(_ptr(x), K, _ptr(inv), M, K, live, _ptr(q), _ptr(s), nthreads)
+    return q, s
+
+
+def quant_rows_groups(x_bf16, gk, live=None, nthreads=0):
+    """bf16 bits [M, K] -> (q int8 [M, K], s fp32 [M, K/gk]) (kernels/w8a8.py:101-112)."""
+    x = _c(np.ascontiguousarray(x_bf16), np.uint16)
+    M, K = x.shape
+    live = M if live is None else live
+    q = np.zeros((M, K), np.int8)
+    s = np.zeros((M, K // gk), np.float32)
+    lib().orc_quant_rows_groups(_ptr(x), M, K, gk, live, _ptr(q), _ptr(s), nthreads)
+    return q, s
+
+
+def w8a8_block_sums(a, w, gk):
+    a = _c(np.ascontiguousarray(a), np.int8)
+    w = _c(np.ascontiguousarray(w), np.int8)
+    M, K = a.shape
+    N = w.shape[0]
+    P = np.empty((M, N, K // gk), np.int32)
+    lib().orc_w8a8_block_sums(_ptr(a), _ptr(w), M, N, K, gk, _ptr(P))
+    return P
+
+
+def w8a8_gemm(a, a_s, w, w_s, gk, epi=0, out=None, live=None, nthreads=0):
+    """(kernels/w8a8.py:64-85).  a int8 [M, K]; a_s fp32 [M] (per token) or [M, K/gk]; w int8 [N, K];
+    w_s fp16 bits uint16 or fp32 [N, K/gk].  epi 0 -> bf16 bits uint16 [M, N] (rows >= live zero unless `out`
+    given); epi 1 -> out fp32 [M, N] updated in place (out = out + y)."""
+    a = _c(np.ascontiguousarray(a), np.int8)
+    w = _c(np.ascontiguousarray(w), np.int8)
+    M, K = a.shape
+    N = w.shape[0]
+    G = K // gk
+    a_s = np.ascontiguousarray(a_s, np.float32)
+    as_sm, as_sg = (1, 0) if a_s.ndim == 1 else (G, 1)
+    ws16 = w_s.dtype == np.uint16
+    w_s = np.ascontiguousarray(w_s)
+    assert w_s.shape == (N, G)
+    live = M if live is None else live
+    if out is None:
+        out = np.zeros((M, N), np.uint16 if epi == 0 else np.float32)
+    assert out.dtype == (np.uint16 if epi == 0 else np.float32) and out.flags["C_CONTIGUOUS"]
+    lib().orc_w8a8_gemm(_ptr(a), _ptr(a_s), as_sm, as_sg, _ptr(w), _ptr(w_s), int(ws16), M, N, K, gk, epi,
+                        _ptr(out), out.shape[1], live, nthreads)
+    return out
+
+
+# ------------------------------------------------------------------------------------------------ Q4_K / W4A8
+def q4k_quantize(w, nthreads=0):
+    """fp32 [N, K] -> GGUF block_q4_K bytes uint8 [N, K/256, 144] (this build's own quantizer)."""
+    w = _c(np.ascontiguousarray(w, np.float32), np.float32)
+    N, K = w.shape
+    out = np.empty((N, K // 256, 144), np.uint8)
+    lib().orc_q4k_quantize(_ptr(w), N, K, _ptr(out), nthreads)
+    return out
+
+
+def q4k_dequant(blocks):
+    blocks = _c(np.ascontiguousarray(blocks), np.uint8)
+    N, NB = blocks.shape[:2]
+    w = np.empty((N, NB * 256), np.float32)
+    lib().orc_q4k_dequant(_ptr(blocks), N, NB * 256, _ptr(w))
+    return w
+
+
+def q4k_repack(blocks):
+    """-> dict(q uint8 [N, K/2], sc uint8 [K/256, N, 8], mn, d fp32 [K/256, N], dm) (kernels/w4a8.py:70-81)."""
+    blocks = _c(np.ascontiguousarray(blocks), np.uint8)
+    N, NB = blocks.shape[:2]
+    K = NB * 256
+    r = dict(q=np.empty((N, K // 2), np.uint8), sc=np.empty((NB, N, 8), np.uint8), mn=np.empty((NB, N, 8), np.uint8),
+             d=np.empty((NB, N), np.float32), dm=np.empty((NB, N), np.float32))
+    lib().orc_q4k_repack(_ptr(blocks), N, K, _ptr(r["q"]), _ptr(r["sc"]), _ptr(r["mn"]), _ptr(r["d"]), _ptr(r["dm"]))
+    return r
+
+
+def quant_rows_g(x, group=256, live=None, nthreads=0):
+    """fp32 [M, K] -> (xq int8 [M, K], a fp32 [K/group, M], xs int8 [K/256, M, 16]) (kernels/w4a8.py:144-155)."""
+    x = _c(np.ascontiguousarray(x, np.float32), np.float32)
+    M, K = x.shape
+    live = M if live is None else live
+    xq = np.zeros((M, K), np.int8)
+    a = np.zeros((K // group, M), np.float32)
+    xs = np.zeros((K // 256, M, 16), np.int8)
+    lib().orc_quant_rows_g(_ptr(x), M, K, group, live, _ptr(xq), _ptr(a), _ptr(xs), nthreads)
+    return xq, a, xs
+
+
+def group_sums(xs):
+    """xs int8 [K/256, M, 16] -> int32 [M, K/32] (kernels/w4a8.py:158-161)."""
+    p = xs.transpose(1, 0, 2).reshape(xs.shape[1], -1, 2, 8).astype(np.int32)
+    return (p[:, :, 0] + 64 * p[:, :, 1]).reshape(xs.shape[1], -1)
+
+
+def w4a8_gemm(xq, a, xs, w4, epi=0, out=None, live=None, sums=False, nthreads=0):
+    """(kernels/w4a8.py:177-199).  a fp32 [K/256, M] or [M] (one scale per token).  Returns bf16 bits [M, N]
+    (epi 0) or the updated fp32 out (epi 1); with sums=True also (acc, mins) int32 [M, N, K/256]."""
+    xq = _c(np.ascontiguousarray(xq), np.int8)
+    M, K = xq.shape
+    N = w4["q"].shape[0]
+    a = np.ascontiguousarray(a, np.float32)
+    a_sb = 0 if a.ndim == 1 else M
+    xs = _c(np.ascontiguousarray(xs), np.int8)
+    live = M if live is None else live
+    if out is None:
+        out = np.zeros((M, N), np.uint16 if epi == 0 else np.float32)
+    acc = mins = None
+    if sums:
+        acc = np.zeros((M, N, K // 256), np.int32)
+        mins = np.zeros((M, N, K // 256), np.int32)
+    lib().orc_w4a8_gemm(_ptr(xq), _ptr(a), a_sb, _ptr(xs), _ptr(w4["q"]), _ptr(w4["sc"]), _ptr(w4["mn"]),
+                        _ptr(w4["d"]), _ptr(w4["dm"]), M, N, K, epi, _ptr(out), out.shape[1], live, _ptr(acc),
+                        _ptr(mins), nthreads)
+    return (out, acc, mins) if sums else out

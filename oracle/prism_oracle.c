@@ -1,0 +1,391 @@
+/*
+ * prism_oracle.c -- CPU restatement of StartLux-Prism's quantized linear-layer arithmetic.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the checker the HIP kernels are compared against; it is never part of
+ * the product path.  Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg load it.
+ *
+ * Every function cites the reference file:line whose arithmetic it restates (paths relative to the
+ * StartLux-Prism source tree).  Build: oracle/Makefile (gcc -O3 -fopenmp -ffp-contract=off: no fused
+ * multiply-adds except where the reference asks for one with an explicit fma).
+ *
+ * Conventions shared with the GPU library:
+ *   bf16 / fp16 values travel as uint16_t bit patterns; conversions to them round to nearest even.
+ *   "live" rows: rows >= live are neither computed nor written (kernels/w8a8.py:44-46, 77-80).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define EXPORT __attribute__((visibility("default")))
+
+/* ------------------------------------------------------------------------------------------- float formats */
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+EXPORT float orc_bf16_to_float(uint16_t h) { return u2f((uint32_t)h << 16); }
+
+/* fp32 -> bf16, round to nearest even; NaN stays a quiet NaN (torch's .to(torch.bfloat16)). */
+EXPORT uint16_t orc_float_to_bf16(float f) {
+    uint32_t u = f2u(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+EXPORT float orc_half_to_float(uint16_t h) {
+    uint32_t s = (uint32_t)(h & 0x8000u) << 16, e = (h >> 10) & 0x1f, m = h & 0x3ffu;
+    if (e == 0x1f) return u2f(s | 0x7f800000u | (m << 13));
+    if (e == 0) {                                   /* zero or subnormal: m * 2^-24, exact in fp32 */
+        float v = (float)m * 0x1p-24f;
+        return s ? -v : v;
+    }
+    return u2f(s | ((e + 112) << 23) | (m << 13));
+}
+
+/* fp32 -> fp16, round to nearest even, overflow to inf (numpy / torch .half()). */
+EXPORT uint16_t orc_float_to_half(float f) {
+    uint32_t u = f2u(f), s = (u >> 16) & 0x8000u, a = u & 0x7fffffffu;
+    if (a > 0x7f800000u) return (uint16_t)(s | 0x7e00u);
+    if (a >= 0x477ff000u) return (uint16_t)(s | 0x7c00u);        /* >= 65520 rounds to inf */
+    if (a < 0x38800000u) {                                         /* below 2^-14: subnormal half */
+        /* value = a_f; half subnormal unit 2^-24: q = rint(a_f * 2^24) (exact scaling, one rounding) */
+        float v = u2f(a) * 0x1p24f;
+        return (uint16_t)(s | (uint32_t)rintf(v));
+    }
+    uint32_t e = (a >> 23) - 112, m = a & 0x7fffffu;
+    uint32_t h = (e << 10) | (m >> 13), rest = m & 0x1fffu;
+    if (rest > 0x1000u || (rest == 0x1000u && (h & 1u))) h++;
+    return (uint16_t)(s | h);
+}
+
+static inline int nthreads_or(int n) {
+#ifdef _OPENMP
+    return n > 0 ? n : omp_get_max_threads();
+#else
+    (void)n;
+    return 1;
+#endif
+}
+
+/* ----------------------------------------------------------------------------------------------- Q8_0 */
+/*
+ * Q8_0 quantizer: gguf_weights.py:121-133 (KQuant.as_q8) -- per 32 values dh = fp16(amax / 127),
+ * inv = 1 / float(dh) (0 when dh == 0), q = clamp(round(w * inv), -127, 127), round half to even.
+ * w fp32 [N, K] -> qs int8 [N, K], d fp16 [N, K / 32].
+ */
+EXPORT void orc_q8_0_quantize(const float* w, int64_t N, int64_t K, int8_t* qs, uint16_t* d, int nthreads) {
+    int64_t G = K / 32;
+#pragma omp parallel for num_threads(nthreads_or(nthreads)) schedule(static)
+    for (int64_t n = 0; n < N; n++) {
+        for (int64_t g = 0; g < G; g++) {
+            const float* x = w + n * K + g * 32;
+            float amax = 0.f;
+            for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(x[i]));
+            uint16_t dh = orc_float_to_half(amax / 127.0f);
+            float df = orc_half_to_float(dh);
+            float inv = df > 0.f ? 1.0f / df : 0.f;
+            for (int i = 0; i < 32; i++) {
+                float q = rintf(x[i] * inv);
+                q = q > 127.f ? 127.f : (q < -127.f ? -127.f : q);
+                qs[n * K + g * 32 + i] = (int8_t)q;
+            }
+            d[n * G + g] = dh;
+        }
+    }
+}
+
+/*
+ * Per-token int8 activation quantization: kernels/quant.py:287-309 (_rows_q8_kernel; MODE 0):
+ * y = x * inv_s (inv_s NULL: y = x), scale = max(amax(|y|), 1e-10) / 127, q = rint(y / scale).
+ * Both divisions are IEEE (correctly rounded), the convention of kernels/quant.py:320-321 and w4a8.py:151.
+ * x bf16 [M, K] with row stride ldx -> q int8 [M, K], s fp32 [M].  Rows >= live are untouched.
+ */
+EXPORT void orc_quant_rows_i8(const uint16_t* x, int64_t ldx, const float* inv_s, int64_t M, int64_t K,
+                              int64_t live, int8_t* q, float* s, int nthreads) {
+    (void)M;
+#pragma omp parallel for num_threads(nthreads_or(nthreads)) schedule(static)
+    for (int64_t m = 0; m < live; m++) {
+        float amax = 0.f;
+        for (int64_t k = 0; k < K; k++) {
+            float y = orc_bf16_to_float(x[m * ldx + k]);
+            if (inv_s) y = y * inv_s[k];
+            amax = fmaxf(amax, fabsf(y));
+        }
+        float scale = fmaxf(amax, 1e-10f) / 127.0f;
+        for (int64_t k = 0; k < K; k++) {
+            float y = orc_bf16_to_float(x[m * ldx + k]);
+            if (inv_s) y = y * inv_s[k];
+            q[m * K + k] = (int8_t)rintf(y / scale);
+        }
+        s[m] = scale;
+    }
+}
+
+/*
+ * Per-(row, group) int8 quantization: kernels/w8a8.py:101-112 (_quant_rows_kernel) and quant_rows (:264-271):
+ * per gk inputs scale = max(amax, 1e-10) / 127, q = rint(x / scale).  x bf16 [M, K] -> q [M, K], s fp32 [M, K/gk].
+ */
+EXPORT void orc_quant_rows_groups(const uint16_t* x, int64_t M, int64_t K, int64_t gk, int64_t live, int8_t* q,
+                                  float* s, int nthreads) {
+    (void)M;
+    int64_t G = K / gk;
+#pragma omp parallel for num_threads(nthreads_or(nthreads)) schedule(static)
+    for (int64_t m = 0; m < live; m++) {
+        for (int64_t g = 0; g < G; g++) {
+            float amax = 0.f;
+            for (int64_t k = g * gk; k < (g + 1) * gk; k++) amax = fmaxf(amax, fabsf(orc_bf16_to_float(x[m * K + k])));
+            float scale = fmaxf(amax, 1e-10f) / 127.0f;
+            for (int64_t k = g * gk; k < (g + 1) * gk; k++)
+                q[m * K + k] = (int8_t)rintf(orc_bf16_to_float(x[m * K + k]) / scale);
+            s[m * G + g] = scale;
+        }
+    }
+}
+
+static inline int32_t dot_i8(const int8_t* a, const int8_t* b, int64_t n) {
+    int32_t acc = 0;
+    for (int64_t i = 0; i < n; i++) acc += (int32_t)a[i] * (int32_t)b[i];
+    return acc;
+}
+
+/* The int32 dot product of every (row, column, group): P[m, n, g] = sum_{k in g} a[m, k] w[n, k]
+ * (kernels/w8a8.py:66-73, tl.dot int8 -> int32).  For tests on small shapes. */
+EXPORT void orc_w8a8_block_sums(const int8_t* a, const int8_t* w, int64_t M, int64_t N, int64_t K, int64_t gk,
+                                int32_t* P) {
+    int64_t G = K / gk;
+    for (int64_t m = 0; m < M; m++)
+        for (int64_t n = 0; n < N; n++)
+            for (int64_t g = 0; g < G; g++) P[(m * N + n) * G + g] = dot_i8(a + m * K + g * gk, w + n * K + g * gk, gk);
+}
+
+/*
+ * W8A8 GEMM with per-group scales along K: kernels/w8a8.py:64-85 (_w8a8_kernel, EPI 0 and 1).
+ *   per group g in increasing order: P = sum_{k in g} a w (int32, exact);
+ *                                    y = RN(y + RN(RN(float(P) * sa[m, g]) * sw[n, g]))     (:74-76)
+ *   epi 0: out bf16 = RN_bf16(y) (:78-80);  epi 1: out fp32 = RN(out + y) (:81-85).
+ * a int8 [M, K]; a_s fp32 with element (m, g) at a_s[m * as_sm + g * as_sg] (as_sg = 0: one scale per token);
+ * w int8 [N, K]; w_s per (n, g) at w_s[n * (K/gk) + g], fp16 bits when ws_fp16 else fp32
+ * (Q8_0's fp16 block scale as fp32 is exact: w8a8.py:277-278).  out row stride ldo (elements).
+ */
+EXPORT void orc_w8a8_gemm(const int8_t* a, const float* a_s, int64_t as_sm, int64_t as_sg, const int8_t* w,
+                          const void* w_s, int ws_fp16, int64_t M, int64_t N, int64_t K, int64_t gk, int epi,
+                          void* out, int64_t ldo, int64_t live, int nthreads) {
+    (void)M;
+    int64_t G = K / gk;
+#pragma omp parallel for num_threads(nthreads_or(nthreads)) schedule(dynamic, 1)
+    for (int64_t m = 0; m < live; m++) {
+        for (int64_t n = 0; n < N; n++) {
+            float y = 0.f;
+            for (int64_t g = 0; g < G; g++) {
+                int32_t p = dot_i8(a + m * K + g * gk, w + n * K + g * gk, gk);
+                float sa = a_s[m * as_sm + g * as_sg];
+                float sw = ws_fp16 ? orc_half_to_float(((const uint16_t*)w_s)[n * G + g]) : ((const float*)w_s)[n * G + g];
+                float t = (float)p * sa;
+                t = t * sw;
+                y = y + t;
+            }
+            if (epi == 0)
+                ((uint16_t*)out)[m * ldo + n] = orc_float_to_bf16(y);
+            else {
+                float* o = (float*)out + m * ldo + n;
+                *o = *o + y;
+            }
+        }
+    }
+}
+
+/* ----------------------------------------------------------------------------------------------- Q4_K */
+/*
+ * A Q4_K quantizer of this build's own (the reference only reads Q4_K from files: gguf_weights.py:100-133).
+ * Per 256-value super-block: per sub-block j of 32, lo_j = min(0, min x), hi_j = max x, scale_j = (hi_j - lo_j)/15,
+ * min_j = -lo_j; d = fp16(max scale_j / 63), dmin = fp16(max min_j / 63); sc_j = clamp(rint(scale_j / d), 0, 63),
+ * m_j = clamp(rint(min_j / dmin), 0, 63); q = clamp(rint((x + dmin m_j) / (d sc_j)), 0, 15).
+ * Output: GGUF block_q4_K bytes [N, K/256, 144]: d, dmin (fp16 LE), scales[12] in ggml's 6-bit packing
+ * (inverse of get_scale_min_k4, gguf_weights.py:56-60), qs[128] (per 32 bytes: low nibbles sub-block 2c, high
+ * nibbles 2c + 1: gguf_weights.py:63-70).
+ */
+EXPORT void orc_q4k_quantize(const float* w, int64_t N, int64_t K, uint8_t* blocks, int nthreads) {
+    int64_t NB = K / 256;
+#pragma omp parallel for num_threads(nthreads_or(nthreads)) schedule(static)
+    for (int64_t n = 0; n < N; n++) {
+        for (int64_t b = 0; b < NB; b++) {
+            const float* x = w + n * K + b * 256;
+            uint8_t* o = blocks + (n * NB + b) * 144;
+            float scale[8], mn[8], smax = 0.f, mmax = 0.f;
+            for (int j = 0; j < 8; j++) {
+                float lo = 0.f, hi = -INFINITY;
+                for (int i = 0; i < 32; i++) { lo = fminf(lo, x[32 * j + i]); hi = fmaxf(hi, x[32 * j + i]); }
+                if (hi < lo) hi = lo;
+                scale[j] = (hi - lo) / 15.f;
+                mn[j] = -lo;
+                smax = fmaxf(smax, scale[j]);
+                mmax = fmaxf(mmax, mn[j]);
+            }
+            uint16_t dh = orc_float_to_half(smax / 63.f), dmh = orc_float_to_half(mmax / 63.f);
+            float d = orc_half_to_float(dh), dmin = orc_half_to_float(dmh);
+            uint8_t sc[8], m[8];
+            for (int j = 0; j < 8; j++) {
+                float s = d > 0.f ? rintf(scale[j] / d) : 0.f, t = dmin > 0.f ? rintf(mn[j] / dmin) : 0.f;
+                sc[j] = (uint8_t)(s < 0.f ? 0.f : (s > 63.f ? 63.f : s));
+                m[j] = (uint8_t)(t < 0.f ? 0.f : (t > 63.f ? 63.f : t));
+            }
+            o[0] = dh & 0xff; o[1] = dh >> 8; o[2] = dmh & 0xff; o[3] = dmh >> 8;
+            uint8_t* s12 = o + 4;
+            for (int j = 0; j < 4; j++) {
+                s12[j] = (uint8_t)((sc[j] & 63) | ((sc[j + 4] >> 4) << 6));
+                s12[j + 4] = (uint8_t)((m[j] & 63) | ((m[j + 4] >> 4) << 6));
+                s12[j + 8] = (uint8_t)((sc[j + 4] & 0xf) | ((m[j + 4] & 0xf) << 4));
+            }
+            uint8_t qv[256];
+            for (int j = 0; j < 8; j++) {
+                float step = d * (float)sc[j], off = dmin * (float)m[j];
+                for (int i = 0; i < 32; i++) {
+                    float q = step > 0.f ? rintf((x[32 * j + i] + off) / step) : 0.f;
+                    qv[32 * j + i] = (uint8_t)(q < 0.f ? 0.f : (q > 15.f ? 15.f : q));
+                }
+            }
+            for (int c = 0; c < 4; c++)
+                for (int t = 0; t < 32; t++) o[16 + 32 * c + t] = (uint8_t)(qv[64 * c + t] | (qv[64 * c + 32 + t] << 4));
+        }
+    }
+}
+
+/* get_scale_min_k4: gguf_weights.py:56-60. */
+static void scale_min_k4(const uint8_t* s, uint8_t* sc, uint8_t* mn) {
+    for (int j = 0; j < 4; j++) {
+        sc[j] = s[j] & 63;
+        mn[j] = s[j + 4] & 63;
+        sc[j + 4] = (uint8_t)((s[j + 8] & 0xf) | ((s[j] >> 6) << 4));
+        mn[j + 4] = (uint8_t)((s[j + 8] >> 4) | ((s[j + 4] >> 6) << 4));
+    }
+}
+
+/* Q4_K dequantization: gguf_weights.py:63-70 (_dq_q4_k), y = (d sc) q - (dmin m), products and difference in fp32. */
+EXPORT void orc_q4k_dequant(const uint8_t* blocks, int64_t N, int64_t K, float* w) {
+    int64_t NB = K / 256;
+    for (int64_t n = 0; n < N; n++)
+        for (int64_t b = 0; b < NB; b++) {
+            const uint8_t* o = blocks + (n * NB + b) * 144;
+            float d = orc_half_to_float((uint16_t)(o[0] | (o[1] << 8))), dmin = orc_half_to_float((uint16_t)(o[2] | (o[3] << 8)));
+            uint8_t sc[8], mn[8];
+            scale_min_k4(o + 4, sc, mn);
+            for (int j = 0; j < 8; j++) {
+                float a = d * (float)sc[j], c = dmin * (float)mn[j];
+                for (int t = 0; t < 32; t++) {
+                    uint8_t byte = o[16 + 32 * (j / 2) + t];
+                    float q = (float)((j & 1) ? (byte >> 4) : (byte & 0xf));
+                    w[n * K + b * 256 + 32 * j + t] = a * q - c;
+                }
+            }
+        }
+}
+
+/*
+ * Q4_K -> the W4 layout the GEMM reads: kernels/w4a8.py:44-81 (W4, repack).
+ *   q uint8 [N, K/2]: per 32 inputs 16 bytes, byte t = q[t] | q[t + 16] << 4 (values in k order);
+ *   sc, mn uint8 [K/256, N, 8]; d, dm fp32 [K/256, N] (super-block-major).
+ */
+EXPORT void orc_q4k_repack(const uint8_t* blocks, int64_t N, int64_t K, uint8_t* q, uint8_t* sc, uint8_t* mn,
+                           float* d, float* dm) {
+    int64_t NB = K / 256;
+    for (int64_t n = 0; n < N; n++)
+        for (int64_t b = 0; b < NB; b++) {
+            const uint8_t* o = blocks + (n * NB + b) * 144;
+            d[b * N + n] = orc_half_to_float((uint16_t)(o[0] | (o[1] << 8)));
+            dm[b * N + n] = orc_half_to_float((uint16_t)(o[2] | (o[3] << 8)));
+            scale_min_k4(o + 4, sc + (b * N + n) * 8, mn + (b * N + n) * 8);
+            for (int j = 0; j < 8; j++) {
+                uint8_t v[32];
+                for (int t = 0; t < 32; t++) {
+                    uint8_t byte = o[16 + 32 * (j / 2) + t];
+                    v[t] = (j & 1) ? (byte >> 4) : (byte & 0xf);
+                }
+                for (int t = 0; t < 16; t++) q[n * (K / 2) + b * 128 + j * 16 + t] = (uint8_t)(v[t] | (v[t + 16] << 4));
+            }
+        }
+}
+
+/*
+ * W4A8 activation producer: kernels/w4a8.py:144-155 (quantize_ref) = kernels/quant.py:314-330 (_store_g).
+ * x fp32 [M, K] (the bf16 input, widened); per `group` inputs (256 in the reference; K for one scale per token)
+ * a = max(amax, 1e-10) / 127 (true division), xq = rint(x / a) (true division); per 32 inputs the int32 sum S of
+ * xq, stored as eight S & 63 then eight S >> 6 per 256 inputs.
+ * Outputs: xq int8 [M, K]; a fp32 [K/group, M]; xs int8 [K/256, M, 16].  Rows >= live untouched.
+ */
+EXPORT void orc_quant_rows_g(const float* x, int64_t M, int64_t K, int64_t group, int64_t live, int8_t* xq, float* a,
+                             int8_t* xs, int nthreads) {
+    int64_t G = K / group, NB = K / 256;
+#pragma omp parallel for num_threads(nthreads_or(nthreads)) schedule(static)
+    for (int64_t m = 0; m < live; m++) {
+        for (int64_t g = 0; g < G; g++) {
+            float amax = 0.f;
+            for (int64_t k = g * group; k < (g + 1) * group; k++) amax = fmaxf(amax, fabsf(x[m * K + k]));
+            float sc = fmaxf(amax, 1e-10f) / 127.0f;
+            for (int64_t k = g * group; k < (g + 1) * group; k++) xq[m * K + k] = (int8_t)rintf(x[m * K + k] / sc);
+            a[g * M + m] = sc;
+        }
+        for (int64_t b = 0; b < NB; b++)
+            for (int j = 0; j < 8; j++) {
+                int32_t S = 0;
+                for (int t = 0; t < 32; t++) S += xq[m * K + b * 256 + 32 * j + t];
+                xs[(b * M + m) * 16 + j] = (int8_t)(S & 63);
+                xs[(b * M + m) * 16 + 8 + j] = (int8_t)(S >> 6);
+            }
+    }
+}
+
+/*
+ * W4A8 GEMM on Q4_K: kernels/w4a8.py:14-22 (arithmetic) and :177-199 (gemm_ref), per super-block b in order:
+ *   acc  = sum_g sc[b,n,g] * (xq . q)_g            int32, exact
+ *   mins = sum_g mn[b,n,g] * S[m, 8b + g]           int32, exact (S = (xs & 63 part) + 64 * (xs >> 6 part), :158-161)
+ *   t = RN(d[b,n] * float(acc));  t = fma(-dm[b,n], float(mins), t);  y = fma(a[b,m], t, y)
+ * then epi 0: bf16(y); epi 1: out = RN(out + y).  fma32 (:164-174) is IEEE fma: C fmaf.
+ * a fp32: element (b, m) at a[b * a_sb + m] (a_sb = 0: one scale per token).
+ * acc_out / mins_out (nullable) receive the int32 super-block sums [M, N, K/256] for bit-exactness tests.
+ */
+EXPORT void orc_w4a8_gemm(const int8_t* xq, const float* a, int64_t a_sb, const int8_t* xs, const uint8_t* q,
+                          const uint8_t* sc, const uint8_t* mn, const float* d, const float* dm, int64_t M, int64_t N,
+                          int64_t K, int epi, void* out, int64_t ldo, int64_t live, int32_t* acc_out,
+                          int32_t* mins_out, int nthreads) {
+    int64_t NB = K / 256;
+#pragma omp parallel for num_threads(nthreads_or(nthreads)) schedule(dynamic, 1)
+    for (int64_t m = 0; m < live; m++) {
+        int8_t qv[256];
+        for (int64_t n = 0; n < N; n++) {
+            float y = 0.f;
+            for (int64_t b = 0; b < NB; b++) {
+                const uint8_t* qb = q + n * (K / 2) + b * 128;
+                for (int j = 0; j < 8; j++)
+                    for (int t = 0; t < 16; t++) {
+                        qv[32 * j + t] = (int8_t)(qb[16 * j + t] & 0xf);
+                        qv[32 * j + 16 + t] = (int8_t)(qb[16 * j + t] >> 4);
+                    }
+                int32_t acc = 0, mins = 0;
+                const int8_t* xb = xs + (b * M + m) * 16;
+                for (int j = 0; j < 8; j++) {
+                    acc += (int32_t)sc[(b * N + n) * 8 + j] * dot_i8(xq + m * K + b * 256 + 32 * j, qv + 32 * j, 32);
+                    int32_t S = (int32_t)xb[j] + 64 * (int32_t)xb[8 + j];
+                    mins += (int32_t)mn[(b * N + n) * 8 + j] * S;
+                }
+                if (acc_out) acc_out[(m * N + n) * NB + b] = acc;
+                if (mins_out) mins_out[(m * N + n) * NB + b] = mins;
+                float t = d[b * N + n] * (float)acc;
+                t = fmaf(-dm[b * N + n], (float)mins, t);
+                y = fmaf(a[b * a_sb + m], t, y);
+            }
+            if (epi == 0)
+                ((uint16_t*)out)[m * ldo + n] = orc_float_to_bf16(y);
+            else {
+                float* o = (float*)out + m * ldo + n;
+                *o = *o + y;
+            }
+        }
+    }
+}
+
+EXPORT double orc_fmaf(float a, float b, float c) { return (double)fmaf(a, b, c); }

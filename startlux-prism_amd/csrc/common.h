@@ -1,0 +1,64 @@
+// Shared device helpers for the gfx950 kernels: float-format conversions with explicit rounding, wave
+// reductions, MFMA operand types and the launch-status plumbing of the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/prism_amd.h"
+
+namespace prism {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+// fp32 -> bf16 bits, round to nearest even; NaN kept quiet (the same rule as torch's .to(torch.bfloat16)).
+__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
+// fp16 bits -> fp32 (exact).
+__device__ __forceinline__ float f16_to_f32(uint32_t h) {
+    _Float16 v = __builtin_bit_cast(_Float16, (uint16_t)h);
+    return (float)v;
+}
+
+// IEEE (correctly rounded) fp32 division; the library is built with -fhip-fp32-correctly-rounded-divide-sqrt,
+// so '/' is the IEEE operation, written through one helper so every kernel rounds alike.
+__device__ __forceinline__ float div_rn(float a, float b) { return __fdiv_rn(a, b); }
+
+// Explicitly rounded fp32 multiply / add: the compiler never contracts these into an fma.
+__device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
+__device__ __forceinline__ float add_rn(float a, float b) { return __fadd_rn(a, b); }
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+    return v;
+}
+
+__device__ __forceinline__ int wave_sum_width(int v, int width) {
+    for (int o = width / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+
+}  // namespace prism
+
+// Launch-status helper for the C ABI: a rejected launch becomes PRISM_ERR_LAUNCH.
+#define PRISM_LAUNCH_CHECK()                                                        \
+    do {                                                                            \
+        hipError_t _e = hipGetLastError();                                          \
+        if (_e != hipSuccess) return PRISM_ERR_LAUNCH;                             \
+    } while (0)
+
+#define PRISM_ALIGNED(p, n) ((((uintptr_t)(p)) & ((n) - 1)) == 0)

@@ -1,0 +1,90 @@
+"""W8A8 projections on gfx950: int8 x int8 MFMA GEMMs with per-group scales along K and fused epilogues.
+
+Drop-in for StartLux-Prism kernels/w8a8.py's engine entry points (gemm :183-231, quant_rows :264-271,
+weight_from_q8 :274-286) with the same argument names and meaning.  Arithmetic (kernels/w8a8.py:64-85): per group
+g of gk inputs, in increasing g, P = sum a w (int32, exact) and y = RN(y + RN(RN(float(P) * a_s[m, g]) * w_s[n, g]));
+epilogue 0 stores bf16(y), epilogue 1 adds y into an fp32 residual (out = RN(out + y)).  With gk = 32 the weights are
+Q8_0's own int8 values and fp16 block scales; with gk = K the per-channel form.
+
+Differences from the reference, by design of this single-GPU MI355X build:
+  * w_s may be the Q8_0 fp16 scales themselves (torch.float16 [N, K/32]); the kernels widen them exactly, so the
+    weight stream is 34 bytes per 32 weights instead of 36.
+  * a_s may be fp32 [M] (or [M, 1]): one activation scale per token, broadcast over the groups.
+  * No split-K: the kernels never defer a residual add, so gemm() always returns None (cfg / slots / pdl are
+    accepted and ignored).  Epilogues 2 (fused SwiGLU) and 3 (raw int32, tensor parallel) are not provided.
+"""
+from typing import NamedTuple
+
+import torch
+
+from . import _lib as L
+from .quant import quant_rows  # noqa: F401  (re-exported: kernels/w8a8.py:264)
+
+KERNELS = {"auto": -1, "tile": 0, "decode": 1}
+
+
+class Deferred(NamedTuple):
+    """The reference's deferred split-K residual add (kernels/w8a8.py:171-180); never produced here."""
+    n: int
+    a_s: torch.Tensor
+    w_s: torch.Tensor
+    parts: torch.Tensor = None
+    sync: object = None
+
+
+def _scales_a(a_s, M, G):
+    """-> (tensor, stride per row, stride per group) of the activation scales."""
+    if a_s.dtype != torch.float32:
+        raise TypeError("a_s must be fp32")
+    if a_s.dim() == 1:
+        if a_s.shape[0] < M:
+            raise ValueError("a_s [M] too short")
+        return a_s, a_s.stride(0), 0
+    if a_s.shape[0] < M or a_s.shape[1] not in (1, G):
+        raise ValueError(f"a_s must be [M], [M, 1] or [M, {G}], got {tuple(a_s.shape)}")
+    return a_s, a_s.stride(0), (0 if a_s.shape[1] == 1 else a_s.stride(1))
+
+
+def gemm(a, a_s, w, w_s, out, n_rows, gk, epi=0, outs=None, cfg=None, slots=None, pdl=False, kernel="auto"):
+    """a int8 [M, K], a_s fp32 [M] / [M, 1] / [M, K/gk], w int8 [N, K], w_s fp16 or fp32 [N, K/gk] -> out
+    (epi 0: bf16 [M, >=N] row stride out.stride(0); epi 1: fp32, out += y).  n_rows: device int32 [1], rows >=
+    n_rows[0] untouched.  Returns None (no deferred split-K)."""
+    if epi not in (0, 1):
+        raise NotImplementedError(f"epilogue {epi}: only 0 (bf16 store) and 1 (fp32 residual add) are provided")
+    M, K = a.shape
+    N = w.shape[0]
+    if w.shape[1] != K or a.dtype != torch.int8 or w.dtype != torch.int8:
+        raise ValueError("a int8 [M, K] and w int8 [N, K] expected")
+    if not (a.is_contiguous() and w.is_contiguous()):
+        raise ValueError("a and w must be contiguous (K-major)")
+    if gk <= 0 or K % gk:
+        raise ValueError("gk must divide K")
+    G = K // gk
+    a_s, as_sm, as_sg = _scales_a(a_s, M, G)
+    if w_s.dtype not in (torch.float16, torch.float32) or tuple(w_s.shape) != (N, G) or not w_s.is_contiguous():
+        raise ValueError(f"w_s must be contiguous fp16/fp32 [{N}, {G}]")
+    want = torch.bfloat16 if epi == 0 else torch.float32
+    if out.dtype != want or out.shape[0] < M or out.shape[1] < N or out.stride(1) != 1:
+        raise ValueError(f"out must be {want} [>= {M}, >= {N}] with unit column stride")
+    if n_rows.dtype != torch.int32:
+        raise ValueError("n_rows must be int32")
+    L.call("prism_w8a8_gemm", L.ptr(a), L.ptr(a_s), as_sm, as_sg, L.ptr(w), L.ptr(w_s),
+           int(w_s.dtype == torch.float16), L.ptr(out), out.stride(0), L.ptr(n_rows), M, N, K, gk, epi,
+           KERNELS[kernel], L.stream_of(a))
+    return None
+
+
+def weight_from_q8(q8, gk, smooth=None):
+    """Q8_0 matrix -> (int8 [N, K], scales [N, K/gk]) (kernels/w8a8.py:274-286).  gk == 32 keeps the Q8_0 values
+    and returns the fp16 block scales as they are (the GEMM reads fp16 scales directly, exactly); otherwise the
+    weights are requantized per gk inputs as the reference does (fp32 scales)."""
+    if gk == 32 and smooth is None:
+        return q8.qs.contiguous(), q8.d.contiguous()
+    w = q8.dequant(torch.float32)
+    if smooth is not None:
+        w = w * smooth[None, :]
+    N, K = w.shape
+    g = w.view(N, K // gk, gk)
+    s = g.abs().amax(-1).clamp_min(1e-10) / 127.0
+    q = torch.round(g / s[..., None]).clamp(-127, 127).to(torch.int8).view(N, K)
+    return q.contiguous(), s.contiguous()

@@ -1,0 +1,27 @@
+"""Seeded CPU inputs shared by the tests (numpy PCG64), following the value distributions of the benchmark
+configs: weights fp32 N(0, 0.02^2) quantized to Q8_0 / Q4_K, activations N(0, 1) rounded to bf16."""
+import numpy as np
+
+import oracle as O
+
+
+def rng(seed):
+    return np.random.default_rng(seed)
+
+
+def weights_f32(N, K, seed, std=0.02):
+    return (rng(seed).standard_normal((N, K), dtype=np.float32) * np.float32(std)).astype(np.float32)
+
+
+def acts_bf16(M, K, seed, std=1.0):
+    """bf16 bit patterns uint16 [M, K]."""
+    x = rng(seed).standard_normal((M, K), dtype=np.float32) * np.float32(std)
+    return O.bf16_bits(x)
+
+
+def q8_weights(N, K, seed):
+    return O.q8_0_quantize(weights_f32(N, K, seed))
+
+
+def int8_acts(M, K, seed):
+    return O.quant_rows_i8(acts_bf16(M, K, seed))

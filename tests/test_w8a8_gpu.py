@@ -1,0 +1,170 @@
+"""GPU parity of the per-token activation quantizer and the Q8_0 / per-channel W8A8 GEMM against the CPU oracle.
+
+Bit-exact throughout: int8 values and fp32 scales of the quantizer; the int32 block sums (checked through outputs
+whose fp32 arithmetic is exact); bf16 outputs and fp32 residual adds of every kernel (decode and tile), for the
+benchmark's config 0 (M = 16, K = N = 4096) and ragged / live-row / odd-K cases, as the reference's
+tests/test_cuda_gemm.py checks every kernel config against one set of bits."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from _inputs import acts_bf16, q8_weights, rng
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(x, dev, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+    return t if dtype is None else t.view(dtype)
+
+
+def _live(n, dev):
+    return torch.tensor([n], dtype=torch.int32, device=dev)
+
+
+@pytest.mark.parametrize("M,K,live", [(16, 4096, 16), (5, 5120, 3), (33, 17408, 33), (1, 256, 1), (64, 128, 50)])
+def test_rows_q8_bit_exact(dev, M, K, live):
+    from prism_amd import quant as KQ
+    x = acts_bf16(M, K, seed=M * 7 + K)
+    if M > 2:
+        x[1] = 0
+        x[2, 3] = O.bf16_bits(np.array([77.0], np.float32))[0]
+    xd = _t(x, dev, torch.bfloat16)
+    q = torch.full((M, K), 99, dtype=torch.int8, device=dev)
+    s = torch.full((M,), -1.0, dtype=torch.float32, device=dev)
+    KQ.rows_q8(xd, None, q, s, _live(live, dev), M)
+    rq, rs = O.quant_rows_i8(x, live=live)
+    torch.cuda.synchronize()
+    assert np.array_equal(q.cpu().numpy()[:live], rq[:live])
+    assert np.array_equal(s.cpu().numpy()[:live], rs[:live])
+    assert (q[live:] == 99).all() and (s[live:] == -1).all()          # rows >= live untouched
+    inv = (rng(K).random(K).astype(np.float32) + 0.5)
+    KQ.rows_q8(xd, _t(inv, dev), q, s, _live(live, dev), M)
+    rq, rs = O.quant_rows_i8(x, inv_s=inv, live=live)
+    assert np.array_equal(q.cpu().numpy()[:live], rq[:live]) and np.array_equal(s.cpu().numpy()[:live], rs[:live])
+
+
+@pytest.mark.parametrize("gk", [32, 64, 256, 1024, 96])
+def test_quant_rows_groups_bit_exact(dev, gk):
+    from prism_amd import quant as KQ
+    K = 3072 if gk == 96 else 4096
+    x = acts_bf16(7, K, seed=gk)
+    q, s = KQ.quant_rows(_t(x, dev, torch.bfloat16), gk)
+    rq, rs = O.quant_rows_groups(x, gk)
+    assert np.array_equal(q.cpu().numpy(), rq) and np.array_equal(s.cpu().numpy(), rs)
+
+
+def _gemm(dev, a, s, qs, d, gk, epi, kernel, live=None, out0=None, ldo=None, as_group=False):
+    from prism_amd import w8a8 as KW
+    M, K = a.shape
+    N = qs.shape[0]
+    live = M if live is None else live
+    ad, wd = _t(a, dev), _t(qs, dev)
+    sd = _t(s, dev)
+    wsd = _t(d, dev, torch.float16) if d.dtype == np.uint16 else _t(d, dev)
+    ldo = N if ldo is None else ldo
+    if epi == 0:
+        out = torch.full((M, ldo), 7, dtype=torch.int16, device=dev).view(torch.bfloat16)
+    else:
+        out = _t(out0, dev).clone()
+    KW.gemm(ad, sd, wd, wsd, out, _live(live, dev), gk, epi=epi, kernel=kernel)
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("kernel", ["decode", "tile"])
+def test_config0_bit_exact(dev, kernel):
+    """M = 16, K = N = 4096, Q8_0 gk = 32, per-token scales, bf16 out."""
+    qs, d = q8_weights(4096, 4096, seed=0)
+    a, s = O.quant_rows_i8(acts_bf16(16, 4096, seed=100))
+    want = O.w8a8_gemm(a, s, qs, d, 32, epi=0)
+    got = _gemm(dev, a, s, qs, d, 32, 0, kernel)
+    assert np.array_equal(got.view(torch.int16).cpu().numpy().view(np.uint16), want)
+
+
+CASES = [  # (M, N, K, live)
+    (1, 16, 32, 1), (3, 48, 96, 2), (16, 256, 512, 16), (17, 64, 4096, 17), (33, 128, 1024, 20), (64, 80, 2048, 64),
+    (100, 272, 640, 77), (130, 256, 1024, 130), (256, 384, 5120, 256),
+]
+
+
+@pytest.mark.parametrize("M,N,K,live", CASES)
+def test_gemm_cases_bit_exact(dev, M, N, K, live):
+    qs, d = q8_weights(N, K, seed=N + K)
+    a, s = O.quant_rows_i8(acts_bf16(M, K, seed=M + K))
+    want0 = O.w8a8_gemm(a, s, qs, d, 32, epi=0, live=live)
+    base = rng(M * N).standard_normal((M, N)).astype(np.float32)
+    want1 = O.w8a8_gemm(a, s, qs, d, 32, epi=1, out=base.copy(), live=live)
+    kernels = ["tile"] + (["decode"] if M <= 64 else [])
+    for kernel in kernels:
+        got0 = _gemm(dev, a, s, qs, d, 32, 0, kernel, live=live).view(torch.int16).cpu().numpy().view(np.uint16)
+        assert np.array_equal(got0[:live], want0[:live]), kernel
+        assert (got0[live:] == 7).all(), kernel                       # rows >= live untouched
+        got1 = _gemm(dev, a, s, qs, d, 32, 1, kernel, live=live, out0=base).cpu().numpy()
+        assert np.array_equal(got1, want1), kernel
+    # fp32 weight scales (the reference's w_s) give the same bits
+    dfl = d.view(np.float16).astype(np.float32)
+    got = _gemm(dev, a, s, qs, dfl, 32, 0, "tile", live=live).view(torch.int16).cpu().numpy().view(np.uint16)
+    assert np.array_equal(got[:live], want0[:live])
+
+
+@pytest.mark.parametrize("kernel", ["decode", "tile"])
+def test_strided_out_and_per_group_activation_scales(dev, kernel):
+    M, N, K = 24, 96, 768
+    qs, d = q8_weights(N, K, seed=5)
+    x = acts_bf16(M, K, seed=6)
+    a, s = O.quant_rows_groups(x, 32)                       # one scale per (row, 32 inputs)
+    want = O.w8a8_gemm(a, s, qs, d, 32, epi=0)
+    got = _gemm(dev, a, s, qs, d, 32, 0, kernel, ldo=N + 32)
+    g = got.view(torch.int16).cpu().numpy().view(np.uint16)
+    assert np.array_equal(g[:, :N], want) and (g[:, N:] == 7).all()
+
+
+def test_int32_block_sums_exact(dev):
+    """With unit scales the fp32 arithmetic is exact, so the output is the int32 sum itself: K = 32 gives one
+    block's sum, gk = K the whole-row sum (|P| < 2^24)."""
+    g = rng(3)
+    for K, gk in ((32, 32), (1024, 1024), (64, 32)):
+        a = g.integers(-127, 128, (40, K), dtype=np.int8)
+        w = g.integers(-127, 128, (64, K), dtype=np.int8)
+        ones_a = np.ones(40, np.float32)
+        ones_w = np.ones((64, K // gk), np.float32)
+        P = a.astype(np.int64) @ w.astype(np.int64).T
+        for kernel in (["tile", "decode"] if gk == 32 else ["tile"]):
+            got = _gemm(dev, a, ones_a, w, ones_w, gk, 1, kernel, out0=np.zeros((40, 64), np.float32)).cpu().numpy()
+            assert np.array_equal(got.astype(np.int64), P), (K, gk, kernel)
+
+
+@pytest.mark.parametrize("M,N,K", [(16, 128, 4096), (200, 256, 5120), (64, 64, 256)])
+def test_per_channel_gk_equals_k(dev, M, N, K):
+    """gk = K (the engine's per-channel weights): one epilogue per output."""
+    g = rng(K)
+    a = g.integers(-127, 128, (M, K), dtype=np.int8)
+    w = g.integers(-127, 128, (N, K), dtype=np.int8)
+    sa = (g.random(M) * 1e-2).astype(np.float32)
+    sw = (g.random((N, 1)) * 1e-3).astype(np.float32)
+    want = O.w8a8_gemm(a, sa, w, sw, K, epi=0)
+    got = _gemm(dev, a, sa, w, sw, K, 0, "tile").view(torch.int16).cpu().numpy().view(np.uint16)
+    assert np.array_equal(got, want)
+
+
+def test_repeat_runs_identical(dev):
+    qs, d = q8_weights(512, 2048, seed=9)
+    a, s = O.quant_rows_i8(acts_bf16(48, 2048, seed=10))
+    outs = [_gemm(dev, a, s, qs, d, 32, 0, k).view(torch.int16).cpu() for k in ("decode", "tile", "decode", "tile")]
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0])
+
+
+def test_bad_arguments_raise(dev):
+    from prism_amd import w8a8 as KW
+    from prism_amd._lib import PrismError
+    a = torch.zeros(4, 48, dtype=torch.int8, device=dev)       # K = 48: not a multiple of 32
+    w = torch.zeros(16, 48, dtype=torch.int8, device=dev)
+    with pytest.raises((PrismError, ValueError)):
+        KW.gemm(a, torch.ones(4, device=dev), w, torch.ones(16, 1, device=dev), torch.empty(4, 16, dtype=torch.bfloat16,
+                device=dev), _live(4, dev), 48)
+    with pytest.raises(NotImplementedError):
+        KW.gemm(a, torch.ones(4, device=dev), w, torch.ones(16, 1, device=dev), torch.empty(4, 16, dtype=torch.bfloat16,
+                device=dev), _live(4, dev), 48, epi=2)
