@@ -1,0 +1,213 @@
+"""Benchmark of the quantized linear-layer hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-sweep] [--no-cpu]
+
+Workload: Q8_0 W8A8 prefill GEMM, fused gate|up, M = 8192 tokens, K = 5120, N = 27648.  One step
+is the hot path over one batch: per-token int8 quantization of the bf16 activations (its own kernel), then the
+W8A8 GEMM on the Q8_0 weights (int8 values + fp16 block scales, gk = 32) into bf16.  Inputs are synthetic with the
+config's distributions (weights N(0, 0.02^2) quantized to Q8_0 on the GPU, activations N(0, 1) in bf16) and are
+resident in HBM before the timed region.  `value` is TOPS of the whole step (2 M N K / step time); `roofline`
+describes the GEMM kernel alone, timed with HIP events on the stream it is launched on, against the MI355X dense
+int8 MFMA peak (5.0 POPS).
+
+Also measured (key "sweep", not the headline): the decode shapes of config 2 (M in 1, 4, 16, 64; (K, N) =
+(5120, 5120) and (17408, 5120)) as GB/s of packed Q8_0 weight bytes, with weight copies rotated through more than
+3 x the 256 MB MALL so that every launch streams its weights from HBM.
+
+cpu_baseline: the CPU oracle (oracle/, the exact restatement of the reference's arithmetic, OpenMP) on a bounded
+row sample of the same workload, on this host's cores.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "startlux-prism_amd"))
+
+PEAK_INT8_TOPS = 5000.0      # MI355X dense int8 MFMA
+PEAK_HBM_GBS = 8000.0        # MI355X HBM3E
+MALL_BYTES = 256 << 20
+
+M1, K1, N1 = 8192, 5120, 27648
+
+
+def q8_bytes(N, K):
+    return N * K // 32 * 34
+
+
+def make_q8_weights(N, K, seed, dev):
+    import torch
+    from prism_amd import gguf_formats as GF
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    w = torch.randn(N, K, generator=g, device=dev, dtype=torch.float32) * 0.02
+    q8 = GF.quantize_q8_0(w)
+    del w
+    return q8.qs, q8.d
+
+
+def make_acts(M, K, seed, dev):
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    return torch.randn(M, K, generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+
+
+def bench_prefill(steps, warmup, dev):
+    import torch
+    from prism_amd import quant as KQ
+    from prism_amd import w8a8 as KW
+    qs, d = make_q8_weights(N1, K1, 1, dev)
+    x = make_acts(M1, K1, 2, dev)
+    q = torch.empty(M1, K1, dtype=torch.int8, device=dev)
+    s = torch.empty(M1, dtype=torch.float32, device=dev)
+    out = torch.empty(M1, N1, dtype=torch.bfloat16, device=dev)
+    n = torch.tensor([M1], dtype=torch.int32, device=dev)
+
+    def step():
+        KQ.rows_q8(x, None, q, s, n, M1)
+        KW.gemm(q, s, qs, d, out, n, 32, epi=0)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
+           torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    t0 = time.perf_counter()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for e0, e1, e2 in ev:
+        e0.record()
+        KQ.rows_q8(x, None, q, s, n, M1)
+        e1.record()
+        KW.gemm(q, s, qs, d, out, n, 32, epi=0)
+        e2.record()
+    stop.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    total_ms = start.elapsed_time(stop)
+    gemm_ms = sum(e1.elapsed_time(e2) for _, e1, e2 in ev) / steps
+    quant_ms = sum(e0.elapsed_time(e1) for e0, e1, _ in ev) / steps
+    ops = 2.0 * M1 * N1 * K1
+    res = dict(ms_per_step=total_ms / steps, wall_s=wall, gemm_ms=gemm_ms, quant_ms=quant_ms, ops=ops,
+               value=ops / (total_ms / steps * 1e-3) / 1e12)
+    sample = dict(q=q, s=s, qs=qs, d=d)
+    return res, sample
+
+
+def bench_decode_sweep(dev, iters=40):
+    """GB/s of packed Q8_0 weight bytes per decode shape, rotating > 3 x MALL of weight copies."""
+    import torch
+    from prism_amd import w8a8 as KW
+    rows = []
+    for (K, N) in ((5120, 5120), (17408, 5120)):
+        wbytes = q8_bytes(N, K)
+        copies = max(3, -(-3 * MALL_BYTES // wbytes))
+        base_qs, base_d = make_q8_weights(N, K, 3, dev)
+        ws = [(base_qs.clone(), base_d.clone()) for _ in range(copies)]
+        for M in (1, 4, 16, 64):
+            x = make_acts(M, K, 4, dev)
+            from prism_amd import quant as KQ
+            q = torch.empty(M, K, dtype=torch.int8, device=dev)
+            s = torch.empty(M, dtype=torch.float32, device=dev)
+            n = torch.tensor([M], dtype=torch.int32, device=dev)
+            KQ.rows_q8(x, None, q, s, n, M)
+            out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+            for i in range(copies):
+                KW.gemm(q, s, ws[i][0], ws[i][1], out, n, 32)
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for i in range(iters):
+                qs_, d_ = ws[i % copies]
+                KW.gemm(q, s, qs_, d_, out, n, 32)
+            b.record()
+            torch.cuda.synchronize()
+            us = a.elapsed_time(b) / iters * 1e3
+            gbs = wbytes / (us * 1e-6) / 1e9
+            rows.append(dict(M=M, K=K, N=N, us=round(us, 2), GBps=round(gbs, 1),
+                             hbm_frac=round(gbs / PEAK_HBM_GBS, 3), TOPS=round(2 * M * N * K / (us * 1e-6) / 1e12, 2)))
+        del ws
+        torch.cuda.empty_cache()
+    return rows
+
+
+def cpu_baseline(sample, rows):
+    """The oracle's exact W8A8 GEMM on the first `rows` rows of the same quantized activations and weights."""
+    import numpy as np
+    import oracle as O
+    a = sample["q"][:rows].cpu().numpy()
+    s = sample["s"][:rows].cpu().numpy()
+    w = sample["qs"].cpu().numpy()
+    d = sample["d"].view(__import__("torch").int16).cpu().numpy().view(np.uint16)
+    threads = min(os.cpu_count() or 1, 16)
+    O.lib()
+    t0 = time.perf_counter()
+    O.w8a8_gemm(a, s, w, d, 32, epi=0, nthreads=threads)
+    dt = time.perf_counter() - t0
+    ops = 2.0 * rows * N1 * K1
+    return dict(value=round(ops / dt / 1e12, 4), unit="TOPS", cores=threads, kind="port",
+                sample=f"{rows} of {M1} rows of config 1 (K={K1}, N={N1}), exact int32-per-block oracle, "
+                       f"{dt:.1f} s")
+
+
+def traffic_from_profiles():
+    """HBM bytes per launch of the GEMM from the committed rocprofv3 --pmc summary, if present."""
+    p = os.path.join(ROOT, "profiles", "w8a8_tile_prefill_traffic.json")
+    if os.path.exists(p):
+        try:
+            return json.load(open(p)).get("traffic_bytes")
+        except (OSError, ValueError):
+            return None
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-rows", type=int, default=2048)
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path (the hot path shards by output "
+              "columns with no exchange; see the sharding notes).  Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    res, sample = bench_prefill(a.steps, a.warmup, dev)
+    sweep = None if a.no_sweep else bench_decode_sweep(dev)
+    cpu = None if a.no_cpu else cpu_baseline(sample, a.cpu_rows)
+    achieved = res["ops"] / (res["gemm_ms"] * 1e-3) / 1e12
+    line = {
+        "metric": "W8A8/W4A8 GEMM TOPS and GB/s vs MI355X roofline, prefill M=8192 and decode M=1..64",
+        "value": round(res["value"], 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(res["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": "Q8_0 W8A8 prefill gate|up (config 1): rows_q8 + GEMM, gk=32, bf16 out",
+                   "M": M1, "K": K1, "N": N1, "gemm_ms": round(res["gemm_ms"], 4),
+                   "quant_ms": round(res["quant_ms"], 4)},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": traffic_from_profiles()},
+        "cpu_baseline": cpu,
+        "sweep": sweep,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -319,6 +319,151 @@ __global__ __launch_bounds__(256, 1) void w8a8_tile_kernel(const int8_t* __restr
         }
 }
 
+// ============================================================================================== Q8_0 tile kernel
+// The prefill path for gk = 32 with one activation scale per token and K % 128 == 0: one
+// v_mfma_i32_32x32x32_i8 per (32 x 32 tile, block) with a zero accumulator input, so each block's int32 sums come
+// out of the MFMA ready for the epilogue and nothing is carried between blocks but the fp32 sums y.  The exact
+// per-block epilogue (cvt, two multiplies, add: 4 VALU ops per output and block) is the bound of this kernel.
+//
+// Tile order: the hardware hands workgroup i to XCD i % 8.  Logical tile t = (i % 8) * (tiles / 8) + i / 8 gives
+// each XCD a contiguous range of tiles, walked in groups of 8 tile-rows (m fastest), so the workgroups that run
+// together on one XCD share 8 activation tiles and 8 weight tiles through that XCD's L2.
+__device__ __forceinline__ void tile_coords(int pid, int tiles_m, int tiles_n, int& pm, int& pn) {
+    const int total = tiles_m * tiles_n;
+    int t = pid;
+    if ((total & 7) == 0) t = (pid & 7) * (total >> 3) + (pid >> 3);
+    constexpr int GM = 8;
+    const int per_group = GM * tiles_n;
+    const int first_m = (t / per_group) * GM;
+    const int gm = min(tiles_m - first_m, GM);
+    const int r = t % per_group;
+    pm = first_m + r % gm;
+    pn = r / gm;
+}
+
+template <bool WS16, int EPI>
+__global__ __launch_bounds__(256, 2) void w8a8_q8_tile_kernel(const int8_t* __restrict__ a,
+                                                              const float* __restrict__ a_s, int64_t as_sm,
+                                                              const int8_t* __restrict__ w,
+                                                              const void* __restrict__ w_s, void* __restrict__ out,
+                                                              int64_t ldo, const int32_t* __restrict__ n_rows, int M,
+                                                              int N, int K, int tiles_m, int tiles_n) {
+    __shared__ __attribute__((aligned(16))) int8_t As[TBM * TLD];
+    __shared__ __attribute__((aligned(16))) int8_t Bs[TBN * TLD];
+    __shared__ float sws[4][TBN];
+
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int wm = wv >> 1, wn = wv & 1;
+    int pm, pn;
+    tile_coords(blockIdx.x, tiles_m, tiles_n, pm, pn);
+    const int m0 = pm * TBM, n0 = pn * TBN;
+    const int live = min(M, __ldg(n_rows));
+    if (m0 >= live) return;
+    const int G = K / 32;
+
+    // loaders: chunk i of this thread is row lr + 32 i, bytes lc .. lc + 15 of the stage (rows clamped in range:
+    // a clamped row is loaded but never stored)
+    const int lr = tid >> 3, lc = (tid & 7) * 16;
+    const int8_t* ap[4];
+    const int8_t* bp[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        ap[i] = a + (int64_t)min(m0 + lr + 32 * i, M - 1) * K + lc;
+        bp[i] = w + (int64_t)min(n0 + lr + 32 * i, N - 1) * K + lc;
+    }
+    // weight scales: element e = tid + 256 i -> row e / 4, block e % 4 of the stage
+    const int64_t sw_off0 = (int64_t)min(n0 + (tid >> 2), N - 1) * G + (tid & 3);
+    const int64_t sw_off1 = (int64_t)min(n0 + 64 + (tid >> 2), N - 1) * G + (tid & 3);
+    auto ldsw = [&](int64_t off) -> float {
+        return WS16 ? f16_to_f32(reinterpret_cast<const uint16_t*>(w_s)[off]) : reinterpret_cast<const float*>(w_s)[off];
+    };
+
+    v4i ra[4], rb[4];
+    float rs0, rs1;
+    auto gload = [&](int kb) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            ra[i] = *reinterpret_cast<const v4i*>(ap[i] + kb * 32);
+            rb[i] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(bp[i] + kb * 32));
+        }
+        rs0 = ldsw(sw_off0 + kb);
+        rs1 = ldsw(sw_off1 + kb);
+    };
+
+    const int lrow = 4 * (lane >> 5);
+    float sa[2][16];
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int m = min(m0 + wm * 64 + mt * 32 + 8 * (r >> 2) + lrow + (r & 3), M - 1);
+            sa[mt][r] = a_s[(int64_t)m * as_sm];
+        }
+    float y[2][2][16];
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+        for (int nt = 0; nt < 2; nt++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) y[mt][nt][r] = 0.f;
+
+    const int arow0 = (wm * 64 + (lane & 31)) * TLD + (lane >> 5) * 16;
+    const int brow0 = (wn * 64 + (lane & 31)) * TLD + (lane >> 5) * 16;
+    const int swc = wn * 64 + (lane & 31);
+    const v16i zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    gload(0);
+    for (int kb = 0; kb < G; kb += 4) {
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            *reinterpret_cast<v4i*>(&As[(lr + 32 * i) * TLD + lc]) = ra[i];
+            *reinterpret_cast<v4i*>(&Bs[(lr + 32 * i) * TLD + lc]) = rb[i];
+        }
+        sws[tid & 3][tid >> 2] = rs0;
+        sws[tid & 3][64 + (tid >> 2)] = rs1;
+        __syncthreads();
+        if (kb + 4 < G) gload(kb + 4);
+#pragma unroll
+        for (int bi = 0; bi < 4; bi++) {
+            v4i fa[2], fb[2];
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                fa[t] = *reinterpret_cast<const v4i*>(&As[arow0 + t * 32 * TLD + bi * 32]);
+                fb[t] = *reinterpret_cast<const v4i*>(&Bs[brow0 + t * 32 * TLD + bi * 32]);
+            }
+            const float sw[2] = {sws[bi][swc], sws[bi][swc + 32]};
+#pragma unroll
+            for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+                for (int nt = 0; nt < 2; nt++) {
+                    const v16i acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[mt], fb[nt], zero, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 16; r++)
+                        y[mt][nt][r] = add_rn(y[mt][nt][r], mul_rn(mul_rn((float)acc[r], sa[mt][r]), sw[nt]));
+                }
+        }
+    }
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+        for (int nt = 0; nt < 2; nt++) {
+            const int n = n0 + wn * 64 + nt * 32 + (lane & 31);
+            if (n >= N) continue;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int m = m0 + wm * 64 + mt * 32 + 8 * (r >> 2) + lrow + (r & 3);
+                if (m < live) {
+                    if (EPI == 0) {
+                        reinterpret_cast<uint16_t*>(out)[(int64_t)m * ldo + n] = (uint16_t)f32_to_bf16(y[mt][nt][r]);
+                    } else {
+                        float* o = reinterpret_cast<float*>(out) + (int64_t)m * ldo + n;
+                        *o = add_rn(*o, y[mt][nt][r]);
+                    }
+                }
+            }
+        }
+}
+
 // ============================================================================================== launch
 template <bool AS_GROUP, bool WS16, int EPI>
 static int launch_w8a8(int kernel, const int8_t* a, const float* a_s, int64_t as_sm, int64_t as_sg, const int8_t* w,
@@ -337,8 +482,12 @@ static int launch_w8a8(int kernel, const int8_t* a, const float* a_s, int64_t as
     } else {
         const int tiles_m = (M + TBM - 1) / TBM, tiles_n = (N + TBN - 1) / TBN;
         dim3 grid(tiles_m * tiles_n), block(256);
-        hipLaunchKernelGGL((w8a8_tile_kernel<AS_GROUP, WS16, EPI>), grid, block, 0, st, a, a_s, as_sm, as_sg, w, w_s,
-                           out, ldo, n_rows, M, N, K, gk / 32, tiles_m);
+        if (!AS_GROUP && gk == 32 && K % TBK == 0)
+            hipLaunchKernelGGL((w8a8_q8_tile_kernel<WS16, EPI>), grid, block, 0, st, a, a_s, as_sm, w, w_s, out, ldo,
+                               n_rows, M, N, K, tiles_m, tiles_n);
+        else
+            hipLaunchKernelGGL((w8a8_tile_kernel<AS_GROUP, WS16, EPI>), grid, block, 0, st, a, a_s, as_sm, as_sg, w,
+                               w_s, out, ldo, n_rows, M, N, K, gk / 32, tiles_m);
     }
     PRISM_LAUNCH_CHECK();
     return PRISM_OK;
