@@ -20,133 +20,209 @@
 //           owner thread adds the round's terms in block order.  HBM-bound on the weight stream.
 #include "common.h"
 
+// Timeline probes for profiling builds (empty in the library).
+#ifndef PRISM_PROBE
+#define PRISM_PROBE(tag)
+#endif
+
 namespace prism {
 
 // ============================================================================================== decode kernel
-// MT: activation tiles of 16 rows (M <= 16 MT); C: blocks per wave per round (4 C blocks per round).
-template <int MT, int C, bool AS_GROUP, bool WS16, int EPI>
-__global__ __launch_bounds__(256) void w8a8_decode_kernel(const int8_t* __restrict__ a, const float* __restrict__ a_s,
-                                                          int64_t as_sm, int64_t as_sg,
-                                                          const int8_t* __restrict__ w, const void* __restrict__ w_s,
-                                                          void* __restrict__ out, int64_t ldo,
-                                                          const int32_t* __restrict__ n_rows, int M, int N, int K) {
-    constexpr int R = 4 * C;                       // blocks per round
-    __shared__ v4f terms[R][MT * 16][4];           // [block][m][n / 4]: 16 n per row as 4 float4
-    __shared__ float sws[R][16];                   // the round's weight scales, fp32, [block][n]
+// A workgroup of NW waves owns 16 weight rows (n0 .. n0 + 15) and every activation row (M <= 64).  K is walked in
+// rounds of R blocks (32 R bytes per row).  Round r:
+//   1. the round's weight rows, activation rows and weight scales, requested during round r - 1 with
+//      row-contiguous 16-byte loads (a wave instruction reads 1 KB of a row), are written to LDS, and round r + 1's
+//      loads are issued;
+//   2. wave w computes blocks w CB .. w CB + CB - 1 of the round with v_mfma_i32_16x16x32_i8 (weights as the A
+//      operand: lane l reads row l % 16, bytes 8 (l / 16) .. +8 of the block from LDS; activations as B), turns each
+//      block's int32 sums into the term RN(RN(float(P) sa) sw) and writes the terms of live rows to one of two LDS
+//      term buffers, [block][m][n];
+//   3. meanwhile the owner thread of each output adds round r - 1's terms, from the other buffer, in block order
+//      (the reference's sequential fp32 sum over groups), so the ordered sum is off the MFMA path.
+template <int NW, int R, int MT, int D, bool AS_GROUP, bool WS16, int EPI>
+__global__ __launch_bounds__(NW * 64) void w8a8_decode_kernel(const int8_t* __restrict__ a,
+                                                              const float* __restrict__ a_s, int64_t as_sm,
+                                                              int64_t as_sg, const int8_t* __restrict__ w,
+                                                              const void* __restrict__ w_s, void* __restrict__ out,
+                                                              int64_t ldo, const int32_t* __restrict__ n_rows, int M,
+                                                              int N, int K) {
+    constexpr int NT = NW * 64;
+    constexpr int CB = R / NW;                     // blocks per wave per round
+    static_assert(CB >= 1 && CB * NW == R, "R must be a multiple of NW");
+    constexpr int RB = R * 32;                     // bytes per row per round
+    constexpr int LD = RB + 16;                    // padded LDS row
+    constexpr int CPR = RB / 16;                   // 16-byte chunks per row per round
+    constexpr int WPT = (16 * CPR + NT - 1) / NT;
+    constexpr int APT = (MT * 16 * CPR + NT - 1) / NT;
+    constexpr int SWV = (16 * R + NT - 1) / NT;
+    extern __shared__ __attribute__((aligned(16))) int8_t dsm[];
+    int8_t* Wl = dsm;                                                   // [16][LD]
+    int8_t* Al = Wl + 16 * LD;                                          // [M][LD]
+    float* sws = reinterpret_cast<float*>(Al + ((M * LD + 15) & ~15));  // [R][16]
+    float* terms = sws + R * 16;                                        // [2][R][M][16]
+    const int tstride = R * M * 16;
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    PRISM_PROBE(0);
     const int n0 = blockIdx.x * 16;
     const int live = min(M, __ldg(n_rows));
     const int G = K / 32;
+    const int lm = lane & 15, kq = (lane >> 4) * 8;
+    const int ach = M * CPR;
 
-    // MFMA lanes: A = weights, row n0 + lane % 16, bytes [8 (lane / 16), +8) of each 32-byte block;
-    //             B = activations, row (column of D) mt * 16 + lane % 16, the same bytes.
-    const int8_t* wrow = w + (int64_t)(n0 + (lane & 15)) * K + (lane >> 4) * 8;
-    const int kq = (lane >> 4) * 8;
     float sa[MT];
 #pragma unroll
-    for (int mt = 0; mt < MT; mt++) {
-        const int m = mt * 16 + (lane & 15);
-        sa[mt] = (!AS_GROUP && m < M) ? a_s[(int64_t)m * as_sm] : 0.f;
-    }
+    for (int mt = 0; mt < MT; mt++) sa[mt] = AS_GROUP ? 0.f : a_s[(int64_t)min(mt * 16 + lm, M - 1) * as_sm];
 
-    // sw staging: 16 rows x R blocks, (16 R) / 256 values per thread
-    constexpr int SWV = (16 * R + 255) / 256;
-    auto load_sw = [&](int rb, float* reg) {
+    struct Stage {
+        v4i w[WPT];
+        v4i a[APT];
+        uint32_t sw[SWV];     // raw scale bits (fp16 or fp32), widened when written to LDS
+    };
+    // Loads are unconditional (indices clamped in range, surplus threads reload a valid chunk): no branch around
+    // them, so the compiler's wait counts stay exact and a round's loads stay in flight across the barriers.
+    auto load = [&](int rb, Stage& st) {
+        const int64_t k0 = (int64_t)rb * 32;
+#pragma unroll
+        for (int i = 0; i < WPT; i++) {
+            const int c = min(tid + i * NT, 16 * CPR - 1);
+            const int row = c / CPR;
+            const int64_t kk = min(k0 + (c % CPR) * 16, (int64_t)K - 16);
+            st.w[i] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(w + (int64_t)(n0 + row) * K + kk));
+        }
+#pragma unroll
+        for (int i = 0; i < APT; i++) {
+            const int c = min(tid + i * NT, ach - 1);
+            const int row = c / CPR;
+            const int64_t kk = min(k0 + (c % CPR) * 16, (int64_t)K - 16);
+            st.a[i] = *reinterpret_cast<const v4i*>(a + (int64_t)row * K + kk);
+        }
 #pragma unroll
         for (int i = 0; i < SWV; i++) {
-            const int e = tid + i * 256;
-            const int row = e / R, blk = e % R;
-            float v = 0.f;
-            if (e < 16 * R && rb + blk < G) {
-                const int64_t off = (int64_t)(n0 + row) * G + rb + blk;
-                v = WS16 ? f16_to_f32(reinterpret_cast<const uint16_t*>(w_s)[off])
-                         : reinterpret_cast<const float*>(w_s)[off];
-            }
-            reg[i] = v;
+            const int e = min(tid + i * NT, 16 * R - 1);
+            const int row = e / R, blk = min(rb + e % R, G - 1);
+            const int64_t off = (int64_t)(n0 + row) * G + blk;
+            st.sw[i] = WS16 ? (uint32_t)reinterpret_cast<const uint16_t*>(w_s)[off]
+                            : reinterpret_cast<const uint32_t*>(w_s)[off];
         }
     };
-    auto store_sw = [&](const float* reg) {
+    // chunks past the end of K were loaded from its last 16 bytes; they land past the round's last block
+    auto store = [&](const Stage& st) {
+#pragma unroll
+        for (int i = 0; i < WPT; i++) {
+            const int c = tid + i * NT;
+            if (c < 16 * CPR) *reinterpret_cast<v4i*>(&Wl[(c / CPR) * LD + (c % CPR) * 16]) = st.w[i];
+        }
+#pragma unroll
+        for (int i = 0; i < APT; i++) {
+            const int c = tid + i * NT;
+            if (c < ach) *reinterpret_cast<v4i*>(&Al[(c / CPR) * LD + (c % CPR) * 16]) = st.a[i];
+        }
 #pragma unroll
         for (int i = 0; i < SWV; i++) {
-            const int e = tid + i * 256;
-            if (e < 16 * R) sws[e % R][e / R] = reg[i];
+            const int e = tid + i * NT;
+            if (e < 16 * R) sws[(e % R) * 16 + e / R] = WS16 ? f16_to_f32(st.sw[i]) : __uint_as_float(st.sw[i]);
         }
     };
-    int64_t wb[C], ab[C][MT];
-    auto load_ops = [&](int rb) {
+    auto compute = [&](int rb, float* tb) {
 #pragma unroll
-        for (int i = 0; i < C; i++) {
-            const int blk = rb + wv * C + i;
-            const bool ok = blk < G;
-            wb[i] = ok ? __builtin_nontemporal_load(reinterpret_cast<const int64_t*>(wrow + (int64_t)blk * 32)) : 0;
-#pragma unroll
-            for (int mt = 0; mt < MT; mt++) {
-                const int m = mt * 16 + (lane & 15);
-                ab[i][mt] = (ok && m < M) ? *reinterpret_cast<const int64_t*>(a + (int64_t)m * K + blk * 32 + kq) : 0;
-            }
-        }
-    };
-
-    float y[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; mt++) y[mt] = 0.f;
-    float swr[SWV];
-    load_sw(0, swr);
-    load_ops(0);
-    for (int rb = 0; rb < G; rb += R) {
-        store_sw(swr);
-        __syncthreads();
-        // ---- produce: the terms RN(RN(float(P) sa) sw) of this wave's C blocks
-#pragma unroll
-        for (int i = 0; i < C; i++) {
-            const int lb = wv * C + i, blk = rb + lb;
+        for (int i = 0; i < CB; i++) {
+            const int lb = wv * CB + i, blk = rb + lb;
             if (blk < G) {
-                const v4f sw4 = *reinterpret_cast<const v4f*>(&sws[lb][(lane >> 4) * 4]);
+                const int64_t wf = *reinterpret_cast<const int64_t*>(&Wl[lm * LD + lb * 32 + kq]);
+                const v4f sw4 = *reinterpret_cast<const v4f*>(&sws[lb * 16 + (lane >> 4) * 4]);
 #pragma unroll
                 for (int mt = 0; mt < MT; mt++) {
-                    v4i acc = {0, 0, 0, 0};
-                    acc = __builtin_amdgcn_mfma_i32_16x16x32_i8(wb[i], ab[i][mt], acc, 0, 0, 0);
+                    const int m = mt * 16 + lm;
+                    const int64_t af = *reinterpret_cast<const int64_t*>(&Al[min(m, M - 1) * LD + lb * 32 + kq]);
+                    const v4i zero = {0, 0, 0, 0};
+                    const v4i acc = __builtin_amdgcn_mfma_i32_16x16x32_i8(wf, af, zero, 0, 0, 0);
                     float s = sa[mt];
-                    if (AS_GROUP) {
-                        const int m = mt * 16 + (lane & 15);
-                        s = m < M ? a_s[(int64_t)m * as_sm + (int64_t)blk * as_sg] : 0.f;
-                    }
+                    if (AS_GROUP) s = a_s[(int64_t)min(m, M - 1) * as_sm + (int64_t)blk * as_sg];
                     v4f t;
 #pragma unroll
                     for (int r = 0; r < 4; r++) t[r] = mul_rn(mul_rn((float)acc[r], s), sw4[r]);
-                    terms[lb][mt * 16 + (lane & 15)][lane >> 4] = t;
+                    if (m < M) *reinterpret_cast<v4f*>(&tb[(lb * M + m) * 16 + (lane >> 4) * 4]) = t;
                 }
             }
         }
-        const int nb = min(R, G - rb);
-        if (rb + R < G) {
-            load_sw(rb + R, swr);
-            load_ops(rb + R);
-        }
-        __syncthreads();
-        // ---- reduce: thread tid owns (m = tid / 16 + 16 mt, n = n0 + tid % 16); add the round's terms in order
-        const float* tf = reinterpret_cast<const float*>(&terms[0][0][0]);
+    };
+    // output o = tid + NT j: m = o / 16, n = n0 + o % 16
+    constexpr int OPT = (64 * 16 + NT - 1) / NT;
+    float y[OPT];
 #pragma unroll
-        for (int mt = 0; mt < MT; mt++) {
-            float acc = y[mt];
-            for (int j = 0; j < nb; j++) acc = add_rn(acc, tf[(j * MT * 16 + mt * 16) * 16 + tid]);
-            y[mt] = acc;
+    for (int j = 0; j < OPT; j++) y[j] = 0.f;
+    auto fold = [&](int rb, const float* tb) {
+        const int nb = min(R, G - rb);
+#pragma unroll
+        for (int jo = 0; jo < OPT; jo++) {
+            const int o = tid + jo * NT;
+            if (o < M * 16) {
+                const float* tp = tb + o;
+                const int st = M * 16;
+                float acc = y[jo];
+                int j = 0;
+                for (; j + 16 <= nb; j += 16) {
+                    float v[16];
+#pragma unroll
+                    for (int u = 0; u < 16; u++) v[u] = tp[(j + u) * st];
+#pragma unroll
+                    for (int u = 0; u < 16; u++) acc = add_rn(acc, v[u]);
+                }
+                for (; j < nb; j++) acc = add_rn(acc, tp[j * st]);
+                y[jo] = acc;
+            }
+        }
+    };
+
+    // D-deep register ring: round r + D - 1 is requested before round r's data are waited for.  Loads and LDS
+    // stores run for every slot (past the end they reload the last chunk of K); only the math is guarded.
+    Stage st[D];
+#pragma unroll
+    for (int d = 0; d < D - 1; d++) load(d * R, st[d]);
+    const int nr = (G + R - 1) / R;
+    for (int r0 = 0; r0 < nr; r0 += D) {
+#pragma unroll
+        for (int d = 0; d < D; d++) {
+            const int r = r0 + d, rb = r * R;
+            PRISM_PROBE(6);
+            load(rb + (D - 1) * R, st[(d + D - 1) % D]);
+            PRISM_PROBE(7);
+            store(st[d]);
+            PRISM_PROBE(8);
+            lds_barrier();
+            PRISM_PROBE(1);
+            if (r < nr) {
+                compute(rb, terms + (r & 1) * tstride);
+                PRISM_PROBE(4);
+                if (r > 0) fold(rb - R, terms + ((r - 1) & 1) * tstride);
+                PRISM_PROBE(5);
+            }
+            lds_barrier();
+            PRISM_PROBE(2);
         }
     }
-    // ---- epilogue
+    const int last = ((G - 1) / R) * R;
+    fold(last, terms + ((last / R) & 1) * tstride);
+    PRISM_PROBE(3);
 #pragma unroll
-    for (int mt = 0; mt < MT; mt++) {
-        const int m = mt * 16 + tid / 16, n = n0 + (tid & 15);
-        if (m < live) {
+    for (int jo = 0; jo < OPT; jo++) {
+        const int o = tid + jo * NT;
+        const int m = o >> 4, n = n0 + (o & 15);
+        if (o < M * 16 && m < live) {
             if (EPI == 0) {
-                reinterpret_cast<uint16_t*>(out)[(int64_t)m * ldo + n] = (uint16_t)f32_to_bf16(y[mt]);
+                reinterpret_cast<uint16_t*>(out)[(int64_t)m * ldo + n] = (uint16_t)f32_to_bf16(y[jo]);
             } else {
-                float* o = reinterpret_cast<float*>(out) + (int64_t)m * ldo + n;
-                *o = add_rn(*o, y[mt]);
+                float* op = reinterpret_cast<float*>(out) + (int64_t)m * ldo + n;
+                *op = add_rn(*op, y[jo]);
             }
         }
     }
+}
+
+static size_t decode_lds(int R, int M) {
+    const size_t LD = (size_t)R * 32 + 16;
+    return 16 * LD + ((M * LD + 15) & ~(size_t)15) + (size_t)R * 16 * 4 + 2 * (size_t)R * M * 64;
 }
 
 // ============================================================================================== tile kernel
@@ -413,7 +489,7 @@ __global__ __launch_bounds__(256, 2) void w8a8_q8_tile_kernel(const int8_t* __re
     const v16i zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
     gload(0);
     for (int kb = 0; kb < G; kb += 4) {
-        __syncthreads();
+        lds_barrier();
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             *reinterpret_cast<v4i*>(&As[(lr + 32 * i) * TLD + lc]) = ra[i];
@@ -421,7 +497,7 @@ __global__ __launch_bounds__(256, 2) void w8a8_q8_tile_kernel(const int8_t* __re
         }
         sws[tid & 3][tid >> 2] = rs0;
         sws[tid & 3][64 + (tid >> 2)] = rs1;
-        __syncthreads();
+        lds_barrier();
         if (kb + 4 < G) gload(kb + 4);
 #pragma unroll
         for (int bi = 0; bi < 4; bi++) {
@@ -470,14 +546,14 @@ static int launch_w8a8(int kernel, const int8_t* a, const float* a_s, int64_t as
                        const void* w_s, void* out, int64_t ldo, const int32_t* n_rows, int M, int N, int K, int gk,
                        hipStream_t st) {
     if (kernel == 1) {
-        dim3 grid(N / 16), block(256);
-        const int mt = (M + 15) / 16;
-#define DEC(MT, C) hipLaunchKernelGGL((w8a8_decode_kernel<MT, C, AS_GROUP, WS16, EPI>), grid, block, 0, st, a, a_s, \
-                                      as_sm, as_sg, w, w_s, out, ldo, n_rows, M, N, K)
-        if (mt == 1) DEC(1, 8);
-        else if (mt == 2) DEC(2, 4);
-        else if (mt == 3) DEC(3, 2);
-        else DEC(4, 2);
+        dim3 grid(N / 16);
+#define DEC(NW, R, MT, D)                                                                                         \
+    hipLaunchKernelGGL((w8a8_decode_kernel<NW, R, MT, D, AS_GROUP, WS16, EPI>), grid, dim3(NW * 64),                \
+                       decode_lds(R, M), st, a, a_s, as_sm, as_sg, w, w_s, out, ldo, n_rows, M, N, K)
+        if (M <= 16) DEC(16, 32, 1, 6);
+        else if (M <= 32) DEC(8, 8, 2, 8);
+        else if (M <= 48) DEC(8, 8, 3, 8);
+        else DEC(8, 8, 4, 8);
 #undef DEC
     } else {
         const int tiles_m = (M + TBM - 1) / TBM, tiles_n = (N + TBN - 1) / TBN;
