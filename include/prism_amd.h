@@ -88,6 +88,26 @@ PRISM_API int prism_w8a8_gemm(const int8_t* a, const float* a_s, int64_t as_sm, 
                     int64_t N, int64_t K, int64_t gk, int epi, int kernel, void* stream);
 
 /*
+ * Repack Q8_0 planes into the MFMA-native layout the packed kernels read (a load-time step, as the reference's
+ * weight_from_q8 (kernels/w8a8.py:274-286) and repack (kernels/w4a8.py:70-94) are).  qs int8 [N, K], d fp16 [N, K/32]
+ * -> qt int8 [N/16][K/64][64][16] (per 16-row tile and block pair a 1 KB chunk; lane slot l: row l % 16,
+ * bytes 0..7 = k 8 (l/16) .. +8 of the pair's first block, bytes 8..15 the same of its second), dt fp16
+ * [N/16][K/64][16][2].  Needs N % 16 == 0, K % 64 == 0.
+ */
+PRISM_API int prism_q8_0_pack(const int8_t* qs, const uint16_t* d, int8_t* qt, uint16_t* dt, int64_t N, int64_t K,
+                              void* stream);
+
+/*
+ * Q8_0 W8A8 GEMM (gk = 32, one activation scale per token) on packed weights: the arithmetic and bits of
+ * prism_w8a8_gemm with gk = 32 (kernels/w8a8.py:64-85), the engine entry kernels/w8a8.py:183-231.
+ * a int8 [M, K]; a_s fp32, row m at a_s[m * as_sm]; qt / dt from prism_q8_0_pack; out as prism_w8a8_gemm.
+ * kernel: -1 picks by M; 0 the prefill tile kernel; 1 the decode kernel (M <= 64).  Needs K % 128 == 0.
+ */
+PRISM_API int prism_w8a8_q8_0_packed_gemm(const int8_t* a, const float* a_s, int64_t as_sm, const int8_t* qt,
+                                          const uint16_t* dt, void* out, int64_t ldo, const int32_t* n_rows,
+                                          int64_t M, int64_t N, int64_t K, int epi, int kernel, void* stream);
+
+/*
  * W4A8 GEMM on Q4_K weights in the repacked W4 layout.  Replaces kernels/w4a8.py:353-366 (gemm, kind "q4k") and
  * the native startlux_prism::w4a8_gemm (csrc/w4a8_gemm.cu:887-961, schema :963-966); arithmetic of
  * kernels/w4a8.py:14-22 / gemm_ref (:177-199), per super-block b of 256 inputs in increasing b:

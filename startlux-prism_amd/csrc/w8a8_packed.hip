@@ -1,0 +1,460 @@
+// Q8_0 W8A8 GEMM on an MFMA-native weight layout (gfx950).
+//
+// Packed layout, made once at load (prism_q8_0_pack), like the reference's own load-time repacks
+// (kernels/w8a8.py:274-286 weight_from_q8, kernels/w4a8.py:70-94 repack):
+//   qt  int8 [N/16][K/64][64][16]: one 1 KB chunk per (16-row tile nt, block pair j).  Lane slot l holds row
+//       16 nt + l % 16, q = l / 16: bytes 0..7 = k 64 j + 8 q .. +8 (block 2 j), bytes 8..15 = k 64 j + 32 + 8 q .. +8
+//       (block 2 j + 1).  One dwordx4 per lane reads a whole chunk (1 KB contiguous per wave instruction) and its
+//       halves are the A operands of v_mfma_i32_16x16x32_i8 for the two blocks, with no re-layout.
+//   dt  fp16 [N/16][K/64][16][2]: the Q8_0 block scales of the chunk, row-major over (row, block of the pair), so a
+//       lane's four output rows 4 (l / 16) .. +3 are one 16-byte load.
+// Arithmetic: identical to the row-major kernels (kernels/w8a8.py:64-85), every output's fp32 sum over blocks in
+// block order, so both layouts give the same bits.
+#include "common.h"
+
+#ifndef PRISM_PROBE
+#define PRISM_PROBE(tag)
+#endif
+
+namespace prism {
+
+// ---------------------------------------------------------------------------------------------- pack
+__global__ __launch_bounds__(256) void q8_0_pack_kernel(const int8_t* __restrict__ qs, const uint16_t* __restrict__ d,
+                                                        int8_t* __restrict__ qt, uint16_t* __restrict__ dt, int N,
+                                                        int K) {
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;     // (nt, j, l)
+    const int KP = K / 64;
+    const int64_t total = (int64_t)(N / 16) * KP * 64;
+    if (e >= total) return;
+    const int l = (int)(e & 63), r = l & 15, q = l >> 4;
+    const int64_t c = e >> 6;
+    const int j = (int)(c % KP), nt = (int)(c / KP);
+    const int8_t* src = qs + (int64_t)(16 * nt + r) * K + 64 * j + 8 * q;
+    v2u lo = *reinterpret_cast<const v2u*>(src), hi = *reinterpret_cast<const v2u*>(src + 32);
+    v4u o;
+    o[0] = lo[0];
+    o[1] = lo[1];
+    o[2] = hi[0];
+    o[3] = hi[1];
+    reinterpret_cast<v4u*>(qt)[e] = o;
+    if (q == 0) {                                      // 16 rows x 2 blocks of scales per chunk
+        const int G = K / 32;
+        dt[(c * 16 + r) * 2 + 0] = d[(int64_t)(16 * nt + r) * G + 2 * j];
+        dt[(c * 16 + r) * 2 + 1] = d[(int64_t)(16 * nt + r) * G + 2 * j + 1];
+    }
+}
+
+// ---------------------------------------------------------------------------------------------- decode
+// A workgroup of NW waves owns one 16-row tile and every activation row (M <= MX <= 64).  Round r covers R blocks;
+// wave w takes block pairs r R / 2 + w CP .. + CP - 1.  Per round, the only per-wave global loads are the weight
+// chunks (one dwordx4 per lane per 1 KB chunk, requested D - 1 rounds ahead); the round's block scales (1 KB) and
+// activation rows (M R 32 bytes) are fetched by all threads with row-contiguous 16-byte loads and staged in one of
+// two LDS buffers a round ahead.  Each block's int32 sums come from one MFMA on a chunk half, become the term
+// RN(RN(float(P) sa) sw) and go to one of two LDS term buffers [block][m][n]; the owner thread of each output adds
+// round r - 1's terms in block order (the reference's sequential fp32 sum over groups) while round r is computed,
+// and one barrier per round separates producers from consumers of every buffer.
+template <int NW, int R, int MX, int D, int EPI>
+__global__ __launch_bounds__(NW * 64) void w8a8_packed_decode_kernel(const int8_t* __restrict__ a,
+                                                                     const float* __restrict__ a_s, int64_t as_sm,
+                                                                     const int8_t* __restrict__ qt,
+                                                                     const uint16_t* __restrict__ dt,
+                                                                     void* __restrict__ out, int64_t ldo,
+                                                                     const int32_t* __restrict__ n_rows, int M, int N,
+                                                                     int K) {
+    constexpr int MT = (MX + 15) / 16;             // activation tiles of 16 rows
+    constexpr int NT = NW * 64;
+    constexpr int CP = R / (2 * NW);               // block pairs per wave per round
+    static_assert(CP >= 1 && CP * 2 * NW == R, "R must be a multiple of 2 NW");
+    constexpr int RB = R * 32;                     // activation bytes per row per round
+    constexpr int LDA = RB + 16;                   // padded LDS activation row
+    constexpr int CPR = RB / 16;                   // 16-byte chunks per activation row per round
+    constexpr int XPT = (MX * CPR + NT - 1) / NT;
+    constexpr int SCH = R * 16 * 2 / 16;           // 16-byte chunks of scales per round (16 rows x R fp16)
+    constexpr int SPT = (SCH + NT - 1) / NT;
+    extern __shared__ __attribute__((aligned(16))) int8_t dsm[];
+    float* terms = reinterpret_cast<float*>(dsm);                              // [2][R][M][16]
+    float* sws = terms + 2 * R * M * 16;                                       // [2][R][16]
+    int8_t* xs = reinterpret_cast<int8_t*>(sws + 2 * R * 16);                  // [2][M][LDA]
+    const int tstride = R * M * 16, xstride = M * LDA;
+
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    PRISM_PROBE(0);
+    const int nt = blockIdx.x;
+    const int live = min(M, __ldg(n_rows));
+    const int KP = K / 64, G = K / 32;
+    const int nr = (G + R - 1) / R;
+    const int lm = lane & 15, q = lane >> 4;
+    const int xch = M * CPR;
+
+    const v4i* cw = reinterpret_cast<const v4i*>(qt) + (int64_t)nt * KP * 64 + lane;
+    const v4u* cs = reinterpret_cast<const v4u*>(dt) + (int64_t)nt * KP * 4;
+    float sa[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) sa[mt] = a_s[(int64_t)min(mt * 16 + lm, M - 1) * as_sm];
+
+    // a round's scales and activation chunks: loaded unconditionally (indices clamped in range), stored to LDS
+    // conditionally
+    struct Staged {
+        v4u s[SPT];
+        v4i x[XPT];
+    };
+    auto stage_load = [&](int r, Staged& sg) {
+        const int p0 = r * (R / 2);
+#pragma unroll
+        for (int i = 0; i < SPT; i++) {
+            const int sc = min(tid + i * NT, SCH - 1);                 // 4 chunks of 16 bytes per pair
+            sg.s[i] = cs[(int64_t)min(p0 + sc / 4, KP - 1) * 4 + (sc & 3)];
+        }
+        const int64_t k0 = (int64_t)r * RB;
+#pragma unroll
+        for (int i = 0; i < XPT; i++) {
+            const int c = min(tid + i * NT, xch - 1);
+            const int64_t kk = min(k0 + (c % CPR) * 16, (int64_t)K - 16);
+            sg.x[i] = *reinterpret_cast<const v4i*>(a + (int64_t)(c / CPR) * K + kk);
+        }
+    };
+    auto stage_store = [&](const Staged& sg, int buf) {
+        float* sp = sws + buf * R * 16;
+#pragma unroll
+        for (int i = 0; i < SPT; i++) {
+            const int sc = tid + i * NT;
+            if (sc < SCH) {                                            // pair sc / 4, rows 4 (sc % 4) .. +3
+                const int pl = sc >> 2, r0 = 4 * (sc & 3);
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    sp[(2 * pl) * 16 + r0 + e] = f16_to_f32(sg.s[i][e] & 0xffffu);
+                    sp[(2 * pl + 1) * 16 + r0 + e] = f16_to_f32(sg.s[i][e] >> 16);
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < XPT; i++) {
+            const int c = tid + i * NT;
+            if (c < xch) *reinterpret_cast<v4i*>(&xs[buf * xstride + (c / CPR) * LDA + (c % CPR) * 16]) = sg.x[i];
+        }
+    };
+    auto load_w = [&](int r, v4i* w) {
+#pragma unroll
+        for (int i = 0; i < CP; i++)
+            w[i] = __builtin_nontemporal_load(cw + (int64_t)min(r * (R / 2) + wv * CP + i, KP - 1) * 64);
+    };
+    auto compute = [&](int r, const v4i* w, int buf) {
+        const float* sp = sws + buf * R * 16;
+        const int8_t* xp = xs + buf * xstride;
+        float* tb = terms + (r & 1) * tstride;
+#pragma unroll
+        for (int i = 0; i < CP; i++) {
+            const int lp = wv * CP + i;                                // pair within the round
+            if (r * (R / 2) + lp < KP) {
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const int lb = 2 * lp + h;
+                    const int64_t wf = h ? ((int64_t)(uint32_t)w[i][2] | ((int64_t)w[i][3] << 32))
+                                         : ((int64_t)(uint32_t)w[i][0] | ((int64_t)w[i][1] << 32));
+                    const v4f sw = *reinterpret_cast<const v4f*>(&sp[lb * 16 + 4 * q]);
+#pragma unroll
+                    for (int mt = 0; mt < MT; mt++) {
+                        const int m = mt * 16 + lm;
+                        const int64_t xf = *reinterpret_cast<const int64_t*>(&xp[min(m, M - 1) * LDA + lb * 32 + 8 * q]);
+                        const v4i zero = {0, 0, 0, 0};
+                        const v4i acc = __builtin_amdgcn_mfma_i32_16x16x32_i8(wf, xf, zero, 0, 0, 0);
+                        v4f t;
+#pragma unroll
+                        for (int e = 0; e < 4; e++) t[e] = mul_rn(mul_rn((float)acc[e], sa[mt]), sw[e]);
+                        if (m < M) *reinterpret_cast<v4f*>(&tb[(lb * M + m) * 16 + 4 * q]) = t;
+                    }
+                }
+            }
+        }
+    };
+    constexpr int OPT = (16 * 16 * MT + NT - 1) / NT;
+    float y[OPT];
+#pragma unroll
+    for (int j = 0; j < OPT; j++) y[j] = 0.f;
+    auto fold = [&](int r) {
+        const float* tb = terms + (r & 1) * tstride;
+        const int nb = min(R, G - r * R);
+        const int st = M * 16;
+#pragma unroll
+        for (int jo = 0; jo < OPT; jo++) {
+            const int o = tid + jo * NT;
+            if (o < M * 16) {
+                const float* tp = tb + o;
+                float acc = y[jo];
+                int j = 0;
+                for (; j + 16 <= nb; j += 16) {
+                    float v[16];
+#pragma unroll
+                    for (int u = 0; u < 16; u++) v[u] = tp[(j + u) * st];
+#pragma unroll
+                    for (int u = 0; u < 16; u++) acc = add_rn(acc, v[u]);
+                }
+                for (; j < nb; j++) acc = add_rn(acc, tp[j * st]);
+                y[jo] = acc;
+            }
+        }
+    };
+
+    // prologue: round 0 staged in LDS buffer 0, round 1's staged operands in registers, weights of rounds 0 .. D-2
+    v4i wr[D][CP];
+    Staged sg;
+#pragma unroll
+    for (int d = 0; d < D - 1; d++) load_w(d, wr[d]);
+    stage_load(0, sg);
+    stage_store(sg, 0);
+    stage_load(1, sg);
+    lds_barrier();
+    for (int r0 = 0; r0 < nr; r0 += D) {
+#pragma unroll
+        for (int d = 0; d < D; d++) {
+            const int r = r0 + d;
+            load_w(r + D - 1, wr[(d + D - 1) % D]);        // past the end: the last chunk again (a cache hit)
+            stage_store(sg, (r + 1) & 1);                   // round r + 1's scales and activations
+            stage_load(r + 2, sg);
+            if (r < nr) compute(r, wr[d], r & 1);
+            if (r >= 1 && r <= nr) fold(r - 1);
+            lds_barrier();
+        }
+    }
+    if (nr % D == 0) fold(nr - 1);
+    PRISM_PROBE(3);
+#pragma unroll
+    for (int jo = 0; jo < OPT; jo++) {
+        const int o = tid + jo * NT;
+        const int m = o >> 4, n = 16 * nt + (o & 15);
+        if (o < M * 16 && m < live) {
+            if (EPI == 0) {
+                reinterpret_cast<uint16_t*>(out)[(int64_t)m * ldo + n] = (uint16_t)f32_to_bf16(y[jo]);
+            } else {
+                float* op = reinterpret_cast<float*>(out) + (int64_t)m * ldo + n;
+                *op = add_rn(*op, y[jo]);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------- prefill tile
+// 128 x 128 output tile per 256-thread workgroup (2 x 2 waves of 64 x 64), v_mfma_i32_32x32x32_i8 per (32 x 32,
+// block), 4 blocks (2 chunk pairs) per stage.  The weight tile of a stage is 8 tiles x 2 chunks = 8 runs of 2 KB,
+// copied to LDS as they are; a B fragment (column n, 16 bytes of a block) is two 8-byte pieces of a chunk.
+constexpr int PBM = 128, PBN = 128;
+constexpr int PLDA = 128 + 16;          // activation tile row (bytes), padded
+constexpr int PLDB = 2048 + 64;         // one 16-row tile's two chunks, padded
+
+__device__ __forceinline__ void packed_tile_coords(int pid, int tiles_m, int tiles_n, int& pm, int& pn) {
+    const int total = tiles_m * tiles_n;
+    int t = pid;
+    if ((total & 7) == 0) t = (pid & 7) * (total >> 3) + (pid >> 3);
+    constexpr int GM = 8;
+    const int per_group = GM * tiles_n;
+    const int first_m = (t / per_group) * GM;
+    const int gm = min(tiles_m - first_m, GM);
+    const int r = t % per_group;
+    pm = first_m + r % gm;
+    pn = r / gm;
+}
+
+template <int EPI>
+__global__ __launch_bounds__(256, 2) void w8a8_packed_tile_kernel(const int8_t* __restrict__ a,
+                                                                  const float* __restrict__ a_s, int64_t as_sm,
+                                                                  const int8_t* __restrict__ qt,
+                                                                  const uint16_t* __restrict__ dt,
+                                                                  void* __restrict__ out, int64_t ldo,
+                                                                  const int32_t* __restrict__ n_rows, int M, int N,
+                                                                  int K, int tiles_m, int tiles_n) {
+    __shared__ __attribute__((aligned(16))) int8_t As[PBM * PLDA];
+    __shared__ __attribute__((aligned(16))) int8_t Bs[8 * PLDB];
+    __shared__ float sws[4][PBN];
+
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int wm = wv >> 1, wn = wv & 1;
+    int pm, pn;
+    packed_tile_coords(blockIdx.x, tiles_m, tiles_n, pm, pn);
+    const int m0 = pm * PBM, n0 = pn * PBN;
+    const int live = min(M, __ldg(n_rows));
+    if (m0 >= live) return;
+    const int G = K / 32, KP = K / 64;
+    const int nt0 = n0 / 16, ntiles = N / 16;
+
+    // activation loader: chunk i = row lr + 32 i, bytes lc .. lc + 15 of the stage's 128 bytes
+    const int lr = tid >> 3, lc = (tid & 7) * 16;
+    const int8_t* ap[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) ap[i] = a + (int64_t)min(m0 + lr + 32 * i, M - 1) * K + lc;
+    // weight loader: chunk c = tid + 256 i -> tile c / 128 (clamped in range), 16 bytes (c % 128) of its 2 KB run
+    const v4i* bp[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int c = tid + 256 * i;
+        const int t = min(nt0 + (c >> 7), ntiles - 1);
+        bp[i] = reinterpret_cast<const v4i*>(qt) + (int64_t)t * KP * 64 + (c & 127);
+    }
+    // scale loader: thread t < 64 -> tile t / 8, 16 bytes (t % 8) of the tile's 2 x 64 bytes (2 pairs)
+    const int st_t = min(nt0 + (tid >> 3), ntiles - 1);
+    const v4u* sp = reinterpret_cast<const v4u*>(dt) + (int64_t)st_t * KP * 4 + (tid & 7);
+
+    v4i ra[4], rb[4];
+    v4u rs;
+    auto gload = [&](int kb) {                       // kb: first block of the stage (a multiple of 4)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            ra[i] = *reinterpret_cast<const v4i*>(ap[i] + kb * 32);
+            rb[i] = __builtin_nontemporal_load(bp[i] + (int64_t)(kb / 2) * 64);
+        }
+        rs = sp[(int64_t)(kb / 2) * 4];
+    };
+
+    const int lrow = 4 * (lane >> 5);
+    float sa[2][16];
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int m = min(m0 + wm * 64 + mt * 32 + 8 * (r >> 2) + lrow + (r & 3), M - 1);
+            sa[mt][r] = a_s[(int64_t)m * as_sm];
+        }
+    float y[2][2][16];
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+        for (int nt = 0; nt < 2; nt++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) y[mt][nt][r] = 0.f;
+
+    const int arow0 = (wm * 64 + (lane & 31)) * PLDA + (lane >> 5) * 16;
+    // B fragment of column j = wn * 64 + nt * 32 + lane % 32 (tile-local), lane group g = lane / 32: pieces
+    // q = 2 g and 2 g + 1 of row j % 16 in 16-row tile j / 16
+    int bofs[2];
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+        const int j = wn * 64 + t * 32 + (lane & 31);
+        bofs[t] = (j >> 4) * PLDB + ((j & 15) + 32 * (lane >> 5)) * 16;
+    }
+    const int swc = wn * 64 + (lane & 31);
+    const v16i zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    gload(0);
+    for (int kb = 0; kb < G; kb += 4) {
+        lds_barrier();
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int c = tid + 256 * i;
+            *reinterpret_cast<v4i*>(&As[(lr + 32 * i) * PLDA + lc]) = ra[i];
+            *reinterpret_cast<v4i*>(&Bs[(c >> 7) * PLDB + (c & 127) * 16]) = rb[i];
+        }
+        if (tid < 64) {
+            // rs: tile tid / 8, pair (tid % 8) / 4, rows 4 ((tid % 8) % 4) .. +3, both blocks of the pair
+            const int tl = tid >> 3, pr = (tid & 7) >> 2, r0 = 4 * (tid & 3);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                sws[2 * pr][16 * tl + r0 + e] = f16_to_f32(rs[e] & 0xffffu);
+                sws[2 * pr + 1][16 * tl + r0 + e] = f16_to_f32(rs[e] >> 16);
+            }
+        }
+        lds_barrier();
+        if (kb + 4 < G) gload(kb + 4);
+#pragma unroll
+        for (int bi = 0; bi < 4; bi++) {
+            v4i fa[2], fb[2];
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                fa[t] = *reinterpret_cast<const v4i*>(&As[arow0 + t * 32 * PLDA + bi * 32]);
+                const int o = bofs[t] + (bi >> 1) * 1024 + 8 * (bi & 1);
+                const int64_t p0 = *reinterpret_cast<const int64_t*>(&Bs[o]);
+                const int64_t p1 = *reinterpret_cast<const int64_t*>(&Bs[o + 16 * 16]);
+                fb[t] = v4i{(int)p0, (int)(p0 >> 32), (int)p1, (int)(p1 >> 32)};
+            }
+            const float sw[2] = {sws[bi][swc], sws[bi][swc + 32]};
+#pragma unroll
+            for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+                for (int nt = 0; nt < 2; nt++) {
+                    const v16i acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[mt], fb[nt], zero, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 16; r++)
+                        y[mt][nt][r] = add_rn(y[mt][nt][r], mul_rn(mul_rn((float)acc[r], sa[mt][r]), sw[nt]));
+                }
+        }
+    }
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+        for (int nt = 0; nt < 2; nt++) {
+            const int n = n0 + wn * 64 + nt * 32 + (lane & 31);
+            if (n >= N) continue;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int m = m0 + wm * 64 + mt * 32 + 8 * (r >> 2) + lrow + (r & 3);
+                if (m < live) {
+                    if (EPI == 0) {
+                        reinterpret_cast<uint16_t*>(out)[(int64_t)m * ldo + n] = (uint16_t)f32_to_bf16(y[mt][nt][r]);
+                    } else {
+                        float* o = reinterpret_cast<float*>(out) + (int64_t)m * ldo + n;
+                        *o = add_rn(*o, y[mt][nt][r]);
+                    }
+                }
+            }
+        }
+}
+
+static size_t packed_decode_lds(int R, int M) {
+    return 2 * (size_t)R * M * 16 * 4 + 2 * (size_t)R * 16 * 4 + 2 * (size_t)M * (R * 32 + 16);
+}
+
+template <int EPI>
+static void launch_packed(int kernel, const int8_t* a, const float* a_s, int64_t as_sm, const int8_t* qt,
+                          const uint16_t* dt, void* out, int64_t ldo, const int32_t* n_rows, int M, int N, int K,
+                          hipStream_t st) {
+    if (kernel == 1) {
+        dim3 grid(N / 16);
+#define PDEC(NW, R, MX, D)                                                                                         \
+    hipLaunchKernelGGL((w8a8_packed_decode_kernel<NW, R, MX, D, EPI>), grid, dim3(NW * 64), packed_decode_lds(R, M), \
+                       st, a, a_s, as_sm, qt, dt, out, ldo, n_rows, M, N, K)
+        if (M <= 4) PDEC(8, 32, 4, 2);
+        else if (M <= 16) PDEC(8, 16, 16, 3);
+        else if (M <= 32) PDEC(4, 16, 32, 3);
+        else if (M <= 48) PDEC(4, 8, 48, 4);
+        else PDEC(4, 8, 64, 4);
+#undef PDEC
+    } else {
+        const int tiles_m = (M + PBM - 1) / PBM, tiles_n = (N + PBN - 1) / PBN;
+        hipLaunchKernelGGL((w8a8_packed_tile_kernel<EPI>), dim3(tiles_m * tiles_n), dim3(256), 0, st, a, a_s, as_sm,
+                           qt, dt, out, ldo, n_rows, M, N, K, tiles_m, tiles_n);
+    }
+}
+
+}  // namespace prism
+
+using namespace prism;
+
+extern "C" int prism_q8_0_pack(const int8_t* qs, const uint16_t* d, int8_t* qt, uint16_t* dt, int64_t N, int64_t K,
+                               void* stream) {
+    if (!qs || !d || !qt || !dt) return PRISM_ERR_ARG;
+    if (N <= 0 || K <= 0 || N % 16 || K % 64 || N > (1 << 30) || K > (1 << 30)) return PRISM_ERR_SHAPE;
+    if (!PRISM_ALIGNED(qs, 16) || !PRISM_ALIGNED(qt, 16) || !PRISM_ALIGNED(dt, 16)) return PRISM_ERR_ALIGN;
+    const int64_t total = N / 16 * (K / 64) * 64;
+    hipLaunchKernelGGL(q8_0_pack_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream, qs,
+                       d, qt, dt, (int)N, (int)K);
+    PRISM_LAUNCH_CHECK();
+    return PRISM_OK;
+}
+
+extern "C" int prism_w8a8_q8_0_packed_gemm(const int8_t* a, const float* a_s, int64_t as_sm, const int8_t* qt,
+                                           const uint16_t* dt, void* out, int64_t ldo, const int32_t* n_rows,
+                                           int64_t M, int64_t N, int64_t K, int epi, int kernel, void* stream) {
+    if (!a || !a_s || !qt || !dt || !out || !n_rows) return PRISM_ERR_ARG;
+    if (epi != 0 && epi != 1) return PRISM_ERR_ARG;
+    if (M < 0 || N <= 0 || K <= 0 || N % 16 || K % 128 || ldo < N || M > (1 << 30) || N > (1 << 30) || K > (1 << 30))
+        return PRISM_ERR_SHAPE;
+    if (!PRISM_ALIGNED(a, 16) || !PRISM_ALIGNED(qt, 16) || !PRISM_ALIGNED(dt, 16)) return PRISM_ERR_ALIGN;
+    if (kernel < -1 || kernel > 1) return PRISM_ERR_ARG;
+    if (kernel == -1) kernel = M <= 64 ? 1 : 0;
+    if (kernel == 1 && M > 64) return PRISM_ERR_ARG;
+    if (M == 0) return PRISM_OK;
+    hipStream_t st = (hipStream_t)stream;
+    if (epi == 0)
+        launch_packed<0>(kernel, a, a_s, as_sm, qt, dt, out, ldo, n_rows, (int)M, (int)N, (int)K, st);
+    else
+        launch_packed<1>(kernel, a, a_s, as_sm, qt, dt, out, ldo, n_rows, (int)M, (int)N, (int)K, st);
+    PRISM_LAUNCH_CHECK();
+    return PRISM_OK;
+}

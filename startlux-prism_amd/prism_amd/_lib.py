@@ -21,6 +21,8 @@ _SIGS = {
     "prism_quant_rows_g": (_int, [_p, _i64, _p, _p, _p, _p, _i64, _i64, _i64, _p]),
     "prism_w8a8_gemm": (_int, [_p, _p, _i64, _i64, _p, _p, _int, _p, _i64, _p, _i64, _i64, _i64, _i64, _int, _int,
                                _p]),
+    "prism_q8_0_pack": (_int, [_p, _p, _p, _p, _i64, _i64, _p]),
+    "prism_w8a8_q8_0_packed_gemm": (_int, [_p, _p, _i64, _p, _p, _p, _i64, _p, _i64, _i64, _i64, _int, _int, _p]),
     "prism_w4a8_q4k_gemm": (_int, [_p, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _i64, _i64, _int, _int,
                                    _p]),
 }

@@ -23,6 +23,33 @@ from .quant import quant_rows  # noqa: F401  (re-exported: kernels/w8a8.py:264)
 KERNELS = {"auto": -1, "tile": 0, "decode": 1}
 
 
+class PackedQ8(NamedTuple):
+    """Q8_0 weights [n, k] in the MFMA-native layout the packed kernels stream: qt int8 [n/16, k/64, 64, 16] (per
+    16-row tile and block pair one 1 KB chunk, a wave's 16-byte-per-lane load), dt fp16 [n/16, k/64, 16, 2] (the
+    chunk's block scales).  The same values and scales as the Q8_0 planes, permuted; made once at load by pack_q8."""
+    qt: torch.Tensor
+    dt: torch.Tensor
+    n: int
+    k: int
+
+    @property
+    def shape(self):
+        return (self.n, self.k)
+
+
+def pack_q8(qs, d):
+    """Q8_0 planes (qs int8 [n, k], d fp16 [n, k/32], on the GPU) -> PackedQ8 (n % 16 == 0, k % 64 == 0)."""
+    n, k = qs.shape
+    if qs.dtype != torch.int8 or d.dtype != torch.float16 or tuple(d.shape) != (n, k // 32):
+        raise ValueError("pack_q8: qs int8 [n, k], d fp16 [n, k/32]")
+    if not (qs.is_contiguous() and d.is_contiguous()):
+        raise ValueError("pack_q8: contiguous planes expected")
+    qt = torch.empty(n // 16, k // 64, 64, 16, dtype=torch.int8, device=qs.device)
+    dt = torch.empty(n // 16, k // 64, 16, 2, dtype=torch.float16, device=qs.device)
+    L.call("prism_q8_0_pack", L.ptr(qs), L.ptr(d), L.ptr(qt), L.ptr(dt), n, k, L.stream_of(qs))
+    return PackedQ8(qt, dt, n, k)
+
+
 class Deferred(NamedTuple):
     """The reference's deferred split-K residual add (kernels/w8a8.py:171-180); never produced here."""
     n: int
@@ -51,6 +78,8 @@ def gemm(a, a_s, w, w_s, out, n_rows, gk, epi=0, outs=None, cfg=None, slots=None
     n_rows[0] untouched.  Returns None (no deferred split-K)."""
     if epi not in (0, 1):
         raise NotImplementedError(f"epilogue {epi}: only 0 (bf16 store) and 1 (fp32 residual add) are provided")
+    if isinstance(w, PackedQ8):
+        return _gemm_packed(a, a_s, w, out, n_rows, gk, epi, kernel)
     M, K = a.shape
     N = w.shape[0]
     if w.shape[1] != K or a.dtype != torch.int8 or w.dtype != torch.int8:
@@ -74,11 +103,30 @@ def gemm(a, a_s, w, w_s, out, n_rows, gk, epi=0, outs=None, cfg=None, slots=None
     return None
 
 
-def weight_from_q8(q8, gk, smooth=None):
-    """Q8_0 matrix -> (int8 [N, K], scales [N, K/gk]) (kernels/w8a8.py:274-286).  gk == 32 keeps the Q8_0 values
-    and returns the fp16 block scales as they are (the GEMM reads fp16 scales directly, exactly); otherwise the
-    weights are requantized per gk inputs as the reference does (fp32 scales)."""
+def _gemm_packed(a, a_s, w, out, n_rows, gk, epi, kernel):
+    M, K = a.shape
+    if gk != 32 or (w.n, w.k) != (w.n, K) or w.k != K:
+        raise ValueError("packed Q8_0 weights: gk must be 32 and K must match")
+    if a.dtype != torch.int8 or not a.is_contiguous():
+        raise ValueError("a must be contiguous int8 [M, K]")
+    if a_s.dtype != torch.float32 or a_s.shape[0] < M or (a_s.dim() == 2 and a_s.shape[1] != 1):
+        raise ValueError("packed kernels take one activation scale per token: a_s [M] or [M, 1]")
+    want = torch.bfloat16 if epi == 0 else torch.float32
+    if out.dtype != want or out.shape[0] < M or out.shape[1] < w.n or out.stride(1) != 1:
+        raise ValueError(f"out must be {want} [>= {M}, >= {w.n}] with unit column stride")
+    L.call("prism_w8a8_q8_0_packed_gemm", L.ptr(a), L.ptr(a_s), a_s.stride(0), L.ptr(w.qt), L.ptr(w.dt), L.ptr(out),
+           out.stride(0), L.ptr(n_rows), M, w.n, K, epi, KERNELS[kernel], L.stream_of(a))
+    return None
+
+
+def weight_from_q8(q8, gk, smooth=None, packed=True):
+    """Q8_0 matrix -> the GEMM's weight operands (kernels/w8a8.py:274-286).  gk == 32 keeps the Q8_0 values: by
+    default as PackedQ8 (the MFMA-native layout; returned as (PackedQ8, None)), or with packed=False as the planes
+    (int8 [N, K], fp16 [N, K/32]).  Otherwise the weights are requantized per gk inputs as the reference does
+    (int8 [N, K], fp32 [N, K/gk])."""
     if gk == 32 and smooth is None:
+        if packed and q8.qs.is_cuda and q8.qs.shape[0] % 16 == 0 and q8.qs.shape[1] % 128 == 0:
+            return pack_q8(q8.qs.contiguous(), q8.d.contiguous()), None
         return q8.qs.contiguous(), q8.d.contiguous()
     w = q8.dequant(torch.float32)
     if smooth is not None:

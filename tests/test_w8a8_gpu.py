@@ -168,3 +168,68 @@ def test_bad_arguments_raise(dev):
     with pytest.raises(NotImplementedError):
         KW.gemm(a, torch.ones(4, device=dev), w, torch.ones(16, 1, device=dev), torch.empty(4, 16, dtype=torch.bfloat16,
                 device=dev), _live(4, dev), 48, epi=2)
+
+
+# ------------------------------------------------------------------------------------------------ packed layout
+def _np_pack(qs, d):
+    N, K = qs.shape
+    r = qs.reshape(N // 16, 16, K // 64, 2, 4, 8)          # [nt, row, pair, half, q, 8]
+    qt = r.transpose(0, 2, 4, 1, 3, 5).reshape(N // 16, K // 64, 64, 16)
+    dt = d.reshape(N // 16, 16, K // 64, 2).transpose(0, 2, 1, 3)
+    return np.ascontiguousarray(qt), np.ascontiguousarray(dt)
+
+
+def test_pack_q8_layout(dev):
+    from prism_amd import w8a8 as KW
+    qs, d = q8_weights(64, 512, seed=31)
+    p = KW.pack_q8(_t(qs, dev), _t(d, dev, torch.float16))
+    torch.cuda.synchronize()
+    qt, dt = _np_pack(qs, d)
+    assert np.array_equal(p.qt.cpu().numpy(), qt)
+    assert np.array_equal(p.dt.view(torch.int16).cpu().numpy().view(np.uint16), dt)
+
+
+def _packed_gemm(dev, a, s, qs, d, epi, kernel, live=None, out0=None, ldo=None):
+    from prism_amd import w8a8 as KW
+    M, K = a.shape
+    N = qs.shape[0]
+    live = M if live is None else live
+    pw = KW.pack_q8(_t(qs, dev), _t(d, dev, torch.float16))
+    ldo = N if ldo is None else ldo
+    if epi == 0:
+        out = torch.full((M, ldo), 7, dtype=torch.int16, device=dev).view(torch.bfloat16)
+    else:
+        out = _t(out0, dev).clone()
+    KW.gemm(_t(a, dev), _t(s, dev), pw, None, out, _live(live, dev), 32, epi=epi, kernel=kernel)
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("kernel", ["decode", "tile"])
+def test_packed_config0_bit_exact(dev, kernel):
+    qs, d = q8_weights(4096, 4096, seed=0)
+    a, s = O.quant_rows_i8(acts_bf16(16, 4096, seed=100))
+    want = O.w8a8_gemm(a, s, qs, d, 32, epi=0)
+    got = _packed_gemm(dev, a, s, qs, d, 0, kernel)
+    assert np.array_equal(got.view(torch.int16).cpu().numpy().view(np.uint16), want)
+
+
+PCASES = [  # (M, N, K, live)
+    (1, 16, 128, 1), (2, 48, 384, 2), (4, 256, 5120, 3), (7, 64, 1024, 7), (16, 128, 4096, 16), (17, 64, 640, 9),
+    (33, 96, 1280, 33), (64, 32, 2048, 60), (100, 272, 640, 77), (256, 384, 5120, 256), (130, 128, 17408, 129),
+]
+
+
+@pytest.mark.parametrize("M,N,K,live", PCASES)
+def test_packed_cases_bit_exact(dev, M, N, K, live):
+    qs, d = q8_weights(N, K, seed=N + 3 * K)
+    a, s = O.quant_rows_i8(acts_bf16(M, K, seed=M + 5 * K))
+    want0 = O.w8a8_gemm(a, s, qs, d, 32, epi=0, live=live)
+    base = rng(M * N + 1).standard_normal((M, N)).astype(np.float32)
+    want1 = O.w8a8_gemm(a, s, qs, d, 32, epi=1, out=base.copy(), live=live)
+    for kernel in ["tile"] + (["decode"] if M <= 64 else []):
+        got0 = _packed_gemm(dev, a, s, qs, d, 0, kernel, live=live).view(torch.int16).cpu().numpy().view(np.uint16)
+        assert np.array_equal(got0[:live], want0[:live]), kernel
+        assert (got0[live:] == 7).all(), kernel
+        got1 = _packed_gemm(dev, a, s, qs, d, 1, kernel, live=live, out0=base).cpu().numpy()
+        assert np.array_equal(got1, want1), kernel
