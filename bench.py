@@ -38,14 +38,18 @@ def q8_bytes(N, K):
 
 
 def make_q8_weights(N, K, seed, dev):
+    """Q8_0 weights of N(0, 0.02^2) values, in the GEMM's operand form (kernels/w8a8.py weight_from_q8, gk = 32):
+    the MFMA-native packed layout."""
     import torch
     from prism_amd import gguf_formats as GF
+    from prism_amd import w8a8 as KW
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
     w = torch.randn(N, K, generator=g, device=dev, dtype=torch.float32) * 0.02
     q8 = GF.quantize_q8_0(w)
     del w
-    return q8.qs, q8.d
+    packed, _ = KW.weight_from_q8(q8, 32)
+    return q8, packed
 
 
 def make_acts(M, K, seed, dev):
@@ -59,7 +63,7 @@ def bench_prefill(steps, warmup, dev):
     import torch
     from prism_amd import quant as KQ
     from prism_amd import w8a8 as KW
-    qs, d = make_q8_weights(N1, K1, 1, dev)
+    q8, pw = make_q8_weights(N1, K1, 1, dev)
     x = make_acts(M1, K1, 2, dev)
     q = torch.empty(M1, K1, dtype=torch.int8, device=dev)
     s = torch.empty(M1, dtype=torch.float32, device=dev)
@@ -68,7 +72,7 @@ def bench_prefill(steps, warmup, dev):
 
     def step():
         KQ.rows_q8(x, None, q, s, n, M1)
-        KW.gemm(q, s, qs, d, out, n, 32, epi=0)
+        KW.gemm(q, s, pw, None, out, n, 32, epi=0)
 
     for _ in range(warmup):
         step()
@@ -83,7 +87,7 @@ def bench_prefill(steps, warmup, dev):
         e0.record()
         KQ.rows_q8(x, None, q, s, n, M1)
         e1.record()
-        KW.gemm(q, s, qs, d, out, n, 32, epi=0)
+        KW.gemm(q, s, pw, None, out, n, 32, epi=0)
         e2.record()
     stop.record()
     torch.cuda.synchronize()
@@ -94,43 +98,52 @@ def bench_prefill(steps, warmup, dev):
     ops = 2.0 * M1 * N1 * K1
     res = dict(ms_per_step=total_ms / steps, wall_s=wall, gemm_ms=gemm_ms, quant_ms=quant_ms, ops=ops,
                value=ops / (total_ms / steps * 1e-3) / 1e12)
-    sample = dict(q=q, s=s, qs=qs, d=d)
+    sample = dict(q=q, s=s, qs=q8.qs, d=q8.d)
     return res, sample
 
 
 def bench_decode_sweep(dev, iters=40):
-    """GB/s of packed Q8_0 weight bytes per decode shape, rotating > 3 x MALL of weight copies."""
+    """GB/s of packed Q8_0 weight bytes per decode shape.  The launches (rotating over weight copies totalling more
+    than 3 x the 256 MB MALL, so every launch streams its weights from HBM) are captured in a HIP graph and replayed:
+    back-to-back kernels as the engine's captured decode steps run them."""
     import torch
+    from prism_amd import quant as KQ
     from prism_amd import w8a8 as KW
     rows = []
     for (K, N) in ((5120, 5120), (17408, 5120)):
         wbytes = q8_bytes(N, K)
         copies = max(3, -(-3 * MALL_BYTES // wbytes))
-        base_qs, base_d = make_q8_weights(N, K, 3, dev)
-        ws = [(base_qs.clone(), base_d.clone()) for _ in range(copies)]
+        _, base = make_q8_weights(N, K, 3, dev)
+        ws = [KW.PackedQ8(base.qt.clone(), base.dt.clone(), N, K) for _ in range(copies)]
         for M in (1, 4, 16, 64):
             x = make_acts(M, K, 4, dev)
-            from prism_amd import quant as KQ
             q = torch.empty(M, K, dtype=torch.int8, device=dev)
             s = torch.empty(M, dtype=torch.float32, device=dev)
             n = torch.tensor([M], dtype=torch.int32, device=dev)
             KQ.rows_q8(x, None, q, s, n, M)
             out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
             for i in range(copies):
-                KW.gemm(q, s, ws[i][0], ws[i][1], out, n, 32)
+                KW.gemm(q, s, ws[i], None, out, n, 32)
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            st = torch.cuda.Stream()
+            with torch.cuda.stream(st):
+                with torch.cuda.graph(g, stream=st):
+                    for i in range(iters):
+                        KW.gemm(q, s, ws[i % copies], None, out, n, 32)
+            g.replay()
             torch.cuda.synchronize()
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             a.record()
-            for i in range(iters):
-                qs_, d_ = ws[i % copies]
-                KW.gemm(q, s, qs_, d_, out, n, 32)
+            g.replay()
             b.record()
             torch.cuda.synchronize()
             us = a.elapsed_time(b) / iters * 1e3
             gbs = wbytes / (us * 1e-6) / 1e9
             rows.append(dict(M=M, K=K, N=N, us=round(us, 2), GBps=round(gbs, 1),
                              hbm_frac=round(gbs / PEAK_HBM_GBS, 3), TOPS=round(2 * M * N * K / (us * 1e-6) / 1e12, 2)))
-        del ws
+            del g
+        del ws, base
         torch.cuda.empty_cache()
     return rows
 

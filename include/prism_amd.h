@@ -108,21 +108,29 @@ PRISM_API int prism_w8a8_q8_0_packed_gemm(const int8_t* a, const float* a_s, int
                                           int64_t M, int64_t N, int64_t K, int epi, int kernel, void* stream);
 
 /*
- * W4A8 GEMM on Q4_K weights in the repacked W4 layout.  Replaces kernels/w4a8.py:353-366 (gemm, kind "q4k") and
- * the native startlux_prism::w4a8_gemm (csrc/w4a8_gemm.cu:887-961, schema :963-966); arithmetic of
- * kernels/w4a8.py:14-22 / gemm_ref (:177-199), per super-block b of 256 inputs in increasing b:
- *   acc  = sum_g sc[b,n,g] (xq . q)_g ;  mins = sum_g mn[b,n,g] S[m, 8b+g]          (int32, exact)
- *   t = RN(d[b,n] float(acc)); t = fma(-dm[b,n], float(mins), t); y = fma(a[b,m], t, y)
- *   epi 0: bf16(y); epi 1: out = RN(out + y).
- * xq int8 [M, K]; a fp32, element (b, m) at a[b * a_sb + m] (a_sb = 0: one scale per token);
- * xs int8 [K/256, M, 16] (split per-32 sums); q uint8 [N, K/2] (per 32 inputs byte t = q[t] | q[t+16] << 4);
- * sc, mn uint8 [K/256, N, 8]; d, dm fp32 [K/256, N].  Needs K % 256 == 0, N % 16 == 0.
- * kernel: -1 picks by shape; 0 the tile kernel; 1 the decode kernel (M <= 64).
+ * Repack Q4_K weights into the MFMA-native layout the W4A8 kernels read: a byte permutation of the GGUF block_q4_K
+ * bytes (the load-time step the reference's repack is: kernels/w4a8.py:70-94).  raw uint8 [N, K/256, 144] ->
+ * qv uint8 [N/16][K/256][2][64][16] (per 16-row tile and super-block, lane slot l = row l % 16, q = l / 16; bytes
+ * 4 i .. 4 i + 3 of half h: sub-block 4 h + i, byte t = v[4 q + t] | v[16 + 4 q + t] << 4), meta uint8
+ * [N/16][K/256][16][16] (per row the block's first 16 bytes: d, dmin, 12 bytes of 6-bit scales and mins).
+ * Needs N % 16 == 0, K % 256 == 0.
  */
-PRISM_API int prism_w4a8_q4k_gemm(const int8_t* xq, const float* a, int64_t a_sb, const int8_t* xs, const uint8_t* q,
-                        const uint8_t* sc, const uint8_t* mn, const float* d, const float* dm, void* out,
-                        int64_t ldo, const int32_t* n_rows, int64_t M, int64_t N, int64_t K, int epi, int kernel,
-                        void* stream);
+PRISM_API int prism_q4k_pack(const uint8_t* raw, uint8_t* qv, uint8_t* meta, int64_t N, int64_t K, void* stream);
+
+/*
+ * W4A8 GEMM on packed Q4_K weights.  Replaces kernels/w4a8.py:353-366 (gemm, kind "q4k") and the native
+ * startlux_prism::w4a8_gemm (csrc/w4a8_gemm.cu:887-961, schema :963-966); arithmetic of kernels/w4a8.py:14-22 /
+ * gemm_ref (:177-199), per super-block b of 256 inputs in increasing b:
+ *   acc  = sum_g sc[n,b,g] (xq . q)_g ;  mins = sum_g mn[n,b,g] S[m, 8b+g]          (int32, exact)
+ *   t = RN(d[n,b] float(acc)); t = fma(-dmin[n,b], float(mins), t); y = fma(a[b,m], t, y)
+ *   epi 0: bf16(y); epi 1: out = RN(out + y).
+ * xq int8 [M, K]; a fp32, element (b, m) at a[b * a_sb + m] (a_sb = 0: one scale per token); xs int8 [K/256, M, 16]
+ * (per super-block eight S & 63 then eight S >> 6); qv / meta from prism_q4k_pack; out row stride ldo.
+ * kernel: -1 picks by M; 0 the prefill tile kernel; 1 the decode kernel (M <= 16).  Needs K % 256 == 0, N % 16 == 0.
+ */
+PRISM_API int prism_w4a8_q4k_gemm(const int8_t* xq, const float* a, int64_t a_sb, const int8_t* xs, const uint8_t* qv,
+                                  const uint8_t* meta, void* out, int64_t ldo, const int32_t* n_rows, int64_t M,
+                                  int64_t N, int64_t K, int epi, int kernel, void* stream);
 
 #ifdef __cplusplus
 }

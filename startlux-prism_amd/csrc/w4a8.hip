@@ -1,7 +1,528 @@
-// W4A8 GEMM on Q4_K (placeholder until the kernels land).
+// W4A8 GEMM on Q4_K weights (gfx950): int8 activations x 4-bit k-quant weights on v_mfma_i32_16x16x32_i8.
+//
+// Arithmetic (StartLux-Prism kernels/w4a8.py:14-22, gemm_ref :177-199), per output (m, n), super-blocks b of 256
+// inputs in increasing b:
+//   acc  = sum_g sc[n,b,g] (xq . q)_g        int32, exact (P_g from one MFMA per 32-input sub-block)
+//   mins = sum_g mn[n,b,g] S[m, 8b + g]       int32, exact (S: the activation sums per 32 inputs)
+//   t = RN(d[n,b] float(acc));  t = fma(-dmin[n,b], float(mins), t);  y = fma(a[b,m], t, y)
+// then bf16(y) (epi 0) or out = RN(out + y) (epi 1).  y's chain over b is kept in super-block order by every kernel.
+//
+// Device layout (prism_q4k_pack, made once at load from the GGUF block_q4_K bytes, as the reference's repack is:
+// kernels/w4a8.py:70-94): a byte permutation of the GGUF blocks, 144 bytes per row and super-block.
+//   qv   uint8 [N/16][K/256][2][64][16]: per (16-row tile nt, super-block b) 2 KB.  Half h, lane slot l (row
+//        r = l % 16, q = l / 16), bytes 4 i .. 4 i + 3 hold sub-block g = 4 h + i of row 16 nt + r: byte t of them is
+//        v[4 q + t] | v[16 + 4 q + t] << 4 (v: the sub-block's 32 values in k order).  Unpacked with two masks, the
+//        word is the 8-byte MFMA operand for k = {4 q .. 4 q + 3, 16 + 4 q .. 16 + 4 q + 3} of the sub-block.
+//   meta uint8 [N/16][K/256][16][16]: per row the GGUF block's first 16 bytes: d, dmin (fp16) and the 12 bytes of
+//        6-bit scales and mins (ggml get_scale_min_k4 order, gguf_weights.py:56-60).
+// Activations: xq int8 [M, K] row-major; a fp32, (b, m) at a[b a_sb + m] (a_sb = 0: one scale per token);
+// xs int8 [K/256, M, 16]: per super-block the eight S & 63 then the eight S >> 6 (kernels/quant.py:314-330).
 #include "common.h"
-extern "C" int prism_w4a8_q4k_gemm(const int8_t*, const float*, int64_t, const int8_t*, const uint8_t*, const uint8_t*,
-                                   const uint8_t*, const float*, const float*, void*, int64_t, const int32_t*, int64_t,
-                                   int64_t, int64_t, int, int, void*) {
-    return PRISM_ERR_ARG;
+
+namespace prism {
+
+__device__ __forceinline__ int64_t unpack_q4(uint32_t w) {
+    return (int64_t)(w & 0x0f0f0f0fu) | ((int64_t)((w >> 4) & 0x0f0f0f0fu) << 32);
+}
+
+// The activation operand of sub-block g for lane group q: k = {4 q .. 4 q + 3, 16 + 4 q .. 16 + 4 q + 3}.
+__device__ __forceinline__ int64_t act_operand(const int8_t* row, int g, int q) {
+    const uint32_t lo = *reinterpret_cast<const uint32_t*>(row + 32 * g + 4 * q);
+    const uint32_t hi = *reinterpret_cast<const uint32_t*>(row + 32 * g + 16 + 4 * q);
+    return (int64_t)lo | ((int64_t)hi << 32);
+}
+
+// One row's 16 meta bytes -> d, dmin (fp32) and the 8 scales and 8 mins (ggml get_scale_min_k4).
+__device__ __forceinline__ void row_meta(v4u m, float& d, float& dm, int* sc, int* mn) {
+    d = f16_to_f32(m[0] & 0xffffu);
+    dm = f16_to_f32(m[0] >> 16);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const uint32_t s0 = (m[1] >> (8 * j)) & 0xff, s4 = (m[2] >> (8 * j)) & 0xff, s8 = (m[3] >> (8 * j)) & 0xff;
+        sc[j] = s0 & 63;
+        mn[j] = s4 & 63;
+        sc[j + 4] = (s8 & 0xf) | ((s0 >> 6) << 4);
+        mn[j + 4] = (s8 >> 4) | ((s4 >> 6) << 4);
+    }
+}
+
+// t = RN(d float(acc)); t = fma(-dm, float(mins), t)   (kernels/w4a8.py:191)
+__device__ __forceinline__ float q4k_term(float d, float dm, int acc, int mins) {
+    return fmaf(-dm, (float)mins, mul_rn(d, (float)acc));
+}
+
+// S = (S & 63) + 64 (S >> 6) per sub-block, from a (super-block, row)'s 16 split-sum bytes
+__device__ __forceinline__ void split_sums(v4i s, int* S) {
+#pragma unroll
+    for (int g = 0; g < 8; g++) {
+        const int lo = (int)(int8_t)(((uint32_t)s[g >> 2]) >> (8 * (g & 3)));
+        const int hi = (int)(int8_t)(((uint32_t)s[2 + (g >> 2)]) >> (8 * (g & 3)));
+        S[g] = lo + 64 * hi;
+    }
+}
+
+// ---------------------------------------------------------------------------------------------- pack
+// One thread per (nt, b, h, l): gathers 4 sub-blocks x 4 bytes from the GGUF block of row 16 nt + l % 16.
+__global__ __launch_bounds__(256) void q4k_pack_kernel(const uint8_t* __restrict__ raw, uint8_t* __restrict__ qv,
+                                                       uint8_t* __restrict__ meta, int N, int K) {
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int NB = K / 256;
+    const int64_t total = (int64_t)(N / 16) * NB * 128;
+    if (e >= total) return;
+    const int l = (int)(e & 63), h = (int)((e >> 6) & 1);
+    const int64_t c = e >> 7;                          // (nt, b)
+    const int b = (int)(c % NB), nt = (int)(c / NB);
+    const int r = l & 15, q = l >> 4;
+    const uint8_t* blk = raw + ((int64_t)(16 * nt + r) * NB + b) * 144;
+    uint32_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int g = 4 * h + i;
+        const uint8_t* qs = blk + 16 + 32 * (g >> 1);  // 32 bytes: low nibbles sub-block 2 c, high 2 c + 1
+        uint32_t w = 0;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const uint32_t lo = (g & 1) ? (qs[4 * q + t] >> 4) : (qs[4 * q + t] & 0xf);
+            const uint32_t hi = (g & 1) ? (qs[16 + 4 * q + t] >> 4) : (qs[16 + 4 * q + t] & 0xf);
+            w |= (lo | (hi << 4)) << (8 * t);
+        }
+        o[i] = w;
+    }
+    reinterpret_cast<v4u*>(qv)[e] = v4u{o[0], o[1], o[2], o[3]};
+    if (h == 0 && q == 0) {                            // blocks are 144 bytes: 16-byte aligned, copy by words
+        const uint32_t* s32 = reinterpret_cast<const uint32_t*>(blk);
+        reinterpret_cast<v4u*>(meta)[c * 16 + r] = v4u{s32[0], s32[1], s32[2], s32[3]};
+    }
+}
+
+// ---------------------------------------------------------------------------------------------- decode
+// A workgroup of NW waves owns one 16-row tile and every activation row (M <= 16).  Round r covers R super-blocks;
+// wave w computes super-blocks r R + w CB .. + CB - 1.  Per round the per-wave global loads are the 2 KB weight
+// chunks (two dwordx4 per lane, requested D - 1 rounds ahead).  The round's meta (unpacked once per row and
+// super-block by a staging thread), activation rows, activation sums and activation scales are fetched with
+// 16-byte loads a round ahead and staged in one of two LDS buffers.  Each super-block's term t of each output goes
+// to one of two LDS term buffers; the owner thread of each output folds round r - 1's terms,
+// y = fma(a[b, m], t, y) in super-block order, while round r is computed; one barrier per round.
+template <int NW, int R, int MX, int D, int EPI>
+__global__ __launch_bounds__(NW * 64) void w4a8_decode_kernel(const int8_t* __restrict__ xq,
+                                                              const float* __restrict__ a, int64_t a_sb,
+                                                              const int8_t* __restrict__ xs,
+                                                              const uint8_t* __restrict__ qv,
+                                                              const uint8_t* __restrict__ meta,
+                                                              void* __restrict__ out, int64_t ldo,
+                                                              const int32_t* __restrict__ n_rows, int M, int N, int K) {
+    constexpr int NT = NW * 64;
+    constexpr int CB = R / NW;                     // super-blocks per wave per round
+    static_assert(CB >= 1 && CB * NW == R, "R must be a multiple of NW");
+    static_assert(MX <= 16 && R * 16 <= NT && R * MX <= NT, "one staging thread per (row, super-block)");
+    constexpr int RB = R * 256;                    // activation bytes per row per round
+    constexpr int LDA = RB + 16;
+    constexpr int CPR = RB / 16;
+    constexpr int XPT = (MX * CPR + NT - 1) / NT;
+    extern __shared__ __attribute__((aligned(16))) int8_t dsm[];
+    float* terms = reinterpret_cast<float*>(dsm);                 // [2][R][M][16]
+    int* scl = reinterpret_cast<int*>(terms + 2 * R * M * 16);    // [2][R][8][16] scales, [sub-block][row]
+    int* mnl = scl + 2 * R * 128;                                 // [2][R][8][16] mins
+    float* dl = reinterpret_cast<float*>(mnl + 2 * R * 128);      // [2][R][16] d
+    float* dml = dl + 2 * R * 16;                                 // [2][R][16] dmin
+    int* sl = reinterpret_cast<int*>(dml + 2 * R * 16);           // [2][R][M][8] activation sums S
+    float* al = reinterpret_cast<float*>(sl + 2 * R * M * 8);     // [3][R][M] activation scales: read by the fold of
+                                                                  // round r - 1 while round r + 1 is staged
+    int8_t* xl = reinterpret_cast<int8_t*>(al + 3 * R * M);       // [2][M][LDA] activations
+    const int tstride = R * M * 16, xstride = M * LDA;
+
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int nt = blockIdx.x;
+    const int live = min(M, __ldg(n_rows));
+    const int NB = K / 256;
+    const int nr = (NB + R - 1) / R;
+    const int lm = lane & 15, q = lane >> 4;
+    const int xch = M * CPR;
+
+    const v4u* cw = reinterpret_cast<const v4u*>(qv) + (int64_t)nt * NB * 128 + lane;
+    const v4u* cm = reinterpret_cast<const v4u*>(meta) + (int64_t)nt * NB * 16;
+
+    struct Staged {
+        v4u m;        // meta row (thread < 16 R: super-block tid / 16, row tid % 16)
+        v4i s;        // split sums (thread < R M: super-block tid / M, activation row tid % M)
+        float as;     // activation scale of the same (super-block, row)
+        v4i x[XPT];
+    };
+    auto stage_load = [&](int r, Staged& sg) {
+        const int b0 = r * R;
+        const int c = min(tid, 16 * R - 1);
+        sg.m = cm[(int64_t)min(b0 + c / 16, NB - 1) * 16 + (c & 15)];
+        const int e = min(tid, R * M - 1);
+        const int bb = min(b0 + e / M, NB - 1), mm = e % M;
+        sg.s = *reinterpret_cast<const v4i*>(xs + ((int64_t)bb * M + mm) * 16);
+        sg.as = a[(int64_t)bb * a_sb + mm];
+        const int64_t k0 = (int64_t)r * RB;
+#pragma unroll
+        for (int i = 0; i < XPT; i++) {
+            const int cc = min(tid + i * NT, xch - 1);
+            const int64_t kk = min(k0 + (cc % CPR) * 16, (int64_t)K - 16);
+            sg.x[i] = *reinterpret_cast<const v4i*>(xq + (int64_t)(cc / CPR) * K + kk);
+        }
+    };
+    auto stage_store = [&](const Staged& sg, int rr) {
+        const int buf = rr & 1;
+        if (tid < 16 * R) {
+            const int lb = tid >> 4, row = tid & 15;
+            float d, dm;
+            int sc[8], mn[8];
+            row_meta(sg.m, d, dm, sc, mn);
+#pragma unroll
+            for (int g = 0; g < 8; g++) {
+                scl[((buf * R + lb) * 8 + g) * 16 + row] = sc[g];
+                mnl[((buf * R + lb) * 8 + g) * 16 + row] = mn[g];
+            }
+            dl[(buf * R + lb) * 16 + row] = d;
+            dml[(buf * R + lb) * 16 + row] = dm;
+        }
+        if (tid < R * M) {
+            int S[8];
+            split_sums(sg.s, S);
+            int* sp = sl + (buf * R * M + tid) * 8;       // tid = lb M + m
+            *reinterpret_cast<v4i*>(sp) = v4i{S[0], S[1], S[2], S[3]};
+            *reinterpret_cast<v4i*>(sp + 4) = v4i{S[4], S[5], S[6], S[7]};
+            al[(rr % 3) * R * M + tid] = sg.as;
+        }
+#pragma unroll
+        for (int i = 0; i < XPT; i++) {
+            const int cc = tid + i * NT;
+            if (cc < xch) *reinterpret_cast<v4i*>(&xl[buf * xstride + (cc / CPR) * LDA + (cc % CPR) * 16]) = sg.x[i];
+        }
+    };
+    auto load_w = [&](int r, v4u (*w)[2]) {
+#pragma unroll
+        for (int i = 0; i < CB; i++) {
+            const int64_t b = min(r * R + wv * CB + i, NB - 1);
+            w[i][0] = __builtin_nontemporal_load(cw + b * 128);
+            w[i][1] = __builtin_nontemporal_load(cw + b * 128 + 64);
+        }
+    };
+    auto compute = [&](int r, v4u (*w)[2], int buf) {
+        float* tb = terms + (r & 1) * tstride;
+        const int8_t* xrow = xl + buf * xstride + min(lm, M - 1) * LDA;
+#pragma unroll
+        for (int i = 0; i < CB; i++) {
+            const int lb = wv * CB + i;
+            if (r * R + lb < NB) {
+                const int* scp = scl + (buf * R + lb) * 128 + 4 * q;
+                const int* mnp = mnl + (buf * R + lb) * 128 + 4 * q;
+                v4i acc = {0, 0, 0, 0}, mins = {0, 0, 0, 0};
+                const int* Sp = sl + ((buf * R + lb) * M + min(lm, M - 1)) * 8;
+                const v4i S0 = *reinterpret_cast<const v4i*>(Sp), S1 = *reinterpret_cast<const v4i*>(Sp + 4);
+#pragma unroll
+                for (int g = 0; g < 8; g++) {
+                    const int64_t wf = unpack_q4(w[i][g >> 2][g & 3]);
+                    const int64_t af = act_operand(xrow + lb * 256, g, q);
+                    const v4i zero = {0, 0, 0, 0};
+                    const v4i P = __builtin_amdgcn_mfma_i32_16x16x32_i8(wf, af, zero, 0, 0, 0);
+                    const v4i sc = *reinterpret_cast<const v4i*>(scp + g * 16);
+                    const v4i mn = *reinterpret_cast<const v4i*>(mnp + g * 16);
+                    const int Sg = g < 4 ? S0[g] : S1[g - 4];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        acc[e] += sc[e] * P[e];
+                        mins[e] += mn[e] * Sg;
+                    }
+                }
+                const v4f d = *reinterpret_cast<const v4f*>(&dl[(buf * R + lb) * 16 + 4 * q]);
+                const v4f dm = *reinterpret_cast<const v4f*>(&dml[(buf * R + lb) * 16 + 4 * q]);
+                v4f t;
+#pragma unroll
+                for (int e = 0; e < 4; e++) t[e] = q4k_term(d[e], dm[e], acc[e], mins[e]);
+                if (lm < M) *reinterpret_cast<v4f*>(&tb[(lb * M + lm) * 16 + 4 * q]) = t;
+            }
+        }
+    };
+    float y = 0.f;
+    const int fo = tid;                                            // output (m = fo / 16, n = 16 nt + fo % 16)
+    auto fold = [&](int r) {
+        if (fo < M * 16) {
+            const float* tb = terms + (r & 1) * tstride;
+            const float* ap = al + (r % 3) * R * M + (fo >> 4);
+            const int nb = min(R, NB - r * R);
+            float acc = y;
+            for (int j = 0; j < nb; j++) acc = fmaf(ap[j * M], tb[j * M * 16 + fo], acc);
+            y = acc;
+        }
+    };
+
+    v4u wr[D][CB][2];
+    Staged sg;
+#pragma unroll
+    for (int d = 0; d < D - 1; d++) load_w(d, wr[d]);
+    stage_load(0, sg);
+    stage_store(sg, 0);
+    stage_load(1, sg);
+    lds_barrier();
+    for (int r0 = 0; r0 < nr; r0 += D) {
+#pragma unroll
+        for (int d = 0; d < D; d++) {
+            const int r = r0 + d;
+            load_w(r + D - 1, wr[(d + D - 1) % D]);        // past the end: the last chunk again (a cache hit)
+            stage_store(sg, r + 1);
+            stage_load(r + 2, sg);
+            if (r < nr) compute(r, wr[d], r & 1);
+            if (r >= 1 && r <= nr) fold(r - 1);
+            lds_barrier();
+        }
+    }
+    if (nr % D == 0) fold(nr - 1);
+    const int m = fo >> 4, n = 16 * nt + (fo & 15);
+    if (fo < M * 16 && m < live) {
+        if (EPI == 0) {
+            reinterpret_cast<uint16_t*>(out)[(int64_t)m * ldo + n] = (uint16_t)f32_to_bf16(y);
+        } else {
+            float* op = reinterpret_cast<float*>(out) + (int64_t)m * ldo + n;
+            *op = add_rn(*op, y);
+        }
+    }
+}
+
+static size_t w4a8_decode_lds(int R, int M) {
+    return 2 * (size_t)R * M * 16 * 4 + 2 * (size_t)R * 128 * 4 * 2 + 2 * (size_t)R * 16 * 4 * 2 +
+           2 * (size_t)R * M * 8 * 4 + 3 * (size_t)R * M * 4 + 2 * (size_t)M * (R * 256 + 16);
+}
+
+// ---------------------------------------------------------------------------------------------- prefill tile
+// 128 (n) x 64 (m) output tile per 256-thread workgroup: 4 waves, each 32 n x 64 m (2 x 4 MFMA tiles of 16 x 16),
+// one super-block per stage.  Staged in LDS per stage: the 8 weight chunks' halves (2 tiles x 2 KB per wave ...
+// 8 tiles x 2 KB), the tile's unpacked meta, the activation rows, sums and scales; the next stage's global data are
+// in registers while the current one is computed.  Each wave keeps its outputs' fp32 sums y over super-blocks.
+constexpr int QBN = 128, QBM = 64;
+constexpr int QLDA = 256 + 16;
+
+template <int EPI>
+__global__ __launch_bounds__(256, 2) void w4a8_tile_kernel(const int8_t* __restrict__ xq, const float* __restrict__ a,
+                                                           int64_t a_sb, const int8_t* __restrict__ xs,
+                                                           const uint8_t* __restrict__ qv,
+                                                           const uint8_t* __restrict__ meta, void* __restrict__ out,
+                                                           int64_t ldo, const int32_t* __restrict__ n_rows, int M,
+                                                           int N, int K, int tiles_m, int tiles_n) {
+    __shared__ __attribute__((aligned(16))) uint8_t Bs[8 * 2048];     // 8 row tiles x (2 halves x 64 lanes x 16 B)
+    __shared__ __attribute__((aligned(16))) int8_t As[QBM * QLDA];
+    __shared__ int scl[8][QBN], mnl[8][QBN];
+    __shared__ float dl[QBN], dml[QBN];
+    __shared__ int sl[QBM][8];
+    __shared__ float al[QBM];
+
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int lm = lane & 15, q = lane >> 4;
+    // tile order as the W8A8 kernels: XCD-contiguous ranges, groups of 8 tile-rows of M
+    int pm, pn;
+    {
+        const int total = tiles_m * tiles_n;
+        int t = blockIdx.x;
+        if ((total & 7) == 0) t = (t & 7) * (total >> 3) + (t >> 3);
+        const int per_group = 8 * tiles_n, first_m = (t / per_group) * 8, gm = min(tiles_m - first_m, 8);
+        pm = first_m + (t % per_group) % gm;
+        pn = (t % per_group) / gm;
+    }
+    const int m0 = pm * QBM, n0 = pn * QBN;
+    const int live = min(M, __ldg(n_rows));
+    if (m0 >= live) return;
+    const int NB = K / 256, ntiles = N / 16;
+
+    // global -> register staging of one super-block
+    // weights: 8 tiles x 128 chunks of 16 B = 1024 chunks, 4 per thread
+    const v4u* wsrc[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int c = tid + 256 * i;
+        wsrc[i] = reinterpret_cast<const v4u*>(qv) + (int64_t)min(n0 / 16 + (c >> 7), ntiles - 1) * NB * 128 + (c & 127);
+    }
+    // meta: 128 rows x 16 B, threads < 128
+    const v4u* msrc = reinterpret_cast<const v4u*>(meta) + (int64_t)min(n0 / 16 + (tid >> 4), ntiles - 1) * NB * 16 + (tid & 15);
+    // activations: 64 rows x 256 B = 1024 chunks, 4 per thread
+    const int8_t* xsrc[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int c = tid + 256 * i;
+        xsrc[i] = xq + (int64_t)min(m0 + (c >> 4), M - 1) * K + (c & 15) * 16;
+    }
+    const int srow = min(m0 + (tid & 63), M - 1);     // sums and scale: threads < 64, one activation row each
+    v4u rw[4], rm;
+    v4i rx[4], rs;
+    float ra;
+    auto gload = [&](int b) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            rw[i] = __builtin_nontemporal_load(wsrc[i] + (int64_t)b * 128);
+            rx[i] = *reinterpret_cast<const v4i*>(xsrc[i] + (int64_t)b * 256);
+        }
+        rm = msrc[(int64_t)b * 16];
+        rs = *reinterpret_cast<const v4i*>(xs + ((int64_t)b * M + srow) * 16);
+        ra = a[(int64_t)b * a_sb + srow];
+    };
+    auto sstore = [&]() {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int c = tid + 256 * i;
+            *reinterpret_cast<v4u*>(&Bs[(c >> 7) * 2048 + (c & 127) * 16]) = rw[i];
+            *reinterpret_cast<v4i*>(&As[(c >> 4) * QLDA + (c & 15) * 16]) = rx[i];
+        }
+        if (tid < 128) {
+            float d, dm;
+            int sc[8], mn[8];
+            row_meta(rm, d, dm, sc, mn);
+#pragma unroll
+            for (int g = 0; g < 8; g++) {
+                scl[g][tid] = sc[g];
+                mnl[g][tid] = mn[g];
+            }
+            dl[tid] = d;
+            dml[tid] = dm;
+        }
+        if (tid < 64) {
+            int S[8];
+            split_sums(rs, S);
+            *reinterpret_cast<v4i*>(&sl[tid][0]) = v4i{S[0], S[1], S[2], S[3]};
+            *reinterpret_cast<v4i*>(&sl[tid][4]) = v4i{S[4], S[5], S[6], S[7]};
+            al[tid] = ra;
+        }
+    };
+
+    // wave wv: n rows 32 wv .. 32 wv + 31 (tiles 2 wv, 2 wv + 1), all 64 m (4 tiles)
+    float y[2][4][4];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) y[i][j][e] = 0.f;
+
+    gload(0);
+    for (int b = 0; b < NB; b++) {
+        lds_barrier();
+        sstore();
+        lds_barrier();
+        if (b + 1 < NB) gload(b + 1);
+        v4i acc[2][4], mins[2][4];
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) acc[i][j] = mins[i][j] = v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int g = 0; g < 8; g++) {
+            int64_t wf[2], af[4];
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const uint32_t word = *reinterpret_cast<const uint32_t*>(
+                    &Bs[(2 * wv + i) * 2048 + (g >> 2) * 1024 + lane * 16 + 4 * (g & 3)]);
+                wf[i] = unpack_q4(word);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) af[j] = act_operand(&As[(16 * j + lm) * QLDA], g, q);
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const v4i sc = *reinterpret_cast<const v4i*>(&scl[g][32 * wv + 16 * i + 4 * q]);
+                const v4i mn = *reinterpret_cast<const v4i*>(&mnl[g][32 * wv + 16 * i + 4 * q]);
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const v4i zero = {0, 0, 0, 0};
+                    const v4i P = __builtin_amdgcn_mfma_i32_16x16x32_i8(wf[i], af[j], zero, 0, 0, 0);
+                    const int Sg = sl[16 * j + lm][g];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        acc[i][j][e] += sc[e] * P[e];
+                        mins[i][j][e] += mn[e] * Sg;
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const v4f d = *reinterpret_cast<const v4f*>(&dl[32 * wv + 16 * i + 4 * q]);
+            const v4f dm = *reinterpret_cast<const v4f*>(&dml[32 * wv + 16 * i + 4 * q]);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float am = al[16 * j + lm];
+#pragma unroll
+                for (int e = 0; e < 4; e++) y[i][j][e] = fmaf(am, q4k_term(d[e], dm[e], acc[i][j][e], mins[i][j][e]), y[i][j][e]);
+            }
+        }
+    }
+    // D element (i, j, e): n = n0 + 32 wv + 16 i + 4 q + e, m = m0 + 16 j + lm
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int m = m0 + 16 * j + lm;
+            const int nb = n0 + 32 * wv + 16 * i + 4 * q;
+            if (m < live && nb < N) {
+                if (EPI == 0) {
+                    uint32_t lo = f32_to_bf16(y[i][j][0]) | (f32_to_bf16(y[i][j][1]) << 16);
+                    uint32_t hi = f32_to_bf16(y[i][j][2]) | (f32_to_bf16(y[i][j][3]) << 16);
+                    uint16_t* o = reinterpret_cast<uint16_t*>(out) + (int64_t)m * ldo + nb;
+                    if ((((uintptr_t)o) & 7) == 0) {
+                        *reinterpret_cast<v2u*>(o) = v2u{lo, hi};
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; e++) o[e] = (uint16_t)f32_to_bf16(y[i][j][e]);
+                    }
+                } else {
+                    float* o = reinterpret_cast<float*>(out) + (int64_t)m * ldo + nb;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) o[e] = add_rn(o[e], y[i][j][e]);
+                }
+            }
+        }
+}
+
+}  // namespace prism
+
+using namespace prism;
+
+extern "C" int prism_q4k_pack(const uint8_t* raw, uint8_t* qv, uint8_t* meta, int64_t N, int64_t K, void* stream) {
+    if (!raw || !qv || !meta) return PRISM_ERR_ARG;
+    if (N <= 0 || K <= 0 || N % 16 || K % 256 || N > (1 << 30) || K > (1 << 30)) return PRISM_ERR_SHAPE;
+    if (!PRISM_ALIGNED(raw, 16) || !PRISM_ALIGNED(qv, 16) || !PRISM_ALIGNED(meta, 16)) return PRISM_ERR_ALIGN;
+    const int64_t total = N / 16 * (K / 256) * 128;
+    hipLaunchKernelGGL(q4k_pack_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream, raw,
+                       qv, meta, (int)N, (int)K);
+    PRISM_LAUNCH_CHECK();
+    return PRISM_OK;
+}
+
+extern "C" int prism_w4a8_q4k_gemm(const int8_t* xq, const float* a, int64_t a_sb, const int8_t* xs,
+                                   const uint8_t* qv, const uint8_t* meta, void* out, int64_t ldo,
+                                   const int32_t* n_rows, int64_t M, int64_t N, int64_t K, int epi, int kernel,
+                                   void* stream) {
+    if (!xq || !a || !xs || !qv || !meta || !out || !n_rows) return PRISM_ERR_ARG;
+    if (epi != 0 && epi != 1) return PRISM_ERR_ARG;
+    if (M < 0 || N <= 0 || K <= 0 || N % 16 || K % 256 || ldo < N || M > (1 << 30) || N > (1 << 30) || K > (1 << 30))
+        return PRISM_ERR_SHAPE;
+    if (!PRISM_ALIGNED(xq, 16) || !PRISM_ALIGNED(xs, 16) || !PRISM_ALIGNED(qv, 16) || !PRISM_ALIGNED(meta, 16))
+        return PRISM_ERR_ALIGN;
+    if (kernel < -1 || kernel > 1) return PRISM_ERR_ARG;
+    if (kernel == -1) kernel = M <= 16 ? 1 : 0;
+    if (kernel == 1 && M > 16) return PRISM_ERR_ARG;
+    if (M == 0) return PRISM_OK;
+    hipStream_t st = (hipStream_t)stream;
+    const int Mi = (int)M, Ni = (int)N, Ki = (int)K;
+    if (kernel == 1) {
+        dim3 grid(Ni / 16);
+#define W4DEC(NW, R, MX, D, E)                                                                                      \
+    hipLaunchKernelGGL((w4a8_decode_kernel<NW, R, MX, D, E>), grid, dim3(NW * 64), w4a8_decode_lds(R, Mi), st, xq, a, \
+                       a_sb, xs, qv, meta, out, ldo, n_rows, Mi, Ni, Ki)
+        if (M <= 4) {
+            if (epi == 0) W4DEC(4, 8, 4, 3, 0); else W4DEC(4, 8, 4, 3, 1);
+        } else {
+            if (epi == 0) W4DEC(4, 4, 16, 4, 0); else W4DEC(4, 4, 16, 4, 1);
+        }
+#undef W4DEC
+    } else {
+        const int tiles_m = (Mi + QBM - 1) / QBM, tiles_n = (Ni + QBN - 1) / QBN;
+        if (epi == 0)
+            hipLaunchKernelGGL((w4a8_tile_kernel<0>), dim3(tiles_m * tiles_n), dim3(256), 0, st, xq, a, a_sb, xs, qv,
+                               meta, out, ldo, n_rows, Mi, Ni, Ki, tiles_m, tiles_n);
+        else
+            hipLaunchKernelGGL((w4a8_tile_kernel<1>), dim3(tiles_m * tiles_n), dim3(256), 0, st, xq, a, a_sb, xs, qv,
+                               meta, out, ldo, n_rows, Mi, Ni, Ki, tiles_m, tiles_n);
+    }
+    PRISM_LAUNCH_CHECK();
+    return PRISM_OK;
 }

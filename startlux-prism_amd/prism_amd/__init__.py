@@ -4,13 +4,6 @@ Modules mirror the reference's kernel ops (startlux_prism/kernels/): quant (acti
 per-channel W8A8 GEMM), w4a8 (Q4_K W4A8 GEMM); gguf_formats holds the weight formats.  All compute runs in
 libprism_amd.so (hand-written HIP for gfx950, C ABI in include/prism_amd.h); there is no CPU fallback.
 """
-from . import _lib, gguf_formats, quant, w8a8  # noqa: F401
+from . import _lib, gguf_formats, quant, w4a8, w8a8  # noqa: F401
 
 __all__ = ["gguf_formats", "quant", "w8a8", "w4a8"]
-
-
-def __getattr__(name):
-    if name == "w4a8":
-        from . import w4a8
-        return w4a8
-    raise AttributeError(name)

@@ -1,0 +1,132 @@
+"""W4A8 projections on gfx950: int8 activations x Q4_K weights on int8 MFMA.
+
+Drop-in for StartLux-Prism kernels/w4a8.py's engine entry points: repack (:70-94), concat (:97-104), segments
+(:107-120), seg_rows (:123-130), seg_width (:133-134), gemm_segs (:137-140) and gemm (:353-366), same argument names
+and meaning.  Arithmetic (kernels/w4a8.py:14-22): per super-block b of 256 inputs, in increasing b,
+acc = sum_g sc (xq . q)_g, mins = sum_g m S_g (int32, exact), t = RN(d float(acc)), t = fma(-dmin, float(mins), t),
+y = fma(a[b, m], t, y); then bf16(y) or out += y.
+
+W4 here holds the MFMA-native device layout made by repack (a byte permutation of the GGUF block_q4_K bytes, 144
+bytes per row and 256 inputs, no size overhead): qv uint8 [n/16, k/256, 2, 64, 16] (per 16-row tile and super-block
+2 KB of nibbles, each lane's 16 bytes unpacking to its MFMA operands) and meta uint8 [n/16, k/256, 16, 16] (per row
+the block's d, dmin and 12 bytes of 6-bit scales and mins).  Rows are sliced and concatenated in whole 16-row
+tiles.  Only Q4_K is provided (Q6_K raises).
+"""
+from __future__ import annotations
+
+from typing import NamedTuple
+
+import torch
+
+from . import _lib as L
+from .gguf_formats import KQuant, Q4_K_BYTES
+
+QK_K = 256
+KERNELS = {"auto": -1, "tile": 0, "decode": 1}
+
+
+class W4(NamedTuple):
+    kind: str               # "q4k"
+    qv: torch.Tensor        # uint8 [n/16, k/256, 2, 64, 16]
+    meta: torch.Tensor      # uint8 [n/16, k/256, 16, 16]
+    n: int
+    k: int
+
+    @property
+    def shape(self):
+        return (self.n, self.k)
+
+    def rows(self, r0, r1):
+        """Rows r0:r1 (multiples of 16): views of whole row tiles."""
+        if r0 % 16 or r1 % 16:
+            raise ValueError("W4 rows are sliced in whole 16-row tiles")
+        return W4(self.kind, self.qv[r0 // 16:r1 // 16], self.meta[r0 // 16:r1 // 16], r1 - r0, self.k)
+
+    def nbytes(self):
+        return self.qv.numel() + self.meta.numel()
+
+
+def repack(kq: KQuant) -> W4:
+    """A Q4_K KQuant (raw uint8 [n, k/256, 144], on the GPU) -> W4."""
+    if kq.type != "q4k":
+        raise ValueError(f"k-quant type {kq.type}: this build provides Q4_K")
+    raw = kq.raw.contiguous()
+    n, k = raw.shape[0], kq.k
+    if raw.dtype != torch.uint8 or raw.shape[-1] != Q4_K_BYTES:
+        raise ValueError("raw Q4_K blocks expected")
+    qv = torch.empty(n // 16, k // 256, 2, 64, 16, dtype=torch.uint8, device=raw.device)
+    meta = torch.empty(n // 16, k // 256, 16, 16, dtype=torch.uint8, device=raw.device)
+    L.call("prism_q4k_pack", L.ptr(raw), L.ptr(qv), L.ptr(meta), n, k, L.stream_of(raw))
+    return W4("q4k", qv, meta, n, k)
+
+
+def concat(ws):
+    """Row-concatenation of W4 matrices (a fused projection)."""
+    if len({w.kind for w in ws}) != 1 or len({w.k for w in ws}) != 1:
+        raise ValueError("cannot fuse different k-quant kinds or widths")
+    return W4(ws[0].kind, torch.cat([w.qv for w in ws]), torch.cat([w.meta for w in ws]), sum(w.n for w in ws),
+              ws[0].k)
+
+
+def segments(kqs, device):
+    """The KQuant matrices of a fused projection -> [(W4, first output column)], neighbours fused."""
+    out, off = [], 0
+    for kq in kqs:
+        if not isinstance(kq, KQuant):
+            raise ValueError(f"the W4A8 path needs k-quant projections, not {type(kq).__name__}")
+        w = repack(kq.to(device))
+        if out and out[-1][0].kind == w.kind:
+            out[-1] = (concat([out[-1][0], w]), out[-1][1])
+        else:
+            out.append((w, off))
+        off += w.n
+    return out
+
+
+def seg_rows(segs, r0, r1):
+    out = []
+    for w, off in segs:
+        a, b = max(r0, off), min(r1, off + w.n)
+        if a < b:
+            out.append((w.rows(a - off, b - off), a - r0))
+    return out
+
+
+def seg_width(segs):
+    return max(off + w.n for w, off in segs)
+
+
+def gemm_segs(xq, a, xs, segs, out, n_rows, epi=0, pdl=0):
+    for w, off in segs:
+        gemm(xq, a, xs, w, out[:, off:off + w.n], n_rows, epi, pdl=pdl)
+
+
+def gemm(xq, a, xs, w: W4, out, n_rows, epi=0, cfg=None, pdl=0, kernel="auto"):
+    """xq int8 [M, K]; a fp32 [K/256, M] (one scale per 256 inputs), [1, M] or [M] (one per token); xs int8
+    [K/256, M, 16] split per-32 sums -> out (epi 0: bf16 [M, >= n]; epi 1: fp32, out += y).  n_rows: device int32
+    [1]; rows >= n_rows[0] untouched."""
+    if epi not in (0, 1):
+        raise NotImplementedError(f"epilogue {epi}")
+    M, K = xq.shape
+    if w.k != K or xq.dtype != torch.int8 or not xq.is_contiguous():
+        raise ValueError("xq must be contiguous int8 [M, K] with K = w.k")
+    if a.dtype != torch.float32:
+        raise TypeError("a must be fp32")
+    if a.dim() == 1 or a.shape[0] == 1:
+        a_sb = 0
+        if a.shape[-1] < M:
+            raise ValueError("a too short")
+    else:
+        if a.shape[0] != K // QK_K or a.shape[1] < M or a.stride(1) != 1:
+            raise ValueError("a must be [K/256, M]")
+        a_sb = a.stride(0)
+    if xs.dtype != torch.int8 or tuple(xs.shape[::2]) != (K // QK_K, 16) or not xs.is_contiguous():
+        raise ValueError("xs must be contiguous int8 [K/256, M, 16]")
+    Mx = xs.shape[1]
+    if Mx != M:
+        raise ValueError("xs rows must equal xq rows")
+    want = torch.bfloat16 if epi == 0 else torch.float32
+    if out.dtype != want or out.shape[0] < M or out.shape[1] < w.n or out.stride(1) != 1:
+        raise ValueError(f"out must be {want} [>= {M}, >= {w.n}] with unit column stride")
+    L.call("prism_w4a8_q4k_gemm", L.ptr(xq), L.ptr(a), a_sb, L.ptr(xs), L.ptr(w.qv), L.ptr(w.meta), L.ptr(out),
+           out.stride(0), L.ptr(n_rows), M, w.n, K, epi, KERNELS[kernel], L.stream_of(xq))
