@@ -132,6 +132,52 @@ PRISM_API int prism_w4a8_q4k_gemm(const int8_t* xq, const float* a, int64_t a_sb
                                   const uint8_t* meta, void* out, int64_t ldo, const int32_t* n_rows, int64_t M,
                                   int64_t N, int64_t K, int epi, int kernel, void* stream);
 
+/* ------------------------------------------------------------------------------------------------ MXFP4 */
+/* Element formats of MX operands (the MFMA format codes): e4m3 (OCP float8_e4m3fn) and e2m1 (fp4). */
+enum { PRISM_MX_E4M3 = 0, PRISM_MX_E2M1 = 4 };
+
+/*
+ * Quantize fp32 weights w [N, K] (row stride ldw) to MXFP4 in the device layout the GEMM reads: 32-input blocks,
+ * e2m1 codes, one e8m0 scale each.  Replaces kernels/mxfp4.py:57-86 (pack; CPU there):
+ *   mode 0 "max": e = ceil(log2(amax / 6)) clipped to +-127, codes by strict thresholds (midpoints toward zero);
+ *   mode 1 "mse": of e and e - 1 the one with the smaller squared error (float32, numpy's summation order);
+ *   mode 2 "ocp": e = floor(log2(amax)) - 2, codes nearest-even saturating at 6 (tests/quant_sim.py:66-72, the C4
+ *                 weights).
+ * Output q uint8 [N/16][K/128][64][16] (tile t, step s, lane 16 p + i: row 16 t + i, inputs 128 s + 32 p .. + 31,
+ * low nibble first) and s uint8 [N/16][K/128][64] (e + 127).  Needs N % 16 == 0, K % 128 == 0.
+ */
+PRISM_API int prism_mxfp4_pack(const float* w, int64_t ldw, uint8_t* q, uint8_t* s, int64_t N, int64_t K, int mode,
+                               void* stream);
+
+/* Row-major MX4 (q [N, K/2], s [N, K/32]: kernels/mxfp4.py:25-30, the layout pack() and the engine's side files
+ * hold) -> the device layout of prism_mxfp4_pack.  A byte permutation. */
+PRISM_API int prism_mxfp4_repack(const uint8_t* q_rows, const uint8_t* s_rows, uint8_t* q, uint8_t* s, int64_t N,
+                                 int64_t K, void* stream);
+
+/*
+ * Per-32 MX activation quantization of x [M, K] (bf16 bits, or fp32 when x_f32; row stride ldx), optionally times
+ * inv [K] first.  fmt PRISM_MX_E2M1: replaces kernels/mxfp4.py:181-185 (quantize_act) and :173-178
+ * (quantize_act_scaled): e = clip(ceil(log2(max(amax, 1e-30) / 6)), +-127), q uint8 [M, K/2].  fmt PRISM_MX_E4M3:
+ * tests/quant_sim.py:75-81 (mxfp8, the C4 activations): e = floor(log2(max(amax, 1e-30))) - 8,
+ * q = e4m3(clamp(x / 2^e, +-448)) nearest even, q uint8 [M, K].  s uint8 [M, K/32] = e + 127.
+ * Rows >= *n_rows (when n_rows is not null) are not written.
+ */
+PRISM_API int prism_mxfp4_quant_act(const void* x, int x_f32, int64_t ldx, const float* inv, uint8_t* q, uint8_t* s,
+                                    const int32_t* n_rows, int64_t M, int64_t K, int fmt, void* stream);
+
+/*
+ * MXFP4 GEMM out[m, n] = sum_k A[m, k] W[n, k] with fp32 accumulation.  Replaces kernels/mxfp4.py:292-317 (gemm,
+ * the Triton _gemm_kernel :260-289 on tl.dot_scaled) and the C ABI mxfp4_gemm of csrc/mxfp4_gemm.cu:96.
+ * aq / as: activations in fmt a_fmt (e4m3 [M, K] or e2m1 [M, K/2]) with e8m0 [M, K/32]; wq / ws: weights from
+ * prism_mxfp4_pack / _repack.  epi 0: bf16 out; epi 1: out (fp32) = out + y.  Output row stride ldo.  n_rows may be
+ * null (all M rows live).  Every kernel sums in the same order (128-input MFMA steps chained within 1024-input
+ * segments, segment sums added left to right), so results do not depend on M or on the kernel.
+ * kernel: -1 picks by M; 0 the tile kernel; 1 the decode kernel (M <= 64).  Needs N % 16 == 0, K % 128 == 0.
+ */
+PRISM_API int prism_mxfp4_gemm(const uint8_t* aq, const uint8_t* as, int a_fmt, const uint8_t* wq, const uint8_t* ws,
+                               void* out, int64_t ldo, const int32_t* n_rows, int64_t M, int64_t N, int64_t K,
+                               int epi, int kernel, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

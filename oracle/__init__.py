@@ -16,6 +16,13 @@ Pinning (each function is checked by tests/test_oracle.py against something othe
   quant_rows_g               per-32 sums vs numpy, split-sum reconstruction, scale special cases
   w4a8_gemm                  int32 super-block sums vs brute force, fmaf vs exact rational arithmetic
                              (fractions.Fraction), fp32 result vs float64 within the rounding bound
+  mx_pack (max, mse)         the reference's exact-grid vector survives (tests/test_mxfp4.py:32-37), every code is
+                             a nearest e2m1 value under the stated tie rule (brute force over the grid), the
+                             scale is the smallest power of two putting amax/6 within the grid, "mse" never has a
+                             larger squared error than "max"
+  mx_pack (ocp), quant_act   scale exponents from numpy's log2 on the same values; e4m3 codes against torch's
+                             float8_e4m3fn conversion over every representable input class
+  mx_gemm                    float64 dot products against numpy's matmul of independently decoded operands
 Parity unpinned: none of the above is checked against the reference's own numbers, because the reference holds
 no numeric fixtures for this path (its GEMM tests compare GPU kernels with each other on CUDA-seeded inputs).
 """
@@ -61,6 +68,12 @@ def lib():
             "orc_w4a8_gemm": (None, [_p, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, ctypes.c_int, _p,
                                      _i64, _i64, _p, _p, ctypes.c_int]),
             "orc_fmaf": (ctypes.c_double, [ctypes.c_float, ctypes.c_float, ctypes.c_float]),
+            "orc_e2m1_value": (ctypes.c_float, [ctypes.c_int]),
+            "orc_e4m3_value": (ctypes.c_float, [ctypes.c_int]),
+            "orc_e4m3_code": (ctypes.c_int, [ctypes.c_float]),
+            "orc_mx_pack": (None, [_p, _i64, _i64, ctypes.c_int, _p, _p, ctypes.c_int]),
+            "orc_mx_quant_act": (None, [_p, _p, _i64, _i64, ctypes.c_int, _i64, _p, _p, ctypes.c_int]),
+            "orc_mx_gemm": (None, [_p, _p, ctypes.c_int, _p, _p, _i64, _i64, _i64, _p, _p, ctypes.c_int]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -242,3 +255,59 @@ def w4a8_gemm(xq, a, xs, w4, epi=0, out=None, live=None, sums=False, nthreads=0)
                         _ptr(w4["d"]), _ptr(w4["dm"]), M, N, K, epi, _ptr(out), out.shape[1], live, _ptr(acc),
                         _ptr(mins), nthreads)
     return (out, acc, mins) if sums else out
+
+
+# ------------------------------------------------------------------------------------------------- MXFP4
+MX_E2M1 = np.array([0, .5, 1, 1.5, 2, 3, 4, 6, -0., -.5, -1, -1.5, -2, -3, -4, -6], np.float32)
+MX_MODES = {"max": 0, "mse": 1, "ocp": 2}
+MX_FMT = {"e4m3": 0, "e2m1": 4}
+
+
+def e4m3_code(v):
+    return int(lib().orc_e4m3_code(float(v)))
+
+
+def e4m3_value(c):
+    return float(lib().orc_e4m3_value(int(c)))
+
+
+def mx_pack(w, mode="max", nthreads=0):
+    """fp32 [N, K] -> (q uint8 [N, K/2] low nibble first, s uint8 [N, K/32]) in the engine's row-major MX4 layout
+    (kernels/mxfp4.py:57-86; mode "ocp" = tests/quant_sim.py:66-72 with round-to-nearest-even codes)."""
+    w = np.ascontiguousarray(w, np.float32)
+    N, K = w.shape
+    q = np.zeros((N, K // 2), np.uint8)
+    s = np.zeros((N, K // 32), np.uint8)
+    lib().orc_mx_pack(w.ctypes.data, N, K, MX_MODES[mode], q.ctypes.data, s.ctypes.data, nthreads)
+    return q, s
+
+
+def mx_quant_act(x, fmt="e4m3", inv=None, live=None, nthreads=0):
+    """fp32 (or bf16-valued fp32) [M, K] -> (q, s): fmt "e2m1" = kernels/mxfp4.py:124-146 (q [M, K/2]); "e4m3" =
+    tests/quant_sim.py:75-81 (q [M, K]); s [M, K/32].  Rows >= live stay zero."""
+    x = np.ascontiguousarray(x, np.float32)
+    M, K = x.shape
+    f = MX_FMT[fmt]
+    q = np.zeros((M, K if f == 0 else K // 2), np.uint8)
+    s = np.zeros((M, K // 32), np.uint8)
+    inv = None if inv is None else np.ascontiguousarray(inv, np.float32)
+    lib().orc_mx_quant_act(x.ctypes.data, _ptr(inv), M, K, f, M if live is None else live, q.ctypes.data,
+                           s.ctypes.data, nthreads)
+    return q, s
+
+
+def mx_gemm(aq, a_s, wq, ws, fmt=None, nthreads=0):
+    """float64 value of the scaled MX product and the sum of |terms| (for error bounds): ([M, N], [M, N])."""
+    aq = np.ascontiguousarray(aq, np.uint8)
+    a_s = np.ascontiguousarray(a_s, np.uint8)
+    wq = np.ascontiguousarray(wq, np.uint8)
+    ws = np.ascontiguousarray(ws, np.uint8)
+    N, K = wq.shape[0], wq.shape[1] * 2
+    M = aq.shape[0]
+    if fmt is None:
+        fmt = "e4m3" if aq.shape[1] == K else "e2m1"
+    y = np.zeros((M, N), np.float64)
+    ya = np.zeros((M, N), np.float64)
+    lib().orc_mx_gemm(aq.ctypes.data, a_s.ctypes.data, MX_FMT[fmt], wq.ctypes.data, ws.ctypes.data, M, N, K,
+                      y.ctypes.data, ya.ctypes.data, nthreads)
+    return y, ya

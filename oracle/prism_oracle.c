@@ -389,3 +389,177 @@ EXPORT void orc_w4a8_gemm(const int8_t* xq, const float* a, int64_t a_sb, const 
 }
 
 EXPORT double orc_fmaf(float a, float b, float c) { return (double)fmaf(a, b, c); }
+
+/* ------------------------------------------------------------------------------------------------ MXFP4 */
+/* Formats (kernels/mxfp4.py:1-6, tests/quant_sim.py:40-81): e2m1 codes 0..7 = {0, .5, 1, 1.5, 2, 3, 4, 6}, bit 3
+ * the sign; e4m3 (OCP float8_e4m3fn, bias 7, max 448, no infinities); e8m0 scale byte b = 2^(b - 127). */
+static const float MX_E2M1[8] = {0.f, .5f, 1.f, 1.5f, 2.f, 3.f, 4.f, 6.f};
+
+EXPORT float orc_e2m1_value(int code) { float v = MX_E2M1[code & 7]; return (code & 8) ? -v : v; }
+
+EXPORT float orc_e4m3_value(int code) {
+    int e = (code >> 3) & 15, m = code & 7;
+    if (e == 15 && m == 7) return NAN;
+    float v = e ? ldexpf(1.f + m / 8.f, e - 7) : ldexpf((float)m, -9);
+    return (code & 0x80) ? -v : v;
+}
+
+/* |x| / scale -> e2m1 magnitude code.  ties == 0: the engine's strict thresholds, midpoints round toward zero
+ * (kernels/mxfp4.py:40-54 for weights, :110-121 for activations; tests/quant_sim.py:43-48 bucketizes the same way).
+ * ties == 1: round to nearest, ties to the even code, saturating at 6 (the OCP MX conversion the C4 workload
+ * specifies). */
+static inline int mx_e2m1_mag(float a, int ties) {
+    if (ties == 0)
+        return (a > .25f) + (a > .75f) + (a > 1.25f) + (a > 1.75f) + (a > 2.5f) + (a > 3.5f) + (a > 5.f);
+    return (a > .25f) + (a >= .75f) + (a > 1.25f) + (a >= 1.75f) + (a > 2.5f) + (a >= 3.5f) + (a > 5.f);
+}
+
+/* floor(log2(v)) and ceil(log2(v)) of a positive normal fp32 value, exactly (from its exponent bits). */
+static inline int ilog2_floor(float v) { int e; float m = frexpf(v, &e); (void)m; return e - 1; }
+static inline int ilog2_ceil(float v) { int e; float m = frexpf(v, &e); return m == .5f ? e - 1 : e; }
+
+/* fp32 -> e4m3 code, round to nearest even, |v| <= 448 assumed (callers clamp first, as tests/quant_sim.py:81
+ * clamps before .to(torch.float8_e4m3fn)).  The sign bit follows the input's (so -0 and tiny negatives -> 0x80). */
+EXPORT int orc_e4m3_code(float v) {
+    int s = signbit(v) ? 0x80 : 0;
+    float a = fabsf(v);
+    if (a < 0x1p-6f) return s | (int)rintf(a * 512.f);       /* subnormal step 2^-9; 2^-6 itself -> code 8 */
+    int E = ilog2_floor(a);
+    int m = (int)rintf(ldexpf(a, 3 - E));                     /* 8..16, exact scaling then one rounding */
+    return s | ((E + 6) * 8 + m);
+}
+
+/* One 32-block: the e8m0 exponent and the 32 codes (low nibble first for e2m1).  mode 0 "max" and 1 "mse"
+ * follow kernels/mxfp4.py:57-86 (pack); mode 2 "ocp" follows tests/quant_sim.py:66-72 (2^(floor(log2 amax) - 2))
+ * with round-to-nearest-even codes. */
+static int mx_block_e2m1(const float* w, int mode, uint8_t* codes) {
+    float amax = 0.f;
+    for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(w[i]));
+    int e;
+    if (mode == 2) {
+        e = ilog2_floor(fmaxf(amax, 1e-30f)) - 2;
+    } else {
+        e = ilog2_ceil(fmaxf(amax, 1e-30f) / 6.0f);
+        if (e > 127) e = 127;
+        if (e < -127) e = -127;
+        if (mode == 1) {
+            /* the power of two among e and e - 1 with the smaller squared error; numpy's float32 sum over the
+             * 32 values (pairwise: eight strided partial sums, then a fixed tree) */
+            int cand[2] = {e, e - 1 < -127 ? -127 : e - 1};
+            float err[2];
+            for (int c = 0; c < 2; c++) {
+                float s = ldexpf(1.f, cand[c]), r[8] = {0};
+                for (int i = 0; i < 32; i++) {
+                    float a = fabsf(w[i]) / s;
+                    int q = mx_e2m1_mag(a, 0);
+                    float v = MX_E2M1[q] * s;
+                    if (w[i] < 0 && q) v = -v;
+                    float d = v - w[i];
+                    r[i % 8] = (i < 8) ? d * d : r[i % 8] + d * d;
+                }
+                err[c] = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+            }
+            if (err[1] < err[0]) e = cand[1];
+        }
+    }
+    float s = ldexpf(1.f, e);
+    for (int i = 0; i < 32; i++) {
+        float a = fabsf(w[i]) / s;
+        int q = mx_e2m1_mag(mode == 2 ? fminf(a, 6.f) : a, mode == 2);
+        if (w[i] < 0 && q) q |= 8;
+        codes[i] = (uint8_t)q;
+    }
+    return e;
+}
+
+/* Weights fp32 [N, K] -> q uint8 [N, K/2] (low nibble first), s uint8 [N, K/32] (e + 127).
+ * kernels/mxfp4.py:57-86 (modes 0, 1); tests/quant_sim.py:66-72 (mode 2). */
+EXPORT void orc_mx_pack(const float* w, int64_t N, int64_t K, int mode, uint8_t* q, uint8_t* s, int nthreads) {
+#pragma omp parallel for num_threads(nthreads_or(nthreads)) schedule(static)
+    for (int64_t n = 0; n < N; n++)
+        for (int64_t b = 0; b < K / 32; b++) {
+            uint8_t c[32];
+            int e = mx_block_e2m1(w + n * K + b * 32, mode, c);
+            s[n * (K / 32) + b] = (uint8_t)(e + 127);
+            for (int i = 0; i < 16; i++) q[n * (K / 2) + b * 16 + i] = (uint8_t)(c[2 * i] | (c[2 * i + 1] << 4));
+        }
+}
+
+/* Activations fp32 [M, K] (bf16 inputs widened exactly), optionally times inv[K] (fp32 multiply,
+ * kernels/mxfp4.py:153-154):
+ *   fmt 4 (e2m1): kernels/mxfp4.py:124-146 (_quant_kernel): e = clip(ceil(log2(max(amax, 1e-30) / 6)), +-127),
+ *                 codes by strict thresholds, sign bit set for every negative input (also when the code is 0);
+ *                 q [M, K/2];
+ *   fmt 0 (e4m3): tests/quant_sim.py:75-81 (mxfp8): e = floor(log2(max(amax, 1e-30))) - 8, codes
+ *                 e4m3(clamp(x / 2^e, +-448)) rounded to nearest even; q [M, K].
+ * s [M, K/32] = e + 127.  Rows >= live are not written. */
+EXPORT void orc_mx_quant_act(const float* x, const float* inv, int64_t M, int64_t K, int fmt, int64_t live,
+                             uint8_t* q, uint8_t* s, int nthreads) {
+    const int64_t rows = live < M ? live : M;
+#pragma omp parallel for num_threads(nthreads_or(nthreads)) schedule(static)
+    for (int64_t m = 0; m < rows; m++)
+        for (int64_t b = 0; b < K / 32; b++) {
+            float v[32], amax = 0.f;
+            for (int i = 0; i < 32; i++) {
+                v[i] = x[m * K + b * 32 + i];
+                if (inv) v[i] = v[i] * inv[b * 32 + i];
+                amax = fmaxf(amax, fabsf(v[i]));
+            }
+            int e;
+            if (fmt == 0) {
+                e = ilog2_floor(fmaxf(amax, 1e-30f)) - 8;
+                float sc = ldexpf(1.f, e);
+                for (int i = 0; i < 32; i++) {
+                    float a = v[i] / sc;
+                    a = fminf(fmaxf(a, -448.f), 448.f);
+                    q[m * K + b * 32 + i] = (uint8_t)orc_e4m3_code(a);
+                }
+            } else {
+                e = ilog2_ceil(fmaxf(amax, 1e-30f) / 6.0f);
+                if (e > 127) e = 127;
+                if (e < -127) e = -127;
+                float sc = ldexpf(1.f, e);
+                uint8_t c[32];
+                for (int i = 0; i < 32; i++) c[i] = (uint8_t)(mx_e2m1_mag(fabsf(v[i]) / sc, 0) | (v[i] < 0 ? 8 : 0));
+                for (int i = 0; i < 16; i++) q[m * (K / 2) + b * 16 + i] = (uint8_t)(c[2 * i] | (c[2 * i + 1] << 4));
+            }
+            s[m * (K / 32) + b] = (uint8_t)(e + 127);
+        }
+}
+
+/* y[m, n] = sum_k a(m, k) 2^(sa(m, k/32) - 127) w(n, k) 2^(sw(n, k/32) - 127), in float64 (every product of two
+ * such values is exact in float64; the sum's relative error is ~1e-16).  The fp32-accumulating GEMM of
+ * kernels/mxfp4.py:260-289 and its test (tests/test_mxfp4.py:56-60: the dequantised product) are compared with
+ * this value within a stated bound.  a: fmt 0 -> e4m3 [M, K], fmt 4 -> e2m1 [M, K/2]; w: e2m1 [N, K/2]. */
+EXPORT void orc_mx_gemm(const uint8_t* aq, const uint8_t* as, int fmt, const uint8_t* wq, const uint8_t* ws,
+                        int64_t M, int64_t N, int64_t K, double* y, double* yabs, int nthreads) {
+    float e4[256];
+    for (int c = 0; c < 256; c++) e4[c] = orc_e4m3_value(c);
+    double* wv = (double*)malloc(sizeof(double) * N * K);
+#pragma omp parallel for num_threads(nthreads_or(nthreads)) schedule(static)
+    for (int64_t n = 0; n < N; n++)
+        for (int64_t k = 0; k < K; k++)
+            wv[n * K + k] = ldexp((double)orc_e2m1_value((wq[n * (K / 2) + k / 2] >> (4 * (k & 1))) & 15),
+                                  (int)ws[n * (K / 32) + k / 32] - 127);
+#pragma omp parallel for num_threads(nthreads_or(nthreads)) schedule(static)
+    for (int64_t m = 0; m < M; m++) {
+        double* av = (double*)malloc(sizeof(double) * K);
+        for (int64_t k = 0; k < K; k++) {
+            float c = fmt == 0 ? e4[aq[m * K + k]]
+                               : orc_e2m1_value((aq[m * (K / 2) + k / 2] >> (4 * (k & 1))) & 15);
+            av[k] = ldexp((double)c, (int)as[m * (K / 32) + k / 32] - 127);
+        }
+        for (int64_t n = 0; n < N; n++) {
+            const double* w = wv + n * K;
+            double acc = 0.0, accabs = 0.0;
+            for (int64_t k = 0; k < K; k++) {
+                acc += av[k] * w[k];
+                accabs += fabs(av[k] * w[k]);
+            }
+            y[m * N + n] = acc;
+            if (yabs) yabs[m * N + n] = accabs;
+        }
+        free(av);
+    }
+    free(wv);
+}

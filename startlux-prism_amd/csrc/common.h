@@ -56,6 +56,22 @@ __device__ __forceinline__ int wave_sum_width(int v, int width) {
     return v;
 }
 
+// Tile order for a grid of tiles_m x tiles_n output tiles: the hardware hands workgroup i to XCD i % 8, so logical
+// tile t = (i % 8) * (tiles / 8) + i / 8 gives each XCD a contiguous range of tiles, walked in groups of 8 tile-rows
+// (m fastest); the workgroups that run together on one XCD then share 8 m-tiles and 8 n-tiles through its L2.
+__device__ __forceinline__ void xcd_tile_coords(int pid, int tiles_m, int tiles_n, int& pm, int& pn) {
+    const int total = tiles_m * tiles_n;
+    int t = pid;
+    if ((total & 7) == 0) t = (pid & 7) * (total >> 3) + (pid >> 3);
+    constexpr int GM = 8;
+    const int per_group = GM * tiles_n;
+    const int first_m = (t / per_group) * GM;
+    const int gm = min(tiles_m - first_m, GM);
+    const int r = t % per_group;
+    pm = first_m + r % gm;
+    pn = r / gm;
+}
+
 }  // namespace prism
 
 // Launch-status helper for the C ABI: a rejected launch becomes PRISM_ERR_LAUNCH.

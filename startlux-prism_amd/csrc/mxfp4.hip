@@ -1,0 +1,595 @@
+// MXFP4 GEMM for gfx950: e2m1 weights (one e8m0 scale per 32 inputs) against e4m3 or e2m1 activations (one e8m0
+// scale per 32 inputs), fp32 accumulation on v_mfma_scale_f32_16x16x128_f8f6f4, bf16 store or fp32 residual add.
+// Restates kernels/mxfp4.py (pack :57-86, quantize_act :124-185, _gemm_kernel :260-289, gemm :292-317) and the C4
+// conventions of tests/quant_sim.py:66-81 (mxfp4 weights, mxfp8 activations).
+//
+// Device weight layout (MX4 on the GPU), N % 16 == 0 and K % 128 == 0:
+//   q [N/16][K/128][64][16] bytes: tile t, step s, lane L = 16 p + i holds the 32 e2m1 codes (low nibble first) of
+//                                  row 16 t + i, inputs 128 s + 32 p .. + 31 -- one MFMA A operand per lane, so a
+//                                  wave's operand for one (tile, step) is 1 KB of contiguous bytes;
+//   s [N/16][K/128][64] bytes:     the e8m0 scale of that lane's 32 inputs.
+// Activations keep the engine's row-major layout: e4m3 q [M, K] or e2m1 q [M, K/2], e8m0 s [M, K/32].
+//
+// MFMA operand mapping (v_mfma_scale_f32_16x16x128_f8f6f4, A = weights, B = activations; measured on gfx950):
+//   e2m1 operand, lane L = 16 p + r: row r, inputs 32 p .. 32 p + 31 (4 dwords, low nibble = lower input);
+//   e4m3 operand, lane L = 16 p + r: row r, bytes 0-15 = inputs 16 p .. + 15, bytes 16-31 = inputs 64 + 16 p .. + 15;
+//   scale operand, lane L = 16 p + r: the e8m0 scale of row r, inputs 32 p .. + 31 (byte 0 of the dword);
+//   D, lane L: activation row L % 16, weight rows 4 (L / 16) .. + 3.
+//
+// Accumulation order (the same in every kernel, so an output's bits do not depend on the batch it is computed in
+// nor on the kernel chosen): inputs are taken in steps of 128, one MFMA each; the steps of one 1024-input segment
+// chain through the MFMA accumulator from zero; the segment sums are added left to right in fp32.
+#include "common.h"
+
+namespace prism {
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+
+constexpr int kMxStep = 128;          // inputs per MFMA
+constexpr int kMxSegSteps = 8;        // MFMA steps per accumulation segment (1024 inputs)
+
+// ------------------------------------------------------------------------------------------------ element codes
+// |x| / scale -> e2m1 magnitude code.  TIES == 0: strict thresholds, midpoints toward zero (kernels/mxfp4.py:40-54,
+// :110-121).  TIES == 1: nearest, ties to the even code (the OCP conversion of the C4 weights).
+template <int TIES>
+__device__ __forceinline__ uint32_t e2m1_mag(float a) {
+    if (TIES == 0)
+        return (a > .25f) + (a > .75f) + (a > 1.25f) + (a > 1.75f) + (a > 2.5f) + (a > 3.5f) + (a > 5.f);
+    return (a > .25f) + (a >= .75f) + (a > 1.25f) + (a >= 1.75f) + (a > 2.5f) + (a >= 3.5f) + (a > 5.f);
+}
+
+// 2^e for an integer e in [-126, 127] (exact).
+__device__ __forceinline__ float pow2i(int e) { return __uint_as_float((uint32_t)(e + 127) << 23); }
+
+// e2m1 code -> value: magnitudes 0, .5, 1, 1.5 (code / 2) and 2^((c >> 1) - 1) * (1 + (c & 1) / 2) above.
+__device__ __forceinline__ float e2m1_val(uint32_t c) {
+    const uint32_t m = c & 7;
+    const float v = m < 2 ? 0.5f * (float)m : pow2i((int)(m >> 1) - 1) * ((m & 1) ? 1.5f : 1.f);
+    return (c & 8) ? -v : v;
+}
+
+// floor / ceil of log2 of a positive normal fp32 value, from its exponent bits.
+__device__ __forceinline__ int ilog2_floor(float v) { return (int)((__float_as_uint(v) >> 23) & 0xff) - 127; }
+__device__ __forceinline__ int ilog2_ceil(float v) {
+    const uint32_t u = __float_as_uint(v);
+    return (int)((u >> 23) & 0xff) - 127 + ((u & 0x7fffffu) != 0);
+}
+
+// fp32 (|v| <= 448) -> e4m3 code, round to nearest even; the sign bit follows the input's.
+__device__ __forceinline__ uint32_t e4m3_code(float v) {
+    const uint32_t sgn = (__float_as_uint(v) >> 24) & 0x80u;
+    const float a = fabsf(v);
+    if (a < 0x1p-6f) return sgn | (uint32_t)__builtin_rintf(a * 512.f);
+    const int E = ilog2_floor(a);
+    const uint32_t m = (uint32_t)__builtin_rintf(a * pow2i(3 - E));
+    return sgn | (uint32_t)((E + 6) * 8 + (int)m);
+}
+
+// ------------------------------------------------------------------------------------------------ weight pack
+// fp32 [N, K] (row stride ldw) -> device layout.  One workgroup of 64 threads per (16-row tile, 128-input step);
+// thread L quantizes row 16 t + L % 16, block 4 s + L / 16 and writes its 16 code bytes and scale byte.
+// MODE 0 "max", 1 "mse" (kernels/mxfp4.py:57-86), 2 "ocp" (tests/quant_sim.py:66-72, nearest-even codes).
+template <int MODE>
+__global__ __launch_bounds__(64) void mx_pack_kernel(const float* __restrict__ w, int64_t ldw,
+                                                     uint8_t* __restrict__ q, uint8_t* __restrict__ s, int K) {
+    const int KS = K / kMxStep;
+    const int t = blockIdx.y, st = blockIdx.x, L = threadIdx.x;
+    const int row = 16 * t + (L & 15), blk = 4 * st + (L >> 4);
+    const float4* src = reinterpret_cast<const float4*>(w + (int64_t)row * ldw + 32 * blk);
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float4 f = src[i];
+        v[4 * i] = f.x; v[4 * i + 1] = f.y; v[4 * i + 2] = f.z; v[4 * i + 3] = f.w;
+    }
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(v[i]));
+    int e;
+    if (MODE == 2) {
+        e = ilog2_floor(fmaxf(amax, 1e-30f)) - 2;
+    } else {
+        e = min(127, max(-127, ilog2_ceil(div_rn(fmaxf(amax, 1e-30f), 6.0f))));
+        if (MODE == 1) {
+            // the power of two among e and e - 1 with the smaller squared error, summed as numpy sums 32 float32
+            // values (eight strided partial sums, then a fixed tree)
+            const int e1 = max(-127, e - 1);
+            float err[2];
+#pragma unroll
+            for (int c = 0; c < 2; c++) {
+                const int ec = c ? e1 : e;
+                const float sc = pow2i(ec), inv = pow2i(-ec);
+                float r[8];
+#pragma unroll
+                for (int i = 0; i < 32; i++) {
+                    const uint32_t m = e2m1_mag<0>(fabsf(v[i]) * inv);
+                    float dq = mul_rn(e2m1_val(m), sc);
+                    if (v[i] < 0.f && m) dq = -dq;
+                    const float d = dq - v[i];
+                    r[i & 7] = i < 8 ? mul_rn(d, d) : add_rn(r[i & 7], mul_rn(d, d));
+                }
+                err[c] = add_rn(add_rn(add_rn(r[0], r[1]), add_rn(r[2], r[3])),
+                                add_rn(add_rn(r[4], r[5]), add_rn(r[6], r[7])));
+            }
+            if (err[1] < err[0]) e = e1;
+        }
+    }
+    const float inv = pow2i(-e);
+    uint32_t words[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 32; i++) {
+        float a = fabsf(v[i]) * inv;
+        uint32_t c = MODE == 2 ? e2m1_mag<1>(fminf(a, 6.f)) : e2m1_mag<0>(a);
+        if (v[i] < 0.f && c) c |= 8;
+        words[i >> 3] |= c << (4 * (i & 7));
+    }
+    const int64_t o = ((int64_t)t * KS + st) * 64 + L;
+    reinterpret_cast<v4u*>(q)[o] = v4u{words[0], words[1], words[2], words[3]};
+    s[o] = (uint8_t)(e + 127);
+}
+
+// Row-major MX4 (q [N, K/2], s [N, K/32], kernels/mxfp4.py:25-30) -> device layout; the same thread mapping.
+__global__ __launch_bounds__(64) void mx_repack_kernel(const uint8_t* __restrict__ qr, const uint8_t* __restrict__ sr,
+                                                       uint8_t* __restrict__ q, uint8_t* __restrict__ s, int K) {
+    const int KS = K / kMxStep;
+    const int t = blockIdx.y, st = blockIdx.x, L = threadIdx.x;
+    const int row = 16 * t + (L & 15), blk = 4 * st + (L >> 4);
+    const int64_t o = ((int64_t)t * KS + st) * 64 + L;
+    reinterpret_cast<v4u*>(q)[o] = *reinterpret_cast<const v4u*>(qr + (int64_t)row * (K / 2) + 16 * blk);
+    s[o] = sr[(int64_t)row * (K / 32) + blk];
+}
+
+// ------------------------------------------------------------------------------------------ activation quantizer
+// One thread per (row, 32-input block).  AF 4: kernels/mxfp4.py:124-146 (_quant_kernel; with inv, :149-170
+// _quant_scaled_kernel): e = clip(ceil(log2(max(amax, 1e-30) / 6)), +-127), strict-threshold codes, the sign bit
+// set for every negative input.  AF 0: tests/quant_sim.py:75-81 (mxfp8): e = floor(log2(max(amax, 1e-30))) - 8,
+// codes e4m3(clamp(x / 2^e, +-448)) nearest even.  XF32: fp32 input, else bf16.  Rows >= n_rows are skipped.
+template <int AF, bool XF32>
+__global__ __launch_bounds__(256) void mx_quant_act_kernel(const void* __restrict__ x, int64_t ldx,
+                                                           const float* __restrict__ inv, uint8_t* __restrict__ q,
+                                                           uint8_t* __restrict__ s,
+                                                           const int32_t* __restrict__ n_rows, int M, int K) {
+    const int row = blockIdx.y;
+    const int blk = blockIdx.x * blockDim.x + threadIdx.x;
+    const int live = n_rows ? min(M, __ldg(n_rows)) : M;
+    if (row >= live || blk >= K / 32) return;
+    float v[32];
+    if (XF32) {
+        const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(x) + row * ldx + 32 * blk);
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float4 f = src[i];
+            v[4 * i] = f.x; v[4 * i + 1] = f.y; v[4 * i + 2] = f.z; v[4 * i + 3] = f.w;
+        }
+    } else {
+        const v4u* src = reinterpret_cast<const v4u*>(static_cast<const uint16_t*>(x) + row * ldx + 32 * blk);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const v4u u = src[i];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                v[8 * i + 2 * j] = bf16_to_f32(u[j] & 0xffffu);
+                v[8 * i + 2 * j + 1] = bf16_to_f32(u[j] >> 16);
+            }
+        }
+    }
+    if (inv) {
+        const float4* iv = reinterpret_cast<const float4*>(inv + 32 * blk);
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float4 f = iv[i];
+            v[4 * i] = mul_rn(v[4 * i], f.x);
+            v[4 * i + 1] = mul_rn(v[4 * i + 1], f.y);
+            v[4 * i + 2] = mul_rn(v[4 * i + 2], f.z);
+            v[4 * i + 3] = mul_rn(v[4 * i + 3], f.w);
+        }
+    }
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(v[i]));
+    int e;
+    if (AF == 0) {
+        e = ilog2_floor(fmaxf(amax, 1e-30f)) - 8;
+        const float r = pow2i(-e);
+        uint32_t words[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < 32; i++) {
+            const float a = fminf(fmaxf(v[i] * r, -448.f), 448.f);
+            words[i >> 2] |= e4m3_code(a) << (8 * (i & 3));
+        }
+        v4u* dst = reinterpret_cast<v4u*>(q + (int64_t)row * K + 32 * blk);
+        dst[0] = v4u{words[0], words[1], words[2], words[3]};
+        dst[1] = v4u{words[4], words[5], words[6], words[7]};
+    } else {
+        e = min(127, max(-127, ilog2_ceil(div_rn(fmaxf(amax, 1e-30f), 6.0f))));
+        const float r = pow2i(-e);
+        uint32_t words[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < 32; i++) {
+            const uint32_t c = e2m1_mag<0>(fabsf(v[i]) * r) | (v[i] < 0.f ? 8u : 0u);
+            words[i >> 3] |= c << (4 * (i & 7));
+        }
+        *reinterpret_cast<v4u*>(q + (int64_t)row * (K / 2) + 16 * blk) = v4u{words[0], words[1], words[2], words[3]};
+    }
+    s[(int64_t)row * (K / 32) + blk] = (uint8_t)(e + 127);
+}
+
+// ------------------------------------------------------------------------------------------------ MFMA helpers
+template <int AF>
+__device__ __forceinline__ v4f mx_mfma(v4i w, v8i a, v4f c, uint32_t ws, uint32_t as) {
+    const v8i wa = {w.x, w.y, w.z, w.w, 0, 0, 0, 0};
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wa, a, c, 4, AF, 0, (int)ws, 0, (int)as);
+}
+
+// Epilogue for one D fragment: activation row m, weight rows n .. n + 3.  EPI 0: bf16 RNE store
+// (kernels/mxfp4.py:286-287); EPI 1: out = out + y in fp32 (:283-285).
+template <int EPI>
+__device__ __forceinline__ void mx_store(void* out, int64_t ldo, int m, int n, v4f y) {
+    if (EPI == 0) {
+        uint16_t* o = static_cast<uint16_t*>(out) + (int64_t)m * ldo + n;
+        *reinterpret_cast<v2u*>(o) = v2u{f32_to_bf16(y.x) | (f32_to_bf16(y.y) << 16),
+                                         f32_to_bf16(y.z) | (f32_to_bf16(y.w) << 16)};
+    } else {
+        float4* o = reinterpret_cast<float4*>(static_cast<float*>(out) + (int64_t)m * ldo + n);
+        const float4 p = *o;
+        *o = make_float4(add_rn(p.x, y.x), add_rn(p.y, y.y), add_rn(p.z, y.z), add_rn(p.w, y.w));
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ decode kernel
+// M <= 16 MT.  One workgroup per 16-row weight tile; wave w owns segments w, w + NW, ...  A wave issues every load
+// of a segment (weights 16 B per lane per step, activations from L2) before its MFMAs, writes the segment's
+// fp32 sums to LDS, and after one barrier the workgroup adds the segments left to right and stores.
+template <int MT, int AF, int EPI>
+__global__ __launch_bounds__(MT == 1 ? 1024 : 512) void mx_decode_kernel(const uint8_t* __restrict__ aq,
+                                                         const uint8_t* __restrict__ as,
+                                                         const uint8_t* __restrict__ wq,
+                                                         const uint8_t* __restrict__ ws, void* __restrict__ out,
+                                                         int64_t ldo, const int32_t* __restrict__ n_rows, int M,
+                                                         int K) {
+    extern __shared__ __attribute__((aligned(16))) v4f part[];    // [nseg][MT][64]
+    const int t = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6, NW = blockDim.x >> 6;
+    const int KS = K / kMxStep, nseg = (KS + kMxSegSteps - 1) / kMxSegSteps;
+    const int live = n_rows ? min(M, __ldg(n_rows)) : M;
+    const int p = lane >> 4, r = lane & 15;
+    const int64_t abytes = AF == 0 ? K : K / 2;
+    const uint8_t* arow[MT];
+    const uint8_t* srow[MT];
+#pragma unroll
+    for (int u = 0; u < MT; u++) {
+        const int m = min(16 * u + r, M - 1);
+        arow[u] = aq + (int64_t)m * abytes + 16 * p;
+        srow[u] = as + (int64_t)m * (K / 32) + p;
+    }
+    const v4u* wbase = reinterpret_cast<const v4u*>(wq) + (int64_t)t * KS * 64 + lane;
+    const uint8_t* sbase = ws + (int64_t)t * KS * 64 + lane;
+
+    // steps loaded per batch: the whole segment while the registers allow it
+    constexpr int B = MT <= 2 ? kMxSegSteps : kMxSegSteps / 2;
+    for (int seg = w; seg < nseg; seg += NW) {
+        const int s0 = seg * kMxSegSteps, ns = min(kMxSegSteps, KS - s0);
+        v4f acc[MT];
+#pragma unroll
+        for (int u = 0; u < MT; u++) acc[u] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j0 = 0; j0 < kMxSegSteps; j0 += B) {
+            if (j0 >= ns) break;
+            v4u wv[B];
+            uint32_t wsc[B];
+            v8i av[B][MT];
+            uint32_t asc[B][MT];
+#pragma unroll
+            for (int j = 0; j < B; j++) {
+                const int st = min(s0 + j0 + j, KS - 1);
+                wv[j] = wbase[(int64_t)st * 64];
+                wsc[j] = sbase[(int64_t)st * 64];
+#pragma unroll
+                for (int u = 0; u < MT; u++) {
+                    if (AF == 0) {
+                        const v4u lo = *reinterpret_cast<const v4u*>(arow[u] + (int64_t)st * 128);
+                        const v4u hi = *reinterpret_cast<const v4u*>(arow[u] + (int64_t)st * 128 + 64);
+                        av[j][u] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z,
+                                       (int)hi.w};
+                    } else {
+                        const v4u lo = *reinterpret_cast<const v4u*>(arow[u] + (int64_t)st * 64);
+                        av[j][u] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, 0, 0, 0, 0};
+                    }
+                    asc[j][u] = srow[u][st * 4];
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < B; j++) {
+                if (j0 + j < ns) {
+                    const v4i wi = {(int)wv[j].x, (int)wv[j].y, (int)wv[j].z, (int)wv[j].w};
+#pragma unroll
+                    for (int u = 0; u < MT; u++) acc[u] = mx_mfma<AF>(wi, av[j][u], acc[u], wsc[j], asc[j][u]);
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < MT; u++) part[(seg * MT + u) * 64 + lane] = acc[u];
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < MT * 64; idx += blockDim.x) {
+        const int u = idx >> 6, l = idx & 63;
+        const int m = 16 * u + (l & 15);
+        if (m >= live) continue;
+        v4f y = part[u * 64 + l];
+        for (int seg = 1; seg < nseg; seg++) {
+            const v4f z = part[(seg * MT + u) * 64 + l];
+            y = v4f{add_rn(y.x, z.x), add_rn(y.y, z.y), add_rn(y.z, z.z), add_rn(y.w, z.w)};
+        }
+        mx_store<EPI>(out, ldo, m, 16 * t + 4 * (l >> 4), y);
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ tile kernel
+// 128 x 128 output tile (8 weight tiles x 8 activation tiles), 4 waves each 64 x 64 (4 x 4 MFMAs per step).
+// Operands move global -> LDS by LDS-DMA (global_load_lds_dwordx4 / _ubyte), NS stages deep, already in MFMA
+// operand order, so each wave reads its fragments with contiguous ds_read_b128 and no VGPR staging.
+constexpr int kTB = 128;
+template <int AF>
+struct MxStage {
+    static constexpr int WQ = 0;                                  // 8 tiles x 1 KB
+    static constexpr int AQ = 8192;                               // 8 tiles x (2 KB e4m3 | 1 KB e2m1)
+    static constexpr int WS = AQ + (AF == 0 ? 16384 : 8192);      // 8 tiles x 64 lanes x 4 B
+    static constexpr int AS = WS + 2048;
+    static constexpr int BYTES = AS + 2048;
+    static constexpr int LOADS = AF == 0 ? 10 : 8;                // DMA instructions per wave per stage
+};
+
+__device__ __forceinline__ void dma16(const void* g, uint8_t* lds) {
+    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+__device__ __forceinline__ void dma1(const void* g, uint8_t* lds) {
+    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 1, 0, 0);
+}
+
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <int AF, int EPI, int NS>
+__global__ __launch_bounds__(256, 2) void mx_tile_kernel(const uint8_t* __restrict__ aq, const uint8_t* __restrict__ as,
+                                                         const uint8_t* __restrict__ wq,
+                                                         const uint8_t* __restrict__ ws, void* __restrict__ out,
+                                                         int64_t ldo, const int32_t* __restrict__ n_rows, int M,
+                                                         int N, int K, int tiles_m, int tiles_n) {
+    using S = MxStage<AF>;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    int pm, pn;
+    xcd_tile_coords(blockIdx.x, tiles_m, tiles_n, pm, pn);
+    const int m0 = pm * kTB, n0 = pn * kTB;
+    const int live = n_rows ? min(M, __ldg(n_rows)) : M;
+    if (m0 >= live) return;
+    const int KS = K / kMxStep, NT = N / 16;
+    const int p = lane >> 4, r = lane & 15;
+    const int64_t abytes = AF == 0 ? K : K / 2;
+
+    // per-wave DMA sources (step 0); each advances by a fixed stride per step
+    const uint8_t* wsrc[2];
+    const uint8_t* wssrc[2];
+    const uint8_t* asrc[4];
+    const uint8_t* assrc[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int tt = min(n0 / 16 + 2 * w + i, NT - 1);
+        wsrc[i] = wq + (int64_t)tt * KS * 1024 + lane * 16;
+        wssrc[i] = ws + (int64_t)tt * KS * 64 + lane;
+        const int m = min(m0 + 16 * (2 * w + i) + r, M - 1);
+        assrc[i] = as + (int64_t)m * (K / 32) + p;
+    }
+#pragma unroll
+    for (int i = 0; i < (AF == 0 ? 4 : 2); i++) {
+        const int idx = (AF == 0 ? 4 : 2) * w + i;
+        const int u = AF == 0 ? idx >> 1 : idx, h = AF == 0 ? idx & 1 : 0;
+        const int m = min(m0 + 16 * u + r, M - 1);
+        asrc[i] = aq + (int64_t)m * abytes + 64 * h + 16 * p;
+    }
+
+    auto issue = [&](int st, int buf) {
+        uint8_t* b = lds + buf * S::BYTES;
+#pragma unroll
+        for (int i = 0; i < 2; i++) dma16(wsrc[i] + (int64_t)st * 1024, b + S::WQ + (2 * w + i) * 1024);
+#pragma unroll
+        for (int i = 0; i < (AF == 0 ? 4 : 2); i++) {
+            const int idx = (AF == 0 ? 4 : 2) * w + i;
+            dma16(asrc[i] + (int64_t)st * (AF == 0 ? 128 : 64), b + S::AQ + idx * 1024);
+        }
+#pragma unroll
+        for (int i = 0; i < 2; i++) dma1(wssrc[i] + (int64_t)st * 64, b + S::WS + (2 * w + i) * 256);
+#pragma unroll
+        for (int i = 0; i < 2; i++) dma1(assrc[i] + st * 4, b + S::AS + (2 * w + i) * 256);
+    };
+
+    const int wn = w & 1, wm = w >> 1;
+    v4f acc[4][4], tot[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) acc[a][c] = tot[a][c] = v4f{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+    for (int i = 0; i < NS - 1; i++)
+        if (i < KS) issue(i, i);
+
+    for (int st = 0; st < KS; st++) {
+        const int pend = min(KS - 1, st + NS - 2) - st;
+        if (NS >= 4 && pend >= 2) vm_wait<2 * S::LOADS>();
+        else if (NS >= 3 && pend >= 1) vm_wait<S::LOADS>();
+        else vm_wait<0>();
+        lds_barrier();
+        if (st + NS - 1 < KS) issue(st + NS - 1, (st + NS - 1) % NS);
+
+        const uint8_t* b = lds + (st % NS) * S::BYTES;
+        v4i wf[4];
+        uint32_t wsf[4], asf[4];
+        v8i af[4];
+#pragma unroll
+        for (int a = 0; a < 4; a++) {
+            wf[a] = *reinterpret_cast<const v4i*>(b + S::WQ + (4 * wn + a) * 1024 + lane * 16);
+            wsf[a] = *reinterpret_cast<const uint32_t*>(b + S::WS + (4 * wn + a) * 256 + lane * 4);
+        }
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const int u = 4 * wm + c;
+            if (AF == 0) {
+                const v4i lo = *reinterpret_cast<const v4i*>(b + S::AQ + u * 2048 + lane * 16);
+                const v4i hi = *reinterpret_cast<const v4i*>(b + S::AQ + u * 2048 + 1024 + lane * 16);
+                af[c] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+            } else {
+                const v4i lo = *reinterpret_cast<const v4i*>(b + S::AQ + u * 1024 + lane * 16);
+                af[c] = v8i{lo.x, lo.y, lo.z, lo.w, 0, 0, 0, 0};
+            }
+            asf[c] = *reinterpret_cast<const uint32_t*>(b + S::AS + u * 256 + lane * 4);
+        }
+#pragma unroll
+        for (int a = 0; a < 4; a++)
+#pragma unroll
+            for (int c = 0; c < 4; c++) acc[a][c] = mx_mfma<AF>(wf[a], af[c], acc[a][c], wsf[a], asf[c]);
+
+        if ((st % kMxSegSteps) == kMxSegSteps - 1 || st == KS - 1) {
+            const bool first = st < kMxSegSteps;
+#pragma unroll
+            for (int a = 0; a < 4; a++)
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    const v4f z = acc[a][c];
+                    tot[a][c] = first ? z
+                                      : v4f{add_rn(tot[a][c].x, z.x), add_rn(tot[a][c].y, z.y),
+                                            add_rn(tot[a][c].z, z.z), add_rn(tot[a][c].w, z.w)};
+                    acc[a][c] = v4f{0.f, 0.f, 0.f, 0.f};
+                }
+        }
+    }
+
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const int m = m0 + 16 * (4 * wm + c) + r;
+        if (m >= live) continue;
+#pragma unroll
+        for (int a = 0; a < 4; a++) {
+            const int n = n0 + 16 * (4 * wn + a) + 4 * p;
+            if (n < N) mx_store<EPI>(out, ldo, m, n, tot[a][c]);
+        }
+    }
+}
+
+static size_t mx_decode_lds(int MT, int K) {
+    const int nseg = (K / kMxStep + kMxSegSteps - 1) / kMxSegSteps;
+    return (size_t)nseg * MT * 64 * sizeof(v4f);
+}
+
+template <typename F>
+static void allow_lds(F* fn, size_t bytes) {
+    if (bytes > 64 * 1024) (void)hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                     (int)bytes);
+}
+
+}  // namespace prism
+
+using namespace prism;
+
+extern "C" int prism_mxfp4_pack(const float* w, int64_t ldw, uint8_t* q, uint8_t* s, int64_t N, int64_t K, int mode,
+                                void* stream) {
+    if (!w || !q || !s) return PRISM_ERR_ARG;
+    if (N <= 0 || K <= 0 || N % 16 || K % kMxStep || ldw < K || ldw % 4 || N / 16 > 65535 || K / kMxStep > (1 << 30))
+        return PRISM_ERR_SHAPE;
+    if (mode < 0 || mode > 2) return PRISM_ERR_ARG;
+    if (!PRISM_ALIGNED(w, 16) || !PRISM_ALIGNED(q, 16)) return PRISM_ERR_ALIGN;
+    dim3 grid((unsigned)(K / kMxStep), (unsigned)(N / 16));
+    hipStream_t st = (hipStream_t)stream;
+    if (mode == 0) hipLaunchKernelGGL(mx_pack_kernel<0>, grid, dim3(64), 0, st, w, ldw, q, s, (int)K);
+    else if (mode == 1) hipLaunchKernelGGL(mx_pack_kernel<1>, grid, dim3(64), 0, st, w, ldw, q, s, (int)K);
+    else hipLaunchKernelGGL(mx_pack_kernel<2>, grid, dim3(64), 0, st, w, ldw, q, s, (int)K);
+    PRISM_LAUNCH_CHECK();
+    return PRISM_OK;
+}
+
+extern "C" int prism_mxfp4_repack(const uint8_t* q_rows, const uint8_t* s_rows, uint8_t* q, uint8_t* s, int64_t N,
+                                  int64_t K, void* stream) {
+    if (!q_rows || !s_rows || !q || !s) return PRISM_ERR_ARG;
+    if (N <= 0 || K <= 0 || N % 16 || K % kMxStep || N / 16 > 65535) return PRISM_ERR_SHAPE;
+    if (!PRISM_ALIGNED(q_rows, 16) || !PRISM_ALIGNED(q, 16)) return PRISM_ERR_ALIGN;
+    dim3 grid((unsigned)(K / kMxStep), (unsigned)(N / 16));
+    hipLaunchKernelGGL(mx_repack_kernel, grid, dim3(64), 0, (hipStream_t)stream, q_rows, s_rows, q, s, (int)K);
+    PRISM_LAUNCH_CHECK();
+    return PRISM_OK;
+}
+
+extern "C" int prism_mxfp4_quant_act(const void* x, int x_f32, int64_t ldx, const float* inv, uint8_t* q, uint8_t* s,
+                                     const int32_t* n_rows, int64_t M, int64_t K, int fmt, void* stream) {
+    if (!x || !q || !s) return PRISM_ERR_ARG;
+    if (fmt != PRISM_MX_E4M3 && fmt != PRISM_MX_E2M1) return PRISM_ERR_ARG;
+    if (M < 0 || K <= 0 || K % 32 || ldx < K || M > 65535) return PRISM_ERR_SHAPE;
+    if ((x_f32 ? ldx % 4 : ldx % 8) || !PRISM_ALIGNED(x, 16) || !PRISM_ALIGNED(q, 16) ||
+        (inv && !PRISM_ALIGNED(inv, 16)))
+        return PRISM_ERR_ALIGN;
+    if (M == 0) return PRISM_OK;
+    dim3 grid((unsigned)((K / 32 + 255) / 256), (unsigned)M);
+    hipStream_t st = (hipStream_t)stream;
+#define QA(AF, F) hipLaunchKernelGGL((mx_quant_act_kernel<AF, F>), grid, dim3(256), 0, st, x, ldx, inv, q, s, n_rows, \
+                                     (int)M, (int)K)
+    if (fmt == PRISM_MX_E4M3) { if (x_f32) QA(0, true); else QA(0, false); }
+    else { if (x_f32) QA(4, true); else QA(4, false); }
+#undef QA
+    PRISM_LAUNCH_CHECK();
+    return PRISM_OK;
+}
+
+extern "C" int prism_mxfp4_gemm(const uint8_t* aq, const uint8_t* as, int a_fmt, const uint8_t* wq,
+                                const uint8_t* ws, void* out, int64_t ldo, const int32_t* n_rows, int64_t M,
+                                int64_t N, int64_t K, int epi, int kernel, void* stream) {
+    if (!aq || !as || !wq || !ws || !out) return PRISM_ERR_ARG;
+    if (a_fmt != PRISM_MX_E4M3 && a_fmt != PRISM_MX_E2M1) return PRISM_ERR_ARG;
+    if (epi != 0 && epi != 1) return PRISM_ERR_ARG;
+    if (M < 0 || N <= 0 || K <= 0 || N % 16 || K % kMxStep || ldo < N || M > (1 << 24) || N / 16 > (1 << 24))
+        return PRISM_ERR_SHAPE;
+    if (!PRISM_ALIGNED(aq, 16) || !PRISM_ALIGNED(wq, 16) || ldo % 4 || !PRISM_ALIGNED(out, epi ? 16 : 8))
+        return PRISM_ERR_ALIGN;
+    if (M == 0) return PRISM_OK;
+    hipStream_t st = (hipStream_t)stream;
+    const int MT = (int)((M + 15) / 16);
+    if (kernel < 0) kernel = (MT <= 4 && mx_decode_lds(MT, (int)K) <= 64 * 1024) ? 1 : 0;
+    if (kernel == 1) {
+        if (MT > 4) return PRISM_ERR_SHAPE;
+        const size_t lds = mx_decode_lds(MT, (int)K);
+        if (lds > 160 * 1024) return PRISM_ERR_SHAPE;
+        const int nseg = (int)((K / kMxStep + kMxSegSteps - 1) / kMxSegSteps);
+        const int nw = min(nseg, MT == 1 ? 16 : 8);
+        dim3 grid((unsigned)(N / 16));
+#define DEC(MTV, AF, E)                                                                                              \
+    do {                                                                                                             \
+        allow_lds(mx_decode_kernel<MTV, AF, E>, lds);                                                                \
+        hipLaunchKernelGGL((mx_decode_kernel<MTV, AF, E>), grid, dim3(64 * nw), lds, st, aq, as, wq, ws, out, ldo,   \
+                           n_rows, (int)M, (int)K);                                                                  \
+    } while (0)
+#define DEC_MT(AF, E)                                                                                                \
+    do {                                                                                                             \
+        if (MT == 1) DEC(1, AF, E); else if (MT == 2) DEC(2, AF, E); else if (MT == 3) DEC(3, AF, E);                \
+        else DEC(4, AF, E);                                                                                          \
+    } while (0)
+        if (a_fmt == PRISM_MX_E4M3) { if (epi) DEC_MT(0, 1); else DEC_MT(0, 0); }
+        else { if (epi) DEC_MT(4, 1); else DEC_MT(4, 0); }
+#undef DEC_MT
+#undef DEC
+    } else {
+        constexpr int NS = 3;
+        const int tiles_m = (int)((M + kTB - 1) / kTB), tiles_n = (int)((N + kTB - 1) / kTB);
+        dim3 grid((unsigned)(tiles_m * tiles_n));
+#define TILE(AF, E)                                                                                                  \
+    do {                                                                                                             \
+        const size_t lds = (size_t)NS * MxStage<AF>::BYTES;                                                          \
+        allow_lds(mx_tile_kernel<AF, E, NS>, lds);                                                                   \
+        hipLaunchKernelGGL((mx_tile_kernel<AF, E, NS>), grid, dim3(256), lds, st, aq, as, wq, ws, out, ldo, n_rows,  \
+                           (int)M, (int)N, (int)K, tiles_m, tiles_n);                                                \
+    } while (0)
+        if (a_fmt == PRISM_MX_E4M3) { if (epi) TILE(0, 1); else TILE(0, 0); }
+        else { if (epi) TILE(4, 1); else TILE(4, 0); }
+#undef TILE
+    }
+    PRISM_LAUNCH_CHECK();
+    return PRISM_OK;
+}

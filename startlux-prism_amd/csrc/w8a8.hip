@@ -404,19 +404,6 @@ __global__ __launch_bounds__(256, 1) void w8a8_tile_kernel(const int8_t* __restr
 // Tile order: the hardware hands workgroup i to XCD i % 8.  Logical tile t = (i % 8) * (tiles / 8) + i / 8 gives
 // each XCD a contiguous range of tiles, walked in groups of 8 tile-rows (m fastest), so the workgroups that run
 // together on one XCD share 8 activation tiles and 8 weight tiles through that XCD's L2.
-__device__ __forceinline__ void tile_coords(int pid, int tiles_m, int tiles_n, int& pm, int& pn) {
-    const int total = tiles_m * tiles_n;
-    int t = pid;
-    if ((total & 7) == 0) t = (pid & 7) * (total >> 3) + (pid >> 3);
-    constexpr int GM = 8;
-    const int per_group = GM * tiles_n;
-    const int first_m = (t / per_group) * GM;
-    const int gm = min(tiles_m - first_m, GM);
-    const int r = t % per_group;
-    pm = first_m + r % gm;
-    pn = r / gm;
-}
-
 template <bool WS16, int EPI>
 __global__ __launch_bounds__(256, 2) void w8a8_q8_tile_kernel(const int8_t* __restrict__ a,
                                                               const float* __restrict__ a_s, int64_t as_sm,
@@ -431,7 +418,7 @@ __global__ __launch_bounds__(256, 2) void w8a8_q8_tile_kernel(const int8_t* __re
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int wm = wv >> 1, wn = wv & 1;
     int pm, pn;
-    tile_coords(blockIdx.x, tiles_m, tiles_n, pm, pn);
+    xcd_tile_coords(blockIdx.x, tiles_m, tiles_n, pm, pn);
     const int m0 = pm * TBM, n0 = pn * TBN;
     const int live = min(M, __ldg(n_rows));
     if (m0 >= live) return;

@@ -241,19 +241,6 @@ constexpr int PBM = 128, PBN = 128;
 constexpr int PLDA = 128 + 16;          // activation tile row (bytes), padded
 constexpr int PLDB = 2048 + 64;         // one 16-row tile's two chunks, padded
 
-__device__ __forceinline__ void packed_tile_coords(int pid, int tiles_m, int tiles_n, int& pm, int& pn) {
-    const int total = tiles_m * tiles_n;
-    int t = pid;
-    if ((total & 7) == 0) t = (pid & 7) * (total >> 3) + (pid >> 3);
-    constexpr int GM = 8;
-    const int per_group = GM * tiles_n;
-    const int first_m = (t / per_group) * GM;
-    const int gm = min(tiles_m - first_m, GM);
-    const int r = t % per_group;
-    pm = first_m + r % gm;
-    pn = r / gm;
-}
-
 template <int EPI>
 __global__ __launch_bounds__(256, 2) void w8a8_packed_tile_kernel(const int8_t* __restrict__ a,
                                                                   const float* __restrict__ a_s, int64_t as_sm,
@@ -269,7 +256,7 @@ __global__ __launch_bounds__(256, 2) void w8a8_packed_tile_kernel(const int8_t* 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int wm = wv >> 1, wn = wv & 1;
     int pm, pn;
-    packed_tile_coords(blockIdx.x, tiles_m, tiles_n, pm, pn);
+    xcd_tile_coords(blockIdx.x, tiles_m, tiles_n, pm, pn);
     const int m0 = pm * PBM, n0 = pn * PBN;
     const int live = min(M, __ldg(n_rows));
     if (m0 >= live) return;
