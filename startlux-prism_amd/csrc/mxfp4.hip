@@ -477,6 +477,110 @@ __global__ __launch_bounds__(256, 2) void mx_tile_kernel(const uint8_t* __restri
     }
 }
 
+
+// ------------------------------------------------------------------------------ decode kernel, staged activations
+// e4m3 activations, M <= 16.  One workgroup per NTG 16-row weight tiles; waves w = (tile w % NTG, segment lane
+// w / NTG), SL segment lanes, segments taken in rounds of SL.  Per round every wave loads its segment's weights
+// into registers while the workgroup copies the round's activation rows (16 rows x 1 KB per segment, one 1 KB row
+// chunk per DMA instruction, rows padded to 1040 bytes so the fragment reads of 16 rows hit distinct banks) and
+// their scales into LDS; the NTG tiles of a segment share one copy.  After the MFMAs each wave leaves its segment
+// sum in LDS and the first NTG waves fold the round's segments, left to right, into their running sums.
+constexpr int kDecRow = 1024 + 16;              // LDS bytes per staged activation row (one segment)
+constexpr int kDecActSlot = 16 * kDecRow;       // one segment's 16 rows
+constexpr int kDecScaleSlot = 16 * 32;          // their 32 scale bytes per row
+
+static size_t mx_decode_staged_lds(int ntg, int sl) {
+    return (size_t)sl * (kDecActSlot + kDecScaleSlot) + (size_t)sl * ntg * 64 * sizeof(v4f);
+}
+
+template <int NTG, int EPI>
+__global__ __launch_bounds__(1024) void mx_decode_staged_kernel(const uint8_t* __restrict__ aq,
+                                                                const uint8_t* __restrict__ as,
+                                                                const uint8_t* __restrict__ wq,
+                                                                const uint8_t* __restrict__ ws,
+                                                                void* __restrict__ out, int64_t ldo,
+                                                                const int32_t* __restrict__ n_rows, int M, int K,
+                                                                int SL) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    uint8_t* act = lds;                                               // [SL][16][kDecRow]
+    uint8_t* asl = lds + SL * kDecActSlot;                            // [SL][16][32]
+    v4f* part = reinterpret_cast<v4f*>(asl + SL * kDecScaleSlot);     // [SL][NTG][64]
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int nt = w % NTG, sl = w / NTG;
+    const int t = blockIdx.x * NTG + nt;
+    const int KS = K / kMxStep, nseg = (KS + kMxSegSteps - 1) / kMxSegSteps;
+    const int live = n_rows ? min(M, __ldg(n_rows)) : M;
+    const int p = lane >> 4, r = lane & 15;
+    const v4u* wbase = reinterpret_cast<const v4u*>(wq) + (int64_t)t * KS * 64 + lane;
+    const uint8_t* sbase = ws + (int64_t)t * KS * 64 + lane;
+    const int nrounds = (nseg + SL - 1) / SL;
+    v4f y = v4f{0.f, 0.f, 0.f, 0.f};
+
+    for (int rd = 0; rd < nrounds; rd++) {
+        const int seg = rd * SL + sl;
+        const bool active = seg < nseg;
+        const int s0 = min(seg, nseg - 1) * kMxSegSteps, ns = min(kMxSegSteps, KS - s0);
+        // weights of the segment (registers)
+        v4u wv[kMxSegSteps];
+        uint32_t wsc[kMxSegSteps];
+#pragma unroll
+        for (int j = 0; j < kMxSegSteps; j++) {
+            const int st = min(s0 + j, KS - 1);
+            wv[j] = wbase[(int64_t)st * 64];
+            wsc[j] = sbase[(int64_t)st * 64];
+        }
+        // activation rows of the segment -> LDS slot sl: the NTG waves of the slot split the 16 rows
+        if (active) {
+            uint8_t* slot = act + sl * kDecActSlot;
+            for (int row = nt; row < 16; row += NTG) {
+                const int m = min(row, M - 1);
+                // a short last segment: lanes past its end re-read its last 16 bytes (never used)
+                const uint8_t* src = aq + (int64_t)m * K + (int64_t)s0 * kMxStep + min(16 * lane, ns * kMxStep - 16);
+                __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(slot + row * kDecRow),
+                                                 16, 0, 0);
+            }
+            if (nt == 0) {   // 16 rows x 32 scale bytes: lane L covers row L / 8, bytes 4 (L % 8) .. + 3 (x2 instr.)
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const int row = 8 * h + (lane >> 3);
+                    const int m = min(row, M - 1);
+                    const uint8_t* src = as + (int64_t)m * (K / 32) + s0 * 4 + min(4 * (lane & 7), 4 * ns - 4);
+                    __builtin_amdgcn_global_load_lds(
+                        src, (__attribute__((address_space(3))) void*)(asl + sl * kDecScaleSlot + h * 256), 4, 0, 0);
+                }
+            }
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        lds_barrier();
+        if (active) {
+            const uint8_t* slot = act + sl * kDecActSlot + r * kDecRow + 16 * p;
+            const uint8_t* sslot = asl + sl * kDecScaleSlot + r * 32 + p;
+            v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < kMxSegSteps; j++) {
+                if (j < ns) {
+                    const v4i lo = *reinterpret_cast<const v4i*>(slot + 128 * j);
+                    const v4i hi = *reinterpret_cast<const v4i*>(slot + 128 * j + 64);
+                    const uint32_t sc = sslot[4 * j];
+                    const v4i wi = {(int)wv[j].x, (int)wv[j].y, (int)wv[j].z, (int)wv[j].w};
+                    acc = mx_mfma<0>(wi, v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w}, acc, wsc[j], sc);
+                }
+            }
+            part[(sl * NTG + nt) * 64 + lane] = acc;
+        }
+        lds_barrier();
+        if (w < NTG) {   // wave w folds tile w's segments of this round in order
+            const int nr = min(SL, nseg - rd * SL);
+            for (int i = 0; i < nr; i++) {
+                const v4f z = part[(i * NTG + w) * 64 + lane];
+                y = (rd == 0 && i == 0) ? z : v4f{add_rn(y.x, z.x), add_rn(y.y, z.y), add_rn(y.z, z.z), add_rn(y.w, z.w)};
+            }
+        }
+        lds_barrier();
+    }
+    if (w < NTG && r < live) mx_store<EPI>(out, ldo, r, 16 * (blockIdx.x * NTG + w) + 4 * p, y);
+}
+
 static size_t mx_decode_lds(int MT, int K) {
     const int nseg = (K / kMxStep + kMxSegSteps - 1) / kMxSegSteps;
     return (size_t)nseg * MT * 64 * sizeof(v4f);
@@ -553,7 +657,22 @@ extern "C" int prism_mxfp4_gemm(const uint8_t* aq, const uint8_t* as, int a_fmt,
     hipStream_t st = (hipStream_t)stream;
     const int MT = (int)((M + 15) / 16);
     if (kernel < 0) kernel = (MT <= 4 && mx_decode_lds(MT, (int)K) <= 64 * 1024) ? 1 : 0;
-    if (kernel == 1) {
+    if (kernel == 1 && MT == 1 && a_fmt == PRISM_MX_E4M3) {
+        const int nseg = (int)((K / kMxStep + kMxSegSteps - 1) / kMxSegSteps);
+        const int ntg = (N % 32 == 0) ? 2 : 1;     // two weight tiles share each staged activation copy
+        const int sl = min(nseg, 8);        // 8 segment lanes: 154 KB of LDS at NTG 2
+        const size_t lds = mx_decode_staged_lds(ntg, sl);
+        dim3 grid((unsigned)(N / (16 * ntg)));
+#define DST(NTGV, E)                                                                                                 \
+    do {                                                                                                             \
+        allow_lds(mx_decode_staged_kernel<NTGV, E>, lds);                                                            \
+        hipLaunchKernelGGL((mx_decode_staged_kernel<NTGV, E>), grid, dim3(64 * NTGV * sl), lds, st, aq, as, wq, ws,  \
+                           out, ldo, n_rows, (int)M, (int)K, sl);                                                    \
+    } while (0)
+        if (ntg == 2) { if (epi) DST(2, 1); else DST(2, 0); }
+        else { if (epi) DST(1, 1); else DST(1, 0); }
+#undef DST
+    } else if (kernel == 1) {
         if (MT > 4) return PRISM_ERR_SHAPE;
         const size_t lds = mx_decode_lds(MT, (int)K);
         if (lds > 160 * 1024) return PRISM_ERR_SHAPE;
@@ -576,7 +695,10 @@ extern "C" int prism_mxfp4_gemm(const uint8_t* aq, const uint8_t* as, int a_fmt,
 #undef DEC_MT
 #undef DEC
     } else {
-        constexpr int NS = 3;
+#ifndef PRISM_MX_NS
+#define PRISM_MX_NS 3
+#endif
+        constexpr int NS = PRISM_MX_NS;
         const int tiles_m = (int)((M + kTB - 1) / kTB), tiles_n = (int)((N + kTB - 1) / kTB);
         dim3 grid((unsigned)(tiles_m * tiles_n));
 #define TILE(AF, E)                                                                                                  \
