@@ -10,9 +10,11 @@ resident in HBM before the timed region.  `value` is TOPS of the whole step (2 M
 describes the GEMM kernel alone, timed with HIP events on the stream it is launched on, against the MI355X dense
 int8 MFMA peak (5.0 POPS).
 
-Also measured (key "sweep", not the headline): the decode shapes of config 2 (M in 1, 4, 16, 64; (K, N) =
-(5120, 5120) and (17408, 5120)) as GB/s of packed Q8_0 weight bytes, with weight copies rotated through more than
-3 x the 256 MB MALL so that every launch streams its weights from HBM.
+Also measured (key "configs", not the headline; GEMM kernels alone, graph-replayed): config 0 (Q8_0, M = 16,
+K = N = 4096) and config 2 (Q8_0 decode, M in 1, 4, 16, 64; (K, N) = (5120, 5120), (17408, 5120)) as GB/s of packed
+Q8_0 weight bytes; config 3 (Q4_K W4A8, M = 16 and 2048) and config 4 (MXFP4, M = 16 and 4096), each against its
+roof (HBM for the decode sizes, the int8 or fp8 MFMA peak for the prefill sizes).  Memory-bound shapes rotate weight
+copies through more than 3 x the 256 MB MALL so that every launch streams its weights from HBM.
 
 cpu_baseline: the CPU oracle (oracle/, the exact restatement of the reference's arithmetic, OpenMP) on a bounded
 row sample of the same workload, on this host's cores.
@@ -28,6 +30,7 @@ sys.path.insert(0, os.path.join(ROOT, "startlux-prism_amd"))
 
 PEAK_INT8_TOPS = 5000.0      # MI355X dense int8 MFMA
 PEAK_HBM_GBS = 8000.0        # MI355X HBM3E
+PEAK_FP8_TFLOPS = 5000.0     # MI355X dense fp8 (and fp8 x fp4) MFMA
 MALL_BYTES = 256 << 20
 
 M1, K1, N1 = 8192, 5120, 27648
@@ -102,50 +105,132 @@ def bench_prefill(steps, warmup, dev):
     return res, sample
 
 
-def bench_decode_sweep(dev, iters=40):
-    """GB/s of packed Q8_0 weight bytes per decode shape.  The launches (rotating over weight copies totalling more
-    than 3 x the 256 MB MALL, so every launch streams its weights from HBM) are captured in a HIP graph and replayed:
-    back-to-back kernels as the engine's captured decode steps run them."""
+def _graph_us(launch, copies, iters):
+    """Mean microseconds per launch of launch(i) (i picks the weight copy), captured back to back in a HIP graph and
+    replayed: the form the engine's captured decode steps run in."""
+    import torch
+    for i in range(min(copies, 3)):
+        launch(i)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    st = torch.cuda.Stream()
+    with torch.cuda.stream(st):
+        with torch.cuda.graph(g, stream=st):
+            for i in range(iters):
+                launch(i % copies)
+    g.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    g.replay()
+    b.record()
+    torch.cuda.synchronize()
+    del g
+    return a.elapsed_time(b) / iters * 1e3
+
+
+def _copies(wbytes, M):
+    """Weight copies rotated per launch: more than 3 x the MALL for the memory-bound shapes, so that every launch
+    streams its weights from HBM."""
+    return max(3, -(-3 * MALL_BYTES // wbytes)) if M <= 64 else 1
+
+
+def _row(M, K, N, us, wbytes, bound, peak=None):
+    gbs = wbytes / (us * 1e-6) / 1e9
+    tops = 2 * M * N * K / (us * 1e-6) / 1e12
+    r = dict(M=M, K=K, N=N, us=round(us, 2), GBps=round(gbs, 1), TOPS=round(tops, 2), bound=bound)
+    r["frac"] = round(gbs / PEAK_HBM_GBS, 3) if bound == "hbm" else round(tops / peak, 4)
+    return r
+
+
+def bench_q8_decode(dev, shapes, Ms, iters=40):
+    """Q8_0 W8A8 GEMMs at decode sizes (configs 0 and 2): GB/s of packed Q8_0 weight bytes."""
     import torch
     from prism_amd import quant as KQ
     from prism_amd import w8a8 as KW
     rows = []
-    for (K, N) in ((5120, 5120), (17408, 5120)):
+    for (K, N) in shapes:
         wbytes = q8_bytes(N, K)
-        copies = max(3, -(-3 * MALL_BYTES // wbytes))
+        copies = _copies(wbytes, 1)
         _, base = make_q8_weights(N, K, 3, dev)
         ws = [KW.PackedQ8(base.qt.clone(), base.dt.clone(), N, K) for _ in range(copies)]
-        for M in (1, 4, 16, 64):
+        for M in Ms:
             x = make_acts(M, K, 4, dev)
             q = torch.empty(M, K, dtype=torch.int8, device=dev)
             s = torch.empty(M, dtype=torch.float32, device=dev)
             n = torch.tensor([M], dtype=torch.int32, device=dev)
             KQ.rows_q8(x, None, q, s, n, M)
             out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
-            for i in range(copies):
-                KW.gemm(q, s, ws[i], None, out, n, 32)
-            torch.cuda.synchronize()
-            g = torch.cuda.CUDAGraph()
-            st = torch.cuda.Stream()
-            with torch.cuda.stream(st):
-                with torch.cuda.graph(g, stream=st):
-                    for i in range(iters):
-                        KW.gemm(q, s, ws[i % copies], None, out, n, 32)
-            g.replay()
-            torch.cuda.synchronize()
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record()
-            g.replay()
-            b.record()
-            torch.cuda.synchronize()
-            us = a.elapsed_time(b) / iters * 1e3
-            gbs = wbytes / (us * 1e-6) / 1e9
-            rows.append(dict(M=M, K=K, N=N, us=round(us, 2), GBps=round(gbs, 1),
-                             hbm_frac=round(gbs / PEAK_HBM_GBS, 3), TOPS=round(2 * M * N * K / (us * 1e-6) / 1e12, 2)))
-            del g
+            us = _graph_us(lambda i: KW.gemm(q, s, ws[i], None, out, n, 32), copies, iters)
+            rows.append(_row(M, K, N, us, wbytes, "hbm"))
         del ws, base
         torch.cuda.empty_cache()
     return rows
+
+
+def bench_w4a8(dev, iters=20):
+    """Config 3: Q4_K W4A8, K = 5120, N = 13824, M = 16 (memory-bound: GB/s of Q4_K bytes, 144 per 256 weights) and
+    M = 2048 (int8 MFMA-bound), one activation scale per token plus per-32 sums (rows_g, not timed here)."""
+    import torch
+    from prism_amd import gguf_formats as GF
+    from prism_amd import quant as KQ
+    from prism_amd import w4a8 as KW4
+    K, N = 5120, 13824
+    wbytes = N * K // 256 * 144
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    kq = GF.quantize_q4k(torch.randn(N, K, generator=g, device=dev) * 0.02)
+    rows = []
+    for M in (16, 2048):
+        copies = _copies(wbytes, M)
+        ws = [KW4.repack(kq) for _ in range(copies)]
+        x = make_acts(M, K, 6, dev)
+        q = torch.empty(M, K, dtype=torch.int8, device=dev)
+        s = torch.empty(1, M, dtype=torch.float32, device=dev)
+        xs = torch.empty(K // 256, M, 16, dtype=torch.int8, device=dev)
+        n = torch.tensor([M], dtype=torch.int32, device=dev)
+        KQ.rows_g(x, q, s, xs, n, M, group=K)
+        out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+        us = _graph_us(lambda i: KW4.gemm(q, s, xs, ws[i], out, n), copies, iters if M <= 64 else 5)
+        rows.append(_row(M, K, N, us, wbytes, "hbm" if M <= 64 else "mfma", PEAK_INT8_TOPS))
+        del ws
+        torch.cuda.empty_cache()
+    return rows
+
+
+def bench_mxfp4(dev, iters=40):
+    """Config 4: MXFP4, K = N = 5120, e2m1 weights (OCP scales) x e4m3 activations (per-32 e8m0), M = 16 (GB/s of
+    weight bytes, 0.5 + 1/32 per weight) and M = 4096 (against the fp8 dense MFMA peak, 5.0 PFLOP/s)."""
+    import torch
+    from prism_amd import mxfp4 as MX
+    K = N = 5120
+    wbytes = N * K // 2 + N * K // 32
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    base = MX.pack(torch.randn(N, K, generator=g, device=dev) * 0.02, "ocp")
+    rows = []
+    for M in (16, 4096):
+        copies = _copies(wbytes, M)
+        ws = [MX.MX4(base.q.clone(), base.s.clone(), N, K) for _ in range(copies)]
+        x = make_acts(M, K, 8, dev)
+        q = torch.empty(M, K, dtype=torch.uint8, device=dev)
+        s = torch.empty(M, K // 32, dtype=torch.uint8, device=dev)
+        MX.quantize_act_fp8(x, q, s)
+        out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+        us = _graph_us(lambda i: MX.gemm(q, s, ws[i], out, M), copies, iters if M <= 64 else 10)
+        rows.append(_row(M, K, N, us, wbytes, "hbm" if M <= 64 else "mfma", PEAK_FP8_TFLOPS))
+        del ws
+        torch.cuda.empty_cache()
+    return rows
+
+
+def bench_configs(dev):
+    return {
+        "c0": bench_q8_decode(dev, [(4096, 4096)], (16,)),
+        "c2": bench_q8_decode(dev, [(5120, 5120), (17408, 5120)], (1, 4, 16, 64)),
+        "c3": bench_w4a8(dev),
+        "c4": bench_mxfp4(dev),
+    }
 
 
 def cpu_baseline(sample, rows):
@@ -183,7 +268,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-sweep", action="store_true", help="skip the per-config measurements")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=M1)
     ap.add_argument("--copy-probe", action="store_true",
@@ -206,7 +291,7 @@ def main():
         print(json.dumps({"copy_bytes_read": src.numel() * 4, "copy_bytes_written": dst.numel() * 4}))
         return
     res, sample = bench_prefill(a.steps, a.warmup, dev)
-    sweep = None if a.no_sweep else bench_decode_sweep(dev)
+    configs = None if a.no_sweep else bench_configs(dev)
     cpu = None if a.no_cpu else cpu_baseline(sample, a.cpu_rows)
     achieved = res["ops"] / (res["gemm_ms"] * 1e-3) / 1e12
     line = {
@@ -228,7 +313,7 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": traffic_from_profiles()},
         "cpu_baseline": cpu,
-        "sweep": sweep,
+        "configs": configs,
     }
     print(json.dumps(line), flush=True)
 

@@ -101,7 +101,9 @@ PRISM_API int prism_q8_0_pack(const int8_t* qs, const uint16_t* d, int8_t* qt, u
  * Q8_0 W8A8 GEMM (gk = 32, one activation scale per token) on packed weights: the arithmetic and bits of
  * prism_w8a8_gemm with gk = 32 (kernels/w8a8.py:64-85), the engine entry kernels/w8a8.py:183-231.
  * a int8 [M, K]; a_s fp32, row m at a_s[m * as_sm]; qt / dt from prism_q8_0_pack; out as prism_w8a8_gemm.
- * kernel: -1 picks by M; 0 the prefill tile kernel; 1 the decode kernel (M <= 64).  Needs K % 128 == 0.
+ * kernel: -1 picks by M; 0 the prefill tile kernel; 1 the decode kernels (M <= 64: M <= 16 folds through LDS,
+ * larger M as kernel 2); 2 the register-fold kernel, one wave per 16 x 16 output tile (M <= 64).
+ * Needs K % 128 == 0.
  */
 PRISM_API int prism_w8a8_q8_0_packed_gemm(const int8_t* a, const float* a_s, int64_t as_sm, const int8_t* qt,
                                           const uint16_t* dt, void* out, int64_t ldo, const int32_t* n_rows,

@@ -41,6 +41,16 @@ __device__ __forceinline__ float div_rn(float a, float b) { return __fdiv_rn(a, 
 __device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
 __device__ __forceinline__ float add_rn(float a, float b) { return __fadd_rn(a, b); }
 
+// RN(x * float(h)) for the fp16 half H (0 low, 1 high) of word, in one v_fma_mix_f32 (fp16 operand widened exactly,
+// one rounding; the -0.0 addend leaves every product, signed zeros included, as the plain product).
+template <int H>
+__device__ __forceinline__ float mul_f16_rn(float x, uint32_t word) {
+    float r;
+    const float nz = -0.0f;
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[0,%4,0] op_sel_hi:[0,1,0]" : "=v"(r) : "v"(x), "v"(word), "v"(nz), "n"(H));
+    return r;
+}
+
 // Workgroup barrier for LDS hand-offs only: waits for this wave's LDS operations, not for its outstanding global
 // loads (__syncthreads() also drains those, which would empty a kernel's prefetch pipeline at every barrier).
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }

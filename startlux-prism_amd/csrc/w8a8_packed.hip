@@ -383,6 +383,108 @@ __global__ __launch_bounds__(256, 2) void w8a8_packed_tile_kernel(const int8_t* 
         }
 }
 
+// ---------------------------------------------------------------------------------------------- mid (17..64 rows)
+// One wave (one workgroup) per (16 activation rows, 16-row weight tile), walking every block pair in order; the
+// m-tiles of one weight tile are grid rows blockIdx.y of the same XCD, so their weight chunks come from HBM once.  Per pair a lane
+// loads its weight chunk slot (16 bytes), the two 8-byte activation pieces of its row and the block scales of its 4
+// output rows, PD pairs ahead; each block's int32 sums come from one v_mfma_i32_16x16x32_i8 with a zero accumulator
+// and the lane folds RN(RN(float(P) sa) sw) into its 4 outputs in block order, in registers.
+template <int PD, int EPI>
+__global__ __launch_bounds__(64) void w8a8_packed_mid_kernel(const int8_t* __restrict__ a,
+                                                              const float* __restrict__ a_s, int64_t as_sm,
+                                                              const int8_t* __restrict__ qt,
+                                                              const uint16_t* __restrict__ dt,
+                                                              void* __restrict__ out, int64_t ldo,
+                                                              const int32_t* __restrict__ n_rows, int M, int N,
+                                                              int K) {
+    const int lane = threadIdx.x & 63, mt = blockIdx.y;
+    const int nt = blockIdx.x;
+    const int live = min(M, __ldg(n_rows));
+    if (mt * 16 >= live) return;
+    const int KP = K / 64;
+    const int lm = lane & 15, q = lane >> 4;
+    const int m = min(mt * 16 + lm, M - 1);
+    const float sa = a_s[(int64_t)m * as_sm];
+    const v4i* cw = reinterpret_cast<const v4i*>(qt) + (int64_t)nt * KP * 64 + lane;
+    const v4u* cs = reinterpret_cast<const v4u*>(dt) + (int64_t)nt * KP * 4 + q;
+    const int8_t* xa = a + (int64_t)m * K + 8 * q;
+
+    struct Pair {
+        v4i w;
+        v4u s;
+        v2u x0, x1;
+    };
+    auto load = [&](int j, Pair& p) {
+        const int jj = min(j, KP - 1);
+        p.w = cw[(int64_t)jj * 64];
+        p.s = cs[(int64_t)jj * 4];
+        p.x0 = *reinterpret_cast<const v2u*>(xa + 64 * jj);
+        p.x1 = *reinterpret_cast<const v2u*>(xa + 64 * jj + 32);
+    };
+    float y[4] = {0.f, 0.f, 0.f, 0.f};
+    const v4i zero = {0, 0, 0, 0};
+    // the int32 sums of a pair's two blocks (one MFMA each, zero accumulator)
+    auto sums = [&](const Pair& p, v4i* acc) {
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int64_t wf = h ? ((int64_t)(uint32_t)p.w[2] | ((int64_t)p.w[3] << 32))
+                                 : ((int64_t)(uint32_t)p.w[0] | ((int64_t)p.w[1] << 32));
+            const v2u xv = h ? p.x1 : p.x0;
+            const int64_t xf = (int64_t)xv[0] | ((int64_t)xv[1] << 32);
+            acc[h] = __builtin_amdgcn_mfma_i32_16x16x32_i8(wf, xf, zero, 0, 0, 0);
+        }
+    };
+    // fold the pair's terms into the 4 outputs, block 2j before 2j + 1
+    auto fold = [&](const v4i* acc, const Pair& p) {
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                // scales of this lane's row 4 q + e: chunk row-major over (row, block of the pair), block h in half h
+                const float x = mul_rn((float)acc[h][e], sa);
+                y[e] = add_rn(y[e], h ? mul_f16_rn<1>(x, p.s[e]) : mul_f16_rn<0>(x, p.s[e]));
+            }
+    };
+    Pair ring[PD];
+#pragma unroll
+    for (int d = 0; d < PD; d++) load(d, ring[d]);
+    // branch-free body, so the compiler's wait counts let the later pairs stay in flight; pairs go two at a time (four
+    // MFMAs, then the two folds in order), so the VALU fold of one waits on MFMAs issued before the other's
+    static_assert(PD % 2 == 0, "pairs are taken two at a time");
+    const int full = KP / PD * PD;
+    v4i acc0[2], acc1[2];
+    for (int j0 = 0; j0 < full; j0 += PD) {
+#pragma unroll
+        for (int d = 0; d < PD; d += 2) {
+            sums(ring[d], acc0);
+            sums(ring[d + 1], acc1);
+            fold(acc0, ring[d]);
+            fold(acc1, ring[d + 1]);
+            load(j0 + d + PD, ring[d]);          // past the end: the last pair again (a cache hit)
+            load(j0 + d + 1 + PD, ring[d + 1]);
+        }
+    }
+#pragma unroll
+    for (int d = 0; d < PD; d++)
+        if (full + d < KP) {
+            sums(ring[d], acc0);
+            fold(acc0, ring[d]);
+        }
+    const int row = mt * 16 + lm;
+    if (row < live) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int n = 16 * nt + 4 * q + e;
+            if (EPI == 0) {
+                reinterpret_cast<uint16_t*>(out)[(int64_t)row * ldo + n] = (uint16_t)f32_to_bf16(y[e]);
+            } else {
+                float* o = reinterpret_cast<float*>(out) + (int64_t)row * ldo + n;
+                *o = add_rn(*o, y[e]);
+            }
+        }
+    }
+}
+
 static size_t packed_decode_lds(int R, int M) {
     return 2 * (size_t)R * M * 16 * 4 + 2 * (size_t)R * 16 * 4 + 2 * (size_t)M * (R * 32 + 16);
 }
@@ -398,11 +500,14 @@ static void launch_packed(int kernel, const int8_t* a, const float* a_s, int64_t
                        st, a, a_s, as_sm, qt, dt, out, ldo, n_rows, M, N, K)
         if (M <= 4) PDEC(8, 32, 4, 2);
         else if (M <= 16) PDEC(8, 16, 16, 3);
-        else if (M <= 32) PDEC(4, 16, 32, 3);
-        else if (M <= 48) PDEC(4, 8, 48, 4);
-        else PDEC(4, 8, 64, 4);
+        else kernel = 2;
 #undef PDEC
-    } else {
+    }
+    if (kernel == 2) {
+        const int mt = (M + 15) / 16;
+        hipLaunchKernelGGL((w8a8_packed_mid_kernel<8, EPI>), dim3(N / 16, mt), dim3(64), 0, st, a, a_s, as_sm,
+                           qt, dt, out, ldo, n_rows, M, N, K);
+    } else if (kernel == 0) {
         const int tiles_m = (M + PBM - 1) / PBM, tiles_n = (N + PBN - 1) / PBN;
         hipLaunchKernelGGL((w8a8_packed_tile_kernel<EPI>), dim3(tiles_m * tiles_n), dim3(256), 0, st, a, a_s, as_sm,
                            qt, dt, out, ldo, n_rows, M, N, K, tiles_m, tiles_n);
@@ -433,9 +538,9 @@ extern "C" int prism_w8a8_q8_0_packed_gemm(const int8_t* a, const float* a_s, in
     if (M < 0 || N <= 0 || K <= 0 || N % 16 || K % 128 || ldo < N || M > (1 << 30) || N > (1 << 30) || K > (1 << 30))
         return PRISM_ERR_SHAPE;
     if (!PRISM_ALIGNED(a, 16) || !PRISM_ALIGNED(qt, 16) || !PRISM_ALIGNED(dt, 16)) return PRISM_ERR_ALIGN;
-    if (kernel < -1 || kernel > 1) return PRISM_ERR_ARG;
+    if (kernel < -1 || kernel > 2) return PRISM_ERR_ARG;
     if (kernel == -1) kernel = M <= 64 ? 1 : 0;
-    if (kernel == 1 && M > 64) return PRISM_ERR_ARG;
+    if ((kernel == 1 || kernel == 2) && M > 64) return PRISM_ERR_ARG;
     if (M == 0) return PRISM_OK;
     hipStream_t st = (hipStream_t)stream;
     if (epi == 0)

@@ -20,7 +20,7 @@ import torch
 from . import _lib as L
 from .quant import quant_rows  # noqa: F401  (re-exported: kernels/w8a8.py:264)
 
-KERNELS = {"auto": -1, "tile": 0, "decode": 1}
+KERNELS = {"auto": -1, "tile": 0, "decode": 1, "mid": 2}
 
 
 class PackedQ8(NamedTuple):

@@ -205,7 +205,7 @@ def _packed_gemm(dev, a, s, qs, d, epi, kernel, live=None, out0=None, ldo=None):
     return out
 
 
-@pytest.mark.parametrize("kernel", ["decode", "tile"])
+@pytest.mark.parametrize("kernel", ["decode", "mid", "tile"])
 def test_packed_config0_bit_exact(dev, kernel):
     qs, d = q8_weights(4096, 4096, seed=0)
     a, s = O.quant_rows_i8(acts_bf16(16, 4096, seed=100))
@@ -227,7 +227,7 @@ def test_packed_cases_bit_exact(dev, M, N, K, live):
     want0 = O.w8a8_gemm(a, s, qs, d, 32, epi=0, live=live)
     base = rng(M * N + 1).standard_normal((M, N)).astype(np.float32)
     want1 = O.w8a8_gemm(a, s, qs, d, 32, epi=1, out=base.copy(), live=live)
-    for kernel in ["tile"] + (["decode"] if M <= 64 else []):
+    for kernel in ["tile"] + (["decode", "mid"] if M <= 64 else []):
         got0 = _packed_gemm(dev, a, s, qs, d, 0, kernel, live=live).view(torch.int16).cpu().numpy().view(np.uint16)
         assert np.array_equal(got0[:live], want0[:live]), kernel
         assert (got0[live:] == 7).all(), kernel
