@@ -304,9 +304,10 @@ __global__ __launch_bounds__(256, 2) void w4a8_tile_kernel(const int8_t* __restr
                                                            int N, int K, int tiles_m, int tiles_n) {
     __shared__ __attribute__((aligned(16))) uint8_t Bs[8 * 2048];     // 8 row tiles x (2 halves x 64 lanes x 16 B)
     __shared__ __attribute__((aligned(16))) int8_t As[QBM * QLDA];
-    __shared__ int scl[8][QBN], mnl[8][QBN];
+    __shared__ int scl[8][QBN];
+    __shared__ __attribute__((aligned(8))) uint8_t mnb[QBN][8];     // the 8 mins of each weight row, as bytes
     __shared__ float dl[QBN], dml[QBN];
-    __shared__ int sl[QBM][8];
+    __shared__ __attribute__((aligned(16))) int8_t xsb[QBM][16];    // per activation row: S & 63 x 8, S >> 6 x 8
     __shared__ float al[QBM];
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -369,18 +370,15 @@ __global__ __launch_bounds__(256, 2) void w4a8_tile_kernel(const int8_t* __restr
             int sc[8], mn[8];
             row_meta(rm, d, dm, sc, mn);
 #pragma unroll
-            for (int g = 0; g < 8; g++) {
-                scl[g][tid] = sc[g];
-                mnl[g][tid] = mn[g];
-            }
+            for (int g = 0; g < 8; g++) scl[g][tid] = sc[g];
+            *reinterpret_cast<v2u*>(&mnb[tid][0]) =
+                v2u{(uint32_t)(mn[0] | (mn[1] << 8) | (mn[2] << 16) | (mn[3] << 24)),
+                    (uint32_t)(mn[4] | (mn[5] << 8) | (mn[6] << 16) | (mn[7] << 24))};
             dl[tid] = d;
             dml[tid] = dm;
         }
         if (tid < 64) {
-            int S[8];
-            split_sums(rs, S);
-            *reinterpret_cast<v4i*>(&sl[tid][0]) = v4i{S[0], S[1], S[2], S[3]};
-            *reinterpret_cast<v4i*>(&sl[tid][4]) = v4i{S[4], S[5], S[6], S[7]};
+            *reinterpret_cast<v4i*>(&xsb[tid][0]) = rs;
             al[tid] = ra;
         }
     };
@@ -400,12 +398,13 @@ __global__ __launch_bounds__(256, 2) void w4a8_tile_kernel(const int8_t* __restr
         sstore();
         lds_barrier();
         if (b + 1 < NB) gload(b + 1);
-        v4i acc[2][4], mins[2][4];
+        v4i acc[2][4];
 #pragma unroll
         for (int i = 0; i < 2; i++)
 #pragma unroll
-            for (int j = 0; j < 4; j++) acc[i][j] = mins[i][j] = v4i{0, 0, 0, 0};
-#pragma unroll
+            for (int j = 0; j < 4; j++) acc[i][j] = v4i{0, 0, 0, 0};
+        const v4i zero = {0, 0, 0, 0};
+#pragma unroll 2
         for (int g = 0; g < 8; g++) {
             int64_t wf[2], af[4];
 #pragma unroll
@@ -419,19 +418,24 @@ __global__ __launch_bounds__(256, 2) void w4a8_tile_kernel(const int8_t* __restr
 #pragma unroll
             for (int i = 0; i < 2; i++) {
                 const v4i sc = *reinterpret_cast<const v4i*>(&scl[g][32 * wv + 16 * i + 4 * q]);
-                const v4i mn = *reinterpret_cast<const v4i*>(&mnl[g][32 * wv + 16 * i + 4 * q]);
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    const v4i zero = {0, 0, 0, 0};
                     const v4i P = __builtin_amdgcn_mfma_i32_16x16x32_i8(wf[i], af[j], zero, 0, 0, 0);
-                    const int Sg = sl[16 * j + lm][g];
 #pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        acc[i][j][e] += sc[e] * P[e];
-                        mins[i][j][e] += mn[e] * Sg;
-                    }
+                    for (int e = 0; e < 4; e++) acc[i][j][e] += __mul24(sc[e], P[e]);   // |sc P| < 2^23
                 }
             }
+        }
+        // mins = sum_g mn[n, g] S[m, g] as two MFMAs over k = 0..7 (lanes q > 0 carry zeros): the weight row's 8
+        // mins against the 8 low parts S & 63, then against the 8 high parts S >> 6; mins = lo + 64 hi (exact)
+        int64_t mnf[2], slo[4], shi[4];
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+            mnf[i] = q == 0 ? *reinterpret_cast<const int64_t*>(&mnb[32 * wv + 16 * i + lm][0]) : 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            slo[j] = q == 0 ? *reinterpret_cast<const int64_t*>(&xsb[16 * j + lm][0]) : 0;
+            shi[j] = q == 0 ? *reinterpret_cast<const int64_t*>(&xsb[16 * j + lm][8]) : 0;
         }
 #pragma unroll
         for (int i = 0; i < 2; i++) {
@@ -439,9 +443,12 @@ __global__ __launch_bounds__(256, 2) void w4a8_tile_kernel(const int8_t* __restr
             const v4f dm = *reinterpret_cast<const v4f*>(&dml[32 * wv + 16 * i + 4 * q]);
 #pragma unroll
             for (int j = 0; j < 4; j++) {
+                const v4i lo = __builtin_amdgcn_mfma_i32_16x16x32_i8(mnf[i], slo[j], zero, 0, 0, 0);
+                const v4i hi = __builtin_amdgcn_mfma_i32_16x16x32_i8(mnf[i], shi[j], zero, 0, 0, 0);
                 const float am = al[16 * j + lm];
 #pragma unroll
-                for (int e = 0; e < 4; e++) y[i][j][e] = fmaf(am, q4k_term(d[e], dm[e], acc[i][j][e], mins[i][j][e]), y[i][j][e]);
+                for (int e = 0; e < 4; e++)
+                    y[i][j][e] = fmaf(am, q4k_term(d[e], dm[e], acc[i][j][e], lo[e] + 64 * hi[e]), y[i][j][e]);
             }
         }
     }
