@@ -528,6 +528,9 @@ __global__ __launch_bounds__(256, 2) void w8a8_q8_tile_kernel(const int8_t* __re
 }
 
 // ============================================================================================== launch
+int launch_w8a8_pc_tile(const int8_t* a, const float* a_s, int64_t as_sm, const int8_t* w, const void* w_s, bool ws16,
+                        void* out, int64_t ldo, const int32_t* n_rows, int M, int N, int K, int epi, hipStream_t st);
+
 template <bool AS_GROUP, bool WS16, int EPI>
 static int launch_w8a8(int kernel, const int8_t* a, const float* a_s, int64_t as_sm, int64_t as_sg, const int8_t* w,
                        const void* w_s, void* out, int64_t ldo, const int32_t* n_rows, int M, int N, int K, int gk,
@@ -543,6 +546,9 @@ static int launch_w8a8(int kernel, const int8_t* a, const float* a_s, int64_t as
         else DEC(8, 8, 4, 8);
 #undef DEC
     } else {
+        // per channel (one group): the int8 MFMA GEMM with an epilogue (w8a8_pc.hip)
+        if (gk == K && K % 64 == 0 && ldo % 4 == 0 && PRISM_ALIGNED(out, EPI ? 16 : 8))
+            return launch_w8a8_pc_tile(a, a_s, as_sm, w, w_s, WS16, out, ldo, n_rows, M, N, K, EPI, st);
         const int tiles_m = (M + TBM - 1) / TBM, tiles_n = (N + TBN - 1) / TBN;
         dim3 grid(tiles_m * tiles_n), block(256);
         if (!AS_GROUP && gk == 32 && K % TBK == 0)

@@ -136,17 +136,28 @@ def test_int32_block_sums_exact(dev):
             assert np.array_equal(got.astype(np.int64), P), (K, gk, kernel)
 
 
-@pytest.mark.parametrize("M,N,K", [(16, 128, 4096), (200, 256, 5120), (64, 64, 256)])
-def test_per_channel_gk_equals_k(dev, M, N, K):
-    """gk = K (the engine's per-channel weights): one epilogue per output."""
-    g = rng(K)
+@pytest.mark.parametrize("M,N,K,live", [(16, 128, 4096, 16), (200, 256, 5120, 200), (64, 64, 256, 64),
+                                         (300, 528, 1024, 290), (513, 272, 2048, 513), (1, 64, 128, 1)])
+def test_per_channel_gk_equals_k(dev, M, N, K, live):
+    """gk = K (the engine's per-channel weights): one epilogue per output, bf16 and residual-add epilogues, live rows,
+    ragged tiles in both directions, fp32 and fp16 weight scales."""
+    g = rng(K + M)
     a = g.integers(-127, 128, (M, K), dtype=np.int8)
     w = g.integers(-127, 128, (N, K), dtype=np.int8)
     sa = (g.random(M) * 1e-2).astype(np.float32)
     sw = (g.random((N, 1)) * 1e-3).astype(np.float32)
-    want = O.w8a8_gemm(a, sa, w, sw, K, epi=0)
-    got = _gemm(dev, a, sa, w, sw, K, 0, "tile").view(torch.int16).cpu().numpy().view(np.uint16)
-    assert np.array_equal(got, want)
+    want = O.w8a8_gemm(a, sa, w, sw, K, epi=0, live=live)
+    got = _gemm(dev, a, sa, w, sw, K, 0, "tile", live=live).view(torch.int16).cpu().numpy().view(np.uint16)
+    assert np.array_equal(got[:live], want[:live])
+    assert (got[live:] == 7).all()
+    base = g.standard_normal((M, N)).astype(np.float32)
+    want1 = O.w8a8_gemm(a, sa, w, sw, K, epi=1, out=base.copy(), live=live)
+    got1 = _gemm(dev, a, sa, w, sw, K, 1, "tile", live=live, out0=base).cpu().numpy()
+    assert np.array_equal(got1, want1)
+    sw16 = sw.astype(np.float16)
+    want16 = O.w8a8_gemm(a, sa, w, sw16.astype(np.float32), K, epi=0, live=live)
+    got16 = _gemm(dev, a, sa, w, sw16, K, 0, "tile", live=live).view(torch.int16).cpu().numpy().view(np.uint16)
+    assert np.array_equal(got16[:live], want16[:live])
 
 
 def test_repeat_runs_identical(dev):
