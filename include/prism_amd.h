@@ -98,6 +98,26 @@ PRISM_API int prism_q8_0_pack(const int8_t* qs, const uint16_t* d, int8_t* qt, u
                               void* stream);
 
 /*
+ * The same chunk permutation for plain int8 weights w [N, K] (per-channel, gk = K): qt int8 [N/16][K/64][64][16] as
+ * prism_q8_0_pack's qt.  The load-time repack of the per-channel weights kernels/w8a8.py:274-286 produces.
+ * Needs N % 16 == 0, K % 64 == 0.
+ */
+PRISM_API int prism_i8_pack(const int8_t* w, int8_t* qt, int64_t N, int64_t K, void* stream);
+
+/*
+ * Per-channel W8A8 GEMM (gk = K) on packed int8 weights (prism_i8_pack): the production projections of
+ * kernels/w8a8.py:183-231 with gk == K (the CUDA w8a8_kernel, csrc/w8a8_gemm.cu:298-402, schema :794-797):
+ * P = sum_k a w (int32, exact), y = RN(RN(float(P) a_s[m]) w_s[n]); epi 0 bf16(y), epi 1 out = RN(out + y).
+ * a int8 [M, K]; a_s fp32, row m at a_s[m * as_sm]; w_s fp32 [N] (fp16 when ws_fp16); out row stride ldo (a
+ * multiple of 4, out 8-byte aligned for bf16, 16 for fp32).  kernel: -1 picks by M; 0 the tile kernel; 1 the
+ * split-K decode kernel (M <= 64).  Needs N % 16 == 0, K % 64 == 0, K <= 131072 (int32 sums stay exact).
+ * prism_w8a8_gemm with gk == K runs the same kernels on row-major weights.
+ */
+PRISM_API int prism_w8a8_pc_packed_gemm(const int8_t* a, const float* a_s, int64_t as_sm, const int8_t* qt,
+                                        const void* w_s, int ws_fp16, void* out, int64_t ldo, const int32_t* n_rows,
+                                        int64_t M, int64_t N, int64_t K, int epi, int kernel, void* stream);
+
+/*
  * Q8_0 W8A8 GEMM (gk = 32, one activation scale per token) on packed weights: the arithmetic and bits of
  * prism_w8a8_gemm with gk = 32 (kernels/w8a8.py:64-85), the engine entry kernels/w8a8.py:183-231.
  * a int8 [M, K]; a_s fp32, row m at a_s[m * as_sm]; qt / dt from prism_q8_0_pack; out as prism_w8a8_gemm.

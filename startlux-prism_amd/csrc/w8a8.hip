@@ -528,13 +528,17 @@ __global__ __launch_bounds__(256, 2) void w8a8_q8_tile_kernel(const int8_t* __re
 }
 
 // ============================================================================================== launch
-int launch_w8a8_pc_tile(const int8_t* a, const float* a_s, int64_t as_sm, const int8_t* w, const void* w_s, bool ws16,
-                        void* out, int64_t ldo, const int32_t* n_rows, int M, int N, int K, int epi, hipStream_t st);
+int launch_w8a8_pc(int kernel, bool wpack, const int8_t* a, const float* a_s, int64_t as_sm, const int8_t* w,
+                   const void* w_s, bool ws16, void* out, int64_t ldo, const int32_t* n_rows, int M, int N, int K,
+                   int epi, hipStream_t st);
 
 template <bool AS_GROUP, bool WS16, int EPI>
 static int launch_w8a8(int kernel, const int8_t* a, const float* a_s, int64_t as_sm, int64_t as_sg, const int8_t* w,
                        const void* w_s, void* out, int64_t ldo, const int32_t* n_rows, int M, int N, int K, int gk,
                        hipStream_t st) {
+    // per channel (one group): the int8 MFMA GEMMs with an epilogue (w8a8_pc.hip)
+    if (gk == K && K % 64 == 0 && ldo % 4 == 0 && PRISM_ALIGNED(out, EPI ? 16 : 8) && (kernel == 0 || M <= 64))
+        return launch_w8a8_pc(kernel, false, a, a_s, as_sm, w, w_s, WS16, out, ldo, n_rows, M, N, K, EPI, st);
     if (kernel == 1) {
         dim3 grid(N / 16);
 #define DEC(NW, R, MT, D)                                                                                         \
@@ -546,9 +550,6 @@ static int launch_w8a8(int kernel, const int8_t* a, const float* a_s, int64_t as
         else DEC(8, 8, 4, 8);
 #undef DEC
     } else {
-        // per channel (one group): the int8 MFMA GEMM with an epilogue (w8a8_pc.hip)
-        if (gk == K && K % 64 == 0 && ldo % 4 == 0 && PRISM_ALIGNED(out, EPI ? 16 : 8))
-            return launch_w8a8_pc_tile(a, a_s, as_sm, w, w_s, WS16, out, ldo, n_rows, M, N, K, EPI, st);
         const int tiles_m = (M + TBM - 1) / TBM, tiles_n = (N + TBN - 1) / TBN;
         dim3 grid(tiles_m * tiles_n), block(256);
         if (!AS_GROUP && gk == 32 && K % TBK == 0)
@@ -576,8 +577,10 @@ extern "C" int prism_w8a8_gemm(const int8_t* a, const float* a_s, int64_t as_sm,
     if ((int64_t)gk * 128 * 128 >= ((int64_t)1 << 31)) return PRISM_ERR_SHAPE;   // int32 group sums stay exact
     if (!PRISM_ALIGNED(a, 16) || !PRISM_ALIGNED(w, 16)) return PRISM_ERR_ALIGN;
     if (kernel < -1 || kernel > 1) return PRISM_ERR_ARG;
-    if (kernel == -1) kernel = (gk == 32 && M <= 64) ? 1 : 0;
-    if (kernel == 1 && (gk != 32 || M > 64)) return PRISM_ERR_ARG;
+    // per channel on the int8 MFMA kernels: one group, 64-input stages, vector epilogue stores
+    const bool pc = gk == K && K % 64 == 0 && ldo % 4 == 0 && PRISM_ALIGNED(out, epi ? 16 : 8);
+    if (kernel == -1) kernel = ((gk == 32 || pc) && M <= 64) ? 1 : 0;
+    if (kernel == 1 && ((gk != 32 && !pc) || M > 64)) return PRISM_ERR_ARG;
     if (M == 0) return PRISM_OK;
     const bool asg = as_sg != 0, ws16 = ws_fp16 != 0;
     hipStream_t st = (hipStream_t)stream;

@@ -37,7 +37,7 @@ __global__ __launch_bounds__(256) void q8_0_pack_kernel(const int8_t* __restrict
     o[2] = hi[0];
     o[3] = hi[1];
     reinterpret_cast<v4u*>(qt)[e] = o;
-    if (q == 0) {                                      // 16 rows x 2 blocks of scales per chunk
+    if (q == 0 && dt) {                                // 16 rows x 2 blocks of scales per chunk
         const int G = K / 32;
         dt[(c * 16 + r) * 2 + 0] = d[(int64_t)(16 * nt + r) * G + 2 * j];
         dt[(c * 16 + r) * 2 + 1] = d[(int64_t)(16 * nt + r) * G + 2 * j + 1];
@@ -526,6 +526,17 @@ extern "C" int prism_q8_0_pack(const int8_t* qs, const uint16_t* d, int8_t* qt, 
     const int64_t total = N / 16 * (K / 64) * 64;
     hipLaunchKernelGGL(q8_0_pack_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream, qs,
                        d, qt, dt, (int)N, (int)K);
+    PRISM_LAUNCH_CHECK();
+    return PRISM_OK;
+}
+
+extern "C" int prism_i8_pack(const int8_t* w, int8_t* qt, int64_t N, int64_t K, void* stream) {
+    if (!w || !qt) return PRISM_ERR_ARG;
+    if (N <= 0 || K <= 0 || N % 16 || K % 64 || N > (1 << 30) || K > (1 << 30)) return PRISM_ERR_SHAPE;
+    if (!PRISM_ALIGNED(w, 16) || !PRISM_ALIGNED(qt, 16)) return PRISM_ERR_ALIGN;
+    const int64_t total = N / 16 * (K / 64) * 64;
+    hipLaunchKernelGGL(q8_0_pack_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream, w,
+                       nullptr, qt, nullptr, (int)N, (int)K);
     PRISM_LAUNCH_CHECK();
     return PRISM_OK;
 }

@@ -30,7 +30,7 @@ __device__ __forceinline__ void pc_vm_wait() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-template <bool WS16, int EPI, int NS>
+template <bool WPACK, bool WS16, int EPI, int NS>
 __global__ __launch_bounds__(256, 1) void w8a8_pc_tile_kernel(const int8_t* __restrict__ a,
                                                               const float* __restrict__ a_s, int64_t as_sm,
                                                               const int8_t* __restrict__ w,
@@ -54,7 +54,8 @@ __global__ __launch_bounds__(256, 1) void w8a8_pc_tile_kernel(const int8_t* __re
         swl[tid] = WS16 ? f16_to_f32(static_cast<const uint16_t*>(w_s)[n]) : static_cast<const float*>(w_s)[n];
     }
 
-    // DMA sources: instruction i of wave wv covers operand rows 16 (4 wv + i) .. + 15
+    // DMA sources: instruction i of wave wv covers operand rows 16 (4 wv + i) .. + 15; packed weights: the 1 KB
+    // chunk of 16-row tile 4 wv + i as it lies (lane slot l: row l % 16, inputs {8 q .. +7, 32 + 8 q .. +7}, q = l / 16)
     const int8_t* asrc[4];
     const int8_t* wsrc[4];
 #pragma unroll
@@ -62,28 +63,39 @@ __global__ __launch_bounds__(256, 1) void w8a8_pc_tile_kernel(const int8_t* __re
         const int row = 16 * (4 * wv + i) + (lane >> 2);
         const int c = (lane & 3) ^ pc_swz(row);
         asrc[i] = a + (int64_t)min(m0 + row, M - 1) * K + 16 * c;
-        wsrc[i] = w + (int64_t)min(n0 + row, N - 1) * K + 16 * c;
+        if (WPACK)
+            wsrc[i] = w + ((int64_t)min(n0 / 16 + 4 * wv + i, N / 16 - 1) * (K / 64)) * 1024 + 16 * lane;
+        else
+            wsrc[i] = w + (int64_t)min(n0 + row, N - 1) * K + 16 * c;
     }
     auto issue = [&](int st, int buf) {
         uint8_t* b = lds + buf * PC_STAGE;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             pc_dma(asrc[i] + (int64_t)st * PCK, b + (4 * wv + i) * 1024);
-            pc_dma(wsrc[i] + (int64_t)st * PCK, b + PC_OPER + (4 * wv + i) * 1024);
+            pc_dma(wsrc[i] + (int64_t)st * (WPACK ? 1024 : PCK), b + PC_OPER + (4 * wv + i) * 1024);
         }
     };
 
     const int wm = wv >> 1, wn = wv & 1;
     const int r = lane & 31, h = lane >> 5;
-    // fragment byte offsets within an operand stage, for the two 32-input steps s
+    // fragment byte offsets within an operand stage, for the two 32-input steps s.  Row-major weights: both
+    // operands' lanes hold inputs 16 (2 s + h) .. + 15.  Packed weights: the chunk's lane slot (q = 2 s + h, row)
+    // holds inputs {8 q .. +7, 32 + 8 q .. +7}, and the activation fragment takes the same two 8-byte pieces.
     int aoff[2][4], woff[2][4];
 #pragma unroll
     for (int s = 0; s < 2; s++)
 #pragma unroll
         for (int t = 0; t < 4; t++) {
             const int ra = 128 * wm + 32 * t + r, rw = 128 * wn + 32 * t + r;
-            aoff[s][t] = ra * PCK + 16 * ((2 * s + h) ^ pc_swz(ra));
-            woff[s][t] = rw * PCK + 16 * ((2 * s + h) ^ pc_swz(rw));
+            if (WPACK) {
+                const int q = 2 * s + h;
+                aoff[s][t] = ra * PCK + 16 * ((q >> 1) ^ pc_swz(ra)) + 8 * (q & 1);
+                woff[s][t] = (rw >> 4) * 1024 + (16 * q + (rw & 15)) * 16;
+            } else {
+                aoff[s][t] = ra * PCK + 16 * ((2 * s + h) ^ pc_swz(ra));
+                woff[s][t] = rw * PCK + 16 * ((2 * s + h) ^ pc_swz(rw));
+            }
         }
 
     v16i acc[4][4];
@@ -111,7 +123,15 @@ __global__ __launch_bounds__(256, 1) void w8a8_pc_tile_kernel(const int8_t* __re
             v4i fa[4], fw[4];
 #pragma unroll
             for (int t = 0; t < 4; t++) {
-                fa[t] = *reinterpret_cast<const v4i*>(b + aoff[s][t]);
+                if (WPACK) {
+                    // inputs 8 q .. (chunk q / 2) and 32 + 8 q .. (chunk 2 + q / 2 = (q / 2) ^ 2: its swizzled slot
+                    // is the first one's ^ 2, 32 bytes away)
+                    const v2u p0 = *reinterpret_cast<const v2u*>(b + aoff[s][t]);
+                    const v2u p1 = *reinterpret_cast<const v2u*>(b + (aoff[s][t] ^ 32));
+                    fa[t] = v4i{(int)p0.x, (int)p0.y, (int)p1.x, (int)p1.y};
+                } else {
+                    fa[t] = *reinterpret_cast<const v4i*>(b + aoff[s][t]);
+                }
                 fw[t] = *reinterpret_cast<const v4i*>(b + PC_OPER + woff[s][t]);
             }
             // D = W x A: lane l holds activation row l % 32 of the m-subtile and weight rows
@@ -153,29 +173,196 @@ __global__ __launch_bounds__(256, 1) void w8a8_pc_tile_kernel(const int8_t* __re
     }
 }
 
+// ---------------------------------------------------------------------------------------------- decode
+// M <= 16 MT.  One workgroup per G 16-row weight tiles; wave w takes the 64-input chunks w, w + NW, ... of every
+// tile (the int32 sums are exact in any order), PD chunks in flight in registers.  Per chunk a lane loads 16 bytes
+// of each tile's weights (packed: the chunk's lane slot, 1 KB per wave instruction; row-major: row l % 16, inputs
+// 16 q .. + 15) and the matching 2 x 8 activation bytes of its row per m-tile, reused across the G tiles; two
+// v_mfma_i32_16x16x32_i8 per (tile, m-tile) accumulate into int32.  The waves' sums meet in LDS, and the epilogue
+// applies the two roundings.
+template <int G, int MT, bool WPACK, bool WS16, int EPI>
+__global__ __launch_bounds__(1024) void w8a8_pc_decode_kernel(const int8_t* __restrict__ a,
+                                                              const float* __restrict__ a_s, int64_t as_sm,
+                                                              const int8_t* __restrict__ w,
+                                                              const void* __restrict__ w_s, void* __restrict__ out,
+                                                              int64_t ldo, const int32_t* __restrict__ n_rows, int M,
+                                                              int N, int K) {
+    constexpr int PD = MT <= 2 ? 4 : 2;
+    extern __shared__ __attribute__((aligned(16))) v4i red[];          // [NW][G][MT][64]
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, NW = blockDim.x >> 6;
+    const int nt0 = blockIdx.x * G;
+    const int KP = K / 64, NT = N / 16;
+    const int live = min(M, __ldg(n_rows));
+    const int lm = lane & 15, q = lane >> 4;
+
+    const int8_t* wb[G];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        const int t = min(nt0 + g, NT - 1);
+        wb[g] = WPACK ? w + (int64_t)t * KP * 1024 + 16 * lane : w + (int64_t)(16 * t + lm) * K + 16 * q;
+    }
+    const int8_t* ab[MT];
+#pragma unroll
+    for (int u = 0; u < MT; u++) ab[u] = a + (int64_t)min(16 * u + lm, M - 1) * K + (WPACK ? 8 * q : 16 * q);
+
+    struct Chunk {
+        v4i w[G];
+        v2u x0[MT], x1[MT];
+    };
+    auto load = [&](int j, Chunk& c) {
+        const int jj = min(j, KP - 1);
+#pragma unroll
+        for (int g = 0; g < G; g++) c.w[g] = *reinterpret_cast<const v4i*>(wb[g] + (int64_t)jj * (WPACK ? 1024 : 64));
+#pragma unroll
+        for (int u = 0; u < MT; u++) {
+            const int8_t* p = ab[u] + (int64_t)jj * 64;
+            c.x0[u] = *reinterpret_cast<const v2u*>(p);
+            c.x1[u] = *reinterpret_cast<const v2u*>(p + (WPACK ? 32 : 8));
+        }
+    };
+    v4i acc[G][MT];
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+        for (int u = 0; u < MT; u++) acc[g][u] = v4i{0, 0, 0, 0};
+    auto mma = [&](const Chunk& c) {
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            const int64_t w0 = (int64_t)(uint32_t)c.w[g].x | ((int64_t)c.w[g].y << 32);
+            const int64_t w1 = (int64_t)(uint32_t)c.w[g].z | ((int64_t)c.w[g].w << 32);
+#pragma unroll
+            for (int u = 0; u < MT; u++) {
+                const int64_t x0 = (int64_t)c.x0[u].x | ((int64_t)c.x0[u].y << 32);
+                const int64_t x1 = (int64_t)c.x1[u].x | ((int64_t)c.x1[u].y << 32);
+                acc[g][u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(w0, x0, acc[g][u], 0, 0, 0);
+                acc[g][u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(w1, x1, acc[g][u], 0, 0, 0);
+            }
+        }
+    };
+    // this wave's chunks: j = wv + NW i, i < cnt; branch-free body over whole rings of PD
+    const int cnt = wv < KP ? (KP - wv + NW - 1) / NW : 0;
+    Chunk ring[PD];
+#pragma unroll
+    for (int d = 0; d < PD; d++) load(wv + NW * d, ring[d]);
+    const int full = cnt / PD * PD;
+    for (int i0 = 0; i0 < full; i0 += PD) {
+#pragma unroll
+        for (int d = 0; d < PD; d++) {
+            mma(ring[d]);
+            load(wv + NW * (i0 + d + PD), ring[d]);
+        }
+    }
+#pragma unroll
+    for (int d = 0; d < PD; d++)
+        if (full + d < cnt) mma(ring[d]);
+
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+        for (int u = 0; u < MT; u++) red[((wv * G + g) * MT + u) * 64 + lane] = acc[g][u];
+    __syncthreads();
+    for (int idx = tid; idx < G * MT * 64; idx += blockDim.x) {
+        const int g = idx / (MT * 64), u = (idx >> 6) % MT, l = idx & 63;
+        const int m = 16 * u + (l & 15), t = nt0 + g;
+        if (m >= live || t >= NT) continue;
+        v4i P = red[idx];
+        for (int v = 1; v < NW; v++) {
+            const v4i z = red[v * G * MT * 64 + idx];
+            P = v4i{P.x + z.x, P.y + z.y, P.z + z.z, P.w + z.w};
+        }
+        const float sa = a_s[(int64_t)m * as_sm];
+        const int n = 16 * t + 4 * (l >> 4);
+        float y[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float sw = WS16 ? f16_to_f32(static_cast<const uint16_t*>(w_s)[n + e])
+                                  : static_cast<const float*>(w_s)[n + e];
+            y[e] = mul_rn(mul_rn((float)P[e], sa), sw);
+        }
+        if (EPI == 0) {
+            uint16_t* o = static_cast<uint16_t*>(out) + (int64_t)m * ldo + n;
+            *reinterpret_cast<v2u*>(o) = v2u{f32_to_bf16(y[0]) | (f32_to_bf16(y[1]) << 16),
+                                             f32_to_bf16(y[2]) | (f32_to_bf16(y[3]) << 16)};
+        } else {
+            float4* o = reinterpret_cast<float4*>(static_cast<float*>(out) + (int64_t)m * ldo + n);
+            const float4 p = *o;
+            *o = make_float4(add_rn(p.x, y[0]), add_rn(p.y, y[1]), add_rn(p.z, y[2]), add_rn(p.w, y[3]));
+        }
+    }
+}
+
 template <typename F>
 static void pc_allow(F* fn, size_t bytes) {
     (void)hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
 }
 
-// Launch the per-channel tile kernel; the caller has checked K % 64 == 0, 16-byte aligned a / w, and (for the
-// vector stores) ldo % 4 == 0 with an 8 / 16-byte aligned out.
-int launch_w8a8_pc_tile(const int8_t* a, const float* a_s, int64_t as_sm, const int8_t* w, const void* w_s, bool ws16,
-                        void* out, int64_t ldo, const int32_t* n_rows, int M, int N, int K, int epi, hipStream_t st) {
+// Per-channel launch: kernel 1 the decode kernel (M <= 64), else the tile kernel.  The caller has checked
+// K % 64 == 0, 16-byte aligned a / w, ldo % 4 == 0 and an 8 / 16-byte aligned out.
+int launch_w8a8_pc(int kernel, bool wpack, const int8_t* a, const float* a_s, int64_t as_sm, const int8_t* w,
+                   const void* w_s, bool ws16, void* out, int64_t ldo, const int32_t* n_rows, int M, int N, int K,
+                   int epi, hipStream_t st) {
+    if (kernel == 1) {
+        const int MT = (M + 15) / 16;
+        const int G = (N % 32 == 0) ? 2 : 1;
+        const int KP = K / 64;
+        int nw = min(16, max(1, KP / 4));
+        const size_t lds = (size_t)nw * G * MT * 64 * sizeof(v4i);
+        dim3 grid((unsigned)(N / (16 * G)));
+#define PDL(GV, MTV, WP, W16, E)                                                                                   \
+    hipLaunchKernelGGL((w8a8_pc_decode_kernel<GV, MTV, WP, W16, E>), grid, dim3(64 * nw), lds, st, a, a_s, as_sm, w, \
+                       w_s, out, ldo, n_rows, M, N, K)
+#define PDL_MT(GV, WP, W16, E)                                                                                     \
+    do {                                                                                                           \
+        if (MT == 1) PDL(GV, 1, WP, W16, E); else if (MT == 2) PDL(GV, 2, WP, W16, E);                             \
+        else if (MT == 3) PDL(GV, 3, WP, W16, E); else PDL(GV, 4, WP, W16, E);                                     \
+    } while (0)
+#define PDL_G(WP, W16, E) do { if (G == 2) PDL_MT(2, WP, W16, E); else PDL_MT(1, WP, W16, E); } while (0)
+#define PDL_WP(W16, E) do { if (wpack) PDL_G(true, W16, E); else PDL_G(false, W16, E); } while (0)
+        if (ws16) { if (epi == 0) PDL_WP(true, 0); else PDL_WP(true, 1); }
+        else { if (epi == 0) PDL_WP(false, 0); else PDL_WP(false, 1); }
+#undef PDL_WP
+#undef PDL_G
+#undef PDL_MT
+#undef PDL
+        PRISM_LAUNCH_CHECK();
+        return PRISM_OK;
+    }
     constexpr int NS = 4;
     const int tiles_m = (M + PCT - 1) / PCT, tiles_n = (N + PCT - 1) / PCT;
     const size_t lds = (size_t)NS * PC_STAGE;
-#define PCL(W16, E)                                                                                                \
+#define PCL(WP, W16, E)                                                                                            \
     do {                                                                                                           \
-        pc_allow(w8a8_pc_tile_kernel<W16, E, NS>, lds);                                                            \
-        hipLaunchKernelGGL((w8a8_pc_tile_kernel<W16, E, NS>), dim3(tiles_m * tiles_n), dim3(256), lds, st, a, a_s,  \
-                           as_sm, w, w_s, out, ldo, n_rows, M, N, K, tiles_m, tiles_n);                             \
+        pc_allow(w8a8_pc_tile_kernel<WP, W16, E, NS>, lds);                                                        \
+        hipLaunchKernelGGL((w8a8_pc_tile_kernel<WP, W16, E, NS>), dim3(tiles_m * tiles_n), dim3(256), lds, st, a,   \
+                           a_s, as_sm, w, w_s, out, ldo, n_rows, M, N, K, tiles_m, tiles_n);                        \
     } while (0)
-    if (ws16) { if (epi == 0) PCL(true, 0); else PCL(true, 1); }
-    else { if (epi == 0) PCL(false, 0); else PCL(false, 1); }
+#define PCL_WP(W16, E) do { if (wpack) PCL(true, W16, E); else PCL(false, W16, E); } while (0)
+    if (ws16) { if (epi == 0) PCL_WP(true, 0); else PCL_WP(true, 1); }
+    else { if (epi == 0) PCL_WP(false, 0); else PCL_WP(false, 1); }
+#undef PCL_WP
 #undef PCL
     PRISM_LAUNCH_CHECK();
     return PRISM_OK;
 }
 
 }  // namespace prism
+
+using namespace prism;
+
+extern "C" int prism_w8a8_pc_packed_gemm(const int8_t* a, const float* a_s, int64_t as_sm, const int8_t* qt,
+                                         const void* w_s, int ws_fp16, void* out, int64_t ldo, const int32_t* n_rows,
+                                         int64_t M, int64_t N, int64_t K, int epi, int kernel, void* stream) {
+    if (!a || !a_s || !qt || !w_s || !out || !n_rows) return PRISM_ERR_ARG;
+    if (epi != 0 && epi != 1) return PRISM_ERR_ARG;
+    if (M < 0 || N <= 0 || K <= 0 || N % 16 || K % 64 || ldo < N || M > (1 << 30) || N > (1 << 30) ||
+        K > (1 << 17))
+        return PRISM_ERR_SHAPE;
+    if (!PRISM_ALIGNED(a, 16) || !PRISM_ALIGNED(qt, 16) || ldo % 4 || !PRISM_ALIGNED(out, epi ? 16 : 8))
+        return PRISM_ERR_ALIGN;
+    if (kernel < -1 || kernel > 1) return PRISM_ERR_ARG;
+    if (kernel == -1) kernel = M <= 64 ? 1 : 0;
+    if (kernel == 1 && M > 64) return PRISM_ERR_ARG;
+    if (M == 0) return PRISM_OK;
+    return launch_w8a8_pc(kernel, true, a, a_s, as_sm, qt, w_s, ws_fp16 != 0, out, ldo, n_rows, (int)M, (int)N,
+                          (int)K, epi, (hipStream_t)stream);
+}

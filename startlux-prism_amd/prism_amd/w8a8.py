@@ -50,6 +50,30 @@ def pack_q8(qs, d):
     return PackedQ8(qt, dt, n, k)
 
 
+class PackedPC(NamedTuple):
+    """Per-channel (gk = K) int8 weights [n, k] in the same MFMA-native chunk layout as PackedQ8.qt (qt int8
+    [n/16, k/64, 64, 16]), with their per-channel scales ws (fp32 [n, 1]).  Made once at load by pack_i8 /
+    weight_from_q8(q8, K); the decode kernels stream it as 1 KB chunks, the tile kernel copies the chunks to LDS."""
+    qt: torch.Tensor
+    ws: torch.Tensor
+    n: int
+    k: int
+
+    @property
+    def shape(self):
+        return (self.n, self.k)
+
+
+def pack_i8(w, ws):
+    """int8 [n, k] and scales [n] / [n, 1] (on the GPU) -> PackedPC (n % 16 == 0, k % 64 == 0)."""
+    n, k = w.shape
+    if w.dtype != torch.int8 or not w.is_contiguous():
+        raise ValueError("pack_i8: w must be contiguous int8 [n, k]")
+    qt = torch.empty(n // 16, k // 64, 64, 16, dtype=torch.int8, device=w.device)
+    L.call("prism_i8_pack", L.ptr(w), L.ptr(qt), n, k, L.stream_of(w))
+    return PackedPC(qt, ws.reshape(n, 1).contiguous(), n, k)
+
+
 class Deferred(NamedTuple):
     """The reference's deferred split-K residual add (kernels/w8a8.py:171-180); never produced here."""
     n: int
@@ -80,6 +104,8 @@ def gemm(a, a_s, w, w_s, out, n_rows, gk, epi=0, outs=None, cfg=None, slots=None
         raise NotImplementedError(f"epilogue {epi}: only 0 (bf16 store) and 1 (fp32 residual add) are provided")
     if isinstance(w, PackedQ8):
         return _gemm_packed(a, a_s, w, out, n_rows, gk, epi, kernel)
+    if isinstance(w, PackedPC):
+        return _gemm_pc_packed(a, a_s, w, out, n_rows, gk, epi, kernel)
     M, K = a.shape
     N = w.shape[0]
     if w.shape[1] != K or a.dtype != torch.int8 or w.dtype != torch.int8:
@@ -119,11 +145,30 @@ def _gemm_packed(a, a_s, w, out, n_rows, gk, epi, kernel):
     return None
 
 
+def _gemm_pc_packed(a, a_s, w, out, n_rows, gk, epi, kernel):
+    M, K = a.shape
+    if gk != K or w.k != K:
+        raise ValueError("packed per-channel weights: gk must equal K and K must match")
+    if a.dtype != torch.int8 or not a.is_contiguous():
+        raise ValueError("a must be contiguous int8 [M, K]")
+    if a_s.dtype != torch.float32 or a_s.shape[0] < M or (a_s.dim() == 2 and a_s.shape[1] != 1):
+        raise ValueError("per-channel kernels take one activation scale per token: a_s [M] or [M, 1]")
+    want = torch.bfloat16 if epi == 0 else torch.float32
+    if out.dtype != want or out.shape[0] < M or out.shape[1] < w.n or out.stride(1) != 1:
+        raise ValueError(f"out must be {want} [>= {M}, >= {w.n}] with unit column stride")
+    if kernel not in ("auto", "tile", "decode"):
+        raise ValueError(f"packed per-channel kernels: auto, tile or decode, not {kernel}")
+    L.call("prism_w8a8_pc_packed_gemm", L.ptr(a), L.ptr(a_s), a_s.stride(0), L.ptr(w.qt), L.ptr(w.ws),
+           int(w.ws.dtype == torch.float16), L.ptr(out), out.stride(0), L.ptr(n_rows), M, w.n, K, epi,
+           KERNELS[kernel], L.stream_of(a))
+    return None
+
+
 def weight_from_q8(q8, gk, smooth=None, packed=True):
     """Q8_0 matrix -> the GEMM's weight operands (kernels/w8a8.py:274-286).  gk == 32 keeps the Q8_0 values: by
     default as PackedQ8 (the MFMA-native layout; returned as (PackedQ8, None)), or with packed=False as the planes
     (int8 [N, K], fp16 [N, K/32]).  Otherwise the weights are requantized per gk inputs as the reference does
-    (int8 [N, K], fp32 [N, K/gk])."""
+    (int8 [N, K], fp32 [N, K/gk]); for gk == K (per channel) on the GPU, by default packed as (PackedPC, None)."""
     if gk == 32 and smooth is None:
         if packed and q8.qs.is_cuda and q8.qs.shape[0] % 16 == 0 and q8.qs.shape[1] % 128 == 0:
             return pack_q8(q8.qs.contiguous(), q8.d.contiguous()), None
@@ -135,4 +180,6 @@ def weight_from_q8(q8, gk, smooth=None, packed=True):
     g = w.view(N, K // gk, gk)
     s = g.abs().amax(-1).clamp_min(1e-10) / 127.0
     q = torch.round(g / s[..., None]).clamp(-127, 127).to(torch.int8).view(N, K)
+    if gk == K and packed and q.is_cuda and N % 16 == 0 and K % 64 == 0:
+        return pack_i8(q.contiguous(), s), None
     return q.contiguous(), s.contiguous()

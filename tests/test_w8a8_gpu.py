@@ -137,7 +137,8 @@ def test_int32_block_sums_exact(dev):
 
 
 @pytest.mark.parametrize("M,N,K,live", [(16, 128, 4096, 16), (200, 256, 5120, 200), (64, 64, 256, 64),
-                                         (300, 528, 1024, 290), (513, 272, 2048, 513), (1, 64, 128, 1)])
+                                         (300, 528, 1024, 290), (513, 272, 2048, 513), (1, 64, 128, 1), (33, 48, 5120, 30),
+                                         (64, 272, 17408, 64)])
 def test_per_channel_gk_equals_k(dev, M, N, K, live):
     """gk = K (the engine's per-channel weights): one epilogue per output, bf16 and residual-add epilogues, live rows,
     ragged tiles in both directions, fp32 and fp16 weight scales."""
@@ -147,17 +148,46 @@ def test_per_channel_gk_equals_k(dev, M, N, K, live):
     sa = (g.random(M) * 1e-2).astype(np.float32)
     sw = (g.random((N, 1)) * 1e-3).astype(np.float32)
     want = O.w8a8_gemm(a, sa, w, sw, K, epi=0, live=live)
-    got = _gemm(dev, a, sa, w, sw, K, 0, "tile", live=live).view(torch.int16).cpu().numpy().view(np.uint16)
-    assert np.array_equal(got[:live], want[:live])
-    assert (got[live:] == 7).all()
     base = g.standard_normal((M, N)).astype(np.float32)
     want1 = O.w8a8_gemm(a, sa, w, sw, K, epi=1, out=base.copy(), live=live)
-    got1 = _gemm(dev, a, sa, w, sw, K, 1, "tile", live=live, out0=base).cpu().numpy()
-    assert np.array_equal(got1, want1)
     sw16 = sw.astype(np.float16)
     want16 = O.w8a8_gemm(a, sa, w, sw16.astype(np.float32), K, epi=0, live=live)
-    got16 = _gemm(dev, a, sa, w, sw16, K, 0, "tile", live=live).view(torch.int16).cpu().numpy().view(np.uint16)
-    assert np.array_equal(got16[:live], want16[:live])
+    for kernel in ["tile"] + (["decode"] if M <= 64 else []):
+        got = _gemm(dev, a, sa, w, sw, K, 0, kernel, live=live).view(torch.int16).cpu().numpy().view(np.uint16)
+        assert np.array_equal(got[:live], want[:live]), kernel
+        assert (got[live:] == 7).all(), kernel
+        got1 = _gemm(dev, a, sa, w, sw, K, 1, kernel, live=live, out0=base).cpu().numpy()
+        assert np.array_equal(got1, want1), kernel
+        got16 = _gemm(dev, a, sa, w, sw16, K, 0, kernel, live=live).view(torch.int16).cpu().numpy().view(np.uint16)
+        assert np.array_equal(got16[:live], want16[:live]), kernel
+    # the packed per-channel layout (weight_from_q8's gk = K operand): same bits from both kernels
+    from prism_amd import w8a8 as KW
+    pw = KW.pack_i8(_t(w, dev), _t(sw, dev))
+    for kernel in ["tile"] + (["decode"] if M <= 64 else []):
+        out = torch.full((M, N), 7, dtype=torch.int16, device=dev).view(torch.bfloat16)
+        KW.gemm(_t(a, dev), _t(sa, dev), pw, None, out, _live(live, dev), K, epi=0, kernel=kernel)
+        o1 = _t(base, dev).clone()
+        KW.gemm(_t(a, dev), _t(sa, dev), pw, None, o1, _live(live, dev), K, epi=1, kernel=kernel)
+        torch.cuda.synchronize()
+        got = out.view(torch.int16).cpu().numpy().view(np.uint16)
+        assert np.array_equal(got[:live], want[:live]), ("packed", kernel)
+        assert np.array_equal(o1.cpu().numpy(), want1), ("packed", kernel)
+
+
+def test_pack_i8_layout(dev):
+    """prism_i8_pack is prism_q8_0_pack's chunk permutation: lane slot l of chunk (t, j) holds row 16 t + l % 16,
+    inputs 64 j + 8 q .. +8 then 64 j + 32 + 8 q .. +8 (q = l / 16)."""
+    from prism_amd import w8a8 as KW
+    N, K = 32, 256
+    w = rng(4).integers(-127, 128, (N, K), dtype=np.int8)
+    pw = KW.pack_i8(_t(w, dev), torch.ones(N, device=dev))
+    torch.cuda.synchronize()
+    qt = pw.qt.cpu().numpy()
+    for t, j, l in [(0, 0, 0), (1, 3, 63), (0, 2, 17), (1, 1, 40)]:
+        r, q = l % 16, l // 16
+        want = np.concatenate([w[16 * t + r, 64 * j + 8 * q:64 * j + 8 * q + 8],
+                               w[16 * t + r, 64 * j + 32 + 8 * q:64 * j + 32 + 8 * q + 8]])
+        assert np.array_equal(qt[t, j, l], want)
 
 
 def test_repeat_runs_identical(dev):
