@@ -13,7 +13,8 @@ int8 MFMA peak (5.0 POPS).
 Also measured (key "configs", not the headline; GEMM kernels alone, graph-replayed): config 0 (Q8_0, M = 16,
 K = N = 4096) and config 2 (Q8_0 decode, M in 1, 4, 16, 64; (K, N) = (5120, 5120), (17408, 5120)) as GB/s of packed
 Q8_0 weight bytes; config 3 (Q4_K W4A8, M = 16 and 2048) and config 4 (MXFP4, M = 16 and 4096), each against its
-roof (HBM for the decode sizes, the int8 or fp8 MFMA peak for the prefill sizes).  Memory-bound shapes rotate weight
+roof (HBM for the decode sizes, the int8 or fp8 MFMA peak for the prefill sizes); and the engine's per-channel
+(gk = K) projections at config 1's shape and config 2's decode sizes.  Memory-bound shapes rotate weight
 copies through more than 3 x the 256 MB MALL so that every launch streams its weights from HBM.
 
 cpu_baseline: the CPU oracle (oracle/, the exact restatement of the reference's arithmetic, OpenMP) on a bounded
@@ -224,8 +225,41 @@ def bench_mxfp4(dev, iters=40):
     return rows
 
 
+def bench_per_channel(dev, iters=40):
+    """The engine's per-channel (gk = K) W8A8 projections, SURVEY's first "next" row: packed int8 weights
+    (weight_from_q8(q8, K)), one activation scale per token; prefill at config 1's shape (against the int8 MFMA peak)
+    and the decode sizes of config 2 (GB/s of the int8 weight bytes)."""
+    import torch
+    from prism_amd import gguf_formats as GF
+    from prism_amd import w8a8 as KW
+    rows = []
+    for (M, K, N) in ((M1, K1, N1), (1, 5120, 5120), (16, 5120, 5120), (64, 5120, 5120), (1, 17408, 5120),
+                      (16, 17408, 5120), (64, 17408, 5120)):
+        g = torch.Generator(device=dev)
+        g.manual_seed(9)
+        q8 = GF.quantize_q8_0(torch.randn(N, K, generator=g, device=dev) * 0.02)
+        base, _ = KW.weight_from_q8(q8, K)
+        del q8
+        wbytes = N * K
+        copies = _copies(wbytes, M)
+        ws = [base] + [KW.PackedPC(base.qt.clone(), base.ws, N, K) for _ in range(copies - 1)]
+        x = make_acts(M, K, 10, dev)
+        from prism_amd import quant as KQ
+        q = torch.empty(M, K, dtype=torch.int8, device=dev)
+        s = torch.empty(M, dtype=torch.float32, device=dev)
+        n = torch.tensor([M], dtype=torch.int32, device=dev)
+        KQ.rows_q8(x, None, q, s, n, M)
+        out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+        us = _graph_us(lambda i: KW.gemm(q, s, ws[i], None, out, n, K), copies, iters if M <= 64 else 3)
+        rows.append(_row(M, K, N, us, wbytes, "hbm" if M <= 64 else "mfma", PEAK_INT8_TOPS))
+        del ws, base, out, x, q
+        torch.cuda.empty_cache()
+    return rows
+
+
 def bench_configs(dev):
     return {
+        "per_channel": bench_per_channel(dev),
         "c0": bench_q8_decode(dev, [(4096, 4096)], (16,)),
         "c2": bench_q8_decode(dev, [(5120, 5120), (17408, 5120)], (1, 4, 16, 64)),
         "c3": bench_w4a8(dev),
