@@ -195,22 +195,24 @@ __global__ __launch_bounds__(NW * 64) void w8a8_packed_decode_kernel(const int8_
         }
     };
 
-    // prologue: round 0 staged in LDS buffer 0, round 1's staged operands in registers, weights of rounds 0 .. D-2
+    // prologue: round 0 staged in LDS buffer 0; rounds 1 .. D's scales and activations in the register ring sg
+    // (round q in slot q % D, loaded D rounds before it is stored); weights of rounds 0 .. D-2
     v4i wr[D][CP];
-    Staged sg;
+    Staged sg[D];
 #pragma unroll
     for (int d = 0; d < D - 1; d++) load_w(d, wr[d]);
-    stage_load(0, sg);
-    stage_store(sg, 0);
-    stage_load(1, sg);
+    stage_load(0, sg[0]);
+    stage_store(sg[0], 0);
+#pragma unroll
+    for (int d = 1; d <= D; d++) stage_load(d, sg[d % D]);
     lds_barrier();
     for (int r0 = 0; r0 < nr; r0 += D) {
 #pragma unroll
         for (int d = 0; d < D; d++) {
             const int r = r0 + d;
             load_w(r + D - 1, wr[(d + D - 1) % D]);        // past the end: the last chunk again (a cache hit)
-            stage_store(sg, (r + 1) & 1);                   // round r + 1's scales and activations
-            stage_load(r + 2, sg);
+            stage_store(sg[(d + 1) % D], (r + 1) & 1);      // round r + 1's scales and activations
+            stage_load(r + 1 + D, sg[(d + 1) % D]);         // the slot's next round
             if (r < nr) compute(r, wr[d], r & 1);
             if (r >= 1 && r <= nr) fold(r - 1);
             lds_barrier();
