@@ -154,6 +154,29 @@ PRISM_API int prism_w4a8_q4k_gemm(const int8_t* xq, const float* a, int64_t a_sb
                                   const uint8_t* meta, void* out, int64_t ldo, const int32_t* n_rows, int64_t M,
                                   int64_t N, int64_t K, int epi, int kernel, void* stream);
 
+/* -------------------------------------------------------------------------------------- fused producers */
+/*
+ * RMSNorm producer: y = RN(RN(h * r) * w), r = RN(1 / RN(sqrt(RN(RN(ss / HID) + eps)))), ss the sum of RN(h * h) in
+ * a fixed order (a 256-thread workgroup's: each thread its inputs 8 (t + 256 c) + j in increasing order, the 64 lanes
+ * of a wave by halving, the four waves left to right).  Replaces kernels/quant.py:418-431 (norm_q8, back 0: q int8
+ * [M, HID] and s fp32 [M]) and :395-397 (norm_g, back 1: q, s [HID/256, M], xs [HID/256, M, 16] as
+ * prism_quant_rows_g; back 2: one scale per row, s [M]).  h fp32 rows of stride ldh; output row i reads input row
+ * rows[i] when rows is not null.  Rows >= *n_rows are not written.  Needs HID % 8 == 0 (% 256 for backs 1, 2).
+ */
+PRISM_API int prism_norm_quant(const float* h, int64_t ldh, const float* w, const int32_t* rows, int8_t* q, float* s,
+                               int8_t* xs, const int32_t* n_rows, int64_t M, int64_t HID, float eps, int back,
+                               void* stream);
+
+/*
+ * SwiGLU producer: y = RN(RN(silu(g) * u) * inv_s) with silu(g) = RN(g / RN(1 + exp(-g))) (exp: Cody-Waite
+ * reduction and a degree-7 Taylor series in fp32 fmas, this library's own).  gu [M, 2 FF] bf16 (fp32 when gu_f32),
+ * row stride ldg, gate = columns 0 .. FF-1, up = FF .. 2 FF - 1; inv_s fp32 [FF] or null.  Replaces
+ * kernels/quant.py:472-478 (swiglu_q8, back 0) and :403-406 (swiglu_g, back 1; back 2 one scale per row), outputs as
+ * prism_norm_quant.  Needs FF % 8 == 0 (% 256 for backs 1, 2).
+ */
+PRISM_API int prism_swiglu_quant(const void* gu, int gu_f32, int64_t ldg, const float* inv_s, int8_t* q, float* s,
+                                 int8_t* xs, const int32_t* n_rows, int64_t M, int64_t FF, int back, void* stream);
+
 /* ------------------------------------------------------------------------------------------------ MXFP4 */
 /* Element formats of MX operands (the MFMA format codes): e4m3 (OCP float8_e4m3fn) and e2m1 (fp4). */
 enum { PRISM_MX_E4M3 = 0, PRISM_MX_E2M1 = 4 };

@@ -23,6 +23,13 @@ Pinning (each function is checked by tests/test_oracle.py against something othe
   mx_pack (ocp), quant_act   scale exponents from numpy's log2 on the same values; e4m3 codes against torch's
                              float8_e4m3fn conversion over every representable input class
   mx_gemm                    float64 dot products against numpy's matmul of independently decoded operands
+  expf                       within 2 ulp of float64 exp over the whole range, exact at 0, inf / 0 at the ends
+  norm_quant, swiglu_quant   y within a few ulp of the float64 formulas; the quantized outputs equal the row / group
+                             quantizers (quant_rows_i8, quant_rows_g) applied to the oracle's own y; the fixed-order
+                             sum of squares against math.fsum within its error bound and against a hand-built case
+                             whose result depends on the order
+  Parity unpinned against the reference's bits for these producers: the reference computes rsqrt, exp and '/' with
+  NVIDIA's approximate instructions in Triton's reduction order, so no specification of its bits exists.
 Parity unpinned: none of the above is checked against the reference's own numbers, because the reference holds
 no numeric fixtures for this path (its GEMM tests compare GPU kernels with each other on CUDA-seeded inputs).
 """
@@ -68,6 +75,11 @@ def lib():
             "orc_w4a8_gemm": (None, [_p, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, ctypes.c_int, _p,
                                      _i64, _i64, _p, _p, ctypes.c_int]),
             "orc_fmaf": (ctypes.c_double, [ctypes.c_float, ctypes.c_float, ctypes.c_float]),
+            "orc_expf": (ctypes.c_float, [ctypes.c_float]),
+            "orc_sumsq_fixed": (ctypes.c_float, [_p, _i64]),
+            "orc_norm_quant": (None, [_p, _i64, _p, _p, _i64, ctypes.c_float, ctypes.c_int, _i64, _p, _p, _p,
+                                      ctypes.c_int]),
+            "orc_swiglu_quant": (None, [_p, _i64, _p, _i64, ctypes.c_int, _i64, _p, _p, _p, ctypes.c_int]),
             "orc_e2m1_value": (ctypes.c_float, [ctypes.c_int]),
             "orc_e4m3_value": (ctypes.c_float, [ctypes.c_int]),
             "orc_e4m3_code": (ctypes.c_int, [ctypes.c_float]),
@@ -311,3 +323,48 @@ def mx_gemm(aq, a_s, wq, ws, fmt=None, nthreads=0):
     lib().orc_mx_gemm(aq.ctypes.data, a_s.ctypes.data, MX_FMT[fmt], wq.ctypes.data, ws.ctypes.data, M, N, K,
                       y.ctypes.data, ya.ctypes.data, nthreads)
     return y, ya
+
+
+# ------------------------------------------------------------------------------------------ fused producers
+BACKS = {"q8": 0, "g256": 1, "grow": 2}
+
+
+def expf(x):
+    return float(lib().orc_expf(float(x)))
+
+
+def sumsq_fixed(y):
+    y = np.ascontiguousarray(y, np.float32)
+    return float(lib().orc_sumsq_fixed(y.ctypes.data, y.shape[0]))
+
+
+def _outs(M, K, back):
+    q = np.zeros((M, K), np.int8)
+    if back == "q8":
+        return q, np.zeros(M, np.float32), None
+    s = np.zeros((K // 256, M) if back == "g256" else M, np.float32)
+    return q, s, np.zeros((K // 256, M, 16), np.int8)
+
+
+def norm_quant(h, w, eps, back="q8", rows=None, live=None, nthreads=0):
+    """h fp32 [*, HID], w fp32 [HID] -> (q, s[, xs]) of rmsnorm(h) * w (kernels/quant.py:144-170, :354-366)."""
+    h = np.ascontiguousarray(h, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    M = h.shape[0] if rows is None else len(rows)
+    HID = h.shape[1]
+    rows = None if rows is None else np.ascontiguousarray(rows, np.int32)
+    q, s, xs = _outs(M, HID, back)
+    lib().orc_norm_quant(h.ctypes.data, HID, w.ctypes.data, _ptr(rows), M, float(eps), BACKS[back],
+                         M if live is None else live, q.ctypes.data, s.ctypes.data, _ptr(xs), nthreads)
+    return (q, s) if xs is None else (q, s, xs)
+
+
+def swiglu_quant(gu, inv_s=None, back="q8", live=None, nthreads=0):
+    """gu fp32 [M, 2 FF] -> (q, s[, xs]) of silu(gate) * up (* inv_s) (kernels/quant.py:249-280, :384-393)."""
+    gu = np.ascontiguousarray(gu, np.float32)
+    M, FF = gu.shape[0], gu.shape[1] // 2
+    inv_s = None if inv_s is None else np.ascontiguousarray(inv_s, np.float32)
+    q, s, xs = _outs(M, FF, back)
+    lib().orc_swiglu_quant(gu.ctypes.data, FF, _ptr(inv_s), M, BACKS[back], M if live is None else live,
+                           q.ctypes.data, s.ctypes.data, _ptr(xs), nthreads)
+    return (q, s) if xs is None else (q, s, xs)

@@ -563,3 +563,110 @@ EXPORT void orc_mx_gemm(const uint8_t* aq, const uint8_t* as, int fmt, const uin
     }
     free(wv);
 }
+
+/* ------------------------------------------------------------------------------------------ fused producers */
+/* kernels/quant.py:144-170 (norm_q8), :249-280 (swiglu_q8), :354-366 / :384-393 (norm_g, swiglu_g), storing as
+ * :287-309 (one scale per row) or _store_g :314-330 (per 256 inputs, or one per row, plus split per-32 sums).
+ * The reference evaluates rsqrt, exp and '/' with NVIDIA's approximate instructions in Triton's reduction order; this
+ * build defines them exactly (the GPU library does the same steps):
+ *   exp(x):  n = rint(RN(x log2 e)), r = fma(-n, LN2_HI, x), r = fma(-n, LN2_LO, r) (Cody-Waite), Taylor series of
+ *            e^r to degree 7 by Horner with fma, times 2^n (ldexp);
+ *   rmsnorm: the sum of RN(h*h) over a row in the order of a 256-thread workgroup - thread t adds inputs
+ *            8 (t + 256 c) + j (c, then j increasing), the 64 threads of each wave combine by halving, the four wave
+ *            sums left to right; r = RN(1 / RN(sqrt(RN(RN(ss / HID) + eps)))), y = RN(RN(h r) w);
+ *   silu:    RN(g / RN(1 + exp(-g))), y = RN(RN(silu(g) u) inv_s). */
+EXPORT float orc_expf(float x) {
+    if (x > 88.72283935546875f) return INFINITY;
+    if (x < -103.97208404541016f) return 0.f;
+    const float n = rintf(x * 1.44269502162933349609375f);
+    float r = fmaf(-n, 0.693145751953125f, x);
+    r = fmaf(-n, 1.428606765330187045e-06f, r);
+    float p = 1.98412701e-04f;
+    p = fmaf(p, r, 1.38888892e-03f);
+    p = fmaf(p, r, 8.33333377e-03f);
+    p = fmaf(p, r, 4.16666679e-02f);
+    p = fmaf(p, r, 1.66666672e-01f);
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    return ldexpf(p, (int)n);
+}
+
+/* the workgroup's fixed-order sum of squares of y[0..K) */
+EXPORT float orc_sumsq_fixed(const float* y, int64_t K) {
+    float part[256];
+    const int64_t nch = K / 8;
+    for (int t = 0; t < 256; t++) {
+        float acc = 0.f;
+        for (int64_t idx = t; idx < nch; idx += 256)
+            for (int j = 0; j < 8; j++) {
+                const float v = y[idx * 8 + j];
+                acc = acc + v * v;
+            }
+        part[t] = acc;
+    }
+    float wsum[4];
+    for (int w = 0; w < 4; w++) {
+        float a[64];
+        for (int l = 0; l < 64; l++) a[l] = part[64 * w + l];
+        for (int o = 32; o > 0; o >>= 1)
+            for (int l = 0; l < o; l++) a[l] = a[l] + a[l + o];
+        wsum[w] = a[0];
+    }
+    return ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
+}
+
+/* y [K] -> back 0: q int8 [K] at row, s[row]; back 1: q, a [K/256, M] at (b, row), xs [K/256, M, 16]; back 2: one
+ * scale per row in a[row]. */
+static void store_back_row(const float* y, int64_t K, int back, int64_t M, int64_t row, int8_t* q, float* s,
+                           int8_t* xs) {
+    const int64_t G = back == 1 ? 256 : K;
+    for (int64_t g0 = 0; g0 < K; g0 += G) {
+        float amax = 0.f;
+        for (int64_t k = g0; k < g0 + G; k++) amax = fmaxf(amax, fabsf(y[k]));
+        const float scale = fmaxf(amax, 1e-10f) / 127.0f;
+        for (int64_t k = g0; k < g0 + G; k++) q[row * K + k] = (int8_t)(int)rintf(y[k] / scale);
+        if (back == 1) s[(g0 / 256) * M + row] = scale;
+        else s[row] = scale;
+    }
+    if (back != 0)
+        for (int64_t sb = 0; sb < K / 32; sb++) {
+            int sum = 0;
+            for (int k = 0; k < 32; k++) sum += q[row * K + sb * 32 + k];
+            xs[((sb / 8) * M + row) * 16 + sb % 8] = (int8_t)(sum & 63);
+            xs[((sb / 8) * M + row) * 16 + 8 + sb % 8] = (int8_t)(sum >> 6);
+        }
+}
+
+EXPORT void orc_norm_quant(const float* h, int64_t HID, const float* w, const int32_t* rows, int64_t M, float eps,
+                           int back, int64_t live, int8_t* q, float* s, int8_t* xs, int nthreads) {
+    const int64_t n = live < M ? live : M;
+#pragma omp parallel for num_threads(nthreads_or(nthreads)) schedule(static)
+    for (int64_t i = 0; i < n; i++) {
+        const float* hr = h + (rows ? (int64_t)rows[i] : i) * HID;
+        float* y = (float*)malloc(sizeof(float) * HID);
+        const float ss = orc_sumsq_fixed(hr, HID);
+        const float r = 1.0f / sqrtf(ss / (float)HID + eps);
+        for (int64_t k = 0; k < HID; k++) y[k] = (hr[k] * r) * w[k];
+        store_back_row(y, HID, back, M, i, q, s, xs);
+        free(y);
+    }
+}
+
+/* gu fp32 [M, 2 FF] (bf16 inputs widened exactly) */
+EXPORT void orc_swiglu_quant(const float* gu, int64_t FF, const float* inv_s, int64_t M, int back, int64_t live,
+                             int8_t* q, float* s, int8_t* xs, int nthreads) {
+    const int64_t n = live < M ? live : M;
+#pragma omp parallel for num_threads(nthreads_or(nthreads)) schedule(static)
+    for (int64_t i = 0; i < n; i++) {
+        float* y = (float*)malloc(sizeof(float) * FF);
+        for (int64_t k = 0; k < FF; k++) {
+            const float g = gu[i * 2 * FF + k], u = gu[i * 2 * FF + FF + k];
+            float v = (g / (1.0f + orc_expf(-g))) * u;
+            if (inv_s) v = v * inv_s[k];
+            y[k] = v;
+        }
+        store_back_row(y, FF, back, M, i, q, s, xs);
+        free(y);
+    }
+}

@@ -37,6 +37,10 @@ __device__ __forceinline__ float f16_to_f32(uint32_t h) {
 // so '/' is the IEEE operation, written through one helper so every kernel rounds alike.
 __device__ __forceinline__ float div_rn(float a, float b) { return __fdiv_rn(a, b); }
 
+// Correctly rounded fp32 square root.  sqrtf under -fhip-fp32-correctly-rounded-divide-sqrt expands to the refined
+// sequence; __fsqrt_rn on this toolchain is the bare v_sqrt_f32 (about 1 ulp), so it is not used.
+__device__ __forceinline__ float sqrt_rn(float a) { return sqrtf(a); }
+
 // Explicitly rounded fp32 multiply / add: the compiler never contracts these into an fma.
 __device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
 __device__ __forceinline__ float add_rn(float a, float b) { return __fadd_rn(a, b); }

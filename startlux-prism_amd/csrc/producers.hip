@@ -1,0 +1,306 @@
+// Fused activation producers (gfx950): the kernels that sit between the engine's GEMMs and write their int8 inputs.
+// Restates kernels/quant.py (StartLux-Prism):
+//   norm_q8    :144-170, :418-431   y = rmsnorm(h) * w          -> int8 rows, one scale per row
+//   swiglu_q8  :249-280, :472-478   y = silu(gate) * up * inv_s -> int8 rows, one scale per row
+//   norm_g     :354-366, :395-397   y = rmsnorm(h) * w          -> W4A8 operands (_store_g, :314-330)
+//   swiglu_g   :384-393, :403-406   y = silu(gate) * up         -> W4A8 operands
+// One workgroup (256 threads) per row; thread t owns the 8-input chunks t, t + 256, ... and keeps them in registers
+// between the row reductions and the stores, so a row is read once.
+//
+// Arithmetic (every step an IEEE fp32 operation, so the CPU oracle reproduces the bits):
+//   rmsnorm: ss = sum of RN(h * h) in a fixed order - each thread adds its own inputs in increasing index, the 64
+//            lanes of a wave combine by halving (lane l + lane l + 32, then + 16, ...), the four waves left to right;
+//            r = RN(1 / RN(sqrt(RN(RN(ss / HID) + eps)))); y = RN(RN(h * r) * w).
+//   silu:    RN(g / RN(1 + exp(-g))), with exp this library's own (prism_expf below).
+//   quantization as the row quantizers: scale = RN(max(amax, 1e-10) / 127), q = rint(RN(y / scale)).
+// The reference evaluates rsqrt, exp and '/' with NVIDIA's approximate instructions and sums in Triton's reduction
+// order, neither of which has a specification; these kernels define the operations exactly instead.
+#include <type_traits>
+
+#include "common.h"
+
+namespace prism {
+
+constexpr int kPThreads = 256;
+
+// e^x in fp32: x = n ln2 + r with n = rint(x log2 e) and r reduced by the two-constant method of Cody and Waite
+// (ln2 = LN2_HI + LN2_LO, LN2_HI with 9 trailing zero bits so n LN2_HI is exact for |n| < 2^9), e^r by its Taylor
+// series to degree 7 evaluated with fmas (|r| <= 0.3466: truncation below 2^-27 relative), then scaled by 2^n.
+__device__ __forceinline__ float prism_expf(float x) {
+    if (x > 88.72283935546875f) return __uint_as_float(0x7f800000u);
+    if (x < -103.97208404541016f) return 0.f;
+    const float n = rintf(mul_rn(x, 1.44269502162933349609375f));
+    float r = fmaf(-n, 0.693145751953125f, x);
+    r = fmaf(-n, 1.428606765330187045e-06f, r);
+    float p = 1.98412701e-04f;                  // 1/5040
+    p = fmaf(p, r, 1.38888892e-03f);            // 1/720
+    p = fmaf(p, r, 8.33333377e-03f);            // 1/120
+    p = fmaf(p, r, 4.16666679e-02f);            // 1/24
+    p = fmaf(p, r, 1.66666672e-01f);            // 1/6
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    return ldexpf(p, (int)n);
+}
+
+__device__ __forceinline__ float silu_rn(float g) { return div_rn(g, add_rn(1.0f, prism_expf(-g))); }
+
+__device__ __forceinline__ uint32_t pack4_i8(const float* f) {
+    uint32_t r = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) r |= ((uint32_t)(int)f[j] & 0xffu) << (8 * j);
+    return r;
+}
+
+// Row reductions over the workgroup: the maximum (exact in any order) and the fixed-order sum of the module comment.
+__device__ __forceinline__ float row_max(float v, float* red) {
+    v = wave_max(v);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    const float r = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    return r;
+}
+
+__device__ __forceinline__ float row_sum_fixed(float v, float* red) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = add_rn(v, __shfl_xor(v, o, kWave));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    const float r = add_rn(add_rn(add_rn(red[0], red[1]), red[2]), red[3]);
+    __syncthreads();
+    return r;
+}
+
+// Back ends.  BACK 0: int8 row + one scale per row (q [M, K], s [M]).  BACK 1: the W4A8 operands with one scale
+// per 256 inputs (xq [M, K], a [K/256, M], xs [K/256, M, 16]); BACK 2: the same with one scale per row (a [M]).
+template <int NCH, int BACK>
+__device__ __forceinline__ void store_back(float (&y)[NCH][8], float rmax, float* red, int64_t row, int out_row,
+                                           int M, int K, int8_t* __restrict__ q, float* __restrict__ s,
+                                           int8_t* __restrict__ xs) {
+    const int nch = K / 8;
+    if (BACK == 0 || BACK == 2) rmax = row_max(rmax, red);
+    v2u* qr = reinterpret_cast<v2u*>(q + (int64_t)out_row * K);
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+        const int idx = threadIdx.x + c * kPThreads;
+        float gmax = rmax;
+        if (BACK == 1) {                     // the 32 chunks of a group of 256 are the lanes of a half-wave
+            float m = 0.f;
+            if (idx < nch) {
+#pragma unroll
+                for (int j = 0; j < 8; j++) m = fmaxf(m, fabsf(y[c][j]));
+            }
+#pragma unroll
+            for (int o = 16; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, kWave));
+            gmax = m;
+        }
+        const float scale = div_rn(fmaxf(gmax, 1e-10f), 127.0f);
+        int sum = 0;
+        if (idx < nch) {
+            float r[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                r[j] = rintf(div_rn(y[c][j], scale));
+                sum += (int)r[j];
+            }
+            qr[idx] = v2u{pack4_i8(r), pack4_i8(r + 4)};
+        }
+        if (BACK != 0) {
+            sum = wave_sum_width(sum, 4);    // the 4 chunks of a sub-block of 32 are neighbouring lanes
+            if (idx < nch) {
+                const int b = idx / 32, j = (idx % 32) / 4;
+                if ((idx % 4) == 0) {
+                    int8_t* p = xs + ((int64_t)b * M + out_row) * 16;
+                    p[j] = (int8_t)(sum & 63);
+                    p[8 + j] = (int8_t)(sum >> 6);
+                }
+                if (BACK == 1 && (idx % 32) == 0) s[(int64_t)b * M + out_row] = scale;
+            }
+        }
+    }
+    if (threadIdx.x == 0) {
+        if (BACK == 0) s[out_row] = div_rn(fmaxf(rmax, 1e-10f), 127.0f);
+        if (BACK == 2) s[out_row] = div_rn(fmaxf(rmax, 1e-10f), 127.0f);
+    }
+    (void)row;
+}
+
+// ---------------------------------------------------------------------------------------------- rmsnorm
+// h fp32 [*, HID] (row stride ldh), w fp32 [HID]; output row i from input row rows[i] when rows is not null.
+template <int NCH, int BACK>
+__global__ __launch_bounds__(kPThreads) void norm_prod_kernel(const float* __restrict__ h, int64_t ldh,
+                                                              const float* __restrict__ w,
+                                                              const int32_t* __restrict__ rows, int8_t* __restrict__ q,
+                                                              float* __restrict__ s, int8_t* __restrict__ xs,
+                                                              const int32_t* __restrict__ n_rows, int M, int HID,
+                                                              float eps) {
+    __shared__ float red[4];
+    const int i = blockIdx.x;
+    if (i >= __ldg(n_rows)) return;
+    const int64_t src = rows ? (int64_t)__ldg(rows + i) : i;
+    const int nch = HID / 8;
+    const v4f* hr = reinterpret_cast<const v4f*>(h + src * ldh);
+    const v4f* wr = reinterpret_cast<const v4f*>(w);
+    float y[NCH][8];
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+        const int idx = threadIdx.x + c * kPThreads;
+        if (idx < nch) {
+            const v4f a = __builtin_nontemporal_load(hr + 2 * idx), b = __builtin_nontemporal_load(hr + 2 * idx + 1);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                y[c][j] = a[j];
+                y[c][j + 4] = b[j];
+            }
+#pragma unroll
+            for (int j = 0; j < 8; j++) ss = add_rn(ss, mul_rn(y[c][j], y[c][j]));
+        }
+    }
+    ss = row_sum_fixed(ss, red);
+    const float r = div_rn(1.0f, sqrt_rn(add_rn(div_rn(ss, (float)HID), eps)));
+    float amax = 0.f;
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+        const int idx = threadIdx.x + c * kPThreads;
+        if (idx < nch) {
+            const v4f a = wr[2 * idx], b = wr[2 * idx + 1];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                y[c][j] = mul_rn(mul_rn(y[c][j], r), a[j]);
+                y[c][j + 4] = mul_rn(mul_rn(y[c][j + 4], r), b[j]);
+            }
+#pragma unroll
+            for (int j = 0; j < 8; j++) amax = fmaxf(amax, fabsf(y[c][j]));
+        }
+    }
+    store_back<NCH, BACK>(y, amax, red, src, i, M, HID, q, s, xs);
+}
+
+// ---------------------------------------------------------------------------------------------- SwiGLU
+// gu [*, 2 FF] (bf16, or fp32 when GU32; row stride ldg): gate = columns 0 .. FF-1, up = FF .. 2 FF - 1; inv_s fp32
+// [FF] or null.
+template <int NCH, int BACK, bool GU32>
+__global__ __launch_bounds__(kPThreads) void swiglu_prod_kernel(const void* __restrict__ gu, int64_t ldg,
+                                                                const float* __restrict__ inv_s,
+                                                                int8_t* __restrict__ q, float* __restrict__ s,
+                                                                int8_t* __restrict__ xs,
+                                                                const int32_t* __restrict__ n_rows, int M, int FF) {
+    __shared__ float red[4];
+    const int i = blockIdx.x;
+    if (i >= __ldg(n_rows)) return;
+    const int nch = FF / 8;
+    float y[NCH][8];
+    float amax = 0.f;
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+        const int idx = threadIdx.x + c * kPThreads;
+        if (idx < nch) {
+            float g[8], u[8];
+            if (GU32) {
+                const v4f* row = reinterpret_cast<const v4f*>(static_cast<const float*>(gu) + (int64_t)i * ldg);
+                const v4f g0 = row[2 * idx], g1 = row[2 * idx + 1];
+                const v4f u0 = row[FF / 4 + 2 * idx], u1 = row[FF / 4 + 2 * idx + 1];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    g[j] = g0[j]; g[j + 4] = g1[j];
+                    u[j] = u0[j]; u[j + 4] = u1[j];
+                }
+            } else {
+                const v4u* row = reinterpret_cast<const v4u*>(static_cast<const uint16_t*>(gu) + (int64_t)i * ldg);
+                const v4u gv = row[idx], uv = row[FF / 8 + idx];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    g[2 * j] = __uint_as_float(gv[j] << 16);
+                    g[2 * j + 1] = __uint_as_float(gv[j] & 0xffff0000u);
+                    u[2 * j] = __uint_as_float(uv[j] << 16);
+                    u[2 * j + 1] = __uint_as_float(uv[j] & 0xffff0000u);
+                }
+            }
+            float is[8];
+            if (inv_s) {
+                const v4f a = reinterpret_cast<const v4f*>(inv_s)[2 * idx], b = reinterpret_cast<const v4f*>(inv_s)[2 * idx + 1];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    is[j] = a[j];
+                    is[j + 4] = b[j];
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                float v = mul_rn(silu_rn(g[j]), u[j]);
+                if (inv_s) v = mul_rn(v, is[j]);
+                y[c][j] = v;
+                amax = fmaxf(amax, fabsf(v));
+            }
+        }
+    }
+    store_back<NCH, BACK>(y, amax, red, i, i, M, FF, q, s, xs);
+}
+
+template <typename KN>
+static int pick_nch(int K, KN&& launch) {
+    const int need = (K / 8 + kPThreads - 1) / kPThreads;
+    if (need <= 1) return launch(std::integral_constant<int, 1>{});
+    if (need <= 2) return launch(std::integral_constant<int, 2>{});
+    if (need <= 3) return launch(std::integral_constant<int, 3>{});
+    if (need <= 4) return launch(std::integral_constant<int, 4>{});
+    if (need <= 6) return launch(std::integral_constant<int, 6>{});
+    if (need <= 9) return launch(std::integral_constant<int, 9>{});
+    if (need <= 12) return launch(std::integral_constant<int, 12>{});
+    return launch(std::integral_constant<int, 16>{});
+}
+
+}  // namespace prism
+
+using namespace prism;
+
+// back: 0 int8 + row scale; 1 W4A8 operands, scale per 256; 2 W4A8 operands, one scale per row.
+extern "C" int prism_norm_quant(const float* h, int64_t ldh, const float* w, const int32_t* rows, int8_t* q, float* s,
+                                int8_t* xs, const int32_t* n_rows, int64_t M, int64_t HID, float eps, int back,
+                                void* stream) {
+    if (!h || !w || !q || !s || !n_rows || (back != 0 && !xs)) return PRISM_ERR_ARG;
+    if (back < 0 || back > 2) return PRISM_ERR_ARG;
+    if (M < 0 || HID <= 0 || HID % 8 || ldh < HID || ldh % 8 || HID > 32768 || M > (1 << 30)) return PRISM_ERR_SHAPE;
+    if (back != 0 && HID % 256) return PRISM_ERR_SHAPE;
+    if (!PRISM_ALIGNED(h, 16) || !PRISM_ALIGNED(w, 16) || !PRISM_ALIGNED(q, 8)) return PRISM_ERR_ALIGN;
+    if (M == 0) return PRISM_OK;
+    hipStream_t st = (hipStream_t)stream;
+    return pick_nch((int)HID, [&](auto nc) {
+        constexpr int NC = decltype(nc)::value;
+        if (back == 0)
+            hipLaunchKernelGGL((norm_prod_kernel<NC, 0>), dim3((unsigned)M), dim3(kPThreads), 0, st, h, ldh, w, rows,
+                               q, s, xs, n_rows, (int)M, (int)HID, eps);
+        else if (back == 1)
+            hipLaunchKernelGGL((norm_prod_kernel<NC, 1>), dim3((unsigned)M), dim3(kPThreads), 0, st, h, ldh, w, rows,
+                               q, s, xs, n_rows, (int)M, (int)HID, eps);
+        else
+            hipLaunchKernelGGL((norm_prod_kernel<NC, 2>), dim3((unsigned)M), dim3(kPThreads), 0, st, h, ldh, w, rows,
+                               q, s, xs, n_rows, (int)M, (int)HID, eps);
+        return hipGetLastError() == hipSuccess ? 0 : (int)PRISM_ERR_LAUNCH;
+    });
+}
+
+extern "C" int prism_swiglu_quant(const void* gu, int gu_f32, int64_t ldg, const float* inv_s, int8_t* q, float* s,
+                                  int8_t* xs, const int32_t* n_rows, int64_t M, int64_t FF, int back, void* stream) {
+    if (!gu || !q || !s || !n_rows || (back != 0 && !xs)) return PRISM_ERR_ARG;
+    if (back < 0 || back > 2) return PRISM_ERR_ARG;
+    if (M < 0 || FF <= 0 || FF % 8 || ldg < 2 * FF || FF > 65536 || M > (1 << 30)) return PRISM_ERR_SHAPE;
+    if (back != 0 && FF % 256) return PRISM_ERR_SHAPE;
+    if ((gu_f32 ? ldg % 4 : ldg % 8) || !PRISM_ALIGNED(gu, 16) || !PRISM_ALIGNED(q, 8) ||
+        (inv_s && !PRISM_ALIGNED(inv_s, 16)))
+        return PRISM_ERR_ALIGN;
+    if (gu_f32 && FF % 4) return PRISM_ERR_SHAPE;
+    if (M == 0) return PRISM_OK;
+    hipStream_t st = (hipStream_t)stream;
+    return pick_nch((int)FF, [&](auto nc) {
+        constexpr int NC = decltype(nc)::value;
+#define SW(B, G32) hipLaunchKernelGGL((swiglu_prod_kernel<NC, B, G32>), dim3((unsigned)M), dim3(kPThreads), 0, st, gu, \
+                                      ldg, inv_s, q, s, xs, n_rows, (int)M, (int)FF)
+        if (gu_f32) { if (back == 0) SW(0, true); else if (back == 1) SW(1, true); else SW(2, true); }
+        else { if (back == 0) SW(0, false); else if (back == 1) SW(1, false); else SW(2, false); }
+#undef SW
+        return hipGetLastError() == hipSuccess ? 0 : (int)PRISM_ERR_LAUNCH;
+    });
+}

@@ -62,3 +62,95 @@ def rows_g(x, q, s, xs, n, T, group=256):
     n = _live(n, T, x.device)
     L.call("prism_quant_rows_g", L.ptr(x), x.stride(0), L.ptr(q), L.ptr(s), L.ptr(xs), L.ptr(n), M, K, group,
            L.stream_of(x))
+
+
+# ---------------------------------------------------------------------------------------------- fused producers
+# kernels/quant.py:144-170 / :418-431 (norm_q8), :249-280 / :472-478 (swiglu_q8), :354-366 / :395-397 (norm_g),
+# :384-393 / :403-406 (swiglu_g).  Arithmetic: IEEE fp32 throughout, rsqrt as 1 / sqrt (both correctly rounded),
+# exp this library's own (Cody-Waite reduction, degree-7 Taylor series), the sum of squares in a fixed order; the
+# reference's NVIDIA approximations (rsqrt.approx, ex2.approx, div.full) have no specification to match bit for bit.
+
+def _rows_arg(n, T, dev):
+    return _live(n, T, dev)
+
+
+def norm_q8(h, w_over_s, q, s, n, T, eps, rows=None, parts=None, pending=None):
+    """h fp32 [*, HID] -> q int8 [>=T, HID], s fp32 [>=T]: y = rmsnorm(h) * w_over_s, one scale per row.  rows int32
+    [T] (optional): output row i from input row rows[i].  A deferred residual add (parts / pending) never exists in
+    this build, whose GEMMs do not split K into slots."""
+    if pending:
+        raise NotImplementedError("deferred split-K residual adds are not produced by this build's GEMMs")
+    HID = h.shape[1]
+    if h.dtype != torch.float32 or w_over_s.dtype != torch.float32 or q.dtype != torch.int8 or s.dtype != torch.float32:
+        raise TypeError("norm_q8: h fp32, w fp32, q int8, s fp32")
+    if h.stride(1) != 1 or q.shape[1] != HID or not q.is_contiguous() or w_over_s.numel() != HID:
+        raise ValueError("norm_q8: shape mismatch")
+    if rows is not None and (rows.dtype != torch.int32 or rows.numel() < T):
+        raise ValueError("norm_q8: rows must be int32 [T]")
+    n = _rows_arg(n, T, h.device)
+    L.call("prism_norm_quant", L.ptr(h), h.stride(0), L.ptr(w_over_s.contiguous()), L.ptr(rows), L.ptr(q), L.ptr(s),
+           None, L.ptr(n), T, HID, float(eps), 0, L.stream_of(h))
+
+
+def fold(h, parts, pending, n, T):
+    """Finish a deferred residual add: nothing to do, no GEMM here defers one."""
+    if pending:
+        raise NotImplementedError("deferred split-K residual adds are not produced by this build's GEMMs")
+
+
+def _swiglu(gu, inv_s, q, s, xs, n, T, back):
+    FF = q.shape[1]
+    if gu.dtype not in (torch.bfloat16, torch.float32) or q.dtype != torch.int8 or s.dtype != torch.float32:
+        raise TypeError("swiglu: gu bf16 or fp32, q int8, s fp32")
+    if gu.stride(1) != 1 or gu.shape[1] < 2 * FF or not q.is_contiguous():
+        raise ValueError("swiglu: gu [*, 2 FF] with unit column stride, q [*, FF] contiguous")
+    if inv_s is not None and (inv_s.dtype != torch.float32 or inv_s.numel() != FF):
+        raise ValueError("swiglu: inv_s fp32 [FF]")
+    n = _rows_arg(n, T, gu.device)
+    L.call("prism_swiglu_quant", L.ptr(gu), int(gu.dtype == torch.float32), gu.stride(0),
+           L.ptr(None if inv_s is None else inv_s.contiguous()), L.ptr(q), L.ptr(s), L.ptr(xs), L.ptr(n), T, FF, back,
+           L.stream_of(gu))
+
+
+def swiglu_q8(gu, inv_s, q, s, n, T, mode=0, amax=None, sync=None):
+    """gu [*, 2 FF] (bf16 GEMM output, or fp32) -> q int8 [>=T, FF], s fp32 [>=T]: y = silu(gate) * up * inv_s."""
+    if mode != 0 or sync is not None:
+        raise NotImplementedError("tensor-parallel quantization modes are not part of the single-GPU build")
+    _swiglu(gu, inv_s, q, s, None, n, T, 0)
+
+
+def _g_back(q, s, xs, group):
+    K, M = q.shape[1], xs.shape[1]
+    if xs.dtype != torch.int8 or tuple(xs.shape) != (K // 256, M, 16) or not xs.is_contiguous():
+        raise ValueError("xs must be int8 [K / 256, M, 16]")
+    if group == 256:
+        if tuple(s.shape) != (K // 256, M):
+            raise ValueError("s must be fp32 [K / 256, M]")
+        return 1
+    if group == K:
+        if s.numel() != M:
+            raise ValueError("s must be fp32 [1, M] (one scale per token)")
+        return 2
+    raise ValueError("group must be 256 or K")
+
+
+def norm_g(h, w, q, s, xs, n, T, eps, group=256):
+    """W4A8 producer of rmsnorm(h) * w: q int8 [>=T, HID], s fp32 [HID / group, M], xs int8 [HID / 256, M, 16]."""
+    HID = h.shape[1]
+    if h.dtype != torch.float32 or w.dtype != torch.float32 or h.stride(1) != 1 or q.shape[1] != HID:
+        raise ValueError("norm_g: h fp32 [*, HID] with unit column stride, w fp32 [HID]")
+    back = _g_back(q, s, xs, group)
+    n = _rows_arg(n, T, h.device)
+    L.call("prism_norm_quant", L.ptr(h), h.stride(0), L.ptr(w.contiguous()), None, L.ptr(q), L.ptr(s), L.ptr(xs),
+           L.ptr(n), xs.shape[1], HID, float(eps), back, L.stream_of(h))
+
+
+def swiglu_g(gu, q, s, xs, n, T, group=256):
+    """W4A8 producer of silu(gate) * up: q int8 [>=T, FF], s fp32 [FF / group, M], xs int8 [FF / 256, M, 16]."""
+    back = _g_back(q, s, xs, group)
+    FF = q.shape[1]
+    if gu.dtype not in (torch.bfloat16, torch.float32) or gu.stride(1) != 1 or gu.shape[1] < 2 * FF:
+        raise ValueError("swiglu_g: gu [*, 2 FF] bf16 or fp32")
+    n = _rows_arg(n, T, gu.device)
+    L.call("prism_swiglu_quant", L.ptr(gu), int(gu.dtype == torch.float32), gu.stride(0), None, L.ptr(q), L.ptr(s),
+           L.ptr(xs), L.ptr(n), xs.shape[1], FF, back, L.stream_of(gu))
