@@ -257,8 +257,44 @@ def bench_per_channel(dev, iters=40):
     return rows
 
 
+def bench_producers(dev, iters=20):
+    """The fused producers at config 1's shapes (HBM-bound: GB/s of bytes read plus written): norm_q8 on the fp32
+    residual (T = 8192, HID = 5120) and swiglu_q8 on the bf16 gate|up output (T = 8192, FF = 13824), plus the
+    per-token quantizer rows_q8 of the headline step; and their decode size (T = 16)."""
+    import torch
+    from prism_amd import quant as KQ
+    rows = []
+    for T in (M1, 16):
+        n = torch.tensor([T], dtype=torch.int32, device=dev)
+        h = torch.randn(T, K1, device=dev)
+        w = torch.rand(K1, device=dev) + 0.5
+        q = torch.empty(T, K1, dtype=torch.int8, device=dev)
+        s = torch.empty(T, dtype=torch.float32, device=dev)
+        us = _graph_us(lambda i: KQ.norm_q8(h, w, q, s, n, T, 1e-6), 1, iters)
+        b = T * K1 * 4 + K1 * 4 + T * K1 + 4 * T
+        rows.append(dict(op="norm_q8", T=T, K=K1, us=round(us, 2), GBps=round(b / us / 1e3, 1),
+                         frac=round(b / us / 1e3 / PEAK_HBM_GBS, 3)))
+        FF = N1 // 2
+        gu = torch.randn(T, 2 * FF, device=dev).to(torch.bfloat16)
+        inv = torch.rand(FF, device=dev) + 0.5
+        q2 = torch.empty(T, FF, dtype=torch.int8, device=dev)
+        us = _graph_us(lambda i: KQ.swiglu_q8(gu, inv, q2, s, n, T), 1, iters)
+        b = T * 2 * FF * 2 + FF * 4 + T * FF + 4 * T
+        rows.append(dict(op="swiglu_q8", T=T, K=FF, us=round(us, 2), GBps=round(b / us / 1e3, 1),
+                         frac=round(b / us / 1e3 / PEAK_HBM_GBS, 3)))
+        x = torch.randn(T, K1, device=dev).to(torch.bfloat16)
+        us = _graph_us(lambda i: KQ.rows_q8(x, None, q, s, n, T), 1, iters)
+        b = T * K1 * 2 + T * K1 + 4 * T
+        rows.append(dict(op="rows_q8", T=T, K=K1, us=round(us, 2), GBps=round(b / us / 1e3, 1),
+                         frac=round(b / us / 1e3 / PEAK_HBM_GBS, 3)))
+        del h, gu, x, q, q2
+        torch.cuda.empty_cache()
+    return rows
+
+
 def bench_configs(dev):
     return {
+        "producers": bench_producers(dev),
         "per_channel": bench_per_channel(dev),
         "c0": bench_q8_decode(dev, [(4096, 4096)], (16,)),
         "c2": bench_q8_decode(dev, [(5120, 5120), (17408, 5120)], (1, 4, 16, 64)),
