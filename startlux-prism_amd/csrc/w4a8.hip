@@ -1,8 +1,8 @@
-// W4A8 GEMM on Q4_K weights (gfx950): int8 activations x 4-bit k-quant weights on v_mfma_i32_16x16x32_i8.
+// W4A8 GEMM on Q4_K weights (gfx950): int8 activations x 4-bit k-quant weights on int8 MFMA.
 //
 // Arithmetic (StartLux-Prism kernels/w4a8.py:14-22, gemm_ref :177-199), per output (m, n), super-blocks b of 256
 // inputs in increasing b:
-//   acc  = sum_g sc[n,b,g] (xq . q)_g        int32, exact (P_g from one MFMA per 32-input sub-block)
+//   acc  = sum_g sc[n,b,g] (xq . q)_g        int32, exact (the scales enter the MFMA's weight operand, two_plane)
 //   mins = sum_g mn[n,b,g] S[m, 8b + g]       int32, exact (S: the activation sums per 32 inputs)
 //   t = RN(d[n,b] float(acc));  t = fma(-dmin[n,b], float(mins), t);  y = fma(a[b,m], t, y)
 // then bf16(y) (epi 0) or out = RN(out + y) (epi 1).  y's chain over b is kept in super-block order by every kernel.
@@ -10,9 +10,10 @@
 // Device layout (prism_q4k_pack, made once at load from the GGUF block_q4_K bytes, as the reference's repack is:
 // kernels/w4a8.py:70-94): a byte permutation of the GGUF blocks, 144 bytes per row and super-block.
 //   qv   uint8 [N/16][K/256][2][64][16]: per (16-row tile nt, super-block b) 2 KB.  Half h, lane slot l (row
-//        r = l % 16, q = l / 16), bytes 4 i .. 4 i + 3 hold sub-block g = 4 h + i of row 16 nt + r: byte t of them is
-//        v[4 q + t] | v[16 + 4 q + t] << 4 (v: the sub-block's 32 values in k order).  Unpacked with two masks, the
-//        word is the 8-byte MFMA operand for k = {4 q .. 4 q + 3, 16 + 4 q .. 16 + 4 q + 3} of the sub-block.
+//        r = l % 16, q = l / 16), byte j: pair p = 2 h + j / 8 of sub-blocks, t = j % 8, k0 = 64 p + 16 q + t (input
+//        index in the super-block), the byte is v[k0] | v[k0 + 8] << 4 for row 16 nt + r.  A lane's 8 bytes of pair
+//        p unpack with two masks into the 16-byte MFMA operand for inputs 64 p + 16 q .. + 15 of the super-block,
+//        the activation operand being those 16 bytes as they lie in the row (one 16-byte read).
 //   meta uint8 [N/16][K/256][16][16]: per row the GGUF block's first 16 bytes: d, dmin (fp16) and the 12 bytes of
 //        6-bit scales and mins (ggml get_scale_min_k4 order, gguf_weights.py:56-60).
 // Activations: xq int8 [M, K] row-major; a fp32, (b, m) at a[b a_sb + m] (a_sb = 0: one scale per token);
@@ -21,15 +22,32 @@
 
 namespace prism {
 
-__device__ __forceinline__ int64_t unpack_q4(uint32_t w) {
-    return (int64_t)(w & 0x0f0f0f0fu) | ((int64_t)((w >> 4) & 0x0f0f0f0fu) << 32);
+typedef unsigned short us2 __attribute__((ext_vector_type(2)));
+
+// A lane's 8 bytes of a sub-block pair (w0, w1) times its sub-block scale sc = 8 hi + lo (3-bit parts) as two
+// MFMA weight operands: the 16 nibbles (<= 15) times lo and times hi (<= 105: still int8, no carry between bytes of
+// a packed 16-bit multiply).  acc = (x . lo q) + 8 (x . hi q) is then exact.
+__device__ __forceinline__ void two_plane(uint32_t w0, uint32_t w1, uint32_t sc, v4i& lo, v4i& hi) {
+    const us2 sl = {(unsigned short)(sc & 7u), (unsigned short)(sc & 7u)};
+    const us2 sh = {(unsigned short)(sc >> 3), (unsigned short)(sc >> 3)};
+    const uint32_t n[4] = {w0 & 0x0f0f0f0fu, w1 & 0x0f0f0f0fu, (w0 >> 4) & 0x0f0f0f0fu, (w1 >> 4) & 0x0f0f0f0fu};
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        lo[e] = (int)__builtin_bit_cast(uint32_t, (us2)(__builtin_bit_cast(us2, n[e]) * sl));
+        hi[e] = (int)__builtin_bit_cast(uint32_t, (us2)(__builtin_bit_cast(us2, n[e]) * sh));
+    }
 }
 
-// The activation operand of sub-block g for lane group q: k = {4 q .. 4 q + 3, 16 + 4 q .. 16 + 4 q + 3}.
-__device__ __forceinline__ int64_t act_operand(const int8_t* row, int g, int q) {
-    const uint32_t lo = *reinterpret_cast<const uint32_t*>(row + 32 * g + 4 * q);
-    const uint32_t hi = *reinterpret_cast<const uint32_t*>(row + 32 * g + 16 + 4 * q);
-    return (int64_t)lo | ((int64_t)hi << 32);
+// mins = sum_g mn[n, g] S[m, g] for a 16 x 16 tile as two MFMAs over k = 0..7 (lanes q > 0 carry zeros): the weight
+// rows' 8 mins (bytes) against the 8 low parts S & 63, then against the 8 high parts S >> 6; mins = lo + 64 hi.
+__device__ __forceinline__ v4i mins_mfma(int64_t mn8, int64_t slo, int64_t shi) {
+    const v4i zero = {0, 0, 0, 0};
+    const v4i lo = __builtin_amdgcn_mfma_i32_16x16x32_i8(mn8, slo, zero, 0, 0, 0);
+    const v4i hi = __builtin_amdgcn_mfma_i32_16x16x32_i8(mn8, shi, zero, 0, 0, 0);
+    v4i r;
+#pragma unroll
+    for (int e = 0; e < 4; e++) r[e] = lo[e] + 64 * hi[e];
+    return r;
 }
 
 // One row's 16 meta bytes -> d, dmin (fp32) and the 8 scales and 8 mins (ggml get_scale_min_k4).
@@ -51,16 +69,6 @@ __device__ __forceinline__ float q4k_term(float d, float dm, int acc, int mins) 
     return fmaf(-dm, (float)mins, mul_rn(d, (float)acc));
 }
 
-// S = (S & 63) + 64 (S >> 6) per sub-block, from a (super-block, row)'s 16 split-sum bytes
-__device__ __forceinline__ void split_sums(v4i s, int* S) {
-#pragma unroll
-    for (int g = 0; g < 8; g++) {
-        const int lo = (int)(int8_t)(((uint32_t)s[g >> 2]) >> (8 * (g & 3)));
-        const int hi = (int)(int8_t)(((uint32_t)s[2 + (g >> 2)]) >> (8 * (g & 3)));
-        S[g] = lo + 64 * hi;
-    }
-}
-
 // ---------------------------------------------------------------------------------------------- pack
 // One thread per (nt, b, h, l): gathers 4 sub-blocks x 4 bytes from the GGUF block of row 16 nt + l % 16.
 __global__ __launch_bounds__(256) void q4k_pack_kernel(const uint8_t* __restrict__ raw, uint8_t* __restrict__ qv,
@@ -74,19 +82,14 @@ __global__ __launch_bounds__(256) void q4k_pack_kernel(const uint8_t* __restrict
     const int b = (int)(c % NB), nt = (int)(c / NB);
     const int r = l & 15, q = l >> 4;
     const uint8_t* blk = raw + ((int64_t)(16 * nt + r) * NB + b) * 144;
-    uint32_t o[4];
+    const uint8_t* qs = blk + 16;                      // 128 bytes: 32-byte group c holds sub-block 2 c (low
+    uint32_t o[4] = {0, 0, 0, 0};                      // nibbles) and 2 c + 1 (high nibbles)
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int g = 4 * h + i;
-        const uint8_t* qs = blk + 16 + 32 * (g >> 1);  // 32 bytes: low nibbles sub-block 2 c, high 2 c + 1
-        uint32_t w = 0;
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-            const uint32_t lo = (g & 1) ? (qs[4 * q + t] >> 4) : (qs[4 * q + t] & 0xf);
-            const uint32_t hi = (g & 1) ? (qs[16 + 4 * q + t] >> 4) : (qs[16 + 4 * q + t] & 0xf);
-            w |= (lo | (hi << 4)) << (8 * t);
-        }
-        o[i] = w;
+    for (int j = 0; j < 16; j++) {
+        const int k = 128 * h + 64 * (j >> 3) + 16 * q + (j & 7);     // this byte: values k and k + 8
+        const uint32_t v0 = (qs[32 * (k >> 6) + (k & 31)] >> (4 * ((k >> 5) & 1))) & 0xf;
+        const uint32_t v1 = (qs[32 * ((k + 8) >> 6) + ((k + 8) & 31)] >> (4 * (((k + 8) >> 5) & 1))) & 0xf;
+        o[j >> 2] |= (v0 | (v1 << 4)) << (8 * (j & 3));
     }
     reinterpret_cast<v4u*>(qv)[e] = v4u{o[0], o[1], o[2], o[3]};
     if (h == 0 && q == 0) {                            // blocks are 144 bytes: 16-byte aligned, copy by words
@@ -122,13 +125,13 @@ __global__ __launch_bounds__(NW * 64) void w4a8_decode_kernel(const int8_t* __re
     extern __shared__ __attribute__((aligned(16))) int8_t dsm[];
     float* terms = reinterpret_cast<float*>(dsm);                 // [2][R][M][16]
     int* scl = reinterpret_cast<int*>(terms + 2 * R * M * 16);    // [2][R][8][16] scales, [sub-block][row]
-    int* mnl = scl + 2 * R * 128;                                 // [2][R][8][16] mins
-    float* dl = reinterpret_cast<float*>(mnl + 2 * R * 128);      // [2][R][16] d
+    float* dl = reinterpret_cast<float*>(scl + 2 * R * 128);      // [2][R][16] d
     float* dml = dl + 2 * R * 16;                                 // [2][R][16] dmin
-    int* sl = reinterpret_cast<int*>(dml + 2 * R * 16);           // [2][R][M][8] activation sums S
-    float* al = reinterpret_cast<float*>(sl + 2 * R * M * 8);     // [3][R][M] activation scales: read by the fold of
+    int8_t* xsb = reinterpret_cast<int8_t*>(dml + 2 * R * 16);    // [2][R][M][16] split activation sums (bytes)
+    uint8_t* mnb = reinterpret_cast<uint8_t*>(xsb + 2 * R * M * 16);  // [2][R][16][8] mins (bytes)
+    int8_t* xl = reinterpret_cast<int8_t*>(mnb + 2 * R * 128);    // [2][M][LDA] activations
+    float* al = reinterpret_cast<float*>(xl + 2 * M * LDA);       // [3][R][M] activation scales: read by the fold of
                                                                   // round r - 1 while round r + 1 is staged
-    int8_t* xl = reinterpret_cast<int8_t*>(al + 3 * R * M);       // [2][M][LDA] activations
     const int tstride = R * M * 16, xstride = M * LDA;
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -172,19 +175,15 @@ __global__ __launch_bounds__(NW * 64) void w4a8_decode_kernel(const int8_t* __re
             int sc[8], mn[8];
             row_meta(sg.m, d, dm, sc, mn);
 #pragma unroll
-            for (int g = 0; g < 8; g++) {
-                scl[((buf * R + lb) * 8 + g) * 16 + row] = sc[g];
-                mnl[((buf * R + lb) * 8 + g) * 16 + row] = mn[g];
-            }
+            for (int g = 0; g < 8; g++) scl[((buf * R + lb) * 8 + g) * 16 + row] = sc[g];
+            *reinterpret_cast<v2u*>(&mnb[((buf * R + lb) * 16 + row) * 8]) =
+                v2u{(uint32_t)(mn[0] | (mn[1] << 8) | (mn[2] << 16) | (mn[3] << 24)),
+                    (uint32_t)(mn[4] | (mn[5] << 8) | (mn[6] << 16) | (mn[7] << 24))};
             dl[(buf * R + lb) * 16 + row] = d;
             dml[(buf * R + lb) * 16 + row] = dm;
         }
         if (tid < R * M) {
-            int S[8];
-            split_sums(sg.s, S);
-            int* sp = sl + (buf * R * M + tid) * 8;       // tid = lb M + m
-            *reinterpret_cast<v4i*>(sp) = v4i{S[0], S[1], S[2], S[3]};
-            *reinterpret_cast<v4i*>(sp + 4) = v4i{S[4], S[5], S[6], S[7]};
+            *reinterpret_cast<v4i*>(&xsb[(buf * R * M + tid) * 16]) = sg.s;     // tid = lb M + m
             al[(rr % 3) * R * M + tid] = sg.as;
         }
 #pragma unroll
@@ -203,36 +202,33 @@ __global__ __launch_bounds__(NW * 64) void w4a8_decode_kernel(const int8_t* __re
     };
     auto compute = [&](int r, v4u (*w)[2], int buf) {
         float* tb = terms + (r & 1) * tstride;
-        const int8_t* xrow = xl + buf * xstride + min(lm, M - 1) * LDA;
+        const int mrow = min(lm, M - 1);
+        const int8_t* xrow = xl + buf * xstride + mrow * LDA;
 #pragma unroll
         for (int i = 0; i < CB; i++) {
             const int lb = wv * CB + i;
             if (r * R + lb < NB) {
-                const int* scp = scl + (buf * R + lb) * 128 + 4 * q;
-                const int* mnp = mnl + (buf * R + lb) * 128 + 4 * q;
-                v4i acc = {0, 0, 0, 0}, mins = {0, 0, 0, 0};
-                const int* Sp = sl + ((buf * R + lb) * M + min(lm, M - 1)) * 8;
-                const v4i S0 = *reinterpret_cast<const v4i*>(Sp), S1 = *reinterpret_cast<const v4i*>(Sp + 4);
+                const int* scp = scl + (buf * R + lb) * 128;
+                v4i alo = {0, 0, 0, 0}, ahi = {0, 0, 0, 0};
 #pragma unroll
-                for (int g = 0; g < 8; g++) {
-                    const int64_t wf = unpack_q4(w[i][g >> 2][g & 3]);
-                    const int64_t af = act_operand(xrow + lb * 256, g, q);
-                    const v4i zero = {0, 0, 0, 0};
-                    const v4i P = __builtin_amdgcn_mfma_i32_16x16x32_i8(wf, af, zero, 0, 0, 0);
-                    const v4i sc = *reinterpret_cast<const v4i*>(scp + g * 16);
-                    const v4i mn = *reinterpret_cast<const v4i*>(mnp + g * 16);
-                    const int Sg = g < 4 ? S0[g] : S1[g - 4];
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        acc[e] += sc[e] * P[e];
-                        mins[e] += mn[e] * Sg;
-                    }
+                for (int p = 0; p < 4; p++) {
+                    v4i wl, wh;
+                    two_plane(w[i][p >> 1][2 * (p & 1)], w[i][p >> 1][2 * (p & 1) + 1],
+                              (uint32_t)scp[(2 * p + (q >> 1)) * 16 + lm], wl, wh);
+                    const v4i af = *reinterpret_cast<const v4i*>(xrow + lb * 256 + 64 * p + 16 * q);
+                    alo = __builtin_amdgcn_mfma_i32_16x16x64_i8(wl, af, alo, 0, 0, 0);
+                    ahi = __builtin_amdgcn_mfma_i32_16x16x64_i8(wh, af, ahi, 0, 0, 0);
                 }
+                const int8_t* xp = xsb + ((buf * R + lb) * M + mrow) * 16;
+                const int64_t mn8 = q == 0 ? *reinterpret_cast<const int64_t*>(&mnb[((buf * R + lb) * 16 + lm) * 8]) : 0;
+                const int64_t slo = q == 0 ? *reinterpret_cast<const int64_t*>(xp) : 0;
+                const int64_t shi = q == 0 ? *reinterpret_cast<const int64_t*>(xp + 8) : 0;
+                const v4i mins = mins_mfma(mn8, slo, shi);
                 const v4f d = *reinterpret_cast<const v4f*>(&dl[(buf * R + lb) * 16 + 4 * q]);
                 const v4f dm = *reinterpret_cast<const v4f*>(&dml[(buf * R + lb) * 16 + 4 * q]);
                 v4f t;
 #pragma unroll
-                for (int e = 0; e < 4; e++) t[e] = q4k_term(d[e], dm[e], acc[e], mins[e]);
+                for (int e = 0; e < 4; e++) t[e] = q4k_term(d[e], dm[e], alo[e] + 8 * ahi[e], mins[e]);
                 if (lm < M) *reinterpret_cast<v4f*>(&tb[(lb * M + lm) * 16 + 4 * q]) = t;
             }
         }
@@ -283,8 +279,8 @@ __global__ __launch_bounds__(NW * 64) void w4a8_decode_kernel(const int8_t* __re
 }
 
 static size_t w4a8_decode_lds(int R, int M) {
-    return 2 * (size_t)R * M * 16 * 4 + 2 * (size_t)R * 128 * 4 * 2 + 2 * (size_t)R * 16 * 4 * 2 +
-           2 * (size_t)R * M * 8 * 4 + 3 * (size_t)R * M * 4 + 2 * (size_t)M * (R * 256 + 16);
+    return 2 * (size_t)R * M * 16 * 4 + 2 * (size_t)R * 128 * 4 + 2 * (size_t)R * 16 * 4 * 2 +
+           2 * (size_t)R * M * 16 + 2 * (size_t)R * 128 + 2 * (size_t)M * (R * 256 + 16) + 3 * (size_t)R * M * 4;
 }
 
 // ---------------------------------------------------------------------------------------------- prefill tile
@@ -398,36 +394,35 @@ __global__ __launch_bounds__(256, 2) void w4a8_tile_kernel(const int8_t* __restr
         sstore();
         lds_barrier();
         if (b + 1 < NB) gload(b + 1);
-        v4i acc[2][4];
+        // acc = sum_g sc[n, g] P_g, two MFMA chains over the 4 sub-block pairs (two_plane): acc = lo + 8 hi
+        v4i alo[2][4], ahi[2][4];
 #pragma unroll
         for (int i = 0; i < 2; i++)
 #pragma unroll
-            for (int j = 0; j < 4; j++) acc[i][j] = v4i{0, 0, 0, 0};
-        const v4i zero = {0, 0, 0, 0};
-#pragma unroll 2
-        for (int g = 0; g < 8; g++) {
-            int64_t wf[2], af[4];
+            for (int j = 0; j < 4; j++) alo[i][j] = ahi[i][j] = v4i{0, 0, 0, 0};
 #pragma unroll
-            for (int i = 0; i < 2; i++) {
-                const uint32_t word = *reinterpret_cast<const uint32_t*>(
-                    &Bs[(2 * wv + i) * 2048 + (g >> 2) * 1024 + lane * 16 + 4 * (g & 3)]);
-                wf[i] = unpack_q4(word);
-            }
+        for (int hh = 0; hh < 2; hh++) {
+            v4u wq[2];
 #pragma unroll
-            for (int j = 0; j < 4; j++) af[j] = act_operand(&As[(16 * j + lm) * QLDA], g, q);
+            for (int i = 0; i < 2; i++) wq[i] = *reinterpret_cast<const v4u*>(&Bs[(2 * wv + i) * 2048 + hh * 1024 + lane * 16]);
 #pragma unroll
-            for (int i = 0; i < 2; i++) {
-                const v4i sc = *reinterpret_cast<const v4i*>(&scl[g][32 * wv + 16 * i + 4 * q]);
+            for (int pp = 0; pp < 2; pp++) {
+                const int p = 2 * hh + pp, g = 2 * p + (q >> 1);
+                v4i wl[2], wh[2], af[4];
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const v4i P = __builtin_amdgcn_mfma_i32_16x16x32_i8(wf[i], af[j], zero, 0, 0, 0);
+                for (int i = 0; i < 2; i++)
+                    two_plane(wq[i][2 * pp], wq[i][2 * pp + 1], (uint32_t)scl[g][32 * wv + 16 * i + lm], wl[i], wh[i]);
 #pragma unroll
-                    for (int e = 0; e < 4; e++) acc[i][j][e] += __mul24(sc[e], P[e]);   // |sc P| < 2^23
-                }
+                for (int j = 0; j < 4; j++) af[j] = *reinterpret_cast<const v4i*>(&As[(16 * j + lm) * QLDA + 64 * p + 16 * q]);
+#pragma unroll
+                for (int i = 0; i < 2; i++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        alo[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wl[i], af[j], alo[i][j], 0, 0, 0);
+                        ahi[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wh[i], af[j], ahi[i][j], 0, 0, 0);
+                    }
             }
         }
-        // mins = sum_g mn[n, g] S[m, g] as two MFMAs over k = 0..7 (lanes q > 0 carry zeros): the weight row's 8
-        // mins against the 8 low parts S & 63, then against the 8 high parts S >> 6; mins = lo + 64 hi (exact)
         int64_t mnf[2], slo[4], shi[4];
 #pragma unroll
         for (int i = 0; i < 2; i++)
@@ -443,12 +438,11 @@ __global__ __launch_bounds__(256, 2) void w4a8_tile_kernel(const int8_t* __restr
             const v4f dm = *reinterpret_cast<const v4f*>(&dml[32 * wv + 16 * i + 4 * q]);
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const v4i lo = __builtin_amdgcn_mfma_i32_16x16x32_i8(mnf[i], slo[j], zero, 0, 0, 0);
-                const v4i hi = __builtin_amdgcn_mfma_i32_16x16x32_i8(mnf[i], shi[j], zero, 0, 0, 0);
+                const v4i mins = mins_mfma(mnf[i], slo[j], shi[j]);
                 const float am = al[16 * j + lm];
 #pragma unroll
                 for (int e = 0; e < 4; e++)
-                    y[i][j][e] = fmaf(am, q4k_term(d[e], dm[e], acc[i][j][e], lo[e] + 64 * hi[e]), y[i][j][e]);
+                    y[i][j][e] = fmaf(am, q4k_term(d[e], dm[e], alo[i][j][e] + 8 * ahi[i][j][e], mins[e]), y[i][j][e]);
             }
         }
     }

@@ -29,10 +29,10 @@ def _np_pack(blocks):
     N, NB, _ = blocks.shape
     qs = blocks[:, :, 16:].reshape(N, NB, 4, 32).astype(np.uint32)
     vals = np.stack([qs & 15, qs >> 4], 3).reshape(N, NB, 8, 32)              # [row, b, sub-block, 32]
-    r = vals.reshape(N // 16, 16, NB, 2, 4, 2, 4, 4)                           # [nt, row, b, h, i, half16, q, t]
-    lo, hi = r[:, :, :, :, :, 0], r[:, :, :, :, :, 1]                          # [nt, row, b, h, i, q, t]
+    r = vals.reshape(N // 16, 16, NB, 2, 2, 4, 2, 8)                           # [nt, row, b, h, pp, q, half8, t]
+    lo, hi = r[..., 0, :], r[..., 1, :]                                         # [nt, row, b, h, pp, q, t]
     byte = (lo | (hi << 4)).astype(np.uint8)
-    qv = byte.transpose(0, 2, 3, 5, 1, 4, 6).reshape(N // 16, NB, 2, 64, 16)  # lane = q * 16 + row
+    qv = byte.transpose(0, 2, 3, 5, 1, 4, 6).reshape(N // 16, NB, 2, 64, 16)  # lane = q * 16 + row, byte = pp 8 + t
     meta = blocks[:, :, :16].reshape(N // 16, 16, NB, 16).transpose(0, 2, 1, 3)
     return np.ascontiguousarray(qv), np.ascontiguousarray(meta)
 
