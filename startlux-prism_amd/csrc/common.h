@@ -59,6 +59,22 @@ __device__ __forceinline__ float mul_f16_rn(float x, uint32_t word) {
 // loads (__syncthreads() also drains those, which would empty a kernel's prefetch pipeline at every barrier).
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// LDS-DMA: each lane's 16 (or 1) bytes from its own global address to the wave's LDS base + lane x 16 (x 4: the
+// one-byte form fills a dword per lane).  `lds` must be the same for every lane of the wave.
+__device__ __forceinline__ void dma16(const void* g, void* lds) {
+    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+__device__ __forceinline__ void dma1(const void* g, void* lds) {
+    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 1, 0, 0);
+}
+
+// Waits until at most N vector-memory operations of this wave are outstanding.  The compiler does not count LDS-DMA
+// writes as producers of later LDS reads, so every DMA stage is closed by an explicit wait (then a barrier).
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));

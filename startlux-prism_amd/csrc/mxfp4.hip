@@ -338,18 +338,6 @@ struct MxStage {
     static constexpr int LOADS = AF == 0 ? 10 : 8;                // DMA instructions per wave per stage
 };
 
-__device__ __forceinline__ void dma16(const void* g, uint8_t* lds) {
-    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
-}
-__device__ __forceinline__ void dma1(const void* g, uint8_t* lds) {
-    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 1, 0, 0);
-}
-
-template <int N>
-__device__ __forceinline__ void vm_wait() {
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
 template <int AF, int EPI, int NS>
 __global__ __launch_bounds__(256, 2) void mx_tile_kernel(const uint8_t* __restrict__ aq, const uint8_t* __restrict__ as,
                                                          const uint8_t* __restrict__ wq,
@@ -695,10 +683,7 @@ extern "C" int prism_mxfp4_gemm(const uint8_t* aq, const uint8_t* as, int a_fmt,
 #undef DEC_MT
 #undef DEC
     } else {
-#ifndef PRISM_MX_NS
-#define PRISM_MX_NS 3
-#endif
-        constexpr int NS = PRISM_MX_NS;
+        constexpr int NS = 3;                                   // LDS stages in flight
         const int tiles_m = (int)((M + kTB - 1) / kTB), tiles_n = (int)((N + kTB - 1) / kTB);
         dim3 grid((unsigned)(tiles_m * tiles_n));
 #define TILE(AF, E)                                                                                                  \

@@ -24,12 +24,14 @@ namespace prism {
 
 typedef unsigned short us2 __attribute__((ext_vector_type(2)));
 
-// A lane's 8 bytes of a sub-block pair (w0, w1) times its sub-block scale sc = 8 hi + lo (3-bit parts) as two
-// MFMA weight operands: the 16 nibbles (<= 15) times lo and times hi (<= 105: still int8, no carry between bytes of
-// a packed 16-bit multiply).  acc = (x . lo q) + 8 (x . hi q) is then exact.
-__device__ __forceinline__ void two_plane(uint32_t w0, uint32_t w1, uint32_t sc, v4i& lo, v4i& hi) {
-    const us2 sl = {(unsigned short)(sc & 7u), (unsigned short)(sc & 7u)};
-    const us2 sh = {(unsigned short)(sc >> 3), (unsigned short)(sc >> 3)};
+// A lane's 8 bytes of a sub-block pair (w0, w1) times its sub-block scale sc = 8 hi + lo (3-bit parts, given packed
+// as split_scale(sc) = lo | hi << 16) as two MFMA weight operands: the 16 nibbles (<= 15) times lo and times hi
+// (<= 105: still int8, no carry between bytes of a packed 16-bit multiply).  acc = (x . lo q) + 8 (x . hi q) exactly.
+__device__ __forceinline__ uint32_t split_scale(int sc) { return (uint32_t)(sc & 7) | ((uint32_t)(sc >> 3) << 16); }
+
+__device__ __forceinline__ void two_plane(uint32_t w0, uint32_t w1, uint32_t sp, v4i& lo, v4i& hi) {
+    const us2 s = __builtin_bit_cast(us2, sp);
+    const us2 sl = __builtin_shufflevector(s, s, 0, 0), sh = __builtin_shufflevector(s, s, 1, 1);
     const uint32_t n[4] = {w0 & 0x0f0f0f0fu, w1 & 0x0f0f0f0fu, (w0 >> 4) & 0x0f0f0f0fu, (w1 >> 4) & 0x0f0f0f0fu};
 #pragma unroll
     for (int e = 0; e < 4; e++) {
@@ -124,7 +126,7 @@ __global__ __launch_bounds__(NW * 64) void w4a8_decode_kernel(const int8_t* __re
     constexpr int XPT = (MX * CPR + NT - 1) / NT;
     extern __shared__ __attribute__((aligned(16))) int8_t dsm[];
     float* terms = reinterpret_cast<float*>(dsm);                 // [2][R][M][16]
-    int* scl = reinterpret_cast<int*>(terms + 2 * R * M * 16);    // [2][R][8][16] scales, [sub-block][row]
+    uint32_t* scl = reinterpret_cast<uint32_t*>(terms + 2 * R * M * 16);  // [2][R][8][16] split scales, [g][row]
     float* dl = reinterpret_cast<float*>(scl + 2 * R * 128);      // [2][R][16] d
     float* dml = dl + 2 * R * 16;                                 // [2][R][16] dmin
     int8_t* xsb = reinterpret_cast<int8_t*>(dml + 2 * R * 16);    // [2][R][M][16] split activation sums (bytes)
@@ -175,7 +177,7 @@ __global__ __launch_bounds__(NW * 64) void w4a8_decode_kernel(const int8_t* __re
             int sc[8], mn[8];
             row_meta(sg.m, d, dm, sc, mn);
 #pragma unroll
-            for (int g = 0; g < 8; g++) scl[((buf * R + lb) * 8 + g) * 16 + row] = sc[g];
+            for (int g = 0; g < 8; g++) scl[((buf * R + lb) * 8 + g) * 16 + row] = split_scale(sc[g]);
             *reinterpret_cast<v2u*>(&mnb[((buf * R + lb) * 16 + row) * 8]) =
                 v2u{(uint32_t)(mn[0] | (mn[1] << 8) | (mn[2] << 16) | (mn[3] << 24)),
                     (uint32_t)(mn[4] | (mn[5] << 8) | (mn[6] << 16) | (mn[7] << 24))};
@@ -208,13 +210,13 @@ __global__ __launch_bounds__(NW * 64) void w4a8_decode_kernel(const int8_t* __re
         for (int i = 0; i < CB; i++) {
             const int lb = wv * CB + i;
             if (r * R + lb < NB) {
-                const int* scp = scl + (buf * R + lb) * 128;
+                const uint32_t* scp = scl + (buf * R + lb) * 128;
                 v4i alo = {0, 0, 0, 0}, ahi = {0, 0, 0, 0};
 #pragma unroll
                 for (int p = 0; p < 4; p++) {
                     v4i wl, wh;
                     two_plane(w[i][p >> 1][2 * (p & 1)], w[i][p >> 1][2 * (p & 1) + 1],
-                              (uint32_t)scp[(2 * p + (q >> 1)) * 16 + lm], wl, wh);
+                              scp[(2 * p + (q >> 1)) * 16 + lm], wl, wh);
                     const v4i af = *reinterpret_cast<const v4i*>(xrow + lb * 256 + 64 * p + 16 * q);
                     alo = __builtin_amdgcn_mfma_i32_16x16x64_i8(wl, af, alo, 0, 0, 0);
                     ahi = __builtin_amdgcn_mfma_i32_16x16x64_i8(wh, af, ahi, 0, 0, 0);
@@ -285,11 +287,12 @@ static size_t w4a8_decode_lds(int R, int M) {
 
 // ---------------------------------------------------------------------------------------------- prefill tile
 // 128 (n) x 64 (m) output tile per 256-thread workgroup: 4 waves, each 32 n x 64 m (2 x 4 MFMA tiles of 16 x 16),
-// one super-block per stage.  Staged in LDS per stage: the 8 weight chunks' halves (2 tiles x 2 KB per wave ...
-// 8 tiles x 2 KB), the tile's unpacked meta, the activation rows, sums and scales; the next stage's global data are
-// in registers while the current one is computed.  Each wave keeps its outputs' fp32 sums y over super-blocks.
+// one super-block per stage, two stage buffers in LDS.  The stage's weight chunks (8 row tiles x 2 KB) and activation
+// rows (64 x 256 B) arrive by LDS-DMA into the free buffer while the other is computed; the tile's meta (unpacked
+// once per row by a staging thread), activation sums and scales go through registers.  One barrier per stage.
+// Activation row r holds its 16-byte chunk c at slot c ^ (r & 15): the 16 rows a 16-lane read spans fall in distinct
+// banks.  Each wave keeps its outputs' fp32 sums y over super-blocks.
 constexpr int QBN = 128, QBM = 64;
-constexpr int QLDA = 256 + 16;
 
 template <int EPI>
 __global__ __launch_bounds__(256, 2) void w4a8_tile_kernel(const int8_t* __restrict__ xq, const float* __restrict__ a,
@@ -298,13 +301,13 @@ __global__ __launch_bounds__(256, 2) void w4a8_tile_kernel(const int8_t* __restr
                                                            const uint8_t* __restrict__ meta, void* __restrict__ out,
                                                            int64_t ldo, const int32_t* __restrict__ n_rows, int M,
                                                            int N, int K, int tiles_m, int tiles_n) {
-    __shared__ __attribute__((aligned(16))) uint8_t Bs[8 * 2048];     // 8 row tiles x (2 halves x 64 lanes x 16 B)
-    __shared__ __attribute__((aligned(16))) int8_t As[QBM * QLDA];
-    __shared__ int scl[8][QBN];
-    __shared__ __attribute__((aligned(8))) uint8_t mnb[QBN][8];     // the 8 mins of each weight row, as bytes
-    __shared__ float dl[QBN], dml[QBN];
-    __shared__ __attribute__((aligned(16))) int8_t xsb[QBM][16];    // per activation row: S & 63 x 8, S >> 6 x 8
-    __shared__ float al[QBM];
+    __shared__ __attribute__((aligned(16))) uint8_t Bs[2][8 * 2048];  // 8 row tiles x (2 halves x 64 lanes x 16 B)
+    __shared__ __attribute__((aligned(16))) int8_t As[2][QBM * 256];  // swizzled activation rows
+    __shared__ uint32_t scl[2][8][QBN];                               // split scales, [sub-block][weight row]
+    __shared__ __attribute__((aligned(8))) uint8_t mnb[2][QBN][8];  // the 8 mins of each weight row, as bytes
+    __shared__ float dl[2][QBN], dml[2][QBN];
+    __shared__ __attribute__((aligned(16))) int8_t xsb[2][QBM][16]; // per activation row: S & 63 x 8, S >> 6 x 8
+    __shared__ float al[2][QBM];
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int lm = lane & 15, q = lane >> 4;
@@ -323,59 +326,51 @@ __global__ __launch_bounds__(256, 2) void w4a8_tile_kernel(const int8_t* __restr
     if (m0 >= live) return;
     const int NB = K / 256, ntiles = N / 16;
 
-    // global -> register staging of one super-block
-    // weights: 8 tiles x 128 chunks of 16 B = 1024 chunks, 4 per thread
-    const v4u* wsrc[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int c = tid + 256 * i;
-        wsrc[i] = reinterpret_cast<const v4u*>(qv) + (int64_t)min(n0 / 16 + (c >> 7), ntiles - 1) * NB * 128 + (c & 127);
-    }
-    // meta: 128 rows x 16 B, threads < 128
-    const v4u* msrc = reinterpret_cast<const v4u*>(meta) + (int64_t)min(n0 / 16 + (tid >> 4), ntiles - 1) * NB * 16 + (tid & 15);
-    // activations: 64 rows x 256 B = 1024 chunks, 4 per thread
+    // DMA sources, chunk c = tid + 256 i: weight chunk c of the stage's 8 x 128, activation row c / 16, slot c % 16
+    const uint8_t* wsrc[4];
     const int8_t* xsrc[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int c = tid + 256 * i;
-        xsrc[i] = xq + (int64_t)min(m0 + (c >> 4), M - 1) * K + (c & 15) * 16;
+        wsrc[i] = qv + ((int64_t)min(n0 / 16 + (c >> 7), ntiles - 1) * NB * 128 + (c & 127)) * 16;
+        const int r = c >> 4;
+        xsrc[i] = xq + (int64_t)min(m0 + r, M - 1) * K + (((c & 15) ^ (r & 15)) * 16);
     }
-    const int srow = min(m0 + (tid & 63), M - 1);     // sums and scale: threads < 64, one activation row each
-    v4u rw[4], rm;
-    v4i rx[4], rs;
-    float ra;
-    auto gload = [&](int b) {
+    auto dma = [&](int b, int buf) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            rw[i] = __builtin_nontemporal_load(wsrc[i] + (int64_t)b * 128);
-            rx[i] = *reinterpret_cast<const v4i*>(xsrc[i] + (int64_t)b * 256);
+            const int base = (256 * i + 64 * wv) * 16;                // this wave's 64 chunks
+            dma16(wsrc[i] + (int64_t)b * 2048, &Bs[buf][base]);
+            dma16(xsrc[i] + (int64_t)b * 256, &As[buf][base]);
         }
+    };
+    // meta: 128 rows x 16 B (threads < 128); sums and scale: one activation row each (threads < 64)
+    const v4u* msrc = reinterpret_cast<const v4u*>(meta) + (int64_t)min(n0 / 16 + (tid >> 4), ntiles - 1) * NB * 16 + (tid & 15);
+    const int srow = min(m0 + (tid & 63), M - 1);
+    v4u rm;
+    v4i rs;
+    float ra;
+    auto gmeta = [&](int b) {
         rm = msrc[(int64_t)b * 16];
         rs = *reinterpret_cast<const v4i*>(xs + ((int64_t)b * M + srow) * 16);
         ra = a[(int64_t)b * a_sb + srow];
     };
-    auto sstore = [&]() {
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int c = tid + 256 * i;
-            *reinterpret_cast<v4u*>(&Bs[(c >> 7) * 2048 + (c & 127) * 16]) = rw[i];
-            *reinterpret_cast<v4i*>(&As[(c >> 4) * QLDA + (c & 15) * 16]) = rx[i];
-        }
+    auto smeta = [&](int buf) {
         if (tid < 128) {
             float d, dm;
             int sc[8], mn[8];
             row_meta(rm, d, dm, sc, mn);
 #pragma unroll
-            for (int g = 0; g < 8; g++) scl[g][tid] = sc[g];
-            *reinterpret_cast<v2u*>(&mnb[tid][0]) =
+            for (int g = 0; g < 8; g++) scl[buf][g][tid] = split_scale(sc[g]);
+            *reinterpret_cast<v2u*>(&mnb[buf][tid][0]) =
                 v2u{(uint32_t)(mn[0] | (mn[1] << 8) | (mn[2] << 16) | (mn[3] << 24)),
                     (uint32_t)(mn[4] | (mn[5] << 8) | (mn[6] << 16) | (mn[7] << 24))};
-            dl[tid] = d;
-            dml[tid] = dm;
+            dl[buf][tid] = d;
+            dml[buf][tid] = dm;
         }
         if (tid < 64) {
-            *reinterpret_cast<v4i*>(&xsb[tid][0]) = rs;
-            al[tid] = ra;
+            *reinterpret_cast<v4i*>(&xsb[buf][tid][0]) = rs;
+            al[buf][tid] = ra;
         }
     };
 
@@ -388,12 +383,17 @@ __global__ __launch_bounds__(256, 2) void w4a8_tile_kernel(const int8_t* __restr
 #pragma unroll
             for (int e = 0; e < 4; e++) y[i][j][e] = 0.f;
 
-    gload(0);
+    gmeta(0);
+    dma(0, 0);
+    smeta(0);
+    vm_wait<0>();
+    lds_barrier();
     for (int b = 0; b < NB; b++) {
-        lds_barrier();
-        sstore();
-        lds_barrier();
-        if (b + 1 < NB) gload(b + 1);
+        const int cb = b & 1;
+        if (b + 1 < NB) {
+            gmeta(b + 1);
+            dma(b + 1, cb ^ 1);
+        }
         // acc = sum_g sc[n, g] P_g, two MFMA chains over the 4 sub-block pairs (two_plane): acc = lo + 8 hi
         v4i alo[2][4], ahi[2][4];
 #pragma unroll
@@ -404,16 +404,18 @@ __global__ __launch_bounds__(256, 2) void w4a8_tile_kernel(const int8_t* __restr
         for (int hh = 0; hh < 2; hh++) {
             v4u wq[2];
 #pragma unroll
-            for (int i = 0; i < 2; i++) wq[i] = *reinterpret_cast<const v4u*>(&Bs[(2 * wv + i) * 2048 + hh * 1024 + lane * 16]);
+            for (int i = 0; i < 2; i++)
+                wq[i] = *reinterpret_cast<const v4u*>(&Bs[cb][(2 * wv + i) * 2048 + hh * 1024 + lane * 16]);
 #pragma unroll
             for (int pp = 0; pp < 2; pp++) {
                 const int p = 2 * hh + pp, g = 2 * p + (q >> 1);
                 v4i wl[2], wh[2], af[4];
 #pragma unroll
                 for (int i = 0; i < 2; i++)
-                    two_plane(wq[i][2 * pp], wq[i][2 * pp + 1], (uint32_t)scl[g][32 * wv + 16 * i + lm], wl[i], wh[i]);
+                    two_plane(wq[i][2 * pp], wq[i][2 * pp + 1], scl[cb][g][32 * wv + 16 * i + lm], wl[i], wh[i]);
 #pragma unroll
-                for (int j = 0; j < 4; j++) af[j] = *reinterpret_cast<const v4i*>(&As[(16 * j + lm) * QLDA + 64 * p + 16 * q]);
+                for (int j = 0; j < 4; j++)
+                    af[j] = *reinterpret_cast<const v4i*>(&As[cb][(16 * j + lm) * 256 + (((4 * p + q) ^ lm) * 16)]);
 #pragma unroll
                 for (int i = 0; i < 2; i++)
 #pragma unroll
@@ -426,25 +428,28 @@ __global__ __launch_bounds__(256, 2) void w4a8_tile_kernel(const int8_t* __restr
         int64_t mnf[2], slo[4], shi[4];
 #pragma unroll
         for (int i = 0; i < 2; i++)
-            mnf[i] = q == 0 ? *reinterpret_cast<const int64_t*>(&mnb[32 * wv + 16 * i + lm][0]) : 0;
+            mnf[i] = q == 0 ? *reinterpret_cast<const int64_t*>(&mnb[cb][32 * wv + 16 * i + lm][0]) : 0;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            slo[j] = q == 0 ? *reinterpret_cast<const int64_t*>(&xsb[16 * j + lm][0]) : 0;
-            shi[j] = q == 0 ? *reinterpret_cast<const int64_t*>(&xsb[16 * j + lm][8]) : 0;
+            slo[j] = q == 0 ? *reinterpret_cast<const int64_t*>(&xsb[cb][16 * j + lm][0]) : 0;
+            shi[j] = q == 0 ? *reinterpret_cast<const int64_t*>(&xsb[cb][16 * j + lm][8]) : 0;
         }
 #pragma unroll
         for (int i = 0; i < 2; i++) {
-            const v4f d = *reinterpret_cast<const v4f*>(&dl[32 * wv + 16 * i + 4 * q]);
-            const v4f dm = *reinterpret_cast<const v4f*>(&dml[32 * wv + 16 * i + 4 * q]);
+            const v4f d = *reinterpret_cast<const v4f*>(&dl[cb][32 * wv + 16 * i + 4 * q]);
+            const v4f dm = *reinterpret_cast<const v4f*>(&dml[cb][32 * wv + 16 * i + 4 * q]);
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const v4i mins = mins_mfma(mnf[i], slo[j], shi[j]);
-                const float am = al[16 * j + lm];
+                const float am = al[cb][16 * j + lm];
 #pragma unroll
                 for (int e = 0; e < 4; e++)
                     y[i][j][e] = fmaf(am, q4k_term(d[e], dm[e], alo[i][j][e] + 8 * ahi[i][j][e], mins[e]), y[i][j][e]);
             }
         }
+        if (b + 1 < NB) smeta(cb ^ 1);
+        vm_wait<0>();
+        lds_barrier();
     }
     // D element (i, j, e): n = n0 + 32 wv + 16 i + 4 q + e, m = m0 + 16 j + lm
 #pragma unroll

@@ -21,14 +21,6 @@ constexpr int PC_STAGE = 2 * PC_OPER;
 
 __device__ __forceinline__ int pc_swz(int row) { return (row >> 1) & 3; }
 
-__device__ __forceinline__ void pc_dma(const void* g, uint8_t* lds) {
-    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
-}
-
-template <int N>
-__device__ __forceinline__ void pc_vm_wait() {
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
 
 template <bool WPACK, bool WS16, int EPI, int NS>
 __global__ __launch_bounds__(256, 1) void w8a8_pc_tile_kernel(const int8_t* __restrict__ a,
@@ -72,8 +64,8 @@ __global__ __launch_bounds__(256, 1) void w8a8_pc_tile_kernel(const int8_t* __re
         uint8_t* b = lds + buf * PC_STAGE;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            pc_dma(asrc[i] + (int64_t)st * PCK, b + (4 * wv + i) * 1024);
-            pc_dma(wsrc[i] + (int64_t)st * (WPACK ? 1024 : PCK), b + PC_OPER + (4 * wv + i) * 1024);
+            dma16(asrc[i] + (int64_t)st * PCK, b + (4 * wv + i) * 1024);
+            dma16(wsrc[i] + (int64_t)st * (WPACK ? 1024 : PCK), b + PC_OPER + (4 * wv + i) * 1024);
         }
     };
 
@@ -112,9 +104,9 @@ __global__ __launch_bounds__(256, 1) void w8a8_pc_tile_kernel(const int8_t* __re
 
     for (int st = 0; st < KS; st++) {
         const int pend = min(KS - 1, st + NS - 2) - st;     // stages issued after this one
-        if (NS >= 4 && pend >= 2) pc_vm_wait<16>();
-        else if (pend >= 1) pc_vm_wait<8>();
-        else pc_vm_wait<0>();
+        if (NS >= 4 && pend >= 2) vm_wait<16>();
+        else if (pend >= 1) vm_wait<8>();
+        else vm_wait<0>();
         lds_barrier();
         if (st + NS - 1 < KS) issue(st + NS - 1, (st + NS - 1) % NS);
         const uint8_t* b = lds + (st % NS) * PC_STAGE;
