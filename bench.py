@@ -260,7 +260,8 @@ def bench_per_channel(dev, iters=40):
 def bench_producers(dev, iters=20):
     """The fused producers at config 1's shapes (HBM-bound: GB/s of bytes read plus written): norm_q8 on the fp32
     residual (T = 8192, HID = 5120) and swiglu_q8 on the bf16 gate|up output (T = 8192, FF = 13824), plus the
-    per-token quantizer rows_q8 of the headline step; and their decode size (T = 16)."""
+    per-token quantizer rows_q8 of the headline step, and gated_norm_q8 on the linear-attention output (48 value heads
+    of 128, gate bf16 from the projection); and their decode size (T = 16)."""
     import torch
     from prism_amd import quant as KQ
     rows = []
@@ -287,7 +288,18 @@ def bench_producers(dev, iters=20):
         b = T * K1 * 2 + T * K1 + 4 * T
         rows.append(dict(op="rows_q8", T=T, K=K1, us=round(us, 2), GBps=round(b / us / 1e3, 1),
                          frac=round(b / us / 1e3 / PEAK_HBM_GBS, 3)))
-        del h, gu, x, q, q2
+        HV, D = 48, 128
+        o = torch.randn(T, HV * D, device=dev)
+        proj = torch.randn(T, 2 * HV * D, device=dev).to(torch.bfloat16)
+        wd = torch.rand(D, device=dev) + 0.5
+        inv3 = torch.rand(HV * D, device=dev) + 0.5
+        q3 = torch.empty(T, HV * D, dtype=torch.int8, device=dev)
+        cfg = type("Cfg", (), {"v_heads": HV, "gdn_dim": D, "eps": 1e-6})()
+        us = _graph_us(lambda i: KQ.gated_norm_q8(o, proj, HV * D, wd, inv3, q3, s, n, T, cfg), 1, iters)
+        b = T * HV * D * (4 + 2 + 1) + HV * D * 4 + 4 * T
+        rows.append(dict(op="gated_norm_q8", T=T, K=HV * D, us=round(us, 2), GBps=round(b / us / 1e3, 1),
+                         frac=round(b / us / 1e3 / PEAK_HBM_GBS, 3)))
+        del h, gu, x, q, q2, o, proj, q3
         torch.cuda.empty_cache()
     return rows
 

@@ -177,6 +177,21 @@ PRISM_API int prism_norm_quant(const float* h, int64_t ldh, const float* w, cons
 PRISM_API int prism_swiglu_quant(const void* gu, int gu_f32, int64_t ldg, const float* inv_s, int8_t* q, float* s,
                                  int8_t* xs, const int32_t* n_rows, int64_t M, int64_t FF, int back, void* stream);
 
+/*
+ * Gated RMSNorm producer of the linear-attention output projection: per head of D values,
+ * r = RN(1 / RN(sqrt(RN(RN(ss / D) + eps)))) with ss the head's sum of squares in a fixed order (8-value chunks in
+ * increasing index, then the D / 8 chunk sums combined by halving), y = RN(RN(RN(o * r) * w[d]) * silu(z)), then
+ * RN(y * inv_s) when inv_s is not null; quantized as prism_norm_quant.  o fp32 [M, HV D] (row stride ldo); z the
+ * row's HV D gate values, bf16 (fp32 when z_f32) with row stride ldz (the caller passes the projection plus its
+ * column offset); w fp32 [D]; inv_s fp32 [HV D] or null.  Replaces kernels/quant.py:460-469 (gated_norm_q8, back 0)
+ * and :399-401 (gated_norm_g, back 1; back 2 one scale per row).  Needs D a power of two in 8 .. 512, HV D <= 32768
+ * (% 256 for backs 1, 2).
+ */
+PRISM_API int prism_gated_norm_quant(const float* o, int64_t ldo, const void* z, int z_f32, int64_t ldz,
+                                     const float* w, const float* inv_s, int8_t* q, float* s, int8_t* xs,
+                                     const int32_t* n_rows, int64_t M, int64_t HV, int64_t D, float eps, int back,
+                                     void* stream);
+
 /* ------------------------------------------------------------------------------------------------ MXFP4 */
 /* Element formats of MX operands (the MFMA format codes): e4m3 (OCP float8_e4m3fn) and e2m1 (fp4). */
 enum { PRISM_MX_E4M3 = 0, PRISM_MX_E2M1 = 4 };

@@ -80,6 +80,9 @@ def lib():
             "orc_norm_quant": (None, [_p, _i64, _p, _p, _i64, ctypes.c_float, ctypes.c_int, _i64, _p, _p, _p,
                                       ctypes.c_int]),
             "orc_swiglu_quant": (None, [_p, _i64, _p, _i64, ctypes.c_int, _i64, _p, _p, _p, ctypes.c_int]),
+            "orc_head_sumsq": (ctypes.c_float, [_p, _i64]),
+            "orc_gated_norm_quant": (None, [_p, _p, _i64, _p, _p, _i64, _i64, _i64, ctypes.c_float, ctypes.c_int,
+                                            _i64, _p, _p, _p, ctypes.c_int]),
             "orc_e2m1_value": (ctypes.c_float, [ctypes.c_int]),
             "orc_e4m3_value": (ctypes.c_float, [ctypes.c_int]),
             "orc_e4m3_code": (ctypes.c_int, [ctypes.c_float]),
@@ -367,4 +370,25 @@ def swiglu_quant(gu, inv_s=None, back="q8", live=None, nthreads=0):
     q, s, xs = _outs(M, FF, back)
     lib().orc_swiglu_quant(gu.ctypes.data, FF, _ptr(inv_s), M, BACKS[back], M if live is None else live,
                            q.ctypes.data, s.ctypes.data, _ptr(xs), nthreads)
+    return (q, s) if xs is None else (q, s, xs)
+
+
+def head_sumsq(y):
+    y = np.ascontiguousarray(y, np.float32)
+    return float(lib().orc_head_sumsq(y.ctypes.data, y.shape[0]))
+
+
+def gated_norm_quant(o, z, w, eps, HV, D, inv_s=None, back="q8", live=None, nthreads=0):
+    """o fp32 [M, HV D], z fp32 [M, >= HV D] (the gate columns), w fp32 [D] -> (q, s[, xs]) of the per-head RMSNorm
+    of o times w times silu(z) (times inv_s) (kernels/quant.py:216-246, :349-365)."""
+    o = np.ascontiguousarray(o, np.float32)
+    z = np.ascontiguousarray(z, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    M, K = o.shape[0], HV * D
+    assert o.shape[1] == K and z.shape[1] >= K and w.shape[0] == D
+    inv_s = None if inv_s is None else np.ascontiguousarray(inv_s, np.float32)
+    q, s, xs = _outs(M, K, back)
+    lib().orc_gated_norm_quant(o.ctypes.data, z.ctypes.data, z.shape[1], w.ctypes.data, _ptr(inv_s), M, HV, D,
+                               float(eps), BACKS[back], M if live is None else live, q.ctypes.data, s.ctypes.data,
+                               _ptr(xs), nthreads)
     return (q, s) if xs is None else (q, s, xs)

@@ -653,6 +653,47 @@ EXPORT void orc_norm_quant(const float* h, int64_t HID, const float* w, const in
     }
 }
 
+/* The fixed-order sum of squares of one head of D values (the GPU kernel's order): each 8-value chunk summed in
+ * increasing index, then the D / 8 chunk sums combined by halving (chunk c + chunk c + D/16, then + D/32, ...). */
+EXPORT float orc_head_sumsq(const float* y, int64_t D) {
+    float a[64];
+    const int64_t n = D / 8;
+    for (int64_t c = 0; c < n; c++) {
+        float acc = 0.f;
+        for (int j = 0; j < 8; j++) acc = acc + y[c * 8 + j] * y[c * 8 + j];
+        a[c] = acc;
+    }
+    for (int64_t o = n / 2; o > 0; o >>= 1)
+        for (int64_t l = 0; l < o; l++) a[l] = a[l] + a[l + o];
+    return a[0];
+}
+
+/* Gated RMSNorm per head (StartLux-Prism kernels/quant.py:216-246 _gated_norm_q8_kernel, :349-365 _gated_norm_g_kernel):
+ * o fp32 [M, HV D], z fp32 [M, ldz] (bf16 inputs widened exactly; the HV D gate values from column 0), w fp32 [D],
+ * inv_s fp32 [HV D] or NULL.  y = RN(RN(RN(o r) w) silu(z)) (then RN(y inv_s)) with r per head, as norm_quant. */
+EXPORT void orc_gated_norm_quant(const float* o, const float* z, int64_t ldz, const float* w, const float* inv_s,
+                                 int64_t M, int64_t HV, int64_t D, float eps, int back, int64_t live, int8_t* q,
+                                 float* s, int8_t* xs, int nthreads) {
+    const int64_t n = live < M ? live : M, K = HV * D;
+#pragma omp parallel for num_threads(nthreads_or(nthreads)) schedule(static)
+    for (int64_t i = 0; i < n; i++) {
+        float* y = (float*)malloc(sizeof(float) * K);
+        for (int64_t hh = 0; hh < HV; hh++) {
+            const float* oh = o + i * K + hh * D;
+            const float ss = orc_head_sumsq(oh, D);
+            const float r = 1.0f / sqrtf(ss / (float)D + eps);
+            for (int64_t d = 0; d < D; d++) {
+                const float g = z[i * ldz + hh * D + d];
+                float v = ((oh[d] * r) * w[d]) * (g / (1.0f + orc_expf(-g)));
+                if (inv_s) v = v * inv_s[hh * D + d];
+                y[hh * D + d] = v;
+            }
+        }
+        store_back_row(y, K, back, M, i, q, s, xs);
+        free(y);
+    }
+}
+
 /* gu fp32 [M, 2 FF] (bf16 inputs widened exactly) */
 EXPORT void orc_swiglu_quant(const float* gu, int64_t FF, const float* inv_s, int64_t M, int back, int64_t live,
                              int8_t* q, float* s, int8_t* xs, int nthreads) {

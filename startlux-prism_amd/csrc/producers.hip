@@ -4,6 +4,8 @@
 //   swiglu_q8  :249-280, :472-478   y = silu(gate) * up * inv_s -> int8 rows, one scale per row
 //   norm_g     :354-366, :395-397   y = rmsnorm(h) * w          -> W4A8 operands (_store_g, :314-330)
 //   swiglu_g   :384-393, :403-406   y = silu(gate) * up         -> W4A8 operands
+//   gated_norm_q8 :216-246, :460-469, gated_norm_g :349-365, :399-401
+//                                   y = rmsnorm_head(o) * w * silu(z) (* inv_s) -> either back end
 // One workgroup (256 threads) per row; thread t owns the 8-input chunks t, t + 256, ... and keeps them in registers
 // between the row reductions and the stores, so a row is read once.
 //
@@ -11,6 +13,9 @@
 //   rmsnorm: ss = sum of RN(h * h) in a fixed order - each thread adds its own inputs in increasing index, the 64
 //            lanes of a wave combine by halving (lane l + lane l + 32, then + 16, ...), the four waves left to right;
 //            r = RN(1 / RN(sqrt(RN(RN(ss / HID) + eps)))); y = RN(RN(h * r) * w).
+//   gated:   per head of D values, ss = the chunk sums (8 values each, increasing index) combined by halving across
+//            the D / 8 neighbouring lanes that hold the head (lane l + lane l ^ D/16, then ^ D/32, ...);
+//            y = RN(RN(RN(o * r) * w[d]) * silu(z)), then RN(y * inv_s) for the q8 form.
 //   silu:    RN(g / RN(1 + exp(-g))), with exp this library's own (prism_expf below).
 //   quantization as the row quantizers: scale = RN(max(amax, 1e-10) / 127), q = rint(RN(y / scale)).
 // The reference evaluates rsqrt, exp and '/' with NVIDIA's approximate instructions and sums in Triton's reduction
@@ -239,6 +244,85 @@ __global__ __launch_bounds__(kPThreads) void swiglu_prod_kernel(const void* __re
     store_back<NCH, BACK>(y, amax, red, i, i, M, FF, q, s, xs);
 }
 
+// ---------------------------------------------------------------------------------------------- gated RMSNorm
+// o fp32 [*, HV D] (row stride ldo); z [*, ldz] (bf16, or fp32 when Z32): the row's gate values from column 0 (the
+// caller offsets the projection's row); w fp32 [D]; inv_s fp32 [HV D] or null.  D / 8 is a power of two <= 64, so
+// a head's chunks are neighbouring lanes of one wave.
+template <int NCH, int BACK, bool Z32>
+__global__ __launch_bounds__(kPThreads) void gated_norm_prod_kernel(const float* __restrict__ o, int64_t ldo,
+                                                                    const void* __restrict__ z, int64_t ldz,
+                                                                    const float* __restrict__ w,
+                                                                    const float* __restrict__ inv_s,
+                                                                    int8_t* __restrict__ q, float* __restrict__ s,
+                                                                    int8_t* __restrict__ xs,
+                                                                    const int32_t* __restrict__ n_rows, int M, int HV,
+                                                                    int D, float eps) {
+    __shared__ float red[4];
+    const int i = blockIdx.x;
+    if (i >= __ldg(n_rows)) return;
+    const int K = HV * D, nch = K / 8, cph = D / 8;
+    const v4f* orow = reinterpret_cast<const v4f*>(o + (int64_t)i * ldo);
+    float y[NCH][8];
+    float amax = 0.f;
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+        const int idx = threadIdx.x + c * kPThreads;
+        const bool in = idx < nch;
+        float ss = 0.f;
+        if (in) {
+            const v4f a = __builtin_nontemporal_load(orow + 2 * idx), b = __builtin_nontemporal_load(orow + 2 * idx + 1);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                y[c][j] = a[j];
+                y[c][j + 4] = b[j];
+            }
+#pragma unroll
+            for (int j = 0; j < 8; j++) ss = add_rn(ss, mul_rn(y[c][j], y[c][j]));
+        }
+        for (int off = cph >> 1; off > 0; off >>= 1) ss = add_rn(ss, __shfl_xor(ss, off, kWave));
+        if (in) {
+            const float r = div_rn(1.0f, sqrt_rn(add_rn(div_rn(ss, (float)D), eps)));
+            const int d0 = (idx & (cph - 1)) * 8;
+            const v4f w0 = reinterpret_cast<const v4f*>(w + d0)[0], w1 = reinterpret_cast<const v4f*>(w + d0)[1];
+            float g[8];
+            if (Z32) {
+                const v4f* zr = reinterpret_cast<const v4f*>(static_cast<const float*>(z) + (int64_t)i * ldz);
+                const v4f g0 = zr[2 * idx], g1 = zr[2 * idx + 1];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    g[j] = g0[j];
+                    g[j + 4] = g1[j];
+                }
+            } else {
+                const v4u gv = reinterpret_cast<const v4u*>(static_cast<const uint16_t*>(z) + (int64_t)i * ldz)[idx];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    g[2 * j] = __uint_as_float(gv[j] << 16);
+                    g[2 * j + 1] = __uint_as_float(gv[j] & 0xffff0000u);
+                }
+            }
+            float is[8];
+            if (inv_s) {
+                const v4f a = reinterpret_cast<const v4f*>(inv_s)[2 * idx], b = reinterpret_cast<const v4f*>(inv_s)[2 * idx + 1];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    is[j] = a[j];
+                    is[j + 4] = b[j];
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const float wj = j < 4 ? w0[j] : w1[j - 4];
+                float v = mul_rn(mul_rn(mul_rn(y[c][j], r), wj), silu_rn(g[j]));
+                if (inv_s) v = mul_rn(v, is[j]);
+                y[c][j] = v;
+                amax = fmaxf(amax, fabsf(v));
+            }
+        }
+    }
+    store_back<NCH, BACK>(y, amax, red, i, i, M, K, q, s, xs);
+}
+
 template <typename KN>
 static int pick_nch(int K, KN&& launch) {
     const int need = (K / 8 + kPThreads - 1) / kPThreads;
@@ -301,6 +385,33 @@ extern "C" int prism_swiglu_quant(const void* gu, int gu_f32, int64_t ldg, const
         if (gu_f32) { if (back == 0) SW(0, true); else if (back == 1) SW(1, true); else SW(2, true); }
         else { if (back == 0) SW(0, false); else if (back == 1) SW(1, false); else SW(2, false); }
 #undef SW
+        return hipGetLastError() == hipSuccess ? 0 : (int)PRISM_ERR_LAUNCH;
+    });
+}
+
+// back as prism_norm_quant.  o: the GDN output rows, z: the gate values of the row (the projection row plus the
+// caller's column offset), both with their row strides.
+extern "C" int prism_gated_norm_quant(const float* o, int64_t ldo, const void* z, int z_f32, int64_t ldz,
+                                      const float* w, const float* inv_s, int8_t* q, float* s, int8_t* xs,
+                                      const int32_t* n_rows, int64_t M, int64_t HV, int64_t D, float eps, int back,
+                                      void* stream) {
+    if (!o || !z || !w || !q || !s || !n_rows || (back != 0 && !xs)) return PRISM_ERR_ARG;
+    if (back < 0 || back > 2) return PRISM_ERR_ARG;
+    if (M < 0 || HV <= 0 || D < 8 || D > 512 || (D & (D - 1)) || HV * D > 32768 || M > (1 << 30)) return PRISM_ERR_SHAPE;
+    const int64_t K = HV * D;
+    if (ldo < K || ldz < K || (back != 0 && K % 256)) return PRISM_ERR_SHAPE;
+    if (ldo % 4 || (z_f32 ? ldz % 4 : ldz % 8) || !PRISM_ALIGNED(o, 16) || !PRISM_ALIGNED(z, 16) ||
+        !PRISM_ALIGNED(w, 16) || !PRISM_ALIGNED(q, 8) || (inv_s && !PRISM_ALIGNED(inv_s, 16)))
+        return PRISM_ERR_ALIGN;
+    if (M == 0) return PRISM_OK;
+    hipStream_t st = (hipStream_t)stream;
+    return pick_nch((int)K, [&](auto nc) {
+        constexpr int NC = decltype(nc)::value;
+#define GN(B, Z) hipLaunchKernelGGL((gated_norm_prod_kernel<NC, B, Z>), dim3((unsigned)M), dim3(kPThreads), 0, st, o, \
+                                    ldo, z, ldz, w, inv_s, q, s, xs, n_rows, (int)M, (int)HV, (int)D, eps)
+        if (z_f32) { if (back == 0) GN(0, true); else if (back == 1) GN(1, true); else GN(2, true); }
+        else { if (back == 0) GN(0, false); else if (back == 1) GN(1, false); else GN(2, false); }
+#undef GN
         return hipGetLastError() == hipSuccess ? 0 : (int)PRISM_ERR_LAUNCH;
     });
 }

@@ -29,6 +29,8 @@ _SIGS = {
     "prism_w8a8_pc_packed_gemm": (_int, [_p, _p, _i64, _p, _p, _int, _p, _i64, _p, _i64, _i64, _i64, _int, _int, _p]),
     "prism_norm_quant": (_int, [_p, _i64, _p, _p, _p, _p, _p, _p, _i64, _i64, ctypes.c_float, _int, _p]),
     "prism_swiglu_quant": (_int, [_p, _int, _i64, _p, _p, _p, _p, _p, _i64, _i64, _int, _p]),
+    "prism_gated_norm_quant": (_int, [_p, _i64, _p, _int, _i64, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64,
+                                      ctypes.c_float, _int, _p]),
     "prism_mxfp4_pack": (_int, [_p, _i64, _p, _p, _i64, _i64, _int, _p]),
     "prism_mxfp4_repack": (_int, [_p, _p, _p, _p, _i64, _i64, _p]),
     "prism_mxfp4_quant_act": (_int, [_p, _int, _i64, _p, _p, _p, _p, _i64, _i64, _int, _p]),

@@ -66,7 +66,7 @@ def rows_g(x, q, s, xs, n, T, group=256):
 
 # ---------------------------------------------------------------------------------------------- fused producers
 # kernels/quant.py:144-170 / :418-431 (norm_q8), :249-280 / :472-478 (swiglu_q8), :354-366 / :395-397 (norm_g),
-# :384-393 / :403-406 (swiglu_g).  Arithmetic: IEEE fp32 throughout, rsqrt as 1 / sqrt (both correctly rounded),
+# :384-393 / :403-406 (swiglu_g), :216-246 / :460-469 (gated_norm_q8), :349-365 / :399-401 (gated_norm_g).  Arithmetic: IEEE fp32 throughout, rsqrt as 1 / sqrt (both correctly rounded),
 # exp this library's own (Cody-Waite reduction, degree-7 Taylor series), the sum of squares in a fixed order; the
 # reference's NVIDIA approximations (rsqrt.approx, ex2.approx, div.full) have no specification to match bit for bit.
 
@@ -154,3 +154,43 @@ def swiglu_g(gu, q, s, xs, n, T, group=256):
     n = _rows_arg(n, T, gu.device)
     L.call("prism_swiglu_quant", L.ptr(gu), int(gu.dtype == torch.float32), gu.stride(0), None, L.ptr(q), L.ptr(s),
            L.ptr(xs), L.ptr(n), xs.shape[1], FF, back, L.stream_of(gu))
+
+
+def _gated(o, proj, z_off, w, inv_s, q, s, xs, n, T, cfg, back):
+    HV, D = cfg.v_heads, cfg.gdn_dim
+    if getattr(cfg, "v_heads_full", HV) != HV:
+        raise NotImplementedError("tensor-parallel head shards are not part of the single-GPU build")
+    K = HV * D
+    if o.dtype != torch.float32 or o.stride(-1) != 1 or o.reshape(o.shape[0], -1).shape[1] != K:
+        raise ValueError("gated norm: o fp32 [*, v_heads, gdn_dim], unit column stride")
+    if proj.dtype not in (torch.bfloat16, torch.float32) or proj.stride(1) != 1 or proj.shape[1] < z_off + K:
+        raise ValueError("gated norm: proj [*, >= z_off + v_heads gdn_dim] bf16 or fp32")
+    if w.dtype != torch.float32 or w.numel() != D:
+        raise ValueError("gated norm: w fp32 [gdn_dim]")
+    if q.dtype != torch.int8 or q.shape[1] != K or not q.is_contiguous() or s.dtype != torch.float32:
+        raise ValueError("gated norm: q int8 [*, v_heads gdn_dim] contiguous, s fp32")
+    if inv_s is not None and (inv_s.dtype != torch.float32 or inv_s.numel() != K):
+        raise ValueError("gated norm: inv_s fp32 [v_heads gdn_dim]")
+    o2 = o.reshape(o.shape[0], K)
+    z = proj[:, z_off:]
+    M = T if back == 0 else xs.shape[1]
+    n = _rows_arg(n, T, o.device)
+    L.call("prism_gated_norm_quant", L.ptr(o2), o2.stride(0), L.ptr(z), int(proj.dtype == torch.float32),
+           proj.stride(0), L.ptr(w.contiguous()), L.ptr(None if inv_s is None else inv_s.contiguous()), L.ptr(q),
+           L.ptr(s), L.ptr(xs), L.ptr(n), M, HV, D, float(cfg.eps), back, L.stream_of(o))
+
+
+def gated_norm_q8(o, proj, z_off, w, inv_s, q, s, n, T, cfg, mode=0, amax=None, sync=None):
+    """o fp32 [*, v_heads, gdn_dim] (the linear-attention output), proj [*, P] (the gate z at columns z_off ..),
+    w fp32 [gdn_dim] -> q int8 [>= T, v_heads gdn_dim], s fp32 [>= T]: y = rmsnorm per head (o) * w * silu(z) *
+    inv_s, one scale per row.  cfg: eps, v_heads, gdn_dim."""
+    if mode != 0 or sync is not None:
+        raise NotImplementedError("tensor-parallel quantization modes are not part of the single-GPU build")
+    _gated(o, proj, z_off, w, inv_s, q, s, None, n, T, cfg, 0)
+
+
+def gated_norm_g(o, proj, z_off, w, q, s, xs, n, T, cfg, group=256):
+    """W4A8 producer of the gated norm: q int8 [>= T, K], s fp32 [K / group, M], xs int8 [K / 256, M, 16]
+    (K = v_heads gdn_dim)."""
+    back = _g_back(q, s, xs, group)
+    _gated(o, proj, z_off, w, None, q, s, xs, n, T, cfg, back)

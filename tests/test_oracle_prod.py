@@ -1,7 +1,8 @@
-"""Pins the oracle's fused producers (orc_expf, orc_sumsq_fixed, orc_norm_quant, orc_swiglu_quant) to things other
-than their own formulas: float64 exp, math.fsum, a hand-built sum whose value depends on the reduction order, the
-float64 RMSNorm / SwiGLU values (every quantized output within half a quantization step of them), closed-form rows,
-and the split-sum layout of the W4A8 operands."""
+"""Pins the oracle's fused producers (orc_expf, orc_sumsq_fixed, orc_head_sumsq, orc_norm_quant, orc_swiglu_quant,
+orc_gated_norm_quant) to things other than their own formulas: float64 exp, math.fsum, hand-built sums whose value
+depends on the reduction order, the float64 RMSNorm / SwiGLU / gated-norm values (every quantized output within half
+a quantization step of them), closed-form rows, a gated norm that reduces exactly to norm_quant, and the split-sum
+layout of the W4A8 operands."""
 import math
 
 import numpy as np
@@ -89,3 +90,55 @@ def test_swiglu_quant_against_float64(back):
     gd, ud = gu[:, :FF].astype(np.float64), gu[:, FF:].astype(np.float64)
     y64 = gd / (1 + np.exp(-gd)) * ud * (1.0 if inv is None else inv)
     _check_dequant(q, s, y64, back, FF)
+
+
+def test_head_sumsq_order_and_bound():
+    y = np.zeros(128, np.float32)
+    y[0], y[8], y[72] = 4096.0, 1.0, 1.0      # chunks 0, 1, 9 of 16: the first halving adds chunk 9 to chunk 1 (1 + 1)
+    assert O.head_sumsq(y) == 2.0 ** 24 + 2.0  # before 2^24 joins; a running sum would give 2^24
+    g = rng(35)
+    for D in (8, 64, 128, 512):
+        v = g.standard_normal(D).astype(np.float32)
+        exact = math.fsum(float(t) * float(t) for t in v)
+        assert abs(O.head_sumsq(v) - exact) <= D * 2.0 ** -23 * exact
+
+
+@pytest.mark.parametrize("back", ["q8", "g256", "grow"])
+def test_gated_norm_quant_against_float64(back):
+    g = rng(36)
+    M, HV, D, eps = 6, 8, 128, 1e-6
+    o = (g.standard_normal((M, HV * D)) * 2).astype(np.float32)
+    o[1, :D] = 0.0                                             # a zero head
+    z = (g.standard_normal((M, HV * D + 32)) * 3).astype(np.float32)
+    w = (0.5 + g.random(D)).astype(np.float32)
+    inv = (0.5 + g.random(HV * D)).astype(np.float32) if back == "q8" else None
+    out = O.gated_norm_quant(o, z, w, eps, HV, D, inv_s=inv, back=back)
+    q, s = out[0], out[1]
+    od = o.astype(np.float64).reshape(M, HV, D)
+    zd = z[:, :HV * D].astype(np.float64).reshape(M, HV, D)
+    y64 = od / np.sqrt((od * od).mean(2, keepdims=True) + eps) * w * (zd / (1 + np.exp(-zd)))
+    y64 = y64.reshape(M, HV * D) * (1.0 if inv is None else inv)
+    _check_dequant(q, s, y64, back, HV * D)
+    assert (q[1, :D] == 0).all()
+
+
+def test_gated_norm_one_head_with_unit_gate_is_norm_quant():
+    """z = 128: exp(-128) underflows, silu(z) = 128 exactly; with one head of D = 128 the chunk-halving sum equals
+    the row sum's order, so q is norm_quant's and every scale is 128 x its scale."""
+    g = rng(37)
+    M, D = 5, 128
+    o = (g.standard_normal((M, D)) * 2).astype(np.float32)
+    w = (0.5 + g.random(D)).astype(np.float32)
+    z = np.full((M, D), 128.0, np.float32)
+    assert O.expf(-128.0) == 0.0
+    for back in ("q8", "grow"):
+        if back == "grow":
+            o2, z2, w2 = np.tile(o, 2), np.tile(z, 2), w        # two identical heads: D 128, row 256
+            gq = O.gated_norm_quant(o2, z2, w2, 1e-6, 2, D, back=back)
+            nq = O.norm_quant(o, w, 1e-6, "q8")
+            assert np.array_equal(gq[0], np.tile(nq[0], 2))
+            assert np.array_equal(gq[1], nq[1] * np.float32(128.0))
+        else:
+            gq = O.gated_norm_quant(o, z, w, 1e-6, 1, D, back=back)
+            nq = O.norm_quant(o, w, 1e-6, back)
+            assert np.array_equal(gq[0], nq[0]) and np.array_equal(gq[1], nq[1] * np.float32(128.0))

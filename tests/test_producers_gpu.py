@@ -1,6 +1,6 @@
-"""GPU parity of the fused producers (norm_q8, norm_g, swiglu_q8, swiglu_g) against the CPU oracle, bit for bit:
-int8 values, scales and split per-32 sums, at the engine's shapes (HID 5120, FF 17408), with gathered rows, live
-rows, bf16 and fp32 SwiGLU inputs, and the smoothing factor."""
+"""GPU parity of the fused producers (norm_q8, norm_g, swiglu_q8, swiglu_g, gated_norm_q8, gated_norm_g) against the
+CPU oracle, bit for bit: int8 values, scales and split per-32 sums, at the engine's shapes (HID 5120, FF 17408, 48
+value heads of 128), with gathered rows, live rows, bf16 and fp32 gate inputs, and the smoothing factor."""
 import numpy as np
 import pytest
 import torch
@@ -91,6 +91,61 @@ def test_swiglu_g_bit_exact(dev, group):
                 group=256 if group == "g256" else FF)
     torch.cuda.synchronize()
     rq, rs, rxs = O.swiglu_quant(O.bf16_to_f32(bits), None, group)
+    assert np.array_equal(q.cpu().numpy(), rq)
+    assert np.array_equal(s.cpu().numpy().reshape(rs.shape), rs)
+    assert np.array_equal(xs.cpu().numpy(), rxs)
+
+
+class _Cfg:
+    def __init__(self, hv, d, eps=1e-6):
+        self.v_heads, self.gdn_dim, self.eps = hv, d, eps
+
+
+@pytest.mark.parametrize("M,HV,D,live,f32,smooth", [(16, 48, 128, 13, False, True), (1, 32, 128, 1, False, True),
+                                                    (40, 16, 64, 40, True, False), (7, 4, 256, 7, False, True),
+                                                    (3, 3, 8, 3, True, True)])
+def test_gated_norm_q8_bit_exact(dev, M, HV, D, live, f32, smooth):
+    from prism_amd import quant as KQ
+    K, zoff = HV * D, 3 * 128
+    g = rng(K + M)
+    o = (g.standard_normal((M, HV, D)) * 2).astype(np.float32)
+    o[0, 1] = 0.0
+    proj = (g.standard_normal((M, zoff + K + 64)) * 3).astype(np.float32)
+    proj[0, zoff:zoff + 3] = [-120.0, 95.0, 0.0]
+    w = (0.5 + g.random(D)).astype(np.float32)
+    inv = (0.5 + g.random(K)).astype(np.float32) if smooth else None
+    if f32:
+        pd = _t(proj, dev)
+    else:
+        bits = O.bf16_bits(proj)
+        proj = O.bf16_to_f32(bits)
+        pd = _t(bits.view(np.int16), dev).view(torch.bfloat16)
+    q = torch.full((M, K), 5, dtype=torch.int8, device=dev)
+    s = torch.zeros(M, dtype=torch.float32, device=dev)
+    KQ.gated_norm_q8(_t(o, dev), pd, zoff, _t(w, dev), None if inv is None else _t(inv, dev), q, s, _n(live, dev), M,
+                     _Cfg(HV, D))
+    torch.cuda.synchronize()
+    rq, rs = O.gated_norm_quant(o.reshape(M, K), proj[:, zoff:], w, 1e-6, HV, D, inv_s=inv, back="q8", live=live)
+    assert np.array_equal(q.cpu().numpy()[:live], rq[:live]) and np.array_equal(s.cpu().numpy()[:live], rs[:live])
+    assert (q.cpu().numpy()[live:] == 5).all()
+
+
+@pytest.mark.parametrize("group", ["g256", "grow"])
+def test_gated_norm_g_bit_exact(dev, group):
+    from prism_amd import quant as KQ
+    M, HV, D = 16, 48, 128
+    K, zoff = HV * D, 1024
+    g = rng(11)
+    o = (g.standard_normal((M, HV, D)) * 2).astype(np.float32)
+    bits = O.bf16_bits((g.standard_normal((M, zoff + K)) * 3).astype(np.float32))
+    w = (0.5 + g.random(D)).astype(np.float32)
+    q = torch.zeros(M, K, dtype=torch.int8, device=dev)
+    s = torch.zeros((K // 256, M) if group == "g256" else (1, M), dtype=torch.float32, device=dev)
+    xs = torch.zeros(K // 256, M, 16, dtype=torch.int8, device=dev)
+    KQ.gated_norm_g(_t(o, dev), _t(bits.view(np.int16), dev).view(torch.bfloat16), zoff, _t(w, dev), q, s, xs,
+                    _n(M, dev), M, _Cfg(HV, D), group=256 if group == "g256" else K)
+    torch.cuda.synchronize()
+    rq, rs, rxs = O.gated_norm_quant(o.reshape(M, K), O.bf16_to_f32(bits)[:, zoff:], w, 1e-6, HV, D, back=group)
     assert np.array_equal(q.cpu().numpy(), rq)
     assert np.array_equal(s.cpu().numpy().reshape(rs.shape), rs)
     assert np.array_equal(xs.cpu().numpy(), rxs)
