@@ -133,7 +133,7 @@ PRISM_API int prism_w8a8_q8_0_packed_gemm(const int8_t* a, const float* a_s, int
  * Repack Q4_K weights into the MFMA-native layout the W4A8 kernels read: a byte permutation of the GGUF block_q4_K
  * bytes (the load-time step the reference's repack is: kernels/w4a8.py:70-94).  raw uint8 [N, K/256, 144] ->
  * qv uint8 [N/16][K/256][2][64][16] (per 16-row tile and super-block, lane slot l = row l % 16, q = l / 16; bytes
- * 4 i .. 4 i + 3 of half h: sub-block 4 h + i, byte t = v[4 q + t] | v[16 + 4 q + t] << 4), meta uint8
+ * j of half h: pair p = 2 h + j / 8, t = j % 8, k0 = 64 p + 16 q + t, byte = v[k0] | v[k0 + 8] << 4), meta uint8
  * [N/16][K/256][16][16] (per row the block's first 16 bytes: d, dmin, 12 bytes of 6-bit scales and mins).
  * Needs N % 16 == 0, K % 256 == 0.
  */
@@ -151,6 +151,26 @@ PRISM_API int prism_q4k_pack(const uint8_t* raw, uint8_t* qv, uint8_t* meta, int
  * kernel: -1 picks by M; 0 the prefill tile kernel; 1 the decode kernel (M <= 16).  Needs K % 256 == 0, N % 16 == 0.
  */
 PRISM_API int prism_w4a8_q4k_gemm(const int8_t* xq, const float* a, int64_t a_sb, const int8_t* xs, const uint8_t* qv,
+                                  const uint8_t* meta, void* out, int64_t ldo, const int32_t* n_rows, int64_t M,
+                                  int64_t N, int64_t K, int epi, int kernel, void* stream);
+
+/*
+ * Repack Q6_K weights for the W4A8 kernels (the load-time step of kernels/w4a8.py:82-90, repack "q6k", which keeps
+ * the values as int8 q - 32).  raw uint8 [N, K/256, 210] (GGUF block_q6_K: ql[128], qh[64], 16 int8 scales, fp16 d)
+ * -> qv int8 [N/16][K/256][4][64][16] (per 16-row tile and super-block, lane slot l = row l % 16, q = l / 16; bytes
+ * 8 u + t of chunk j: window w = 2 j + u of 32 inputs, input 32 w + 8 q + t) and meta uint8 [N/16][K/256][288]
+ * (the 16 rows' 16 scales, then their fp16 d).  Needs N % 16 == 0, K % 256 == 0; raw needs no alignment.
+ */
+PRISM_API int prism_q6k_pack(const uint8_t* raw, uint8_t* qv, uint8_t* meta, int64_t N, int64_t K, void* stream);
+
+/*
+ * W4A8 GEMM on packed Q6_K weights.  Replaces kernels/w4a8.py:353-366 (gemm, kind "q6k") and the Q6_K branch of
+ * startlux_prism::w4a8_gemm (csrc/w4a8_gemm.cu); arithmetic of kernels/w4a8.py:19-20 / gemm_ref (:193-197), per
+ * super-block b in increasing b: acc = sum_h sc[n,b,h] (xq . q)_h over its 16 sub-blocks of 16 (int32, exact),
+ * y = fma(a[b,m], RN(d[n,b] float(acc)), y); epi 0: bf16(y); epi 1: out = RN(out + y).  xq, a, a_sb, out, ldo,
+ * n_rows and kernel as prism_w4a8_q4k_gemm (Q6_K has no mins: no activation sums).
+ */
+PRISM_API int prism_w4a8_q6k_gemm(const int8_t* xq, const float* a, int64_t a_sb, const uint8_t* qv,
                                   const uint8_t* meta, void* out, int64_t ldo, const int32_t* n_rows, int64_t M,
                                   int64_t N, int64_t K, int epi, int kernel, void* stream);
 

@@ -81,6 +81,11 @@ def lib():
                                       ctypes.c_int]),
             "orc_swiglu_quant": (None, [_p, _i64, _p, _i64, ctypes.c_int, _i64, _p, _p, _p, ctypes.c_int]),
             "orc_head_sumsq": (ctypes.c_float, [_p, _i64]),
+            "orc_q6k_quantize": (None, [_p, _i64, _i64, _p, ctypes.c_int]),
+            "orc_q6k_dequant": (None, [_p, _i64, _i64, _p]),
+            "orc_q6k_repack": (None, [_p, _i64, _i64, _p, _p, _p]),
+            "orc_w4a8_gemm_q6k": (None, [_p, _p, _i64, _p, _p, _p, _i64, _i64, _i64, ctypes.c_int, _p, _i64, _i64,
+                                         _p, ctypes.c_int]),
             "orc_gated_norm_quant": (None, [_p, _p, _i64, _p, _p, _i64, _i64, _i64, ctypes.c_float, ctypes.c_int,
                                             _i64, _p, _p, _p, ctypes.c_int]),
             "orc_e2m1_value": (ctypes.c_float, [ctypes.c_int]),
@@ -270,6 +275,50 @@ def w4a8_gemm(xq, a, xs, w4, epi=0, out=None, live=None, sums=False, nthreads=0)
                         _ptr(w4["d"]), _ptr(w4["dm"]), M, N, K, epi, _ptr(out), out.shape[1], live, _ptr(acc),
                         _ptr(mins), nthreads)
     return (out, acc, mins) if sums else out
+
+
+def q6k_quantize(w, nthreads=0):
+    """fp32 [N, K] -> GGUF block_q6_K bytes uint8 [N, K/256, 210] (this build's own quantizer)."""
+    w = _c(np.ascontiguousarray(w, np.float32), np.float32)
+    N, K = w.shape
+    out = np.empty((N, K // 256, 210), np.uint8)
+    lib().orc_q6k_quantize(_ptr(w), N, K, _ptr(out), nthreads)
+    return out
+
+
+def q6k_dequant(blocks):
+    blocks = _c(np.ascontiguousarray(blocks), np.uint8)
+    N, NB = blocks.shape[:2]
+    w = np.empty((N, NB * 256), np.float32)
+    lib().orc_q6k_dequant(_ptr(blocks), N, NB * 256, _ptr(w))
+    return w
+
+
+def q6k_repack(blocks):
+    """-> dict(kind "q6k", q int8 [N, K], sc int8 [K/256, N, 16], d fp32 [K/256, N]) (kernels/w4a8.py:82-90)."""
+    blocks = _c(np.ascontiguousarray(blocks), np.uint8)
+    N, NB = blocks.shape[:2]
+    K = NB * 256
+    r = dict(kind="q6k", q=np.empty((N, K), np.int8), sc=np.empty((NB, N, 16), np.int8), d=np.empty((NB, N), np.float32))
+    lib().orc_q6k_repack(_ptr(blocks), N, K, _ptr(r["q"]), _ptr(r["sc"]), _ptr(r["d"]))
+    return r
+
+
+def w4a8_gemm_q6k(xq, a, w6, epi=0, out=None, live=None, sums=False, nthreads=0):
+    """(kernels/w4a8.py:193-197).  a fp32 [K/256, M] or [M].  Returns bf16 bits [M, N] (epi 0) or the updated fp32
+    out (epi 1); with sums=True also acc int32 [M, N, K/256]."""
+    xq = _c(np.ascontiguousarray(xq), np.int8)
+    M, K = xq.shape
+    N = w6["q"].shape[0]
+    a = np.ascontiguousarray(a, np.float32)
+    a_sb = 0 if a.ndim == 1 else M
+    live = M if live is None else live
+    if out is None:
+        out = np.zeros((M, N), np.uint16 if epi == 0 else np.float32)
+    acc = np.zeros((M, N, K // 256), np.int32) if sums else None
+    lib().orc_w4a8_gemm_q6k(_ptr(xq), _ptr(a), a_sb, _ptr(w6["q"]), _ptr(w6["sc"]), _ptr(w6["d"]), M, N, K, epi,
+                            _ptr(out), out.shape[1], live, _ptr(acc), nthreads)
+    return (out, acc) if sums else out
 
 
 # ------------------------------------------------------------------------------------------------- MXFP4

@@ -388,6 +388,130 @@ EXPORT void orc_w4a8_gemm(const int8_t* xq, const float* a, int64_t a_sb, const 
     }
 }
 
+/* ----------------------------------------------------------------------------------------------- Q6_K */
+/*
+ * GGUF block_q6_K (210 bytes per 256 values; ggml's layout as gguf_weights.py:85-97 _dq_q6_k reads it): ql[128]
+ * low 4 bits, qh[64] high 2 bits, scales int8[16] (one per 16 values), d fp16.  Per half h of 128 values and
+ * l < 32, with Q = q + 32 in 0..63 of values v = 128 h + l + 32 i (i = 0..3):
+ *   ql[64 h + l] = Q0 & 15 | (Q2 & 15) << 4,  ql[64 h + 32 + l] = Q1 & 15 | (Q3 & 15) << 4,
+ *   qh[32 h + l] = Q0 >> 4 | (Q1 >> 4) << 2 | (Q2 >> 4) << 4 | (Q3 >> 4) << 6.
+ */
+static int q6k_value(const uint8_t* o, int v) {
+    const int h = v / 128, r = v % 128, i = r / 32, l = r % 32;
+    const uint8_t lq = o[64 * h + 32 * (i & 1) + l];
+    const int lo = (i < 2) ? (lq & 15) : (lq >> 4);
+    const int hi = (o[128 + 32 * h + l] >> (2 * i)) & 3;
+    return (lo | (hi << 4)) - 32;
+}
+
+/*
+ * A Q6_K quantizer of this build's own (the reference only reads Q6_K from files).  Per sub-block j of 16:
+ * scale_j = max|x| / 31; d = fp16(max scale_j / 127); sc_j = clamp(rint(scale_j / d), -128, 127);
+ * q = clamp(rint(x / (d sc_j)), -32, 31).
+ */
+EXPORT void orc_q6k_quantize(const float* w, int64_t N, int64_t K, uint8_t* blocks, int nthreads) {
+    const int64_t NB = K / 256;
+#pragma omp parallel for num_threads(nthreads_or(nthreads)) schedule(static)
+    for (int64_t n = 0; n < N; n++)
+        for (int64_t b = 0; b < NB; b++) {
+            const float* x = w + n * K + b * 256;
+            uint8_t* o = blocks + (n * NB + b) * 210;
+            float scale[16], smax = 0.f;
+            for (int j = 0; j < 16; j++) {
+                float a = 0.f;
+                for (int t = 0; t < 16; t++) a = fmaxf(a, fabsf(x[16 * j + t]));
+                scale[j] = a / 31.f;
+                smax = fmaxf(smax, scale[j]);
+            }
+            const uint16_t dh = orc_float_to_half(smax / 127.f);
+            const float d = orc_half_to_float(dh);
+            int8_t sc[16];
+            int Q[256];
+            for (int j = 0; j < 16; j++) {
+                float t = d > 0.f ? rintf(scale[j] / d) : 0.f;
+                sc[j] = (int8_t)(t < -128.f ? -128.f : (t > 127.f ? 127.f : t));
+                const float step = d * (float)sc[j];
+                for (int u = 0; u < 16; u++) {
+                    float q = step != 0.f ? rintf(x[16 * j + u] / step) : 0.f;
+                    q = q < -32.f ? -32.f : (q > 31.f ? 31.f : q);
+                    Q[16 * j + u] = (int)q + 32;
+                }
+            }
+            for (int h = 0; h < 2; h++)
+                for (int l = 0; l < 32; l++) {
+                    const int* P = Q + 128 * h + l;
+                    o[64 * h + l] = (uint8_t)((P[0] & 15) | ((P[64] & 15) << 4));
+                    o[64 * h + 32 + l] = (uint8_t)((P[32] & 15) | ((P[96] & 15) << 4));
+                    o[128 + 32 * h + l] = (uint8_t)((P[0] >> 4) | ((P[32] >> 4) << 2) | ((P[64] >> 4) << 4) | ((P[96] >> 4) << 6));
+                }
+            for (int j = 0; j < 16; j++) o[192 + j] = (uint8_t)sc[j];
+            o[208] = dh & 0xff;
+            o[209] = dh >> 8;
+        }
+}
+
+/* Q6_K dequantization: gguf_weights.py:85-97 (_dq_q6_k), y = RN(d sc) (q - 32) in fp32. */
+EXPORT void orc_q6k_dequant(const uint8_t* blocks, int64_t N, int64_t K, float* w) {
+    const int64_t NB = K / 256;
+    for (int64_t n = 0; n < N; n++)
+        for (int64_t b = 0; b < NB; b++) {
+            const uint8_t* o = blocks + (n * NB + b) * 210;
+            const float d = orc_half_to_float((uint16_t)(o[208] | (o[209] << 8)));
+            for (int v = 0; v < 256; v++) {
+                const float ds = d * (float)(int8_t)o[192 + v / 16];
+                w[n * K + b * 256 + v] = ds * (float)q6k_value(o, v);
+            }
+        }
+}
+
+/*
+ * Q6_K -> the W4 layout of kernels/w4a8.py:82-90 (repack): q int8 [N, K] (values - 32, k order), sc int8
+ * [K/256, N, 16], d fp32 [K/256, N].
+ */
+EXPORT void orc_q6k_repack(const uint8_t* blocks, int64_t N, int64_t K, int8_t* q, int8_t* sc, float* d) {
+    const int64_t NB = K / 256;
+    for (int64_t n = 0; n < N; n++)
+        for (int64_t b = 0; b < NB; b++) {
+            const uint8_t* o = blocks + (n * NB + b) * 210;
+            for (int v = 0; v < 256; v++) q[n * K + b * 256 + v] = (int8_t)q6k_value(o, v);
+            for (int j = 0; j < 16; j++) sc[(b * N + n) * 16 + j] = (int8_t)o[192 + j];
+            d[b * N + n] = orc_half_to_float((uint16_t)(o[208] | (o[209] << 8)));
+        }
+}
+
+/*
+ * W4A8 GEMM on Q6_K: kernels/w4a8.py:19-20 (arithmetic) and :193-197 (gemm_ref), per super-block b in order:
+ *   acc = sum_h sc[b,n,h] * (xq . q)_h    int32, exact (16 sub-blocks of 16)
+ *   y = fma(a[b,m], RN(d[b,n] * float(acc)), y)
+ * then epi 0 bf16(y), epi 1 out = RN(out + y).  acc_out (nullable): the int32 super-block sums [M, N, K/256].
+ */
+EXPORT void orc_w4a8_gemm_q6k(const int8_t* xq, const float* a, int64_t a_sb, const int8_t* q, const int8_t* sc,
+                              const float* d, int64_t M, int64_t N, int64_t K, int epi, void* out, int64_t ldo,
+                              int64_t live, int32_t* acc_out, int nthreads) {
+    const int64_t NB = K / 256;
+    (void)M;
+#pragma omp parallel for num_threads(nthreads_or(nthreads)) schedule(dynamic, 1)
+    for (int64_t m = 0; m < live; m++)
+        for (int64_t n = 0; n < N; n++) {
+            float y = 0.f;
+            for (int64_t b = 0; b < NB; b++) {
+                int32_t acc = 0;
+                for (int h = 0; h < 16; h++)
+                    acc += (int32_t)sc[(b * N + n) * 16 + h] *
+                           dot_i8(xq + m * K + b * 256 + 16 * h, q + n * K + b * 256 + 16 * h, 16);
+                if (acc_out) acc_out[(m * N + n) * NB + b] = acc;
+                const float t = d[b * N + n] * (float)acc;
+                y = fmaf(a[b * a_sb + m], t, y);
+            }
+            if (epi == 0)
+                ((uint16_t*)out)[m * ldo + n] = orc_float_to_bf16(y);
+            else {
+                float* o = (float*)out + m * ldo + n;
+                *o = *o + y;
+            }
+        }
+}
+
 EXPORT double orc_fmaf(float a, float b, float c) { return (double)fmaf(a, b, c); }
 
 /* ------------------------------------------------------------------------------------------------ MXFP4 */

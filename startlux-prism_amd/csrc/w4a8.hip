@@ -52,6 +52,11 @@ __device__ __forceinline__ v4i mins_mfma(int64_t mn8, int64_t slo, int64_t shi) 
     return r;
 }
 
+// Q6_K meta per (16-row tile, super-block): the 16 rows' 16 int8 scales, then their fp16 d.
+constexpr int Q6_META = 288;
+
+__device__ __forceinline__ int sbyte(v4u m, int j) { return (int)(int8_t)(m[j >> 2] >> (8 * (j & 3))); }
+
 // One row's 16 meta bytes -> d, dmin (fp32) and the 8 scales and 8 mins (ggml get_scale_min_k4).
 __device__ __forceinline__ void row_meta(v4u m, float& d, float& dm, int* sc, int* mn) {
     d = f16_to_f32(m[0] & 0xffffu);
@@ -100,16 +105,55 @@ __global__ __launch_bounds__(256) void q4k_pack_kernel(const uint8_t* __restrict
     }
 }
 
+// Q6_K value v (0..255) of a block_q6_K (ggml's layout, gguf_weights.py:85-97): low 4 bits from ql, high 2 from qh,
+// minus 32.
+__device__ __forceinline__ int q6k_val(const uint8_t* blk, int v) {
+    const int h = v >> 7, i = (v >> 5) & 3, l = v & 31;
+    const uint32_t lq = blk[64 * h + 32 * (i & 1) + l];
+    const uint32_t lo = (i < 2) ? (lq & 15) : (lq >> 4);
+    const uint32_t hi = (blk[128 + 32 * h + l] >> (2 * i)) & 3;
+    return (int)(lo | (hi << 4)) - 32;
+}
+
+// One thread per (nt, b, j, l): the 16 bytes of lane l = 16 q + r, chunk j of the Q6_K device layout.
+__global__ __launch_bounds__(256) void q6k_pack_kernel(const uint8_t* __restrict__ raw, uint8_t* __restrict__ qv,
+                                                       uint8_t* __restrict__ meta, int N, int K) {
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int NB = K / 256;
+    const int64_t total = (int64_t)(N / 16) * NB * 256;
+    if (e >= total) return;
+    const int l = (int)(e & 63), j = (int)((e >> 6) & 3);
+    const int64_t c = e >> 8;                          // (nt, b)
+    const int b = (int)(c % NB), nt = (int)(c / NB);
+    const int r = l & 15, q = l >> 4;
+    const uint8_t* blk = raw + ((int64_t)(16 * nt + r) * NB + b) * 210;
+    uint32_t o[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int t = 0; t < 16; t++) {
+        const int k = 32 * (2 * j + (t >> 3)) + 8 * q + (t & 7);
+        o[t >> 2] |= ((uint32_t)q6k_val(blk, k) & 0xffu) << (8 * (t & 3));
+    }
+    reinterpret_cast<v4u*>(qv)[e] = v4u{o[0], o[1], o[2], o[3]};
+    if (j == 0 && q == 0) {                            // 210-byte blocks: copy by bytes
+        uint8_t* m = meta + c * Q6_META;
+#pragma unroll
+        for (int t = 0; t < 16; t++) m[16 * r + t] = blk[192 + t];
+        m[256 + 2 * r] = blk[208];
+        m[256 + 2 * r + 1] = blk[209];
+    }
+}
+
 // ---------------------------------------------------------------------------------------------- decode
+// KIND 0: Q4_K (qv / meta of prism_q4k_pack); KIND 1: Q6_K (prism_q6k_pack).
 // A workgroup of NW waves owns one 16-row tile and every activation row (M <= 16).  Round r covers R super-blocks;
-// wave w computes super-blocks r R + w CB .. + CB - 1.  Per round the per-wave global loads are the 2 KB weight
-// chunks (two dwordx4 per lane, requested D - 1 rounds ahead).  The round's meta (unpacked once per row and
+// wave w computes super-blocks r R + w CB .. + CB - 1.  Per round the per-wave global loads are the weight chunks
+// (2 KB per super-block for Q4_K, 4 KB for Q6_K: two or four dwordx4 per lane, requested D - 1 rounds ahead).  The round's meta (unpacked once per row and
 // super-block by a staging thread), activation rows, activation sums and activation scales are fetched with
 // 16-byte loads a round ahead and staged in one of two LDS buffers.  Each super-block's term t of each output goes
 // to one of two LDS term buffers; the owner thread of each output folds round r - 1's terms,
 // y = fma(a[b, m], t, y) in super-block order, while round r is computed; one barrier per round.
-template <int NW, int R, int MX, int D, int EPI>
-__global__ __launch_bounds__(NW * 64) void w4a8_decode_kernel(const int8_t* __restrict__ xq,
+template <int KIND, int NW, int R, int MX, int D, int EPI>
+__global__ __launch_bounds__(NW * 64, KIND == 0 ? 1 : 2) void w4a8_decode_kernel(const int8_t* __restrict__ xq,
                                                               const float* __restrict__ a, int64_t a_sb,
                                                               const int8_t* __restrict__ xs,
                                                               const uint8_t* __restrict__ qv,
@@ -124,14 +168,18 @@ __global__ __launch_bounds__(NW * 64) void w4a8_decode_kernel(const int8_t* __re
     constexpr int LDA = RB + 16;
     constexpr int CPR = RB / 16;
     constexpr int XPT = (MX * CPR + NT - 1) / NT;
+    constexpr int WCH = KIND == 0 ? 2 : 4;        // 16-byte weight chunks per lane and super-block
     extern __shared__ __attribute__((aligned(16))) int8_t dsm[];
+    // LDS (w4a8_decode_lds): terms, then the unpacked meta, activations and activation scales
     float* terms = reinterpret_cast<float*>(dsm);                 // [2][R][M][16]
-    uint32_t* scl = reinterpret_cast<uint32_t*>(terms + 2 * R * M * 16);  // [2][R][8][16] split scales, [g][row]
+    uint32_t* scl = reinterpret_cast<uint32_t*>(terms + 2 * R * M * 16);  // [2][R][8][16], [g or window][row]: Q4_K
+                                                                  // split scales; Q6_K the window's second scale
     float* dl = reinterpret_cast<float*>(scl + 2 * R * 128);      // [2][R][16] d
-    float* dml = dl + 2 * R * 16;                                 // [2][R][16] dmin
-    int8_t* xsb = reinterpret_cast<int8_t*>(dml + 2 * R * 16);    // [2][R][M][16] split activation sums (bytes)
-    uint8_t* mnb = reinterpret_cast<uint8_t*>(xsb + 2 * R * M * 16);  // [2][R][16][8] mins (bytes)
-    int8_t* xl = reinterpret_cast<int8_t*>(mnb + 2 * R * 128);    // [2][M][LDA] activations
+    float* dml = dl + 2 * R * 16;                                 // Q4_K [2][R][16] dmin; Q6_K [2][R][8][16] the
+                                                                  // window's first scale minus its second
+    int8_t* xsb = reinterpret_cast<int8_t*>(dml + (KIND == 0 ? 2 * R * 16 : 2 * R * 128));  // Q4_K [2][R][M][16]
+    uint8_t* mnb = reinterpret_cast<uint8_t*>(xsb + (KIND == 0 ? 2 * R * M * 16 : 0));        // Q4_K [2][R][16][8]
+    int8_t* xl = reinterpret_cast<int8_t*>(mnb + (KIND == 0 ? 2 * R * 128 : 0));  // [2][M][LDA] activations
     float* al = reinterpret_cast<float*>(xl + 2 * M * LDA);       // [3][R][M] activation scales: read by the fold of
                                                                   // round r - 1 while round r + 1 is staged
     const int tstride = R * M * 16, xstride = M * LDA;
@@ -144,11 +192,13 @@ __global__ __launch_bounds__(NW * 64) void w4a8_decode_kernel(const int8_t* __re
     const int lm = lane & 15, q = lane >> 4;
     const int xch = M * CPR;
 
-    const v4u* cw = reinterpret_cast<const v4u*>(qv) + (int64_t)nt * NB * 128 + lane;
+    const v4u* cw = reinterpret_cast<const v4u*>(qv) + (int64_t)nt * NB * 64 * WCH + lane;
     const v4u* cm = reinterpret_cast<const v4u*>(meta) + (int64_t)nt * NB * 16;
+    const uint8_t* cm6 = meta + (int64_t)nt * NB * Q6_META;
 
     struct Staged {
-        v4u m;        // meta row (thread < 16 R: super-block tid / 16, row tid % 16)
+        v4u m;        // meta row (thread < 16 R: super-block tid / 16, row tid % 16); Q6_K: its 16 scales
+        uint32_t dh;  // Q6_K: the row's fp16 d
         v4i s;        // split sums (thread < R M: super-block tid / M, activation row tid % M)
         float as;     // activation scale of the same (super-block, row)
         v4i x[XPT];
@@ -156,10 +206,16 @@ __global__ __launch_bounds__(NW * 64) void w4a8_decode_kernel(const int8_t* __re
     auto stage_load = [&](int r, Staged& sg) {
         const int b0 = r * R;
         const int c = min(tid, 16 * R - 1);
-        sg.m = cm[(int64_t)min(b0 + c / 16, NB - 1) * 16 + (c & 15)];
+        if (KIND == 0) {
+            sg.m = cm[(int64_t)min(b0 + c / 16, NB - 1) * 16 + (c & 15)];
+        } else {
+            const uint8_t* mp = cm6 + (int64_t)min(b0 + c / 16, NB - 1) * Q6_META;
+            sg.m = reinterpret_cast<const v4u*>(mp)[c & 15];
+            sg.dh = reinterpret_cast<const uint16_t*>(mp + 256)[c & 15];
+        }
         const int e = min(tid, R * M - 1);
         const int bb = min(b0 + e / M, NB - 1), mm = e % M;
-        sg.s = *reinterpret_cast<const v4i*>(xs + ((int64_t)bb * M + mm) * 16);
+        if (KIND == 0) sg.s = *reinterpret_cast<const v4i*>(xs + ((int64_t)bb * M + mm) * 16);
         sg.as = a[(int64_t)bb * a_sb + mm];
         const int64_t k0 = (int64_t)r * RB;
 #pragma unroll
@@ -173,19 +229,31 @@ __global__ __launch_bounds__(NW * 64) void w4a8_decode_kernel(const int8_t* __re
         const int buf = rr & 1;
         if (tid < 16 * R) {
             const int lb = tid >> 4, row = tid & 15;
-            float d, dm;
-            int sc[8], mn[8];
-            row_meta(sg.m, d, dm, sc, mn);
+            if (KIND == 0) {
+                float d, dm;
+                int sc[8], mn[8];
+                row_meta(sg.m, d, dm, sc, mn);
 #pragma unroll
-            for (int g = 0; g < 8; g++) scl[((buf * R + lb) * 8 + g) * 16 + row] = split_scale(sc[g]);
-            *reinterpret_cast<v2u*>(&mnb[((buf * R + lb) * 16 + row) * 8]) =
-                v2u{(uint32_t)(mn[0] | (mn[1] << 8) | (mn[2] << 16) | (mn[3] << 24)),
-                    (uint32_t)(mn[4] | (mn[5] << 8) | (mn[6] << 16) | (mn[7] << 24))};
-            dl[(buf * R + lb) * 16 + row] = d;
-            dml[(buf * R + lb) * 16 + row] = dm;
+                for (int g = 0; g < 8; g++) scl[((buf * R + lb) * 8 + g) * 16 + row] = split_scale(sc[g]);
+                *reinterpret_cast<v2u*>(&mnb[((buf * R + lb) * 16 + row) * 8]) =
+                    v2u{(uint32_t)(mn[0] | (mn[1] << 8) | (mn[2] << 16) | (mn[3] << 24)),
+                        (uint32_t)(mn[4] | (mn[5] << 8) | (mn[6] << 16) | (mn[7] << 24))};
+                dl[(buf * R + lb) * 16 + row] = d;
+                dml[(buf * R + lb) * 16 + row] = dm;
+            } else {
+                int* sa = reinterpret_cast<int*>(scl) + (buf * R + lb) * 128 + row;
+                int* sb = reinterpret_cast<int*>(dml) + (buf * R + lb) * 128 + row;
+#pragma unroll
+                for (int w = 0; w < 8; w++) {
+                    const int s0 = sbyte(sg.m, 2 * w), s1 = sbyte(sg.m, 2 * w + 1);
+                    sa[16 * w] = s1;
+                    sb[16 * w] = s0 - s1;
+                }
+                dl[(buf * R + lb) * 16 + row] = f16_to_f32(sg.dh);
+            }
         }
         if (tid < R * M) {
-            *reinterpret_cast<v4i*>(&xsb[(buf * R * M + tid) * 16]) = sg.s;     // tid = lb M + m
+            if (KIND == 0) *reinterpret_cast<v4i*>(&xsb[(buf * R * M + tid) * 16]) = sg.s;     // tid = lb M + m
             al[(rr % 3) * R * M + tid] = sg.as;
         }
 #pragma unroll
@@ -194,22 +262,46 @@ __global__ __launch_bounds__(NW * 64) void w4a8_decode_kernel(const int8_t* __re
             if (cc < xch) *reinterpret_cast<v4i*>(&xl[buf * xstride + (cc / CPR) * LDA + (cc % CPR) * 16]) = sg.x[i];
         }
     };
-    auto load_w = [&](int r, v4u (*w)[2]) {
+    auto load_w = [&](int r, v4u (*w)[WCH]) {
 #pragma unroll
         for (int i = 0; i < CB; i++) {
             const int64_t b = min(r * R + wv * CB + i, NB - 1);
-            w[i][0] = __builtin_nontemporal_load(cw + b * 128);
-            w[i][1] = __builtin_nontemporal_load(cw + b * 128 + 64);
+#pragma unroll
+            for (int j = 0; j < WCH; j++) w[i][j] = __builtin_nontemporal_load(cw + b * 64 * WCH + 64 * j);
         }
     };
-    auto compute = [&](int r, v4u (*w)[2], int buf) {
+    auto compute = [&](int r, v4u (*w)[WCH], int buf) {
         float* tb = terms + (r & 1) * tstride;
         const int mrow = min(lm, M - 1);
         const int8_t* xrow = xl + buf * xstride + mrow * LDA;
 #pragma unroll
         for (int i = 0; i < CB; i++) {
             const int lb = wv * CB + i;
-            if (r * R + lb < NB) {
+            if (KIND == 1 && r * R + lb < NB) {
+                // per 32-input window: P over both sub-blocks, Pl over the first (activations of lanes q >= 2,
+                // which hold the second, zeroed): acc += sc1 P + (sc0 - sc1) Pl
+                const int* sa = reinterpret_cast<const int*>(scl) + (buf * R + lb) * 128 + 4 * q;
+                const int* sb = reinterpret_cast<const int*>(dml) + (buf * R + lb) * 128 + 4 * q;
+                v4i acc = {0, 0, 0, 0};
+                const v4i zero = {0, 0, 0, 0};
+#pragma unroll
+                for (int wn = 0; wn < 8; wn++) {
+                    const v4u& c16 = w[i][wn >> 1];
+                    const int64_t wf = (int64_t)c16[2 * (wn & 1)] | ((int64_t)c16[2 * (wn & 1) + 1] << 32);
+                    const int64_t af = *reinterpret_cast<const int64_t*>(xrow + lb * 256 + 32 * wn + 8 * q);
+                    const v4i P = __builtin_amdgcn_mfma_i32_16x16x32_i8(wf, af, zero, 0, 0, 0);
+                    const v4i Pl = __builtin_amdgcn_mfma_i32_16x16x32_i8(wf, q < 2 ? af : 0, zero, 0, 0, 0);
+                    const v4i A = *reinterpret_cast<const v4i*>(sa + 16 * wn), B = *reinterpret_cast<const v4i*>(sb + 16 * wn);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) acc[e] += __mul24(A[e], P[e]) + __mul24(B[e], Pl[e]);
+                }
+                const v4f d = *reinterpret_cast<const v4f*>(&dl[(buf * R + lb) * 16 + 4 * q]);
+                v4f t;
+#pragma unroll
+                for (int e = 0; e < 4; e++) t[e] = mul_rn(d[e], (float)acc[e]);
+                if (lm < M) *reinterpret_cast<v4f*>(&tb[(lb * M + lm) * 16 + 4 * q]) = t;
+            }
+            if (KIND == 0 && r * R + lb < NB) {
                 const uint32_t* scp = scl + (buf * R + lb) * 128;
                 v4i alo = {0, 0, 0, 0}, ahi = {0, 0, 0, 0};
 #pragma unroll
@@ -248,7 +340,7 @@ __global__ __launch_bounds__(NW * 64) void w4a8_decode_kernel(const int8_t* __re
         }
     };
 
-    v4u wr[D][CB][2];
+    v4u wr[D][CB][WCH];
     Staged sg;
 #pragma unroll
     for (int d = 0; d < D - 1; d++) load_w(d, wr[d]);
@@ -280,9 +372,11 @@ __global__ __launch_bounds__(NW * 64) void w4a8_decode_kernel(const int8_t* __re
     }
 }
 
-static size_t w4a8_decode_lds(int R, int M) {
-    return 2 * (size_t)R * M * 16 * 4 + 2 * (size_t)R * 128 * 4 + 2 * (size_t)R * 16 * 4 * 2 +
-           2 * (size_t)R * M * 16 + 2 * (size_t)R * 128 + 2 * (size_t)M * (R * 256 + 16) + 3 * (size_t)R * M * 4;
+static size_t w4a8_decode_lds(int kind, int R, int M) {
+    const size_t base = 2 * (size_t)R * M * 16 * 4 + 2 * (size_t)R * 128 * 4 + 2 * (size_t)R * 16 * 4 +
+                        2 * (size_t)M * (R * 256 + 16) + 3 * (size_t)R * M * 4;
+    return kind == 0 ? base + 2 * (size_t)R * 16 * 4 + 2 * (size_t)R * M * 16 + 2 * (size_t)R * 128
+                     : base + 2 * (size_t)R * 128 * 4;
 }
 
 // ---------------------------------------------------------------------------------------------- prefill tile
@@ -478,6 +572,166 @@ __global__ __launch_bounds__(256, 2) void w4a8_tile_kernel(const int8_t* __restr
         }
 }
 
+// ---------------------------------------------------------------------------------------------- Q6_K prefill tile
+// 64 (n) x 64 (m) output tile per 256-thread workgroup: wave wv owns weight row tile wv (16 rows) and all 64
+// activation rows (4 MFMA tiles of 16 x 16).  Staging as the Q4_K tile kernel: per stage (one super-block) the 4 row
+// tiles' 4 KB of weights and the 64 activation rows by LDS-DMA into the free buffer, the scales through registers.
+// Per 32-input window two MFMAs: P over both of its sub-blocks and Pl over the first (lanes q >= 2, which hold the
+// second, give zeros): acc += sc1 P + (sc0 - sc1) Pl, exact.
+constexpr int Q6BN = 64;
+
+template <int EPI>
+__global__ __launch_bounds__(256, 2) void w4a8_q6k_tile_kernel(const int8_t* __restrict__ xq,
+                                                               const float* __restrict__ a, int64_t a_sb,
+                                                               const uint8_t* __restrict__ qv,
+                                                               const uint8_t* __restrict__ meta,
+                                                               void* __restrict__ out, int64_t ldo,
+                                                               const int32_t* __restrict__ n_rows, int M, int N,
+                                                               int K, int tiles_m, int tiles_n) {
+    __shared__ __attribute__((aligned(16))) uint8_t Bs[2][4 * 4096];   // 4 row tiles x (4 chunks x 64 lanes x 16 B)
+    __shared__ __attribute__((aligned(16))) int8_t As[2][QBM * 256];   // swizzled activation rows
+    __shared__ __attribute__((aligned(16))) int sca[2][8][Q6BN];       // per window: second scale
+    __shared__ __attribute__((aligned(16))) int scb[2][8][Q6BN];       // per window: first scale - second
+    __shared__ __attribute__((aligned(16))) float dl[2][Q6BN];
+    __shared__ float al[2][QBM];
+
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int lm = lane & 15, q = lane >> 4;
+    int pm, pn;
+    {
+        const int total = tiles_m * tiles_n;
+        int t = blockIdx.x;
+        if ((total & 7) == 0) t = (t & 7) * (total >> 3) + (t >> 3);
+        const int per_group = 8 * tiles_n, first_m = (t / per_group) * 8, gm = min(tiles_m - first_m, 8);
+        pm = first_m + (t % per_group) % gm;
+        pn = (t % per_group) / gm;
+    }
+    const int m0 = pm * QBM, n0 = pn * Q6BN;
+    const int live = min(M, __ldg(n_rows));
+    if (m0 >= live) return;
+    const int NB = K / 256, ntiles = N / 16;
+
+    const uint8_t* wsrc[4];
+    const int8_t* xsrc[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int c = tid + 256 * i;
+        wsrc[i] = qv + ((int64_t)min(n0 / 16 + (c >> 8), ntiles - 1) * NB * 256 + (c & 255)) * 16;
+        const int r = c >> 4;
+        xsrc[i] = xq + (int64_t)min(m0 + r, M - 1) * K + (((c & 15) ^ (r & 15)) * 16);
+    }
+    auto dma = [&](int b, int buf) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int base = (256 * i + 64 * wv) * 16;
+            dma16(wsrc[i] + (int64_t)b * 4096, &Bs[buf][base]);
+            dma16(xsrc[i] + (int64_t)b * 256, &As[buf][base]);
+        }
+    };
+    // threads < 64: weight row tid's scales and d, activation row tid's scale
+    const uint8_t* msrc = meta + (int64_t)min(n0 / 16 + (tid >> 4), ntiles - 1) * NB * Q6_META;
+    const int srow = min(m0 + (tid & 63), M - 1);
+    v4u rm;
+    uint32_t rd;
+    float ra;
+    auto gmeta = [&](int b) {
+        if (tid < 64) {
+            const uint8_t* mp = msrc + (int64_t)b * Q6_META;
+            rm = reinterpret_cast<const v4u*>(mp)[tid & 15];
+            rd = reinterpret_cast<const uint16_t*>(mp + 256)[tid & 15];
+            ra = a[(int64_t)b * a_sb + srow];
+        }
+    };
+    auto smeta = [&](int buf) {
+        if (tid < 64) {
+#pragma unroll
+            for (int w = 0; w < 8; w++) {
+                const int s0 = sbyte(rm, 2 * w), s1 = sbyte(rm, 2 * w + 1);
+                sca[buf][w][tid] = s1;
+                scb[buf][w][tid] = s0 - s1;
+            }
+            dl[buf][tid] = f16_to_f32(rd);
+            al[buf][tid] = ra;
+        }
+    };
+
+    float y[4][4];
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) y[j][e] = 0.f;
+
+    gmeta(0);
+    dma(0, 0);
+    smeta(0);
+    vm_wait<0>();
+    lds_barrier();
+    for (int b = 0; b < NB; b++) {
+        const int cb = b & 1;
+        if (b + 1 < NB) {
+            gmeta(b + 1);
+            dma(b + 1, cb ^ 1);
+        }
+        v4i acc[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[j] = v4i{0, 0, 0, 0};
+        const v4i zero = {0, 0, 0, 0};
+#pragma unroll 1
+        for (int jj = 0; jj < 4; jj++) {
+            const v4u wq = *reinterpret_cast<const v4u*>(&Bs[cb][wv * 4096 + jj * 1024 + lane * 16]);
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const int wn = 2 * jj + u;
+                const int64_t wf = (int64_t)wq[2 * u] | ((int64_t)wq[2 * u + 1] << 32);
+                const v4i A = *reinterpret_cast<const v4i*>(&sca[cb][wn][16 * wv + 4 * q]);
+                const v4i B = *reinterpret_cast<const v4i*>(&scb[cb][wn][16 * wv + 4 * q]);
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int8_t* ap = &As[cb][(16 * j + lm) * 256 + (((2 * wn + (q >> 1)) ^ lm) * 16) + 8 * (q & 1)];
+                    const int64_t af = *reinterpret_cast<const int64_t*>(ap);
+                    const v4i P = __builtin_amdgcn_mfma_i32_16x16x32_i8(wf, af, zero, 0, 0, 0);
+                    const v4i Pl = __builtin_amdgcn_mfma_i32_16x16x32_i8(wf, q < 2 ? af : 0, zero, 0, 0, 0);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) acc[j][e] += __mul24(A[e], P[e]) + __mul24(B[e], Pl[e]);
+                }
+            }
+        }
+        const v4f d = *reinterpret_cast<const v4f*>(&dl[cb][16 * wv + 4 * q]);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float am = al[cb][16 * j + lm];
+#pragma unroll
+            for (int e = 0; e < 4; e++) y[j][e] = fmaf(am, mul_rn(d[e], (float)acc[j][e]), y[j][e]);
+        }
+        if (b + 1 < NB) smeta(cb ^ 1);
+        vm_wait<0>();
+        lds_barrier();
+    }
+    // D element (j, e): n = n0 + 16 wv + 4 q + e, m = m0 + 16 j + lm
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int m = m0 + 16 * j + lm;
+        const int nb = n0 + 16 * wv + 4 * q;
+        if (m < live && nb < N) {
+            if (EPI == 0) {
+                const uint32_t lo = f32_to_bf16(y[j][0]) | (f32_to_bf16(y[j][1]) << 16);
+                const uint32_t hi = f32_to_bf16(y[j][2]) | (f32_to_bf16(y[j][3]) << 16);
+                uint16_t* o = reinterpret_cast<uint16_t*>(out) + (int64_t)m * ldo + nb;
+                if ((((uintptr_t)o) & 7) == 0) {
+                    *reinterpret_cast<v2u*>(o) = v2u{lo, hi};
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; e++) o[e] = (uint16_t)f32_to_bf16(y[j][e]);
+                }
+            } else {
+                float* o = reinterpret_cast<float*>(out) + (int64_t)m * ldo + nb;
+#pragma unroll
+                for (int e = 0; e < 4; e++) o[e] = add_rn(o[e], y[j][e]);
+            }
+        }
+    }
+}
+
 }  // namespace prism
 
 using namespace prism;
@@ -512,7 +766,7 @@ extern "C" int prism_w4a8_q4k_gemm(const int8_t* xq, const float* a, int64_t a_s
     if (kernel == 1) {
         dim3 grid(Ni / 16);
 #define W4DEC(NW, R, MX, D, E)                                                                                      \
-    hipLaunchKernelGGL((w4a8_decode_kernel<NW, R, MX, D, E>), grid, dim3(NW * 64), w4a8_decode_lds(R, Mi), st, xq, a, \
+    hipLaunchKernelGGL((w4a8_decode_kernel<0, NW, R, MX, D, E>), grid, dim3(NW * 64), w4a8_decode_lds(0, R, Mi), st, xq, a, \
                        a_sb, xs, qv, meta, out, ldo, n_rows, Mi, Ni, Ki)
         if (M <= 4) {
             if (epi == 0) W4DEC(4, 8, 4, 3, 0); else W4DEC(4, 8, 4, 3, 1);
@@ -527,6 +781,55 @@ extern "C" int prism_w4a8_q4k_gemm(const int8_t* xq, const float* a, int64_t a_s
                                meta, out, ldo, n_rows, Mi, Ni, Ki, tiles_m, tiles_n);
         else
             hipLaunchKernelGGL((w4a8_tile_kernel<1>), dim3(tiles_m * tiles_n), dim3(256), 0, st, xq, a, a_sb, xs, qv,
+                               meta, out, ldo, n_rows, Mi, Ni, Ki, tiles_m, tiles_n);
+    }
+    PRISM_LAUNCH_CHECK();
+    return PRISM_OK;
+}
+
+extern "C" int prism_q6k_pack(const uint8_t* raw, uint8_t* qv, uint8_t* meta, int64_t N, int64_t K, void* stream) {
+    if (!raw || !qv || !meta) return PRISM_ERR_ARG;
+    if (N <= 0 || K <= 0 || N % 16 || K % 256 || N > (1 << 30) || K > (1 << 30)) return PRISM_ERR_SHAPE;
+    if (!PRISM_ALIGNED(qv, 16) || !PRISM_ALIGNED(meta, 16)) return PRISM_ERR_ALIGN;
+    const int64_t total = N / 16 * (K / 256) * 256;
+    hipLaunchKernelGGL(q6k_pack_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream, raw,
+                       qv, meta, (int)N, (int)K);
+    PRISM_LAUNCH_CHECK();
+    return PRISM_OK;
+}
+
+extern "C" int prism_w4a8_q6k_gemm(const int8_t* xq, const float* a, int64_t a_sb, const uint8_t* qv,
+                                   const uint8_t* meta, void* out, int64_t ldo, const int32_t* n_rows, int64_t M,
+                                   int64_t N, int64_t K, int epi, int kernel, void* stream) {
+    if (!xq || !a || !qv || !meta || !out || !n_rows) return PRISM_ERR_ARG;
+    if (epi != 0 && epi != 1) return PRISM_ERR_ARG;
+    if (M < 0 || N <= 0 || K <= 0 || N % 16 || K % 256 || ldo < N || M > (1 << 30) || N > (1 << 30) || K > (1 << 30))
+        return PRISM_ERR_SHAPE;
+    if (!PRISM_ALIGNED(xq, 16) || !PRISM_ALIGNED(qv, 16) || !PRISM_ALIGNED(meta, 16)) return PRISM_ERR_ALIGN;
+    if (kernel < -1 || kernel > 1) return PRISM_ERR_ARG;
+    if (kernel == -1) kernel = M <= 16 ? 1 : 0;
+    if (kernel == 1 && M > 16) return PRISM_ERR_ARG;
+    if (M == 0) return PRISM_OK;
+    hipStream_t st = (hipStream_t)stream;
+    const int Mi = (int)M, Ni = (int)N, Ki = (int)K;
+    if (kernel == 1) {
+        dim3 grid(Ni / 16);
+#define Q6DEC(NW, R, MX, D, E)                                                                                      \
+    hipLaunchKernelGGL((w4a8_decode_kernel<1, NW, R, MX, D, E>), grid, dim3(NW * 64), w4a8_decode_lds(1, R, Mi), st, xq, \
+                       a, a_sb, nullptr, qv, meta, out, ldo, n_rows, Mi, Ni, Ki)
+        if (M <= 4) {
+            if (epi == 0) Q6DEC(4, 4, 4, 3, 0); else Q6DEC(4, 4, 4, 3, 1);
+        } else {
+            if (epi == 0) Q6DEC(4, 4, 16, 3, 0); else Q6DEC(4, 4, 16, 3, 1);
+        }
+#undef Q6DEC
+    } else {
+        const int tiles_m = (Mi + QBM - 1) / QBM, tiles_n = (Ni + Q6BN - 1) / Q6BN;
+        if (epi == 0)
+            hipLaunchKernelGGL((w4a8_q6k_tile_kernel<0>), dim3(tiles_m * tiles_n), dim3(256), 0, st, xq, a, a_sb, qv,
+                               meta, out, ldo, n_rows, Mi, Ni, Ki, tiles_m, tiles_n);
+        else
+            hipLaunchKernelGGL((w4a8_q6k_tile_kernel<1>), dim3(tiles_m * tiles_n), dim3(256), 0, st, xq, a, a_sb, qv,
                                meta, out, ldo, n_rows, Mi, Ni, Ki, tiles_m, tiles_n);
     }
     PRISM_LAUNCH_CHECK();

@@ -1,10 +1,12 @@
-"""GGUF weight formats on the hot path: Q8_0 (32 values: fp16 scale + 32 int8) and Q4_K (256 values: fp16 d, dmin,
-12 bytes of 6-bit sub-block scales and mins, 128 bytes of 4-bit quants), as torch tensors on any device.
+"""GGUF weight formats on the hot path: Q8_0 (32 values: fp16 scale + 32 int8), Q4_K (256 values: fp16 d, dmin,
+12 bytes of 6-bit sub-block scales and mins, 128 bytes of 4-bit quants) and Q6_K (256 values: 128 bytes of low 4
+bits, 64 of high 2 bits, 16 int8 scales of 16 values, fp16 d), as torch tensors on any device.
 
 Restated from StartLux-Prism gguf.py:413-416 (block sizes), gguf_weights.py:30-46 (Q8), :56-70 (get_scale_min_k4,
-Q4_K dequantization), :100-133 (KQuant, as_q8) and :221-227 (_q8: 34-byte blocks split into the qs / d planes).
-The quantizers produce synthetic weights for tests and benchmarks; the reference itself only reads these formats
-from files (its Q8_0 quantizer as_q8 is followed here; the Q4_K quantizer is this build's own).
+Q4_K dequantization), :85-97 (Q6_K dequantization), :100-133 (KQuant, as_q8) and :221-227 (_q8: 34-byte blocks
+split into the qs / d planes).  The quantizers produce synthetic weights for tests and benchmarks; the reference
+itself only reads these formats from files (its Q8_0 quantizer as_q8 is followed here; the Q4_K and Q6_K quantizers
+are this build's own).
 """
 import dataclasses
 
@@ -14,6 +16,7 @@ QK = 32            # Q8_0 block
 QK_K = 256         # k-quant super-block
 Q8_0_BYTES = 34
 Q4_K_BYTES = 144
+Q6_K_BYTES = 210
 
 
 @dataclasses.dataclass
@@ -75,7 +78,8 @@ def scale_min_k4(s):
 
 @dataclasses.dataclass
 class KQuant:
-    """A Q4_K matrix [n, k] as its raw super-blocks: raw uint8 [n, k / 256, 144] (gguf_weights.py:100-119)."""
+    """A k-quant matrix [n, k] as its raw super-blocks: raw uint8 [n, k / 256, 144] for Q4_K, [n, k / 256, 210]
+    for Q6_K (gguf_weights.py:100-119)."""
     raw: torch.Tensor
     k: int
     type: str = "q4k"
@@ -88,7 +92,13 @@ class KQuant:
         return KQuant(self.raw.to(device), self.k, self.type)
 
     def dequant(self, dtype=torch.float32):
-        """y = (d sc) q - (dmin m) in fp32, ggml's order of products (gguf_weights.py:63-70)."""
+        """Q4_K: y = (d sc) q - (dmin m) in fp32, ggml's order of products (gguf_weights.py:63-70).  Q6_K:
+        y = (d sc) (q - 32) (:85-97)."""
+        if self.type == "q6k":
+            b = self.raw.reshape(-1, Q6_K_BYTES)
+            sc = b[:, 192:208].contiguous().view(torch.int8).float()
+            d = b[:, 208:210].contiguous().view(torch.float16).float()
+            return ((d * sc).repeat_interleave(16, 1) * q6k_values(b).float()).reshape(self.raw.shape[0], self.k).to(dtype)
         b = self.raw.reshape(-1, Q4_K_BYTES)
         d = b[:, 0:2].contiguous().view(torch.float16).float()
         dmin = b[:, 2:4].contiguous().view(torch.float16).float()
@@ -133,3 +143,37 @@ def quantize_q4k(w):
                      dmh.view(torch.uint8).reshape(n, k // QK_K, 2).to(torch.int32),
                      s12, qs.reshape(n, k // QK_K, 128)], -1).to(torch.uint8)
     return KQuant(raw.contiguous(), k)
+
+
+def q6k_values(b):
+    """uint8 [..., 210] block_q6_K bytes -> int32 [..., 256] values q - 32 in k order: per half of 128, the four
+    32-value parts from the low / high nibbles of ql and the 2-bit fields of qh (gguf_weights.py:85-97)."""
+    ql, qh = b[..., 0:128].to(torch.int32), b[..., 128:192].to(torch.int32)
+    parts = []
+    for h in range(2):
+        lo, hi, top = ql[..., 64 * h:64 * h + 32], ql[..., 64 * h + 32:64 * h + 64], qh[..., 32 * h:32 * h + 32]
+        parts += [(lo & 0xF) | ((top & 3) << 4), (hi & 0xF) | (((top >> 2) & 3) << 4),
+                  (lo >> 4) | (((top >> 4) & 3) << 4), (hi >> 4) | (((top >> 6) & 3) << 4)]
+    return torch.cat(parts, -1) - 32
+
+
+def quantize_q6k(w):
+    """fp32 [n, k] -> KQuant (type "q6k"): this build's Q6_K quantizer.  Per sub-block j of 16: scale_j =
+    max|x| / 31; d = fp16(max scale / 127); sc_j = clamp(rint(scale_j / d), -128, 127);
+    q = clamp(rint(x / (d sc_j)), -32, 31); stored as q + 32 in ggml's block_q6_K layout."""
+    n, k = w.shape
+    nb = k // QK_K
+    x = w.to(torch.float32).reshape(n, nb, 16, 16)
+    scale = x.abs().amax(-1) / 31.0
+    dh = (scale.amax(-1) / 127.0).half()
+    d = dh.float()[..., None]
+    sc = torch.where(d > 0, torch.round(scale / torch.where(d > 0, d, 1.0)), torch.zeros_like(scale)).clamp(-128, 127)
+    step = (d * sc)[..., None]
+    q = torch.where(step != 0, torch.round(x / torch.where(step != 0, step, 1.0)), torch.zeros_like(x))
+    Q = (q.clamp(-32, 31) + 32).to(torch.int32).reshape(n, nb, 2, 4, 32)       # [n, nb, half, part, l]
+    ql = torch.cat([(Q[:, :, :, 0] & 15) | ((Q[:, :, :, 2] & 15) << 4),
+                    (Q[:, :, :, 1] & 15) | ((Q[:, :, :, 3] & 15) << 4)], -1)     # [n, nb, half, 64]
+    qh = (Q[:, :, :, 0] >> 4) | ((Q[:, :, :, 1] >> 4) << 2) | ((Q[:, :, :, 2] >> 4) << 4) | ((Q[:, :, :, 3] >> 4) << 6)
+    raw = torch.cat([ql.reshape(n, nb, 128), qh.reshape(n, nb, 64), sc.to(torch.int32) & 0xFF,
+                     dh.view(torch.uint8).reshape(n, nb, 2).to(torch.int32)], -1).to(torch.uint8)
+    return KQuant(raw.contiguous(), k, "q6k")

@@ -6,11 +6,13 @@ and meaning.  Arithmetic (kernels/w4a8.py:14-22): per super-block b of 256 input
 acc = sum_g sc (xq . q)_g, mins = sum_g m S_g (int32, exact), t = RN(d float(acc)), t = fma(-dmin, float(mins), t),
 y = fma(a[b, m], t, y); then bf16(y) or out += y.
 
-W4 here holds the MFMA-native device layout made by repack (a byte permutation of the GGUF block_q4_K bytes, 144
-bytes per row and 256 inputs, no size overhead): qv uint8 [n/16, k/256, 2, 64, 16] (per 16-row tile and super-block
-2 KB of nibbles, each lane's 16 bytes unpacking to its MFMA operands) and meta uint8 [n/16, k/256, 16, 16] (per row
-the block's d, dmin and 12 bytes of 6-bit scales and mins).  Rows are sliced and concatenated in whole 16-row
-tiles.  Only Q4_K is provided (Q6_K raises).
+W4 here holds the MFMA-native device layout made by repack.  Q4_K: a byte permutation of the GGUF block_q4_K bytes
+(144 bytes per row and 256 inputs, no size overhead): qv uint8 [n/16, k/256, 2, 64, 16] (per 16-row tile and
+super-block 2 KB of nibbles, each lane's 16 bytes unpacking to its MFMA operands) and meta uint8 [n/16, k/256, 16,
+16] (per row the block's d, dmin and 12 bytes of 6-bit scales and mins).  Q6_K: the values as int8 q - 32, as the
+reference's repack keeps them (kernels/w4a8.py:82-90): qv int8 [n/16, k/256, 4, 64, 16] (each lane's 16 bytes two
+32-input MFMA operands) and meta uint8 [n/16, k/256, 288] (16 rows' 16 int8 scales, then their fp16 d).  Rows are
+sliced and concatenated in whole 16-row tiles; a fused projection mixing the kinds is split into segments.
 """
 from __future__ import annotations
 
@@ -19,16 +21,16 @@ from typing import NamedTuple
 import torch
 
 from . import _lib as L
-from .gguf_formats import KQuant, Q4_K_BYTES
+from .gguf_formats import KQuant, Q4_K_BYTES, Q6_K_BYTES
 
 QK_K = 256
 KERNELS = {"auto": -1, "tile": 0, "decode": 1}
 
 
 class W4(NamedTuple):
-    kind: str               # "q4k"
-    qv: torch.Tensor        # uint8 [n/16, k/256, 2, 64, 16]
-    meta: torch.Tensor      # uint8 [n/16, k/256, 16, 16]
+    kind: str               # "q4k" or "q6k"
+    qv: torch.Tensor        # q4k: uint8 [n/16, k/256, 2, 64, 16]; q6k: int8 [n/16, k/256, 4, 64, 16]
+    meta: torch.Tensor      # q4k: uint8 [n/16, k/256, 16, 16]; q6k: uint8 [n/16, k/256, 288]
     n: int
     k: int
 
@@ -47,11 +49,18 @@ class W4(NamedTuple):
 
 
 def repack(kq: KQuant) -> W4:
-    """A Q4_K KQuant (raw uint8 [n, k/256, 144], on the GPU) -> W4."""
-    if kq.type != "q4k":
-        raise ValueError(f"k-quant type {kq.type}: this build provides Q4_K")
+    """A KQuant (raw uint8 [n, k/256, 144] Q4_K or [n, k/256, 210] Q6_K, on the GPU) -> W4."""
+    if kq.type not in ("q4k", "q6k"):
+        raise ValueError(f"k-quant type {kq.type}: Q4_K and Q6_K are supported")
     raw = kq.raw.contiguous()
     n, k = raw.shape[0], kq.k
+    if kq.type == "q6k":
+        if raw.dtype != torch.uint8 or raw.shape[-1] != Q6_K_BYTES:
+            raise ValueError("raw Q6_K blocks expected")
+        qv = torch.empty(n // 16, k // 256, 4, 64, 16, dtype=torch.int8, device=raw.device)
+        meta = torch.empty(n // 16, k // 256, 288, dtype=torch.uint8, device=raw.device)
+        L.call("prism_q6k_pack", L.ptr(raw), L.ptr(qv), L.ptr(meta), n, k, L.stream_of(raw))
+        return W4("q6k", qv, meta, n, k)
     if raw.dtype != torch.uint8 or raw.shape[-1] != Q4_K_BYTES:
         raise ValueError("raw Q4_K blocks expected")
     qv = torch.empty(n // 16, k // 256, 2, 64, 16, dtype=torch.uint8, device=raw.device)
@@ -103,8 +112,8 @@ def gemm_segs(xq, a, xs, segs, out, n_rows, epi=0, pdl=0):
 
 def gemm(xq, a, xs, w: W4, out, n_rows, epi=0, cfg=None, pdl=0, kernel="auto"):
     """xq int8 [M, K]; a fp32 [K/256, M] (one scale per 256 inputs), [1, M] or [M] (one per token); xs int8
-    [K/256, M, 16] split per-32 sums -> out (epi 0: bf16 [M, >= n]; epi 1: fp32, out += y).  n_rows: device int32
-    [1]; rows >= n_rows[0] untouched."""
+    [K/256, M, 16] split per-32 sums (Q4_K's mins; Q6_K does not read it) -> out (epi 0: bf16 [M, >= n]; epi 1: fp32,
+    out += y).  n_rows: device int32 [1]; rows >= n_rows[0] untouched."""
     if epi not in (0, 1):
         raise NotImplementedError(f"epilogue {epi}")
     M, K = xq.shape
@@ -120,13 +129,17 @@ def gemm(xq, a, xs, w: W4, out, n_rows, epi=0, cfg=None, pdl=0, kernel="auto"):
         if a.shape[0] != K // QK_K or a.shape[1] < M or a.stride(1) != 1:
             raise ValueError("a must be [K/256, M]")
         a_sb = a.stride(0)
+    want = torch.bfloat16 if epi == 0 else torch.float32
+    if out.dtype != want or out.shape[0] < M or out.shape[1] < w.n or out.stride(1) != 1:
+        raise ValueError(f"out must be {want} [>= {M}, >= {w.n}] with unit column stride")
+    if w.kind == "q6k":              # no mins: xs is not read
+        L.call("prism_w4a8_q6k_gemm", L.ptr(xq), L.ptr(a), a_sb, L.ptr(w.qv), L.ptr(w.meta), L.ptr(out),
+               out.stride(0), L.ptr(n_rows), M, w.n, K, epi, KERNELS[kernel], L.stream_of(xq))
+        return
     if xs.dtype != torch.int8 or tuple(xs.shape[::2]) != (K // QK_K, 16) or not xs.is_contiguous():
         raise ValueError("xs must be contiguous int8 [K/256, M, 16]")
     Mx = xs.shape[1]
     if Mx != M:
         raise ValueError("xs rows must equal xq rows")
-    want = torch.bfloat16 if epi == 0 else torch.float32
-    if out.dtype != want or out.shape[0] < M or out.shape[1] < w.n or out.stride(1) != 1:
-        raise ValueError(f"out must be {want} [>= {M}, >= {w.n}] with unit column stride")
     L.call("prism_w4a8_q4k_gemm", L.ptr(xq), L.ptr(a), a_sb, L.ptr(xs), L.ptr(w.qv), L.ptr(w.meta), L.ptr(out),
            out.stride(0), L.ptr(n_rows), M, w.n, K, epi, KERNELS[kernel], L.stream_of(xq))

@@ -25,3 +25,14 @@ def q8_weights(N, K, seed):
 
 def int8_acts(M, K, seed):
     return O.quant_rows_i8(acts_bf16(M, K, seed))
+
+
+def q6k_random_blocks(N, NB, seed):
+    """Arbitrary block_q6_K bytes (every bit pattern of ql, qh and the int8 scales, -128 included) with finite
+    positive fp16 d: the GEMM takes the file's bytes as they are."""
+    g = rng(seed)
+    b = g.integers(0, 256, (N, NB, 210), dtype=np.uint8)
+    b[..., 192] = 0x80                                    # one scale of -128 per super-block
+    d = (g.random((N, NB)) * 1e-3 + 1e-5).astype(np.float16)
+    b[..., 208:210] = d.view(np.uint8).reshape(N, NB, 2)
+    return b

@@ -9,7 +9,7 @@ import pytest
 import torch
 
 import oracle as O
-from _inputs import acts_bf16, q8_weights, rng, weights_f32
+from _inputs import acts_bf16, q6k_random_blocks, q8_weights, rng, weights_f32
 
 F = fractions.Fraction
 
@@ -337,3 +337,76 @@ def test_w4a8_integer_sums_and_error_bound():
     o_tok = O.w4a8_gemm(xq, np.repeat(a[:1], K // 256, 0), xs, W, epi=0)
     o_b = O.w4a8_gemm(xq, a[0].copy(), xs, W, epi=0)
     assert np.array_equal(o_tok, o_b)                   # a [M] broadcast == a [K/256, M] of equal rows
+
+
+# --------------------------------------------------------------------------------------------------------- Q6_K
+def _np_q6k_values(blocks):
+    """The reference's reading of block_q6_K (kernels/w4a8.py:82-90): per half, the four 32-value parts built from
+    ql low / ql high nibbles and the 2-bit fields of qh, minus 32."""
+    ql = blocks[..., 0:128].astype(np.int32)
+    qh = blocks[..., 128:192].astype(np.int32)
+    parts = []
+    for h in range(2):
+        lo, hi, top = ql[..., 64 * h:64 * h + 32], ql[..., 64 * h + 32:64 * h + 64], qh[..., 32 * h:32 * h + 32]
+        parts += [(lo & 0xF) | ((top & 3) << 4), (hi & 0xF) | (((top >> 2) & 3) << 4),
+                  (lo >> 4) | (((top >> 4) & 3) << 4), (hi >> 4) | (((top >> 6) & 3) << 4)]
+    return np.concatenate(parts, -1) - 32                # [N, NB, 256]
+
+
+def test_q6k_layout_dequant_and_repack():
+    N, NB = 7, 3
+    blocks = q6k_random_blocks(N, NB, 51)
+    v = _np_q6k_values(blocks)
+    W = O.q6k_repack(blocks)
+    assert np.array_equal(W["q"], v.reshape(N, NB * 256).astype(np.int8))
+    sc = blocks[..., 192:208].view(np.int8)
+    assert np.array_equal(W["sc"], sc.transpose(1, 0, 2))
+    d = blocks[..., 208:210].copy().view(np.float16)[..., 0].astype(np.float32)
+    assert np.array_equal(W["d"], d.T)
+    want = (d[..., None] * sc.astype(np.float32)).astype(np.float32).repeat(16, -1) * v.astype(np.float32)
+    assert np.array_equal(O.q6k_dequant(blocks), want.reshape(N, NB * 256))
+
+
+def test_q6k_quantizer_round_trip_and_torch():
+    from prism_amd import gguf_formats as GF
+    w = weights_f32(6, 512, seed=52)
+    blocks = O.q6k_quantize(w)
+    v = _np_q6k_values(blocks)
+    assert v.min() >= -32 and v.max() <= 31
+    deq = O.q6k_dequant(blocks)
+    d = blocks[..., 208:210].copy().view(np.float16)[..., 0].astype(np.float32)
+    eff = (d[..., None] * blocks[..., 192:208].view(np.int8)).reshape(6, 32)          # each sub-block's step
+    err = np.abs(deq - w).reshape(6, 32, 16)
+    wa = np.abs(w).reshape(6, 32, 16)
+    clamped = wa > 31.5 * eff[..., None]
+    assert ((err <= 0.5 * eff[..., None] * (1 + 1e-6)) | clamped).all()
+    assert (err[clamped] <= (wa - 31 * eff[..., None])[clamped] * (1 + 1e-6)).all()
+    assert err.mean() < 0.3 * eff.mean()
+    t = GF.quantize_q6k(torch.from_numpy(w))
+    assert np.array_equal(t.raw.numpy(), blocks)
+    assert np.array_equal(t.dequant().numpy(), deq)
+
+
+def test_w4a8_q6k_integer_sums_and_error_bound():
+    N, K, M = 16, 768, 5
+    blocks = q6k_random_blocks(N, K // 256, 53)
+    W = O.q6k_repack(blocks)
+    x = O.bf16_to_f32(acts_bf16(M, K, seed=54))
+    xq, a, _ = O.quant_rows_g(x, 256)
+    out, acc = O.w4a8_gemm_q6k(xq, a, W, epi=1, out=np.zeros((M, N), np.float32), sums=True)
+    P = np.einsum("mbhk,nbhk->mnbh", xq.reshape(M, K // 256, 16, 16).astype(np.int64),
+                  W["q"].reshape(N, K // 256, 16, 16).astype(np.int64))
+    sc = W["sc"].transpose(1, 0, 2).astype(np.int64)          # [N, NB, 16]
+    assert np.array_equal(acc, (P * sc[None]).sum(-1))
+    t = W["d"].T[None].astype(np.float64) * acc
+    exact = (a.T[:, None, :].astype(np.float64) * t).sum(-1)
+    mag = (np.abs(a.T[:, None, :].astype(np.float64)) * np.abs(t)).sum(-1)
+    assert np.all(np.abs(out - exact) <= 4 * (K // 256 + 2) * 2.0 ** -24 * mag)
+    m, n = 2, 9                                               # one element replayed: mul then fma per super-block
+    y = np.float32(0)
+    for b in range(K // 256):
+        y = np.float32(O.fmaf(a[b, m], np.float32(np.float32(W["d"][b, n]) * np.float32(acc[m, n, b])), y))
+    assert out[m, n] == y
+    assert np.array_equal(O.w4a8_gemm_q6k(xq, a, W, epi=0), O.bf16_bits(out))
+    o_tok = O.w4a8_gemm_q6k(xq, np.repeat(a[:1], K // 256, 0), W, epi=0)
+    assert np.array_equal(o_tok, O.w4a8_gemm_q6k(xq, a[0].copy(), W, epi=0))
