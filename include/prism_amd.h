@@ -81,7 +81,7 @@ PRISM_API int prism_quant_rows_g(const uint16_t* x, int64_t ldx, int8_t* xq, flo
  * a int8 [M, K]; a_s fp32, element (m, g) at a_s[m * as_sm + g * as_sg] (as_sg = 0: one scale per token);
  * w int8 [N, K]; w_s [N, K / gk], fp16 bits (ws_fp16 = 1, Q8_0's own block scales) or fp32 (ws_fp16 = 0);
  * out row stride ldo (elements).  kernel: -1 picks by shape; 0 the tile kernel; 1 the decode kernel (gk == 32,
- * M <= 64).  Needs K % 32 == 0, gk % 32 == 0, K % gk == 0, N % 16 == 0, 16-byte aligned a and w.
+ * M <= 64; per channel any M).  Needs K % 32 == 0, gk % 32 == 0, K % gk == 0, N % 16 == 0, 16-byte aligned a and w.
  */
 PRISM_API int prism_w8a8_gemm(const int8_t* a, const float* a_s, int64_t as_sm, int64_t as_sg, const int8_t* w,
                     const void* w_s, int ws_fp16, void* out, int64_t ldo, const int32_t* n_rows, int64_t M,
@@ -110,7 +110,8 @@ PRISM_API int prism_i8_pack(const int8_t* w, int8_t* qt, int64_t N, int64_t K, v
  * P = sum_k a w (int32, exact), y = RN(RN(float(P) a_s[m]) w_s[n]); epi 0 bf16(y), epi 1 out = RN(out + y).
  * a int8 [M, K]; a_s fp32, row m at a_s[m * as_sm]; w_s fp32 [N] (fp16 when ws_fp16); out row stride ldo (a
  * multiple of 4, out 8-byte aligned for bf16, 16 for fp32).  kernel: -1 picks by M; 0 the tile kernel; 1 the
- * split-K decode kernel (M <= 64).  Needs N % 16 == 0, K % 64 == 0, K <= 131072 (int32 sums stay exact).
+ * split-K decode kernel (64 rows per workgroup, grid rows beyond: the choice for narrow projections).  Needs
+ * N % 16 == 0, K % 64 == 0, K <= 131072 (int32 sums stay exact).
  * prism_w8a8_gemm with gk == K runs the same kernels on row-major weights.
  */
 PRISM_API int prism_w8a8_pc_packed_gemm(const int8_t* a, const float* a_s, int64_t as_sm, const int8_t* qt,
@@ -122,7 +123,8 @@ PRISM_API int prism_w8a8_pc_packed_gemm(const int8_t* a, const float* a_s, int64
  * prism_w8a8_gemm with gk = 32 (kernels/w8a8.py:64-85), the engine entry kernels/w8a8.py:183-231.
  * a int8 [M, K]; a_s fp32, row m at a_s[m * as_sm]; qt / dt from prism_q8_0_pack; out as prism_w8a8_gemm.
  * kernel: -1 picks by M; 0 the prefill tile kernel; 1 the decode kernels (M <= 64: M <= 16 folds through LDS,
- * larger M as kernel 2); 2 the register-fold kernel, one wave per 16 x 16 output tile (M <= 64).
+ * larger M as kernel 2); 2 the register-fold kernel, one wave per 16 x 16 output tile (any M up to 65535 x 16: the
+ * choice for narrow projections, whose few 256 x 256 tiles leave CUs idle).
  * Needs K % 128 == 0.
  */
 PRISM_API int prism_w8a8_q8_0_packed_gemm(const int8_t* a, const float* a_s, int64_t as_sm, const int8_t* qt,

@@ -537,7 +537,7 @@ static int launch_w8a8(int kernel, const int8_t* a, const float* a_s, int64_t as
                        const void* w_s, void* out, int64_t ldo, const int32_t* n_rows, int M, int N, int K, int gk,
                        hipStream_t st) {
     // per channel (one group): the int8 MFMA GEMMs with an epilogue (w8a8_pc.hip)
-    if (gk == K && K % 64 == 0 && ldo % 4 == 0 && PRISM_ALIGNED(out, EPI ? 16 : 8) && (kernel == 0 || M <= 64))
+    if (gk == K && K % 64 == 0 && ldo % 4 == 0 && PRISM_ALIGNED(out, EPI ? 16 : 8))
         return launch_w8a8_pc(kernel, false, a, a_s, as_sm, w, w_s, WS16, out, ldo, n_rows, M, N, K, EPI, st);
     if (kernel == 1) {
         dim3 grid(N / 16);
@@ -580,7 +580,7 @@ extern "C" int prism_w8a8_gemm(const int8_t* a, const float* a_s, int64_t as_sm,
     // per channel on the int8 MFMA kernels: one group, 64-input stages, vector epilogue stores
     const bool pc = gk == K && K % 64 == 0 && ldo % 4 == 0 && PRISM_ALIGNED(out, epi ? 16 : 8);
     if (kernel == -1) kernel = ((gk == 32 || pc) && M <= 64) ? 1 : 0;
-    if (kernel == 1 && ((gk != 32 && !pc) || M > 64)) return PRISM_ERR_ARG;
+    if (kernel == 1 && ((gk != 32 && !pc) || (!pc && M > 64) || M > 65535 * 64)) return PRISM_ERR_ARG;
     if (M == 0) return PRISM_OK;
     const bool asg = as_sg != 0, ws16 = ws_fp16 != 0;
     hipStream_t st = (hipStream_t)stream;

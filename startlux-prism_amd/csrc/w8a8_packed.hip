@@ -385,8 +385,9 @@ __global__ __launch_bounds__(256, 2) void w8a8_packed_tile_kernel(const int8_t* 
         }
 }
 
-// ---------------------------------------------------------------------------------------------- mid (17..64 rows)
-// One wave (one workgroup) per (16 activation rows, 16-row weight tile), walking every block pair in order; the
+// ---------------------------------------------------------------------------------------------- mid
+// From 17 rows (and for narrow projections at any row count, where the tile kernel's 256 x 256 tiles leave most CUs
+// idle): one wave (one workgroup) per (16 activation rows, 16-row weight tile), walking every block pair in order; the
 // m-tiles of one weight tile are grid rows blockIdx.y of the same XCD, so their weight chunks come from HBM once.  Per pair a lane
 // loads its weight chunk slot (16 bytes), the two 8-byte activation pieces of its row and the block scales of its 4
 // output rows, PD pairs ahead; each block's int32 sums come from one v_mfma_i32_16x16x32_i8 with a zero accumulator
@@ -553,7 +554,8 @@ extern "C" int prism_w8a8_q8_0_packed_gemm(const int8_t* a, const float* a_s, in
     if (!PRISM_ALIGNED(a, 16) || !PRISM_ALIGNED(qt, 16) || !PRISM_ALIGNED(dt, 16)) return PRISM_ERR_ALIGN;
     if (kernel < -1 || kernel > 2) return PRISM_ERR_ARG;
     if (kernel == -1) kernel = M <= 64 ? 1 : 0;
-    if ((kernel == 1 || kernel == 2) && M > 64) return PRISM_ERR_ARG;
+    if (kernel == 1 && M > 64) return PRISM_ERR_ARG;
+    if (kernel == 2 && M > 65535 * 16) return PRISM_ERR_SHAPE;         // grid rows: one per 16 activation rows
     if (M == 0) return PRISM_OK;
     hipStream_t st = (hipStream_t)stream;
     if (epi == 0)

@@ -166,7 +166,9 @@ __global__ __launch_bounds__(256, 1) void w8a8_pc_tile_kernel(const int8_t* __re
 }
 
 // ---------------------------------------------------------------------------------------------- decode
-// M <= 16 MT.  One workgroup per G 16-row weight tiles; wave w takes the 64-input chunks w, w + NW, ... of every
+// Rows r0 .. r0 + 16 MT - 1 with r0 = 16 MT blockIdx.y (grid rows cover M beyond 64: for narrow projections, whose
+// few 256 x 256 tiles leave the tile kernel's CUs idle, the weight tiles then come from L2 / MALL once per 64 rows).
+// One workgroup per G 16-row weight tiles; wave w takes the 64-input chunks w, w + NW, ... of every
 // tile (the int32 sums are exact in any order), PD chunks in flight in registers.  Per chunk a lane loads 16 bytes
 // of each tile's weights (packed: the chunk's lane slot, 1 KB per wave instruction; row-major: row l % 16, inputs
 // 16 q .. + 15) and the matching 2 x 8 activation bytes of its row per m-tile, reused across the G tiles; two
@@ -182,9 +184,10 @@ __global__ __launch_bounds__(1024) void w8a8_pc_decode_kernel(const int8_t* __re
     constexpr int PD = MT <= 2 ? 4 : 2;
     extern __shared__ __attribute__((aligned(16))) v4i red[];          // [NW][G][MT][64]
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, NW = blockDim.x >> 6;
-    const int nt0 = blockIdx.x * G;
+    const int nt0 = blockIdx.x * G, r0 = 16 * MT * blockIdx.y;
     const int KP = K / 64, NT = N / 16;
     const int live = min(M, __ldg(n_rows));
+    if (r0 >= live) return;                                             // the whole workgroup: before any barrier
     const int lm = lane & 15, q = lane >> 4;
 
     const int8_t* wb[G];
@@ -195,7 +198,7 @@ __global__ __launch_bounds__(1024) void w8a8_pc_decode_kernel(const int8_t* __re
     }
     const int8_t* ab[MT];
 #pragma unroll
-    for (int u = 0; u < MT; u++) ab[u] = a + (int64_t)min(16 * u + lm, M - 1) * K + (WPACK ? 8 * q : 16 * q);
+    for (int u = 0; u < MT; u++) ab[u] = a + (int64_t)min(r0 + 16 * u + lm, M - 1) * K + (WPACK ? 8 * q : 16 * q);
 
     struct Chunk {
         v4i w[G];
@@ -255,7 +258,7 @@ __global__ __launch_bounds__(1024) void w8a8_pc_decode_kernel(const int8_t* __re
     __syncthreads();
     for (int idx = tid; idx < G * MT * 64; idx += blockDim.x) {
         const int g = idx / (MT * 64), u = (idx >> 6) % MT, l = idx & 63;
-        const int m = 16 * u + (l & 15), t = nt0 + g;
+        const int m = r0 + 16 * u + (l & 15), t = nt0 + g;
         if (m >= live || t >= NT) continue;
         v4i P = red[idx];
         for (int v = 1; v < NW; v++) {
@@ -288,18 +291,19 @@ static void pc_allow(F* fn, size_t bytes) {
     (void)hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
 }
 
-// Per-channel launch: kernel 1 the decode kernel (M <= 64), else the tile kernel.  The caller has checked
+// Per-channel launch: kernel 1 the decode kernel (up to 64 rows per workgroup, grid rows beyond), else the tile
+// kernel.  The caller has checked
 // K % 64 == 0, 16-byte aligned a / w, ldo % 4 == 0 and an 8 / 16-byte aligned out.
 int launch_w8a8_pc(int kernel, bool wpack, const int8_t* a, const float* a_s, int64_t as_sm, const int8_t* w,
                    const void* w_s, bool ws16, void* out, int64_t ldo, const int32_t* n_rows, int M, int N, int K,
                    int epi, hipStream_t st) {
     if (kernel == 1) {
-        const int MT = (M + 15) / 16;
+        const int MT = min(4, (M + 15) / 16);
         const int G = (N % 32 == 0) ? 2 : 1;
         const int KP = K / 64;
         int nw = min(16, max(1, KP / 4));
         const size_t lds = (size_t)nw * G * MT * 64 * sizeof(v4i);
-        dim3 grid((unsigned)(N / (16 * G)));
+        dim3 grid((unsigned)(N / (16 * G)), (unsigned)((M + 16 * MT - 1) / (16 * MT)));
 #define PDL(GV, MTV, WP, W16, E)                                                                                   \
     hipLaunchKernelGGL((w8a8_pc_decode_kernel<GV, MTV, WP, W16, E>), grid, dim3(64 * nw), lds, st, a, a_s, as_sm, w, \
                        w_s, out, ldo, n_rows, M, N, K)
@@ -353,7 +357,7 @@ extern "C" int prism_w8a8_pc_packed_gemm(const int8_t* a, const float* a_s, int6
         return PRISM_ERR_ALIGN;
     if (kernel < -1 || kernel > 1) return PRISM_ERR_ARG;
     if (kernel == -1) kernel = M <= 64 ? 1 : 0;
-    if (kernel == 1 && M > 64) return PRISM_ERR_ARG;
+    if (kernel == 1 && M > 65535 * 64) return PRISM_ERR_SHAPE;           // grid rows: one per 64 activation rows
     if (M == 0) return PRISM_OK;
     return launch_w8a8_pc(kernel, true, a, a_s, as_sm, qt, w_s, ws_fp16 != 0, out, ldo, n_rows, (int)M, (int)N,
                           (int)K, epi, (hipStream_t)stream);

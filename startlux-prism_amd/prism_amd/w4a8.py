@@ -21,6 +21,7 @@ from typing import NamedTuple
 import torch
 
 from . import _lib as L
+from . import dispatch
 from .gguf_formats import KQuant, Q4_K_BYTES, Q6_K_BYTES
 
 QK_K = 256
@@ -132,6 +133,9 @@ def gemm(xq, a, xs, w: W4, out, n_rows, epi=0, cfg=None, pdl=0, kernel="auto"):
     want = torch.bfloat16 if epi == 0 else torch.float32
     if out.dtype != want or out.shape[0] < M or out.shape[1] < w.n or out.stride(1) != 1:
         raise ValueError(f"out must be {want} [>= {M}, >= {w.n}] with unit column stride")
+    if kernel == "auto":             # the MI355X table's choice for the shape, where valid (dispatch.w4a8_kernel)
+        c = dispatch.w4a8_kernel(w.kind, w.n, K, M)
+        kernel = c if c == "tile" or (c == "decode" and M <= 16) else "auto"
     if w.kind == "q6k":              # no mins: xs is not read
         L.call("prism_w4a8_q6k_gemm", L.ptr(xq), L.ptr(a), a_sb, L.ptr(w.qv), L.ptr(w.meta), L.ptr(out),
                out.stride(0), L.ptr(n_rows), M, w.n, K, epi, KERNELS[kernel], L.stream_of(xq))

@@ -18,6 +18,7 @@ from typing import NamedTuple
 import torch
 
 from . import _lib as L
+from . import dispatch
 from .quant import quant_rows  # noqa: F401  (re-exported: kernels/w8a8.py:264)
 
 KERNELS = {"auto": -1, "tile": 0, "decode": 1, "mid": 2}
@@ -129,8 +130,18 @@ def gemm(a, a_s, w, w_s, out, n_rows, gk, epi=0, outs=None, cfg=None, slots=None
     return None
 
 
+def _tabled(kernel, N, K, M, gk):
+    """kernel "auto": the MI355X table's choice for the shape (dispatch.w8a8_kernel) where it is valid at M."""
+    if kernel != "auto":
+        return kernel
+    c = dispatch.w8a8_kernel(N, K, M, gk)
+    ok = c == "tile" or (c == "decode" and (M <= 64 or gk == K)) or (c == "mid" and gk == 32)
+    return c if ok else "auto"
+
+
 def _gemm_packed(a, a_s, w, out, n_rows, gk, epi, kernel):
     M, K = a.shape
+    kernel = _tabled(kernel, w.n, K, M, gk)
     if gk != 32 or (w.n, w.k) != (w.n, K) or w.k != K:
         raise ValueError("packed Q8_0 weights: gk must be 32 and K must match")
     if a.dtype != torch.int8 or not a.is_contiguous():
@@ -147,6 +158,7 @@ def _gemm_packed(a, a_s, w, out, n_rows, gk, epi, kernel):
 
 def _gemm_pc_packed(a, a_s, w, out, n_rows, gk, epi, kernel):
     M, K = a.shape
+    kernel = _tabled(kernel, w.n, K, M, gk)
     if gk != K or w.k != K:
         raise ValueError("packed per-channel weights: gk must equal K and K must match")
     if a.dtype != torch.int8 or not a.is_contiguous():

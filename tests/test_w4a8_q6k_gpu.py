@@ -1,7 +1,8 @@
 """GPU parity of the W4A8 GEMM on Q6_K weights (kernels/w4a8.py:19-20, gemm_ref :193-197) against the CPU oracle,
 bit for bit: the load-time pack's layout, bf16 stores and fp32 residual adds from the decode and tile kernels, one
 activation scale per 256 inputs or per token, live rows, blocks of every bit pattern (negative and -128 scales), the
-integer super-block sums, and a fused projection mixing Q4_K and Q6_K segments."""
+integer super-block sums, a fused projection mixing Q4_K and Q6_K segments, and the load step from a GGUF tensor's
+bytes (prism_amd.weights) for Q8_0, Q4_K and Q6_K."""
 import numpy as np
 import pytest
 import torch
@@ -129,3 +130,32 @@ def test_mixed_segments(dev):
                 O.w4a8_gemm_q6k(xq, a, O.q6k_repack(r)))
         assert np.array_equal(got[:, off:off + n], want), kind
         off += n
+
+
+@pytest.mark.parametrize("ggml_type", [8, 12, 14])
+def test_from_gguf_bytes(dev, ggml_type):
+    """prism_amd.weights.from_gguf: a tensor's GGUF bytes (ggml dims [inputs, outputs]) to the device operand, then
+    the GEMM bit-equal to the oracle on the same bytes."""
+    from prism_amd import w4a8 as KW4
+    from prism_amd import w8a8 as KW
+    from prism_amd import weights as PW
+    N, K, M = 64, 1024, 5
+    w = weights_f32(N, K, seed=80 + ggml_type)
+    x = O.bf16_to_f32(acts_bf16(M, K, seed=90))
+    out = torch.zeros(M, N, dtype=torch.bfloat16, device=dev)
+    if ggml_type == 8:
+        qs, d = O.q8_0_quantize(w)                          # block_q8_0: fp16 d, then 32 int8
+        raw = np.concatenate([d.reshape(N, K // 32, 1).view(np.uint8), qs.view(np.uint8).reshape(N, K // 32, 32)], -1)
+        op = PW.from_gguf(raw.reshape(-1), ggml_type, (K, N), dev)
+        q, s = O.quant_rows_i8(O.bf16_bits(x))
+        want = O.w8a8_gemm(q, s, qs, d, 32, epi=0)
+        KW.gemm(_t(q, dev), _t(s, dev), op[0], op[1], out, _live(M, dev), 32)
+    else:
+        raw = O.q4k_quantize(w) if ggml_type == 12 else O.q6k_quantize(w)
+        op = PW.from_gguf(raw.reshape(-1), ggml_type, (K, N), dev)
+        xq, a, xs = O.quant_rows_g(x, 256)
+        want = (O.w4a8_gemm(xq, a, xs, O.q4k_repack(raw)) if ggml_type == 12 else
+                O.w4a8_gemm_q6k(xq, a, O.q6k_repack(raw)))
+        KW4.gemm(_t(xq, dev), _t(a, dev), _t(xs, dev), op, out, _live(M, dev))
+    torch.cuda.synchronize()
+    assert np.array_equal(out.view(torch.int16).cpu().numpy().view(np.uint16), want)

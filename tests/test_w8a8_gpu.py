@@ -152,7 +152,7 @@ def test_per_channel_gk_equals_k(dev, M, N, K, live):
     want1 = O.w8a8_gemm(a, sa, w, sw, K, epi=1, out=base.copy(), live=live)
     sw16 = sw.astype(np.float16)
     want16 = O.w8a8_gemm(a, sa, w, sw16.astype(np.float32), K, epi=0, live=live)
-    for kernel in ["tile"] + (["decode"] if M <= 64 else []):
+    for kernel in ("tile", "decode"):                  # decode: 64 rows per workgroup, grid rows beyond
         got = _gemm(dev, a, sa, w, sw, K, 0, kernel, live=live).view(torch.int16).cpu().numpy().view(np.uint16)
         assert np.array_equal(got[:live], want[:live]), kernel
         assert (got[live:] == 7).all(), kernel
@@ -163,7 +163,7 @@ def test_per_channel_gk_equals_k(dev, M, N, K, live):
     # the packed per-channel layout (weight_from_q8's gk = K operand): same bits from both kernels
     from prism_amd import w8a8 as KW
     pw = KW.pack_i8(_t(w, dev), _t(sw, dev))
-    for kernel in ["tile"] + (["decode"] if M <= 64 else []):
+    for kernel in ("tile", "decode"):
         out = torch.full((M, N), 7, dtype=torch.int16, device=dev).view(torch.bfloat16)
         KW.gemm(_t(a, dev), _t(sa, dev), pw, None, out, _live(live, dev), K, epi=0, kernel=kernel)
         o1 = _t(base, dev).clone()
@@ -268,7 +268,7 @@ def test_packed_cases_bit_exact(dev, M, N, K, live):
     want0 = O.w8a8_gemm(a, s, qs, d, 32, epi=0, live=live)
     base = rng(M * N + 1).standard_normal((M, N)).astype(np.float32)
     want1 = O.w8a8_gemm(a, s, qs, d, 32, epi=1, out=base.copy(), live=live)
-    for kernel in ["tile"] + (["decode", "mid"] if M <= 64 else []):
+    for kernel in ["tile", "mid"] + (["decode"] if M <= 64 else []):     # mid: any M
         got0 = _packed_gemm(dev, a, s, qs, d, 0, kernel, live=live).view(torch.int16).cpu().numpy().view(np.uint16)
         assert np.array_equal(got0[:live], want0[:live]), kernel
         assert (got0[live:] == 7).all(), kernel
