@@ -12,9 +12,10 @@ int8 MFMA peak (5.0 POPS).
 
 Also measured (key "configs", not the headline; GEMM kernels alone, graph-replayed): config 0 (Q8_0, M = 16,
 K = N = 4096) and config 2 (Q8_0 decode, M in 1, 4, 16, 64; (K, N) = (5120, 5120), (17408, 5120)) as GB/s of packed
-Q8_0 weight bytes; config 3 (Q4_K W4A8, M = 16 and 2048) and config 4 (MXFP4, M = 16 and 4096), each against its
-roof (HBM for the decode sizes, the int8 or fp8 MFMA peak for the prefill sizes); and the engine's per-channel
-(gk = K) projections at config 1's shape and config 2's decode sizes.  Memory-bound shapes rotate weight
+Q8_0 weight bytes; config 3 (Q4_K W4A8, M = 16 and 2048; and the same shape on Q6_K weights) and config 4 (MXFP4,
+M = 16 and 4096), each against its roof (HBM for the decode sizes, the int8 or fp8 MFMA peak for the prefill
+sizes); the engine's per-channel (gk = K) projections at config 1's shape and config 2's decode sizes; and the fused
+producers.  Memory-bound shapes rotate weight
 copies through more than 3 x the 256 MB MALL so that every launch streams its weights from HBM.
 
 cpu_baseline: the CPU oracle (oracle/, the exact restatement of the reference's arithmetic, OpenMP) on a bounded
@@ -169,18 +170,24 @@ def bench_q8_decode(dev, shapes, Ms, iters=40):
     return rows
 
 
-def bench_w4a8(dev, iters=20):
-    """Config 3: Q4_K W4A8, K = 5120, N = 13824, M = 16 (memory-bound: GB/s of Q4_K bytes, 144 per 256 weights) and
-    M = 2048 (int8 MFMA-bound), one activation scale per token plus per-32 sums (rows_g, not timed here)."""
+def bench_w4a8(dev, iters=20, kind="q4k"):
+    """Config 3: Q4_K W4A8, K = 5120, N = 13824, M = 16 (memory-bound: GB/s of the device weight bytes, for Q4_K the
+    file's 144 per 256 weights) and M = 2048 (int8 MFMA-bound), one activation scale per token plus per-32 sums
+    (rows_g, not timed here).  kind "q6k": the same shape on Q6_K weights (device layout int8 values plus scales,
+    4384 bytes per 16 rows x 256 inputs)."""
     import torch
     from prism_amd import gguf_formats as GF
     from prism_amd import quant as KQ
     from prism_amd import w4a8 as KW4
     K, N = 5120, 13824
-    wbytes = N * K // 256 * 144
     g = torch.Generator(device=dev)
     g.manual_seed(5)
-    kq = GF.quantize_q4k(torch.randn(N, K, generator=g, device=dev) * 0.02)
+    w0 = torch.randn(N, K, generator=g, device=dev) * 0.02
+    kq = GF.quantize_q6k(w0) if kind == "q6k" else GF.quantize_q4k(w0)
+    del w0
+    w1 = KW4.repack(kq)
+    wbytes = w1.qv.numel() + w1.meta.numel()
+    del w1
     rows = []
     for M in (16, 2048):
         copies = _copies(wbytes, M)
@@ -311,6 +318,7 @@ def bench_configs(dev):
         "c0": bench_q8_decode(dev, [(4096, 4096)], (16,)),
         "c2": bench_q8_decode(dev, [(5120, 5120), (17408, 5120)], (1, 4, 16, 64)),
         "c3": bench_w4a8(dev),
+        "c3_q6k": bench_w4a8(dev, kind="q6k"),
         "c4": bench_mxfp4(dev),
     }
 
