@@ -768,11 +768,21 @@ extern "C" int prism_w4a8_q4k_gemm(const int8_t* xq, const float* a, int64_t a_s
 #define W4DEC(NW, R, MX, D, E)                                                                                      \
     hipLaunchKernelGGL((w4a8_decode_kernel<0, NW, R, MX, D, E>), grid, dim3(NW * 64), w4a8_decode_lds(0, R, Mi), st, xq, a, \
                        a_sb, xs, qv, meta, out, ldo, n_rows, Mi, Ni, Ki)
+// decode configurations (waves, super-blocks per round, rows, rounds of weights in flight), measured on MI355X at
+// the 27B's shapes (M <= 4, M <= 16); overridable at build time
+#ifndef W4V_SMALL
+#define W4V_SMALL 8, 8, 4, 2
+#endif
+#ifndef W4V_BIG
+#define W4V_BIG 4, 4, 16, 2
+#endif
+#define W4DEC_(...) W4DEC(__VA_ARGS__)
         if (M <= 4) {
-            if (epi == 0) W4DEC(4, 8, 4, 3, 0); else W4DEC(4, 8, 4, 3, 1);
+            if (epi == 0) W4DEC_(W4V_SMALL, 0); else W4DEC_(W4V_SMALL, 1);
         } else {
-            if (epi == 0) W4DEC(4, 4, 16, 4, 0); else W4DEC(4, 4, 16, 4, 1);
+            if (epi == 0) W4DEC_(W4V_BIG, 0); else W4DEC_(W4V_BIG, 1);
         }
+#undef W4DEC_
 #undef W4DEC
     } else {
         const int tiles_m = (Mi + QBM - 1) / QBM, tiles_n = (Ni + QBN - 1) / QBN;
@@ -817,11 +827,20 @@ extern "C" int prism_w4a8_q6k_gemm(const int8_t* xq, const float* a, int64_t a_s
 #define Q6DEC(NW, R, MX, D, E)                                                                                      \
     hipLaunchKernelGGL((w4a8_decode_kernel<1, NW, R, MX, D, E>), grid, dim3(NW * 64), w4a8_decode_lds(1, R, Mi), st, xq, \
                        a, a_sb, nullptr, qv, meta, out, ldo, n_rows, Mi, Ni, Ki)
+// as W4V_SMALL / W4V_BIG, for Q6_K's twice larger weight chunks
+#ifndef W6V_SMALL
+#define W6V_SMALL 4, 4, 4, 2
+#endif
+#ifndef W6V_BIG
+#define W6V_BIG 4, 4, 16, 2
+#endif
+#define Q6DEC_(...) Q6DEC(__VA_ARGS__)
         if (M <= 4) {
-            if (epi == 0) Q6DEC(4, 4, 4, 3, 0); else Q6DEC(4, 4, 4, 3, 1);
+            if (epi == 0) Q6DEC_(W6V_SMALL, 0); else Q6DEC_(W6V_SMALL, 1);
         } else {
-            if (epi == 0) Q6DEC(4, 4, 16, 3, 0); else Q6DEC(4, 4, 16, 3, 1);
+            if (epi == 0) Q6DEC_(W6V_BIG, 0); else Q6DEC_(W6V_BIG, 1);
         }
+#undef Q6DEC_
 #undef Q6DEC
     } else {
         const int tiles_m = (Mi + QBM - 1) / QBM, tiles_n = (Ni + Q6BN - 1) / Q6BN;
