@@ -50,11 +50,12 @@ __global__ __launch_bounds__(256) void q8_0_pack_kernel(const int8_t* __restrict
 // chunks (one dwordx4 per lane per 1 KB chunk, requested D - 1 rounds ahead); the round's block scales (1 KB) and
 // activation rows (M R 32 bytes) are fetched by all threads with row-contiguous 16-byte loads and staged in one of
 // two LDS buffers a round ahead.  Each block's int32 sums come from one MFMA on a chunk half, become the term
-// RN(RN(float(P) sa) sw) and go to one of two LDS term buffers [block][m][n]; the owner thread of each output adds
-// round r - 1's terms in block order (the reference's sequential fp32 sum over groups) while round r is computed,
-// and one barrier per round separates producers from consumers of every buffer.
-template <int NW, int R, int MX, int D, int EPI>
-__global__ __launch_bounds__(NW * 64) void w8a8_packed_decode_kernel(const int8_t* __restrict__ a,
+// RN(RN(float(P) sa) sw) and go to one of two LDS term buffers [block][m][n].  FW more waves own the outputs: each
+// of their threads adds round r - 1's terms of one output in block order (the reference's sequential fp32 sum over
+// groups) while the NW compute waves compute round r, so the fold's serial chain overlaps the weight stream; one
+// barrier per round separates producers from consumers of every buffer.
+template <int NW, int FW, int R, int MX, int D, int EPI>
+__global__ __launch_bounds__((NW + FW) * 64) void w8a8_packed_decode_kernel(const int8_t* __restrict__ a,
                                                                      const float* __restrict__ a_s, int64_t as_sm,
                                                                      const int8_t* __restrict__ qt,
                                                                      const uint16_t* __restrict__ dt,
@@ -62,7 +63,8 @@ __global__ __launch_bounds__(NW * 64) void w8a8_packed_decode_kernel(const int8_
                                                                      const int32_t* __restrict__ n_rows, int M, int N,
                                                                      int K) {
     constexpr int MT = (MX + 15) / 16;             // activation tiles of 16 rows
-    constexpr int NT = NW * 64;
+    constexpr int NT = NW * 64;                    // compute threads; threads NT .. NT + 64 FW - 1 fold
+    static_assert(FW * 64 >= MX * 16, "one fold thread per output");
     constexpr int CP = R / (2 * NW);               // block pairs per wave per round
     static_assert(CP >= 1 && CP * 2 * NW == R, "R must be a multiple of 2 NW");
     constexpr int RB = R * 32;                     // activation bytes per row per round
@@ -167,31 +169,25 @@ __global__ __launch_bounds__(NW * 64) void w8a8_packed_decode_kernel(const int8_
             }
         }
     };
-    constexpr int OPT = (16 * 16 * MT + NT - 1) / NT;
-    float y[OPT];
-#pragma unroll
-    for (int j = 0; j < OPT; j++) y[j] = 0.f;
+    const bool folder = wv >= NW;
+    const int fo = tid - NT;                                           // the fold thread's output (m = fo / 16)
+    float y = 0.f;
     auto fold = [&](int r) {
-        const float* tb = terms + (r & 1) * tstride;
-        const int nb = min(R, G - r * R);
-        const int st = M * 16;
+        if (fo < M * 16) {
+            const float* tp = terms + (r & 1) * tstride + fo;
+            const int nb = min(R, G - r * R);
+            const int st = M * 16;
+            float acc = y;
+            int j = 0;
+            for (; j + 16 <= nb; j += 16) {
+                float v[16];
 #pragma unroll
-        for (int jo = 0; jo < OPT; jo++) {
-            const int o = tid + jo * NT;
-            if (o < M * 16) {
-                const float* tp = tb + o;
-                float acc = y[jo];
-                int j = 0;
-                for (; j + 16 <= nb; j += 16) {
-                    float v[16];
+                for (int u = 0; u < 16; u++) v[u] = tp[(j + u) * st];
 #pragma unroll
-                    for (int u = 0; u < 16; u++) v[u] = tp[(j + u) * st];
-#pragma unroll
-                    for (int u = 0; u < 16; u++) acc = add_rn(acc, v[u]);
-                }
-                for (; j < nb; j++) acc = add_rn(acc, tp[j * st]);
-                y[jo] = acc;
+                for (int u = 0; u < 16; u++) acc = add_rn(acc, v[u]);
             }
+            for (; j < nb; j++) acc = add_rn(acc, tp[j * st]);
+            y = acc;
         }
     };
 
@@ -199,38 +195,39 @@ __global__ __launch_bounds__(NW * 64) void w8a8_packed_decode_kernel(const int8_
     // (round q in slot q % D, loaded D rounds before it is stored); weights of rounds 0 .. D-2
     v4i wr[D][CP];
     Staged sg[D];
+    if (!folder) {
 #pragma unroll
-    for (int d = 0; d < D - 1; d++) load_w(d, wr[d]);
-    stage_load(0, sg[0]);
-    stage_store(sg[0], 0);
+        for (int d = 0; d < D - 1; d++) load_w(d, wr[d]);
+        stage_load(0, sg[0]);
+        stage_store(sg[0], 0);
 #pragma unroll
-    for (int d = 1; d <= D; d++) stage_load(d, sg[d % D]);
+        for (int d = 1; d <= D; d++) stage_load(d, sg[d % D]);
+    }
     lds_barrier();
     for (int r0 = 0; r0 < nr; r0 += D) {
 #pragma unroll
         for (int d = 0; d < D; d++) {
             const int r = r0 + d;
-            load_w(r + D - 1, wr[(d + D - 1) % D]);        // past the end: the last chunk again (a cache hit)
-            stage_store(sg[(d + 1) % D], (r + 1) & 1);      // round r + 1's scales and activations
-            stage_load(r + 1 + D, sg[(d + 1) % D]);         // the slot's next round
-            if (r < nr) compute(r, wr[d], r & 1);
-            if (r >= 1 && r <= nr) fold(r - 1);
+            if (!folder) {
+                load_w(r + D - 1, wr[(d + D - 1) % D]);    // past the end: the last chunk again (a cache hit)
+                stage_store(sg[(d + 1) % D], (r + 1) & 1);  // round r + 1's scales and activations
+                stage_load(r + 1 + D, sg[(d + 1) % D]);     // the slot's next round
+                if (r < nr) compute(r, wr[d], r & 1);
+            } else if (r >= 1 && r <= nr) {
+                fold(r - 1);
+            }
             lds_barrier();
         }
     }
-    if (nr % D == 0) fold(nr - 1);
+    if (nr % D == 0 && folder) fold(nr - 1);
     PRISM_PROBE(3);
-#pragma unroll
-    for (int jo = 0; jo < OPT; jo++) {
-        const int o = tid + jo * NT;
-        const int m = o >> 4, n = 16 * nt + (o & 15);
-        if (o < M * 16 && m < live) {
-            if (EPI == 0) {
-                reinterpret_cast<uint16_t*>(out)[(int64_t)m * ldo + n] = (uint16_t)f32_to_bf16(y[jo]);
-            } else {
-                float* op = reinterpret_cast<float*>(out) + (int64_t)m * ldo + n;
-                *op = add_rn(*op, y[jo]);
-            }
+    const int m = fo >> 4, n = 16 * nt + (fo & 15);
+    if (folder && fo < M * 16 && m < live) {
+        if (EPI == 0) {
+            reinterpret_cast<uint16_t*>(out)[(int64_t)m * ldo + n] = (uint16_t)f32_to_bf16(y);
+        } else {
+            float* op = reinterpret_cast<float*>(out) + (int64_t)m * ldo + n;
+            *op = add_rn(*op, y);
         }
     }
 }
@@ -499,11 +496,20 @@ static void launch_packed(int kernel, const int8_t* a, const float* a_s, int64_t
     if (kernel == 1) {
         dim3 grid(N / 16);
 #define PDEC(NW, R, MX, D)                                                                                         \
-    hipLaunchKernelGGL((w8a8_packed_decode_kernel<NW, R, MX, D, EPI>), grid, dim3(NW * 64), packed_decode_lds(R, M), \
+    hipLaunchKernelGGL((w8a8_packed_decode_kernel<NW, (MX * 16 + 63) / 64, R, MX, D, EPI>), grid,                   \
+                       dim3((NW + (MX * 16 + 63) / 64) * 64), packed_decode_lds(R, M),                              \
                        st, a, a_s, as_sm, qt, dt, out, ldo, n_rows, M, N, K)
-        if (M <= 4) PDEC(8, 32, 4, 2);
-        else if (M <= 16) PDEC(8, 16, 16, 3);
+#ifndef Q8V_SMALL
+#define Q8V_SMALL 8, 32, 4, 2
+#endif
+#ifndef Q8V_BIG
+#define Q8V_BIG 8, 16, 16, 3
+#endif
+#define PDEC_(...) PDEC(__VA_ARGS__)
+        if (M <= 4) PDEC_(Q8V_SMALL);
+        else if (M <= 16) PDEC_(Q8V_BIG);
         else kernel = 2;
+#undef PDEC_
 #undef PDEC
     }
     if (kernel == 2) {
