@@ -6,7 +6,8 @@
 //   swiglu_g   :384-393, :403-406   y = silu(gate) * up         -> W4A8 operands
 //   gated_norm_q8 :216-246, :460-469, gated_norm_g :349-365, :399-401
 //                                   y = rmsnorm_head(o) * w * silu(z) (* inv_s) -> either back end
-// One workgroup (256 threads) per row; thread t owns the 8-input chunks t, t + 256, ... and keeps them in registers
+// One workgroup per row (256 threads; the SwiGLU and gated-norm kernels take 1024 for up to 64 rows, the decode sizes,
+// which their results do not depend on); thread t owns the 8-input chunks t, t + TPB, ... and keeps them in registers
 // between the row reductions and the stores, so a row is read once.
 //
 // Arithmetic (every step an IEEE fp32 operation, so the CPU oracle reproduces the bits):
@@ -57,12 +58,16 @@ __device__ __forceinline__ uint32_t pack4_i8(const float* f) {
     return r;
 }
 
-// Row reductions over the workgroup: the maximum (exact in any order) and the fixed-order sum of the module comment.
+// Row reductions over the workgroup: the maximum (exact in any order, so for any workgroup size TPB) and the
+// fixed-order sum of the module comment (256 threads).
+template <int TPB>
 __device__ __forceinline__ float row_max(float v, float* red) {
     v = wave_max(v);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();
-    const float r = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float r = red[0];
+#pragma unroll
+    for (int i = 1; i < TPB / 64; i++) r = fmaxf(r, red[i]);
     __syncthreads();
     return r;
 }
@@ -79,16 +84,17 @@ __device__ __forceinline__ float row_sum_fixed(float v, float* red) {
 
 // Back ends.  BACK 0: int8 row + one scale per row (q [M, K], s [M]).  BACK 1: the W4A8 operands with one scale
 // per 256 inputs (xq [M, K], a [K/256, M], xs [K/256, M, 16]); BACK 2: the same with one scale per row (a [M]).
-template <int NCH, int BACK>
+// TPB: the workgroup size (thread t owns chunks t, t + TPB, ...); every result is independent of it.
+template <int NCH, int BACK, int TPB = kPThreads>
 __device__ __forceinline__ void store_back(float (&y)[NCH][8], float rmax, float* red, int64_t row, int out_row,
                                            int M, int K, int8_t* __restrict__ q, float* __restrict__ s,
                                            int8_t* __restrict__ xs) {
     const int nch = K / 8;
-    if (BACK == 0 || BACK == 2) rmax = row_max(rmax, red);
+    if (BACK == 0 || BACK == 2) rmax = row_max<TPB>(rmax, red);
     v2u* qr = reinterpret_cast<v2u*>(q + (int64_t)out_row * K);
 #pragma unroll
     for (int c = 0; c < NCH; c++) {
-        const int idx = threadIdx.x + c * kPThreads;
+        const int idx = threadIdx.x + c * TPB;
         float gmax = rmax;
         if (BACK == 1) {                     // the 32 chunks of a group of 256 are the lanes of a half-wave
             float m = 0.f;
@@ -186,13 +192,13 @@ __global__ __launch_bounds__(kPThreads) void norm_prod_kernel(const float* __res
 // ---------------------------------------------------------------------------------------------- SwiGLU
 // gu [*, 2 FF] (bf16, or fp32 when GU32; row stride ldg): gate = columns 0 .. FF-1, up = FF .. 2 FF - 1; inv_s fp32
 // [FF] or null.
-template <int NCH, int BACK, bool GU32>
-__global__ __launch_bounds__(kPThreads) void swiglu_prod_kernel(const void* __restrict__ gu, int64_t ldg,
+template <int NCH, int BACK, bool GU32, int TPB>
+__global__ __launch_bounds__(TPB) void swiglu_prod_kernel(const void* __restrict__ gu, int64_t ldg,
                                                                 const float* __restrict__ inv_s,
                                                                 int8_t* __restrict__ q, float* __restrict__ s,
                                                                 int8_t* __restrict__ xs,
                                                                 const int32_t* __restrict__ n_rows, int M, int FF) {
-    __shared__ float red[4];
+    __shared__ float red[TPB / 64];
     const int i = blockIdx.x;
     if (i >= __ldg(n_rows)) return;
     const int nch = FF / 8;
@@ -200,7 +206,7 @@ __global__ __launch_bounds__(kPThreads) void swiglu_prod_kernel(const void* __re
     float amax = 0.f;
 #pragma unroll
     for (int c = 0; c < NCH; c++) {
-        const int idx = threadIdx.x + c * kPThreads;
+        const int idx = threadIdx.x + c * TPB;
         if (idx < nch) {
             float g[8], u[8];
             if (GU32) {
@@ -241,15 +247,15 @@ __global__ __launch_bounds__(kPThreads) void swiglu_prod_kernel(const void* __re
             }
         }
     }
-    store_back<NCH, BACK>(y, amax, red, i, i, M, FF, q, s, xs);
+    store_back<NCH, BACK, TPB>(y, amax, red, i, i, M, FF, q, s, xs);
 }
 
 // ---------------------------------------------------------------------------------------------- gated RMSNorm
 // o fp32 [*, HV D] (row stride ldo); z [*, ldz] (bf16, or fp32 when Z32): the row's gate values from column 0 (the
 // caller offsets the projection's row); w fp32 [D]; inv_s fp32 [HV D] or null.  D / 8 is a power of two <= 64, so
 // a head's chunks are neighbouring lanes of one wave.
-template <int NCH, int BACK, bool Z32>
-__global__ __launch_bounds__(kPThreads) void gated_norm_prod_kernel(const float* __restrict__ o, int64_t ldo,
+template <int NCH, int BACK, bool Z32, int TPB>
+__global__ __launch_bounds__(TPB) void gated_norm_prod_kernel(const float* __restrict__ o, int64_t ldo,
                                                                     const void* __restrict__ z, int64_t ldz,
                                                                     const float* __restrict__ w,
                                                                     const float* __restrict__ inv_s,
@@ -257,7 +263,7 @@ __global__ __launch_bounds__(kPThreads) void gated_norm_prod_kernel(const float*
                                                                     int8_t* __restrict__ xs,
                                                                     const int32_t* __restrict__ n_rows, int M, int HV,
                                                                     int D, float eps) {
-    __shared__ float red[4];
+    __shared__ float red[TPB / 64];
     const int i = blockIdx.x;
     if (i >= __ldg(n_rows)) return;
     const int K = HV * D, nch = K / 8, cph = D / 8;
@@ -266,7 +272,7 @@ __global__ __launch_bounds__(kPThreads) void gated_norm_prod_kernel(const float*
     float amax = 0.f;
 #pragma unroll
     for (int c = 0; c < NCH; c++) {
-        const int idx = threadIdx.x + c * kPThreads;
+        const int idx = threadIdx.x + c * TPB;
         const bool in = idx < nch;
         float ss = 0.f;
         if (in) {
@@ -320,12 +326,12 @@ __global__ __launch_bounds__(kPThreads) void gated_norm_prod_kernel(const float*
             }
         }
     }
-    store_back<NCH, BACK>(y, amax, red, i, i, M, K, q, s, xs);
+    store_back<NCH, BACK, TPB>(y, amax, red, i, i, M, K, q, s, xs);
 }
 
 template <typename KN>
-static int pick_nch(int K, KN&& launch) {
-    const int need = (K / 8 + kPThreads - 1) / kPThreads;
+static int pick_nch(int K, KN&& launch, int tpb = kPThreads) {
+    const int need = (K / 8 + tpb - 1) / tpb;
     if (need <= 1) return launch(std::integral_constant<int, 1>{});
     if (need <= 2) return launch(std::integral_constant<int, 2>{});
     if (need <= 3) return launch(std::integral_constant<int, 3>{});
@@ -378,15 +384,19 @@ extern "C" int prism_swiglu_quant(const void* gu, int gu_f32, int64_t ldg, const
     if (gu_f32 && FF % 4) return PRISM_ERR_SHAPE;
     if (M == 0) return PRISM_OK;
     hipStream_t st = (hipStream_t)stream;
+    // few rows (decode): 1024 threads per row; the results do not depend on the workgroup size
+    const bool wide = M <= 64;
     return pick_nch((int)FF, [&](auto nc) {
         constexpr int NC = decltype(nc)::value;
-#define SW(B, G32) hipLaunchKernelGGL((swiglu_prod_kernel<NC, B, G32>), dim3((unsigned)M), dim3(kPThreads), 0, st, gu, \
-                                      ldg, inv_s, q, s, xs, n_rows, (int)M, (int)FF)
-        if (gu_f32) { if (back == 0) SW(0, true); else if (back == 1) SW(1, true); else SW(2, true); }
-        else { if (back == 0) SW(0, false); else if (back == 1) SW(1, false); else SW(2, false); }
+#define SW(B, G32, T) hipLaunchKernelGGL((swiglu_prod_kernel<NC, B, G32, T>), dim3((unsigned)M), dim3(T), 0, st, gu,  \
+                                         ldg, inv_s, q, s, xs, n_rows, (int)M, (int)FF)
+#define SWT(B, G32) do { if (wide) SW(B, G32, 1024); else SW(B, G32, kPThreads); } while (0)
+        if (gu_f32) { if (back == 0) SWT(0, true); else if (back == 1) SWT(1, true); else SWT(2, true); }
+        else { if (back == 0) SWT(0, false); else if (back == 1) SWT(1, false); else SWT(2, false); }
+#undef SWT
 #undef SW
         return hipGetLastError() == hipSuccess ? 0 : (int)PRISM_ERR_LAUNCH;
-    });
+    }, wide ? 1024 : kPThreads);
 }
 
 // back as prism_norm_quant.  o: the GDN output rows, z: the gate values of the row (the projection row plus the
@@ -405,13 +415,16 @@ extern "C" int prism_gated_norm_quant(const float* o, int64_t ldo, const void* z
         return PRISM_ERR_ALIGN;
     if (M == 0) return PRISM_OK;
     hipStream_t st = (hipStream_t)stream;
+    const bool wide = M <= 64;                       // as prism_swiglu_quant
     return pick_nch((int)K, [&](auto nc) {
         constexpr int NC = decltype(nc)::value;
-#define GN(B, Z) hipLaunchKernelGGL((gated_norm_prod_kernel<NC, B, Z>), dim3((unsigned)M), dim3(kPThreads), 0, st, o, \
-                                    ldo, z, ldz, w, inv_s, q, s, xs, n_rows, (int)M, (int)HV, (int)D, eps)
-        if (z_f32) { if (back == 0) GN(0, true); else if (back == 1) GN(1, true); else GN(2, true); }
-        else { if (back == 0) GN(0, false); else if (back == 1) GN(1, false); else GN(2, false); }
+#define GN(B, Z, T) hipLaunchKernelGGL((gated_norm_prod_kernel<NC, B, Z, T>), dim3((unsigned)M), dim3(T), 0, st, o,  \
+                                       ldo, z, ldz, w, inv_s, q, s, xs, n_rows, (int)M, (int)HV, (int)D, eps)
+#define GNT(B, Z) do { if (wide) GN(B, Z, 1024); else GN(B, Z, kPThreads); } while (0)
+        if (z_f32) { if (back == 0) GNT(0, true); else if (back == 1) GNT(1, true); else GNT(2, true); }
+        else { if (back == 0) GNT(0, false); else if (back == 1) GNT(1, false); else GNT(2, false); }
+#undef GNT
 #undef GN
         return hipGetLastError() == hipSuccess ? 0 : (int)PRISM_ERR_LAUNCH;
-    });
+    }, wide ? 1024 : kPThreads);
 }

@@ -1,6 +1,7 @@
 """GPU parity of the fused producers (norm_q8, norm_g, swiglu_q8, swiglu_g, gated_norm_q8, gated_norm_g) against the
 CPU oracle, bit for bit: int8 values, scales and split per-32 sums, at the engine's shapes (HID 5120, FF 17408, 48
-value heads of 128), with gathered rows, live rows, bf16 and fp32 gate inputs, and the smoothing factor."""
+value heads of 128), with gathered rows, live rows, bf16 and fp32 gate inputs, the smoothing factor, and both
+workgroup sizes of the SwiGLU and gated-norm kernels (1024 threads up to 64 rows, 256 beyond)."""
 import numpy as np
 import pytest
 import torch
@@ -56,7 +57,8 @@ def test_norm_g_bit_exact(dev, group):
 
 
 @pytest.mark.parametrize("M,FF,live,f32,smooth", [(16, 17408, 16, False, True), (5, 13824, 4, False, False),
-                                                  (64, 1024, 64, True, True), (3, 264, 3, False, True)])
+                                                  (64, 1024, 64, True, True), (3, 264, 3, False, True),
+                                                  (100, 13824, 97, False, True)])
 def test_swiglu_q8_bit_exact(dev, M, FF, live, f32, smooth):
     from prism_amd import quant as KQ
     g = rng(FF + M)
@@ -103,7 +105,7 @@ class _Cfg:
 
 @pytest.mark.parametrize("M,HV,D,live,f32,smooth", [(16, 48, 128, 13, False, True), (1, 32, 128, 1, False, True),
                                                     (40, 16, 64, 40, True, False), (7, 4, 256, 7, False, True),
-                                                    (3, 3, 8, 3, True, True)])
+                                                    (3, 3, 8, 3, True, True), (80, 48, 128, 77, False, True)])
 def test_gated_norm_q8_bit_exact(dev, M, HV, D, live, f32, smooth):
     from prism_amd import quant as KQ
     K, zoff = HV * D, 3 * 128
