@@ -324,32 +324,37 @@ __global__ __launch_bounds__(MT == 1 ? 1024 : 512) void mx_decode_kernel(const u
 }
 
 // ------------------------------------------------------------------------------------------------ tile kernel
-// 128 x 128 output tile (8 weight tiles x 8 activation tiles), 4 waves each 64 x 64 (4 x 4 MFMAs per step).
-// Operands move global -> LDS by LDS-DMA (global_load_lds_dwordx4 / _ubyte), NS stages deep, already in MFMA
-// operand order, so each wave reads its fragments with contiguous ds_read_b128 and no VGPR staging.
-constexpr int kTB = 128;
-template <int AF>
+// Workgroup tile: WM x WN waves of 64 x 64 outputs (4 x 4 MFMAs per step), 64 WM activation rows by 64 WN weight
+// rows; by default 128 x 256 (8 waves, one workgroup per CU), which halves the operand traffic per MFMA of a
+// 128 x 128 tile.  Operands move global -> LDS by LDS-DMA (global_load_lds_dwordx4 / _ubyte), NS stages deep,
+// already in MFMA operand order, so each wave reads its fragments with contiguous ds_read_b128 and no VGPR staging.
+template <int AF, int WM, int WN>
 struct MxStage {
-    static constexpr int WQ = 0;                                  // 8 tiles x 1 KB
-    static constexpr int AQ = 8192;                               // 8 tiles x (2 KB e4m3 | 1 KB e2m1)
-    static constexpr int WS = AQ + (AF == 0 ? 16384 : 8192);      // 8 tiles x 64 lanes x 4 B
-    static constexpr int AS = WS + 2048;
-    static constexpr int BYTES = AS + 2048;
-    static constexpr int LOADS = AF == 0 ? 10 : 8;                // DMA instructions per wave per stage
+    static constexpr int TW = 4 * WN, TA = 4 * WM;                // 16-row weight / activation tiles
+    static constexpr int WQ = 0;                                  // TW tiles x 1 KB
+    static constexpr int AQ = TW * 1024;                          // TA tiles x (2 KB e4m3 | 1 KB e2m1)
+    static constexpr int WS = AQ + TA * (AF == 0 ? 2048 : 1024);  // TW tiles x 64 lanes x 4 B
+    static constexpr int AS = WS + TW * 256;                      // TA tiles x 64 lanes x 4 B
+    static constexpr int BYTES = AS + TA * 256;
+    // DMA instructions per wave per stage: weights, activations, weight scales, activation scales
+    static constexpr int W_PW = TW / (WM * WN), A_PW = TA * (AF == 0 ? 2 : 1) / (WM * WN);
+    static constexpr int WS_PW = W_PW, AS_PW = TA / (WM * WN);
+    static_assert(W_PW >= 1 && A_PW >= 1 && AS_PW >= 1, "every wave copies a share of each operand");
+    static constexpr int LOADS = W_PW + A_PW + WS_PW + AS_PW;
 };
 
-template <int AF, int EPI, int NS>
-__global__ __launch_bounds__(256, 2) void mx_tile_kernel(const uint8_t* __restrict__ aq, const uint8_t* __restrict__ as,
+template <int AF, int EPI, int NS, int WM, int WN>
+__global__ __launch_bounds__(64 * WM * WN, WM * WN <= 4 ? 2 : 1) void mx_tile_kernel(const uint8_t* __restrict__ aq, const uint8_t* __restrict__ as,
                                                          const uint8_t* __restrict__ wq,
                                                          const uint8_t* __restrict__ ws, void* __restrict__ out,
                                                          int64_t ldo, const int32_t* __restrict__ n_rows, int M,
                                                          int N, int K, int tiles_m, int tiles_n) {
-    using S = MxStage<AF>;
+    using S = MxStage<AF, WM, WN>;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     int pm, pn;
     xcd_tile_coords(blockIdx.x, tiles_m, tiles_n, pm, pn);
-    const int m0 = pm * kTB, n0 = pn * kTB;
+    const int m0 = pm * 64 * WM, n0 = pn * 64 * WN;
     const int live = n_rows ? min(M, __ldg(n_rows)) : M;
     if (m0 >= live) return;
     const int KS = K / kMxStep, NT = N / 16;
@@ -357,21 +362,24 @@ __global__ __launch_bounds__(256, 2) void mx_tile_kernel(const uint8_t* __restri
     const int64_t abytes = AF == 0 ? K : K / 2;
 
     // per-wave DMA sources (step 0); each advances by a fixed stride per step
-    const uint8_t* wsrc[2];
-    const uint8_t* wssrc[2];
-    const uint8_t* asrc[4];
-    const uint8_t* assrc[2];
+    const uint8_t* wsrc[S::W_PW];
+    const uint8_t* wssrc[S::WS_PW];
+    const uint8_t* asrc[S::A_PW];
+    const uint8_t* assrc[S::AS_PW];
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-        const int tt = min(n0 / 16 + 2 * w + i, NT - 1);
+    for (int i = 0; i < S::W_PW; i++) {
+        const int tt = min(n0 / 16 + S::W_PW * w + i, NT - 1);
         wsrc[i] = wq + (int64_t)tt * KS * 1024 + lane * 16;
         wssrc[i] = ws + (int64_t)tt * KS * 64 + lane;
-        const int m = min(m0 + 16 * (2 * w + i) + r, M - 1);
+    }
+#pragma unroll
+    for (int i = 0; i < S::AS_PW; i++) {
+        const int m = min(m0 + 16 * (S::AS_PW * w + i) + r, M - 1);
         assrc[i] = as + (int64_t)m * (K / 32) + p;
     }
 #pragma unroll
-    for (int i = 0; i < (AF == 0 ? 4 : 2); i++) {
-        const int idx = (AF == 0 ? 4 : 2) * w + i;
+    for (int i = 0; i < S::A_PW; i++) {
+        const int idx = S::A_PW * w + i;
         const int u = AF == 0 ? idx >> 1 : idx, h = AF == 0 ? idx & 1 : 0;
         const int m = min(m0 + 16 * u + r, M - 1);
         asrc[i] = aq + (int64_t)m * abytes + 64 * h + 16 * p;
@@ -380,19 +388,20 @@ __global__ __launch_bounds__(256, 2) void mx_tile_kernel(const uint8_t* __restri
     auto issue = [&](int st, int buf) {
         uint8_t* b = lds + buf * S::BYTES;
 #pragma unroll
-        for (int i = 0; i < 2; i++) dma16(wsrc[i] + (int64_t)st * 1024, b + S::WQ + (2 * w + i) * 1024);
+        for (int i = 0; i < S::W_PW; i++)
+            dma16(wsrc[i] + (int64_t)st * 1024, b + S::WQ + (S::W_PW * w + i) * 1024);
 #pragma unroll
-        for (int i = 0; i < (AF == 0 ? 4 : 2); i++) {
-            const int idx = (AF == 0 ? 4 : 2) * w + i;
+        for (int i = 0; i < S::A_PW; i++) {
+            const int idx = S::A_PW * w + i;
             dma16(asrc[i] + (int64_t)st * (AF == 0 ? 128 : 64), b + S::AQ + idx * 1024);
         }
 #pragma unroll
-        for (int i = 0; i < 2; i++) dma1(wssrc[i] + (int64_t)st * 64, b + S::WS + (2 * w + i) * 256);
+        for (int i = 0; i < S::WS_PW; i++) dma1(wssrc[i] + (int64_t)st * 64, b + S::WS + (S::WS_PW * w + i) * 256);
 #pragma unroll
-        for (int i = 0; i < 2; i++) dma1(assrc[i] + st * 4, b + S::AS + (2 * w + i) * 256);
+        for (int i = 0; i < S::AS_PW; i++) dma1(assrc[i] + st * 4, b + S::AS + (S::AS_PW * w + i) * 256);
     };
 
-    const int wn = w & 1, wm = w >> 1;
+    const int wn = w % WN, wm = w / WN;
     v4f acc[4][4], tot[4][4];
 #pragma unroll
     for (int a = 0; a < 4; a++)
@@ -683,15 +692,23 @@ extern "C" int prism_mxfp4_gemm(const uint8_t* aq, const uint8_t* as, int a_fmt,
 #undef DEC_MT
 #undef DEC
     } else {
-        constexpr int NS = 3;                                   // LDS stages in flight
-        const int tiles_m = (int)((M + kTB - 1) / kTB), tiles_n = (int)((N + kTB - 1) / kTB);
+        // tile configuration: LDS stages in flight, waves along M, waves along N (64 x 64 outputs each)
+#ifndef MXV_TILE
+#define MXV_TILE 3, 2, 4
+#endif
+#define MXT_(NS, WM, WN) constexpr int kNS = NS, kWM = WM, kWN = WN;
+#define MXT(...) MXT_(__VA_ARGS__)
+        MXT(MXV_TILE)
+#undef MXT
+#undef MXT_
+        const int tiles_m = (int)((M + 64 * kWM - 1) / (64 * kWM)), tiles_n = (int)((N + 64 * kWN - 1) / (64 * kWN));
         dim3 grid((unsigned)(tiles_m * tiles_n));
 #define TILE(AF, E)                                                                                                  \
     do {                                                                                                             \
-        const size_t lds = (size_t)NS * MxStage<AF>::BYTES;                                                          \
-        allow_lds(mx_tile_kernel<AF, E, NS>, lds);                                                                   \
-        hipLaunchKernelGGL((mx_tile_kernel<AF, E, NS>), grid, dim3(256), lds, st, aq, as, wq, ws, out, ldo, n_rows,  \
-                           (int)M, (int)N, (int)K, tiles_m, tiles_n);                                                \
+        const size_t lds = (size_t)kNS * MxStage<AF, kWM, kWN>::BYTES;                                               \
+        allow_lds(mx_tile_kernel<AF, E, kNS, kWM, kWN>, lds);                                                        \
+        hipLaunchKernelGGL((mx_tile_kernel<AF, E, kNS, kWM, kWN>), grid, dim3(64 * kWM * kWN), lds, st, aq, as, wq,  \
+                           ws, out, ldo, n_rows, (int)M, (int)N, (int)K, tiles_m, tiles_n);                          \
     } while (0)
         if (a_fmt == PRISM_MX_E4M3) { if (epi) TILE(0, 1); else TILE(0, 0); }
         else { if (epi) TILE(4, 1); else TILE(4, 0); }
