@@ -75,6 +75,13 @@ __device__ __forceinline__ void vm_wait() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// Dynamic LDS above the default 64 KB needs the kernel's limit raised (up to the CU's 160 KB) before its launch.
+template <typename F>
+inline void allow_lds(F* fn, size_t bytes) {
+    if (bytes > 64 * 1024)
+        (void)hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));

@@ -583,12 +583,6 @@ static size_t mx_decode_lds(int MT, int K) {
     return (size_t)nseg * MT * 64 * sizeof(v4f);
 }
 
-template <typename F>
-static void allow_lds(F* fn, size_t bytes) {
-    if (bytes > 64 * 1024) (void)hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                     (int)bytes);
-}
-
 }  // namespace prism
 
 using namespace prism;
