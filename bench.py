@@ -264,6 +264,43 @@ def bench_per_channel(dev, iters=40):
     return rows
 
 
+def bench_deferred(dev, iters=40):
+    """The engine's down projection at 64 decode rows (K 17408 -> HID 5120, per channel, residual add) followed by the
+    norm_q8 that reads the residual: unsplit (epilogue 1, then norm_q8) against deferred (K in defer_split parts
+    into int32 slots, then norm_q8 finishing the add); both leave the same bits in the residual and the int8 rows."""
+    import torch
+    from prism_amd import quant as KQ
+    from prism_amd import w8a8 as KW
+    M, K, N = 64, 17408, 5120
+    g = torch.Generator(device=dev)
+    g.manual_seed(11)
+    w = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8, device=dev)
+    copies = _copies(N * K, 1)
+    ws = [KW.pack_i8(w, torch.rand(N, generator=g, device=dev)) for _ in range(copies)]
+    del w
+    a = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8, device=dev)
+    sa = torch.rand(M, generator=g, device=dev)
+    n = torch.tensor([M], dtype=torch.int32, device=dev)
+    h = torch.randn(M, N, generator=g, device=dev)
+    nw = torch.rand(N, generator=g, device=dev) + 0.5
+    q = torch.empty(M, N, dtype=torch.int8, device=dev)
+    s = torch.empty(M, dtype=torch.float32, device=dev)
+    slots = torch.empty(4, M, N, dtype=torch.int32, device=dev)
+
+    def unsplit(i):
+        KW.gemm(a, sa, ws[i], None, h, n, K, epi=1)
+        KQ.norm_q8(h, nw, q, s, n, M, 1e-6)
+
+    def deferred(i):
+        KQ.norm_q8(h, nw, q, s, n, M, 1e-6, pending=KW.gemm(a, sa, ws[i], None, h, n, K, epi=1, slots=slots))
+
+    u = _graph_us(unsplit, copies, iters)
+    d = _graph_us(deferred, copies, iters)
+    del ws
+    torch.cuda.empty_cache()
+    return [dict(M=M, K=K, N=N, split=KW.defer_split(M, N, K, 4), us_unsplit=round(u, 2), us_deferred=round(d, 2))]
+
+
 def bench_producers(dev, iters=20):
     """The fused producers at config 1's shapes (HBM-bound: GB/s of bytes read plus written): norm_q8 on the fp32
     residual (T = 8192, HID = 5120) and swiglu_q8 on the bf16 gate|up output (T = 8192, FF = 13824), plus the
@@ -315,6 +352,7 @@ def bench_configs(dev):
     return {
         "producers": bench_producers(dev),
         "per_channel": bench_per_channel(dev),
+        "per_channel_deferred": bench_deferred(dev),
         "c0": bench_q8_decode(dev, [(4096, 4096)], (16,)),
         "c2": bench_q8_decode(dev, [(5120, 5120), (17408, 5120)], (1, 4, 16, 64)),
         "c3": bench_w4a8(dev),

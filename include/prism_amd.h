@@ -119,6 +119,18 @@ PRISM_API int prism_w8a8_pc_packed_gemm(const int8_t* a, const float* a_s, int64
                                         int64_t M, int64_t N, int64_t K, int epi, int kernel, void* stream);
 
 /*
+ * The deferred split-K form of the per-channel GEMM (the CUDA kernel's SPLIT_DEFER mode, csrc/w8a8_gemm.cu:266-271,
+ * :433-440, behind kernels/w8a8.py:200-204): K in `split` parts of whole 64-input chunks (part z: chunks
+ * floor(z KP / split) .. floor((z + 1) KP / split) - 1), part z's raw int32 sums sum_k a w written to
+ * slots + z slot_stride, row m at m * lds.  No scales: the reader of the residual (prism_norm_quant_fold,
+ * prism_fold_parts) adds the parts and applies epilogue 1.  Rows >= *n_rows are not written.  Needs N % 16 == 0,
+ * K % 64 == 0, K / 64 >= split, 1 <= split <= 16, lds >= N and slot_stride >= M lds (multiples of 4).
+ */
+PRISM_API int prism_w8a8_pc_packed_gemm_split(const int8_t* a, const int8_t* qt, int32_t* slots, int64_t slot_stride,
+                                              int64_t lds, const int32_t* n_rows, int64_t M, int64_t N, int64_t K,
+                                              int split, void* stream);
+
+/*
  * Q8_0 W8A8 GEMM (gk = 32, one activation scale per token) on packed weights: the arithmetic and bits of
  * prism_w8a8_gemm with gk = 32 (kernels/w8a8.py:64-85), the engine entry kernels/w8a8.py:183-231.
  * a int8 [M, K]; a_s fp32, row m at a_s[m * as_sm]; qt / dt from prism_q8_0_pack; out as prism_w8a8_gemm.
@@ -188,6 +200,27 @@ PRISM_API int prism_w4a8_q6k_gemm(const int8_t* xq, const float* a, int64_t a_sb
 PRISM_API int prism_norm_quant(const float* h, int64_t ldh, const float* w, const int32_t* rows, int8_t* q, float* s,
                                int8_t* xs, const int32_t* n_rows, int64_t M, int64_t HID, float eps, int back,
                                void* stream);
+
+/*
+ * prism_norm_quant that first finishes a residual add deferred by prism_w8a8_pc_packed_gemm_split (norm_q8 with
+ * `pending`, kernels/quant.py:418-431 and _fold_parts :129-141): per row r and column c, tot = the sum of the np
+ * slots' parts[p part_stride + r ldp + c] (int32, exact), h = RN(h + RN(RN(float(tot) psa[r psa_sm]) psw[c])) (psw
+ * fp32 [HID], fp16 when psw16), stored back to h; then the norm of the updated row.  psa may be s itself (a row reads
+ * its scale before writing its own).  No row gather.  Needs what prism_norm_quant needs, ldp >= HID and
+ * part_stride >= M ldp (multiples of 4), 1 <= np <= 64.
+ */
+PRISM_API int prism_norm_quant_fold(float* h, int64_t ldh, const float* w, int8_t* q, float* s, int8_t* xs,
+                                    const int32_t* n_rows, int64_t M, int64_t HID, float eps, int back,
+                                    const int32_t* parts, int64_t part_stride, int64_t ldp, int np, const float* psa,
+                                    int64_t psa_sm, const void* psw, int psw16, void* stream);
+
+/*
+ * The deferred residual add alone, when no norm follows (kernels/quant.py:435-457 fold): h updated as in
+ * prism_norm_quant_fold for rows < *n_rows.  Needs HID % 8 == 0, ldh % 4 == 0, M <= 65535.
+ */
+PRISM_API int prism_fold_parts(float* h, int64_t ldh, const int32_t* parts, int64_t part_stride, int64_t ldp, int np,
+                               const float* psa, int64_t psa_sm, const void* psw, int psw16, const int32_t* n_rows,
+                               int64_t M, int64_t HID, void* stream);
 
 /*
  * SwiGLU producer: y = RN(RN(silu(g) * u) * inv_s) with silu(g) = RN(g / RN(1 + exp(-g))) (exp: Cody-Waite

@@ -11,6 +11,8 @@ Pinning (each function is checked by tests/test_oracle.py against something othe
   quant_rows_i8 / _groups    special cases (zero row -> scale 1e-10/127, absmax -> +-127), numpy IEEE division
   w8a8_gemm                  int32 block sums vs brute-force int64 (numpy), fp32 result vs float64 within the
                              rounding bound, gk == K reducing to the per-channel formula, epi 1 = out + epi 0 value
+  fold_parts                 one slot holding numpy's int64 sums gives w8a8_gemm's gk = K, epi 1 residual bit for
+                             bit; any split of those sums into slots gives the same bits
   q4k_quantize / dequant     an independent numpy decoder of the GGUF block_q4_K layout (ggml get_scale_min_k4)
   q4k_repack                 the W4 nibble order re-derived from the dequantised values
   quant_rows_g               per-32 sums vs numpy, split-sum reconstruction, scale special cases
@@ -68,6 +70,8 @@ def lib():
             "orc_w8a8_block_sums": (None, [_p, _p, _i64, _i64, _i64, _i64, _p]),
             "orc_w8a8_gemm": (None, [_p, _p, _i64, _i64, _p, _p, ctypes.c_int, _i64, _i64, _i64, _i64,
                                      ctypes.c_int, _p, _i64, _i64, ctypes.c_int]),
+            "orc_fold_parts": (None, [_p, _i64, _p, _i64, _i64, ctypes.c_int, _p, _i64, _p, ctypes.c_int, _i64,
+                                      _i64]),
             "orc_q4k_quantize": (None, [_p, _i64, _i64, _p, ctypes.c_int]),
             "orc_q4k_dequant": (None, [_p, _i64, _i64, _p]),
             "orc_q4k_repack": (None, [_p, _i64, _i64, _p, _p, _p, _p, _p]),
@@ -206,6 +210,21 @@ def w8a8_gemm(a, a_s, w, w_s, gk, epi=0, out=None, live=None, nthreads=0):
     lib().orc_w8a8_gemm(_ptr(a), _ptr(a_s), as_sm, as_sg, _ptr(w), _ptr(w_s), int(ws16), M, N, K, gk, epi,
                         _ptr(out), out.shape[1], live, nthreads)
     return out
+
+
+def fold_parts(h, parts, psa, psw, live=None):
+    """(kernels/quant.py:129-141) h fp32 [M, HID] updated in place and returned: the deferred residual add of the
+    int32 slots parts [np, M, HID] with activation scales psa fp32 [M] and weight scales psw fp32 / fp16 bits
+    uint16 [HID]."""
+    assert h.dtype == np.float32 and h.flags["C_CONTIGUOUS"]
+    parts = np.ascontiguousarray(parts, np.int32)
+    psa = np.ascontiguousarray(psa, np.float32).reshape(-1)
+    psw16 = psw.dtype == np.uint16
+    psw = np.ascontiguousarray(psw).reshape(-1)
+    S, M, HID = parts.shape
+    lib().orc_fold_parts(_ptr(h), h.shape[1], _ptr(parts), M * HID, HID, S, _ptr(psa), 1, _ptr(psw), int(psw16),
+                         M if live is None else live, HID)
+    return h
 
 
 # ------------------------------------------------------------------------------------------------ Q4_K / W4A8

@@ -199,6 +199,26 @@ EXPORT void orc_w8a8_gemm(const int8_t* a, const float* a_s, int64_t as_sm, int6
     }
 }
 
+/*
+ * The residual add deferred by a split-K per-channel projection (kernels/quant.py:129-141 _fold_parts, run by norm_q8
+ * :160-166 and fold :435-457): tot = the sum over the np slots of parts[p][r][c] (int32: the splits' sums add up to
+ * the unsplit product's exact sum), then h[r][c] = RN(h + RN(RN(float(tot) psa[r]) psw[c])), the epilogue 1 of the
+ * unsplit product (orc_w8a8_gemm with gk = K, epi 1).  parts: slot stride part_stride, row stride ldp (elements);
+ * psa row r at psa[r * psa_sm]; psw fp32, fp16 bits when psw16.  Rows >= live untouched.
+ */
+EXPORT void orc_fold_parts(float* h, int64_t ldh, const int32_t* parts, int64_t part_stride, int64_t ldp, int np,
+                           const float* psa, int64_t psa_sm, const void* psw, int psw16, int64_t live, int64_t HID) {
+    for (int64_t r = 0; r < live; r++)
+        for (int64_t c = 0; c < HID; c++) {
+            int64_t tot = 0;
+            for (int p = 0; p < np; p++) tot += parts[p * part_stride + r * ldp + c];
+            float sw = psw16 ? orc_half_to_float(((const uint16_t*)psw)[c]) : ((const float*)psw)[c];
+            float t = (float)(int32_t)tot * psa[r * psa_sm];
+            t = t * sw;
+            h[r * ldh + c] = h[r * ldh + c] + t;
+        }
+}
+
 /* ----------------------------------------------------------------------------------------------- Q4_K */
 /*
  * A Q4_K quantizer of this build's own (the reference only reads Q4_K from files: gguf_weights.py:100-133).

@@ -137,21 +137,80 @@ __device__ __forceinline__ void store_back(float (&y)[NCH][8], float rmax, float
     (void)row;
 }
 
+// ---------------------------------------------------------------------------------------------- deferred fold
+// A residual add deferred by a split-K per-channel projection (prism_w8a8_pc_packed_gemm_split): the np int32 slots'
+// sums of 8 inputs of row r from column c, tot = slot 0 + slot 1 + ... (exact), then h = RN(h + RN(RN(float(tot) sa)
+// sw)) with sa = psa[r psa_sm] and sw = psw[c .. c + 7] (fp32, or fp16 when PSW16): the epilogue 1 of the unsplit
+// projection, so the residual gets the same bits whichever way the projection ran (kernels/quant.py:129-141).
+struct Fold {
+    const int32_t* parts;
+    int64_t part_stride, ldp;
+    int np;
+    const float* psa;
+    int64_t psa_sm;
+    const void* psw;
+    int psw16;
+};
+
+__device__ __forceinline__ void fold8(float* hv, const Fold& f, int64_t r, int c) {
+    int tot[8];
+    const int32_t* p0 = f.parts + r * f.ldp + c;
+    {
+        const v4i a = *reinterpret_cast<const v4i*>(p0), b = *reinterpret_cast<const v4i*>(p0 + 4);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            tot[j] = a[j];
+            tot[j + 4] = b[j];
+        }
+    }
+    for (int p = 1; p < f.np; p++) {
+        const int32_t* pp = p0 + p * f.part_stride;
+        const v4i a = *reinterpret_cast<const v4i*>(pp), b = *reinterpret_cast<const v4i*>(pp + 4);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            tot[j] += a[j];
+            tot[j + 4] += b[j];
+        }
+    }
+    const float sa = f.psa[r * f.psa_sm];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const float sw = f.psw16 ? f16_to_f32(static_cast<const uint16_t*>(f.psw)[c + j])
+                                 : static_cast<const float*>(f.psw)[c + j];
+        hv[j] = add_rn(hv[j], mul_rn(mul_rn((float)tot[j], sa), sw));
+    }
+}
+
+// h fp32 [*, HID] (row stride ldh): one thread per 8 values of a live row.
+__global__ __launch_bounds__(256) void fold_parts_kernel(float* __restrict__ h, int64_t ldh, Fold f,
+                                                         const int32_t* __restrict__ n_rows, int HID) {
+    const int64_t r = blockIdx.y;
+    const int c = 8 * (blockIdx.x * 256 + threadIdx.x);
+    if (r >= __ldg(n_rows) || c >= HID) return;
+    v4f* hp = reinterpret_cast<v4f*>(h + r * ldh + c);
+    const v4f a = hp[0], b = hp[1];
+    float hv[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+    fold8(hv, f, r, c);
+    hp[0] = v4f{hv[0], hv[1], hv[2], hv[3]};
+    hp[1] = v4f{hv[4], hv[5], hv[6], hv[7]};
+}
+
 // ---------------------------------------------------------------------------------------------- rmsnorm
-// h fp32 [*, HID] (row stride ldh), w fp32 [HID]; output row i from input row rows[i] when rows is not null.
-template <int NCH, int BACK>
-__global__ __launch_bounds__(kPThreads) void norm_prod_kernel(const float* __restrict__ h, int64_t ldh,
+// h fp32 [*, HID] (row stride ldh), w fp32 [HID]; output row i from input row rows[i] when rows is not null.  FOLD:
+// first finish a deferred residual add in the row (fold8) and store the row back to h.
+template <int NCH, int BACK, bool FOLD = false>
+__global__ __launch_bounds__(kPThreads) void norm_prod_kernel(float* __restrict__ h, int64_t ldh,
                                                               const float* __restrict__ w,
                                                               const int32_t* __restrict__ rows, int8_t* __restrict__ q,
                                                               float* __restrict__ s, int8_t* __restrict__ xs,
                                                               const int32_t* __restrict__ n_rows, int M, int HID,
-                                                              float eps) {
+                                                              float eps, Fold f) {
     __shared__ float red[4];
     const int i = blockIdx.x;
     if (i >= __ldg(n_rows)) return;
     const int64_t src = rows ? (int64_t)__ldg(rows + i) : i;
     const int nch = HID / 8;
-    const v4f* hr = reinterpret_cast<const v4f*>(h + src * ldh);
+    v4f* hr = reinterpret_cast<v4f*>(h + src * ldh);
     const v4f* wr = reinterpret_cast<const v4f*>(w);
     float y[NCH][8];
     float ss = 0.f;
@@ -164,6 +223,11 @@ __global__ __launch_bounds__(kPThreads) void norm_prod_kernel(const float* __res
             for (int j = 0; j < 4; j++) {
                 y[c][j] = a[j];
                 y[c][j + 4] = b[j];
+            }
+            if (FOLD) {
+                fold8(y[c], f, src, 8 * idx);
+                hr[2 * idx] = v4f{y[c][0], y[c][1], y[c][2], y[c][3]};
+                hr[2 * idx + 1] = v4f{y[c][4], y[c][5], y[c][6], y[c][7]};
             }
 #pragma unroll
             for (int j = 0; j < 8; j++) ss = add_rn(ss, mul_rn(y[c][j], y[c][j]));
@@ -346,30 +410,67 @@ static int pick_nch(int K, KN&& launch, int tpb = kPThreads) {
 
 using namespace prism;
 
-// back: 0 int8 + row scale; 1 W4A8 operands, scale per 256; 2 W4A8 operands, one scale per row.
-extern "C" int prism_norm_quant(const float* h, int64_t ldh, const float* w, const int32_t* rows, int8_t* q, float* s,
-                                int8_t* xs, const int32_t* n_rows, int64_t M, int64_t HID, float eps, int back,
-                                void* stream) {
+static int norm_launch(float* h, int64_t ldh, const float* w, const int32_t* rows, int8_t* q, float* s, int8_t* xs,
+                       const int32_t* n_rows, int64_t M, int64_t HID, float eps, int back, const Fold& f,
+                       hipStream_t st) {
     if (!h || !w || !q || !s || !n_rows || (back != 0 && !xs)) return PRISM_ERR_ARG;
     if (back < 0 || back > 2) return PRISM_ERR_ARG;
     if (M < 0 || HID <= 0 || HID % 8 || ldh < HID || ldh % 8 || HID > 32768 || M > (1 << 30)) return PRISM_ERR_SHAPE;
     if (back != 0 && HID % 256) return PRISM_ERR_SHAPE;
     if (!PRISM_ALIGNED(h, 16) || !PRISM_ALIGNED(w, 16) || !PRISM_ALIGNED(q, 8)) return PRISM_ERR_ALIGN;
     if (M == 0) return PRISM_OK;
-    hipStream_t st = (hipStream_t)stream;
+    const bool fold = f.np > 0;
     return pick_nch((int)HID, [&](auto nc) {
         constexpr int NC = decltype(nc)::value;
-        if (back == 0)
-            hipLaunchKernelGGL((norm_prod_kernel<NC, 0>), dim3((unsigned)M), dim3(kPThreads), 0, st, h, ldh, w, rows,
-                               q, s, xs, n_rows, (int)M, (int)HID, eps);
-        else if (back == 1)
-            hipLaunchKernelGGL((norm_prod_kernel<NC, 1>), dim3((unsigned)M), dim3(kPThreads), 0, st, h, ldh, w, rows,
-                               q, s, xs, n_rows, (int)M, (int)HID, eps);
-        else
-            hipLaunchKernelGGL((norm_prod_kernel<NC, 2>), dim3((unsigned)M), dim3(kPThreads), 0, st, h, ldh, w, rows,
-                               q, s, xs, n_rows, (int)M, (int)HID, eps);
+#define NQ(B, F) hipLaunchKernelGGL((norm_prod_kernel<NC, B, F>), dim3((unsigned)M), dim3(kPThreads), 0, st, h, ldh, w, \
+                                    rows, q, s, xs, n_rows, (int)M, (int)HID, eps, f)
+        if (fold) { if (back == 0) NQ(0, true); else if (back == 1) NQ(1, true); else NQ(2, true); }
+        else { if (back == 0) NQ(0, false); else if (back == 1) NQ(1, false); else NQ(2, false); }
+#undef NQ
         return hipGetLastError() == hipSuccess ? 0 : (int)PRISM_ERR_LAUNCH;
     });
+}
+
+static int check_fold(const Fold& f, int64_t M, int64_t HID) {
+    if (f.np < 1 || f.np > 64 || !f.parts || !f.psa || !f.psw) return PRISM_ERR_ARG;
+    if (f.ldp < HID || (f.np > 1 && f.part_stride < M * f.ldp)) return PRISM_ERR_SHAPE;
+    if (!PRISM_ALIGNED(f.parts, 16) || f.ldp % 4 || f.part_stride % 4) return PRISM_ERR_ALIGN;
+    return PRISM_OK;
+}
+
+// back: 0 int8 + row scale; 1 W4A8 operands, scale per 256; 2 W4A8 operands, one scale per row.
+extern "C" int prism_norm_quant(const float* h, int64_t ldh, const float* w, const int32_t* rows, int8_t* q, float* s,
+                                int8_t* xs, const int32_t* n_rows, int64_t M, int64_t HID, float eps, int back,
+                                void* stream) {
+    const Fold none{};
+    return norm_launch(const_cast<float*>(h), ldh, w, rows, q, s, xs, n_rows, M, HID, eps, back, none,
+                       (hipStream_t)stream);
+}
+
+extern "C" int prism_norm_quant_fold(float* h, int64_t ldh, const float* w, int8_t* q, float* s, int8_t* xs,
+                                     const int32_t* n_rows, int64_t M, int64_t HID, float eps, int back,
+                                     const int32_t* parts, int64_t part_stride, int64_t ldp, int np, const float* psa,
+                                     int64_t psa_sm, const void* psw, int psw16, void* stream) {
+    const Fold f{parts, part_stride, ldp, np, psa, psa_sm, psw, psw16};
+    const int rc = check_fold(f, M, HID);
+    if (rc != PRISM_OK) return rc;
+    return norm_launch(h, ldh, w, nullptr, q, s, xs, n_rows, M, HID, eps, back, f, (hipStream_t)stream);
+}
+
+extern "C" int prism_fold_parts(float* h, int64_t ldh, const int32_t* parts, int64_t part_stride, int64_t ldp, int np,
+                                const float* psa, int64_t psa_sm, const void* psw, int psw16, const int32_t* n_rows,
+                                int64_t M, int64_t HID, void* stream) {
+    if (!h || !n_rows) return PRISM_ERR_ARG;
+    if (M < 0 || HID <= 0 || HID % 8 || ldh < HID || ldh % 4 || M > 65535 || HID > (1 << 24)) return PRISM_ERR_SHAPE;
+    const Fold f{parts, part_stride, ldp, np, psa, psa_sm, psw, psw16};
+    const int rc = check_fold(f, M, HID);
+    if (rc != PRISM_OK) return rc;
+    if (!PRISM_ALIGNED(h, 16)) return PRISM_ERR_ALIGN;
+    if (M == 0) return PRISM_OK;
+    hipLaunchKernelGGL(fold_parts_kernel, dim3((unsigned)((HID / 8 + 255) / 256), (unsigned)M), dim3(256), 0,
+                       (hipStream_t)stream, h, ldh, f, n_rows, (int)HID);
+    PRISM_LAUNCH_CHECK();
+    return PRISM_OK;
 }
 
 extern "C" int prism_swiglu_quant(const void* gu, int gu_f32, int64_t ldg, const float* inv_s, int8_t* q, float* s,

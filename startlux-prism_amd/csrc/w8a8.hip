@@ -530,7 +530,7 @@ __global__ __launch_bounds__(256, 2) void w8a8_q8_tile_kernel(const int8_t* __re
 // ============================================================================================== launch
 int launch_w8a8_pc(int kernel, bool wpack, const int8_t* a, const float* a_s, int64_t as_sm, const int8_t* w,
                    const void* w_s, bool ws16, void* out, int64_t ldo, const int32_t* n_rows, int M, int N, int K,
-                   int epi, hipStream_t st);
+                   int epi, hipStream_t st, int split, int64_t zstride);
 
 template <bool AS_GROUP, bool WS16, int EPI>
 static int launch_w8a8(int kernel, const int8_t* a, const float* a_s, int64_t as_sm, int64_t as_sg, const int8_t* w,
@@ -538,7 +538,7 @@ static int launch_w8a8(int kernel, const int8_t* a, const float* a_s, int64_t as
                        hipStream_t st) {
     // per channel (one group): the int8 MFMA GEMMs with an epilogue (w8a8_pc.hip)
     if (gk == K && K % 64 == 0 && ldo % 4 == 0 && PRISM_ALIGNED(out, EPI ? 16 : 8))
-        return launch_w8a8_pc(kernel, false, a, a_s, as_sm, w, w_s, WS16, out, ldo, n_rows, M, N, K, EPI, st);
+        return launch_w8a8_pc(kernel, false, a, a_s, as_sm, w, w_s, WS16, out, ldo, n_rows, M, N, K, EPI, st, 1, 0);
     if (kernel == 1) {
         dim3 grid(N / 16);
 #define DEC(NW, R, MT, D)                                                                                         \

@@ -180,12 +180,15 @@ __global__ __launch_bounds__(1024) void w8a8_pc_decode_kernel(const int8_t* __re
                                                               const int8_t* __restrict__ w,
                                                               const void* __restrict__ w_s, void* __restrict__ out,
                                                               int64_t ldo, const int32_t* __restrict__ n_rows, int M,
-                                                              int N, int K) {
+                                                              int N, int K, int64_t zstride) {
     constexpr int PD = MT <= 2 ? 4 : 2;
     extern __shared__ __attribute__((aligned(16))) v4i red[];          // [NW][G][MT][64]
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, NW = blockDim.x >> 6;
     const int nt0 = blockIdx.x * G, r0 = 16 * MT * blockIdx.y;
     const int KP = K / 64, NT = N / 16;
+    // split z of gridDim.z takes the 64-input chunks kc0 .. kc1 - 1 (EPI 2: its int32 sums go to slot z)
+    const int z = blockIdx.z;
+    const int kc0 = (int)((int64_t)KP * z / gridDim.z), KC = (int)((int64_t)KP * (z + 1) / gridDim.z) - kc0;
     const int live = min(M, __ldg(n_rows));
     if (r0 >= live) return;                                             // the whole workgroup: before any barrier
     const int lm = lane & 15, q = lane >> 4;
@@ -205,7 +208,7 @@ __global__ __launch_bounds__(1024) void w8a8_pc_decode_kernel(const int8_t* __re
         v2u x0[MT], x1[MT];
     };
     auto load = [&](int j, Chunk& c) {
-        const int jj = min(j, KP - 1);
+        const int jj = kc0 + min(j, KC - 1);
 #pragma unroll
         for (int g = 0; g < G; g++) c.w[g] = *reinterpret_cast<const v4i*>(wb[g] + (int64_t)jj * (WPACK ? 1024 : 64));
 #pragma unroll
@@ -235,7 +238,7 @@ __global__ __launch_bounds__(1024) void w8a8_pc_decode_kernel(const int8_t* __re
         }
     };
     // this wave's chunks: j = wv + NW i, i < cnt; branch-free body over whole rings of PD
-    const int cnt = wv < KP ? (KP - wv + NW - 1) / NW : 0;
+    const int cnt = wv < KC ? (KC - wv + NW - 1) / NW : 0;
     Chunk ring[PD];
 #pragma unroll
     for (int d = 0; d < PD; d++) load(wv + NW * d, ring[d]);
@@ -262,11 +265,15 @@ __global__ __launch_bounds__(1024) void w8a8_pc_decode_kernel(const int8_t* __re
         if (m >= live || t >= NT) continue;
         v4i P = red[idx];
         for (int v = 1; v < NW; v++) {
-            const v4i z = red[v * G * MT * 64 + idx];
-            P = v4i{P.x + z.x, P.y + z.y, P.z + z.z, P.w + z.w};
+            const v4i u = red[v * G * MT * 64 + idx];
+            P = v4i{P.x + u.x, P.y + u.y, P.z + u.z, P.w + u.w};
+        }
+        const int n = 16 * t + 4 * (l >> 4);
+        if (EPI == 2) {                                                 // a deferred split: the raw int32 sums
+            *reinterpret_cast<v4i*>(static_cast<int32_t*>(out) + z * zstride + (int64_t)m * ldo + n) = P;
+            continue;
         }
         const float sa = a_s[(int64_t)m * as_sm];
-        const int n = 16 * t + 4 * (l >> 4);
         float y[4];
 #pragma unroll
         for (int e = 0; e < 4; e++) {
@@ -288,21 +295,21 @@ __global__ __launch_bounds__(1024) void w8a8_pc_decode_kernel(const int8_t* __re
 
 
 // Per-channel launch: kernel 1 the decode kernel (up to 64 rows per workgroup, grid rows beyond), else the tile
-// kernel.  The caller has checked
-// K % 64 == 0, 16-byte aligned a / w, ldo % 4 == 0 and an 8 / 16-byte aligned out.
+// kernel.  epi 2 (decode kernel only): K in `split` parts, part z's int32 sums to out + z zstride.  The caller has
+// checked K % 64 == 0, 16-byte aligned a / w, ldo % 4 == 0 and an 8 / 16-byte aligned out.
 int launch_w8a8_pc(int kernel, bool wpack, const int8_t* a, const float* a_s, int64_t as_sm, const int8_t* w,
                    const void* w_s, bool ws16, void* out, int64_t ldo, const int32_t* n_rows, int M, int N, int K,
-                   int epi, hipStream_t st) {
+                   int epi, hipStream_t st, int split, int64_t zstride) {
     if (kernel == 1) {
         const int MT = min(4, (M + 15) / 16);
         const int G = (N % 32 == 0) ? 2 : 1;
-        const int KP = K / 64;
+        const int KP = K / 64 / split;
         int nw = min(8, max(1, KP / 4));               // 8 waves: 64 KB in flight per workgroup (16 measured slower)
         const size_t lds = (size_t)nw * G * MT * 64 * sizeof(v4i);
-        dim3 grid((unsigned)(N / (16 * G)), (unsigned)((M + 16 * MT - 1) / (16 * MT)));
+        dim3 grid((unsigned)(N / (16 * G)), (unsigned)((M + 16 * MT - 1) / (16 * MT)), (unsigned)split);
 #define PDL(GV, MTV, WP, W16, E)                                                                                   \
     hipLaunchKernelGGL((w8a8_pc_decode_kernel<GV, MTV, WP, W16, E>), grid, dim3(64 * nw), lds, st, a, a_s, as_sm, w, \
-                       w_s, out, ldo, n_rows, M, N, K)
+                       w_s, out, ldo, n_rows, M, N, K, zstride)
 #define PDL_MT(GV, WP, W16, E)                                                                                     \
     do {                                                                                                           \
         if (MT == 1) PDL(GV, 1, WP, W16, E); else if (MT == 2) PDL(GV, 2, WP, W16, E);                             \
@@ -310,7 +317,8 @@ int launch_w8a8_pc(int kernel, bool wpack, const int8_t* a, const float* a_s, in
     } while (0)
 #define PDL_G(WP, W16, E) do { if (G == 2) PDL_MT(2, WP, W16, E); else PDL_MT(1, WP, W16, E); } while (0)
 #define PDL_WP(W16, E) do { if (wpack) PDL_G(true, W16, E); else PDL_G(false, W16, E); } while (0)
-        if (ws16) { if (epi == 0) PDL_WP(true, 0); else PDL_WP(true, 1); }
+        if (epi == 2) PDL_WP(false, 2);
+        else if (ws16) { if (epi == 0) PDL_WP(true, 0); else PDL_WP(true, 1); }
         else { if (epi == 0) PDL_WP(false, 0); else PDL_WP(false, 1); }
 #undef PDL_WP
 #undef PDL_G
@@ -356,5 +364,21 @@ extern "C" int prism_w8a8_pc_packed_gemm(const int8_t* a, const float* a_s, int6
     if (kernel == 1 && M > 65535 * 64) return PRISM_ERR_SHAPE;           // grid rows: one per 64 activation rows
     if (M == 0) return PRISM_OK;
     return launch_w8a8_pc(kernel, true, a, a_s, as_sm, qt, w_s, ws_fp16 != 0, out, ldo, n_rows, (int)M, (int)N,
-                          (int)K, epi, (hipStream_t)stream);
+                          (int)K, epi, (hipStream_t)stream, 1, 0);
+}
+
+extern "C" int prism_w8a8_pc_packed_gemm_split(const int8_t* a, const int8_t* qt, int32_t* slots, int64_t slot_stride,
+                                               int64_t lds, const int32_t* n_rows, int64_t M, int64_t N, int64_t K,
+                                               int split, void* stream) {
+    if (!a || !qt || !slots || !n_rows) return PRISM_ERR_ARG;
+    if (split < 1 || split > 16) return PRISM_ERR_ARG;
+    if (M < 0 || N <= 0 || K <= 0 || N % 16 || K % 64 || lds < N || M > 65535 * 64 || N > (1 << 30) ||
+        K > (1 << 17) || K / 64 < split)
+        return PRISM_ERR_SHAPE;
+    if (split > 1 && slot_stride < M * lds) return PRISM_ERR_SHAPE;    // the slots must not overlap
+    if (!PRISM_ALIGNED(a, 16) || !PRISM_ALIGNED(qt, 16) || !PRISM_ALIGNED(slots, 16) || lds % 4 || slot_stride % 4)
+        return PRISM_ERR_ALIGN;
+    if (M == 0) return PRISM_OK;
+    return launch_w8a8_pc(1, true, a, nullptr, 0, qt, nullptr, false, slots, lds, n_rows, (int)M, (int)N, (int)K, 2,
+                          (hipStream_t)stream, split, slot_stride);
 }

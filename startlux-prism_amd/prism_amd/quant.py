@@ -74,12 +74,31 @@ def _rows_arg(n, T, dev):
     return _live(n, T, dev)
 
 
+def _fold_args(h, parts, pending, T):
+    """(parts, part stride, row stride, count, psa, psa row stride, psw, psw fp16) of a Deferred."""
+    if pending.sync is not None:
+        raise NotImplementedError("tensor-parallel deferred adds (Sync) are out of scope on one GPU")
+    if pending.parts is not None:
+        parts = pending.parts
+    HID = h.shape[1]
+    if parts is None or parts.dtype != torch.int32 or parts.dim() != 3 or parts.shape[0] < pending.n \
+            or parts.shape[1] < T or parts.shape[2] < HID or parts.stride(2) != 1:
+        raise ValueError("parts must be int32 [>= n, >= T, >= HID] with unit column stride")
+    psa = pending.a_s
+    if psa.dtype != torch.float32:
+        raise TypeError("the deferred activation scales must be fp32")
+    psw = pending.w_s.reshape(-1)
+    if psw.dtype not in (torch.float32, torch.float16) or psw.numel() < HID or not psw.is_contiguous():
+        raise ValueError("the deferred weight scales must be contiguous fp32 / fp16 [HID]")
+    return (L.ptr(parts), parts.stride(0), parts.stride(1), int(pending.n), L.ptr(psa), psa.stride(0), L.ptr(psw),
+            int(psw.dtype == torch.float16))
+
+
 def norm_q8(h, w_over_s, q, s, n, T, eps, rows=None, parts=None, pending=None):
     """h fp32 [*, HID] -> q int8 [>=T, HID], s fp32 [>=T]: y = rmsnorm(h) * w_over_s, one scale per row.  rows int32
-    [T] (optional): output row i from input row rows[i].  A deferred residual add (parts / pending) never exists in
-    this build, whose GEMMs do not split K into slots."""
-    if pending:
-        raise NotImplementedError("deferred split-K residual adds are not produced by this build's GEMMs")
+    [T] (optional): output row i from input row rows[i].  pending (w8a8.Deferred or None): a residual add deferred
+    by a split-K projection, finished in h first (its own slots when it names them, else `parts`) and kept there
+    (kernels/quant.py:418-431); the deferred projection's activation scales may be `s` itself."""
     HID = h.shape[1]
     if h.dtype != torch.float32 or w_over_s.dtype != torch.float32 or q.dtype != torch.int8 or s.dtype != torch.float32:
         raise TypeError("norm_q8: h fp32, w fp32, q int8, s fp32")
@@ -88,14 +107,25 @@ def norm_q8(h, w_over_s, q, s, n, T, eps, rows=None, parts=None, pending=None):
     if rows is not None and (rows.dtype != torch.int32 or rows.numel() < T):
         raise ValueError("norm_q8: rows must be int32 [T]")
     n = _rows_arg(n, T, h.device)
+    if pending:
+        if rows is not None:
+            raise ValueError("norm_q8: a deferred add and a row gather together (the reference asserts rows is None)")
+        L.call("prism_norm_quant_fold", L.ptr(h), h.stride(0), L.ptr(w_over_s.contiguous()), L.ptr(q), L.ptr(s), None,
+               L.ptr(n), T, HID, float(eps), 0, *_fold_args(h, parts, pending, T), L.stream_of(h))
+        return
     L.call("prism_norm_quant", L.ptr(h), h.stride(0), L.ptr(w_over_s.contiguous()), L.ptr(rows), L.ptr(q), L.ptr(s),
            None, L.ptr(n), T, HID, float(eps), 0, L.stream_of(h))
 
 
 def fold(h, parts, pending, n, T):
-    """Finish a deferred residual add: nothing to do, no GEMM here defers one."""
-    if pending:
-        raise NotImplementedError("deferred split-K residual adds are not produced by this build's GEMMs")
+    """Finish a deferred residual add (w8a8.Deferred) in h when no norm follows (kernels/quant.py:449-457)."""
+    if not pending:
+        return
+    if h.dtype != torch.float32 or h.stride(1) != 1:
+        raise TypeError("fold: h must be fp32 rows")
+    n = _rows_arg(n, T, h.device)
+    L.call("prism_fold_parts", L.ptr(h), h.stride(0), *_fold_args(h, parts, pending, T), L.ptr(n), T, h.shape[1],
+           L.stream_of(h))
 
 
 def _swiglu(gu, inv_s, q, s, xs, n, T, back):

@@ -10,8 +10,11 @@ Differences from the reference, by design of this single-GPU MI355X build:
   * w_s may be the Q8_0 fp16 scales themselves (torch.float16 [N, K/32]); the kernels widen them exactly, so the
     weight stream is 34 bytes per 32 weights instead of 36.
   * a_s may be fp32 [M] (or [M, 1]): one activation scale per token, broadcast over the groups.
-  * No split-K: the kernels never defer a residual add, so gemm() always returns None (cfg / slots / pdl are
-    accepted and ignored).  Epilogues 2 (fused SwiGLU) and 3 (raw int32, tensor parallel) are not provided.
+  * The deferred split-K residual add (kernels/w8a8.py:200-204) is produced for per-channel packed weights only
+    (PackedPC, epilogue 1, up to 64 rows, the decode kernel's domain, where K split over more workgroups feeds
+    every CU): its int32 parts go to `slots` and gemm returns a Deferred for quant.norm_q8 / quant.fold, which give
+    the residual the unsplit product's bits.  cfg / outs / pdl are accepted and ignored.  Epilogues 2 (fused
+    SwiGLU) and 3 (raw int32, tensor parallel) are not provided.
 """
 from typing import NamedTuple
 
@@ -76,7 +79,10 @@ def pack_i8(w, ws):
 
 
 class Deferred(NamedTuple):
-    """The reference's deferred split-K residual add (kernels/w8a8.py:171-180); never produced here."""
+    """A residual add left to the next kernel that reads the residual (quant.norm_q8 or quant.fold), as the
+    reference's (kernels/w8a8.py:171-180): `n` int32 slots of partial sums, and the projection's activation and
+    weight scales to apply to their total.  parts: the slots when they are not the reader's own `parts` buffer (this
+    build always names them); sync: tensor-parallel readers, not used on one GPU."""
     n: int
     a_s: torch.Tensor
     w_s: torch.Tensor
@@ -100,12 +106,17 @@ def _scales_a(a_s, M, G):
 def gemm(a, a_s, w, w_s, out, n_rows, gk, epi=0, outs=None, cfg=None, slots=None, pdl=False, kernel="auto"):
     """a int8 [M, K], a_s fp32 [M] / [M, 1] / [M, K/gk], w int8 [N, K], w_s fp16 or fp32 [N, K/gk] -> out
     (epi 0: bf16 [M, >=N] row stride out.stride(0); epi 1: fp32, out += y).  n_rows: device int32 [1], rows >=
-    n_rows[0] untouched.  Returns None (no deferred split-K)."""
+    n_rows[0] untouched.  Returns None, or a Deferred when an epi 1 per-channel product split K into `slots` (int32
+    [S, >= M, N]): then `out` is untouched and the residual add is finished by quant.norm_q8 / quant.fold."""
     if epi not in (0, 1):
         raise NotImplementedError(f"epilogue {epi}: only 0 (bf16 store) and 1 (fp32 residual add) are provided")
     if isinstance(w, PackedQ8):
         return _gemm_packed(a, a_s, w, out, n_rows, gk, epi, kernel)
     if isinstance(w, PackedPC):
+        if slots is not None and epi == 1 and gk == w.k:
+            d = _gemm_pc_deferred(a, a_s, w, slots, n_rows, kernel)
+            if d is not None:
+                return d
         return _gemm_pc_packed(a, a_s, w, out, n_rows, gk, epi, kernel)
     M, K = a.shape
     N = w.shape[0]
@@ -174,6 +185,36 @@ def _gemm_pc_packed(a, a_s, w, out, n_rows, gk, epi, kernel):
            int(w.ws.dtype == torch.float16), L.ptr(out), out.stride(0), L.ptr(n_rows), M, w.n, K, epi,
            KERNELS[kernel], L.stream_of(a))
     return None
+
+
+# When a per-channel epilogue-1 product defers (the reference takes the split from its dispatch table,
+# kernels/w8a8.py:199-204): measured on MI355X with the norm that finishes the add, splitting the decode kernel's K
+# pays only for long K at 16-64 rows (5120 x 17408 at 64 rows: 79.6 -> 64.5 us for projection plus norm_q8; 2% at 16
+# rows; 10-40% slower at 1-4 rows or K <= 6144, where the slots' extra traffic and launch outweigh the spread).  The
+# count keeps the workgroups (two 16-row weight tiles each) within two per CU: 512.
+def defer_split(M, N, K, S):
+    """The number of K parts a deferred per-channel product uses with S slots available (1: do not defer)."""
+    if M < 16 or M > 64 or K < 12288 or S < 2:
+        return 1
+    wgs = N // 32 if N % 32 == 0 else N // 16
+    return max(1, min(4, S, 512 // max(1, wgs), K // (64 * 16)))
+
+
+def _gemm_pc_deferred(a, a_s, w, slots, n_rows, kernel):
+    M, K = a.shape
+    if kernel not in ("auto", "decode"):
+        return None
+    if slots.dtype != torch.int32 or slots.dim() != 3 or slots.shape[1] < M or slots.shape[2] < w.n \
+            or slots.stride(2) != 1:
+        raise ValueError("slots must be int32 [S, >= M, >= N] with unit column stride")
+    split = defer_split(M, w.n, K, slots.shape[0])
+    if split < 2:
+        return None
+    if a.dtype != torch.int8 or not a.is_contiguous() or w.k != K:
+        raise ValueError("a must be contiguous int8 [M, K] matching the weights")
+    L.call("prism_w8a8_pc_packed_gemm_split", L.ptr(a), L.ptr(w.qt), L.ptr(slots), slots.stride(0), slots.stride(1),
+           L.ptr(n_rows), M, w.n, K, split, L.stream_of(a))
+    return Deferred(split, a_s, w.ws, slots)
 
 
 def weight_from_q8(q8, gk, smooth=None, packed=True):

@@ -258,6 +258,31 @@ def _np_dequant_q4k(blocks):
     return out
 
 
+def test_fold_parts_is_the_unsplit_epilogue():
+    """The deferred residual add: one slot holding numpy's brute-force int64 sums gives the oracle GEMM's gk = K,
+    epi 1 residual bit for bit; random splits of those sums into 2-5 slots give the same bits; rows >= live keep
+    their values; fp16 weight scales give the same bits as the same values in fp32."""
+    g = rng(41)
+    M, N, K = 9, 80, 512
+    a = g.integers(-127, 128, (M, K)).astype(np.int8)
+    w = g.integers(-127, 128, (N, K)).astype(np.int8)
+    sa = (g.random(M) * 0.02).astype(np.float32)
+    sw16 = (g.random(N) * 0.01).astype(np.float16)
+    sw = sw16.astype(np.float32)
+    h = (g.standard_normal((M, N)) * 3).astype(np.float32)
+    ref = O.w8a8_gemm(a, sa, w, sw.reshape(N, 1), K, epi=1, out=h.copy())
+    P = a.astype(np.int64) @ w.astype(np.int64).T
+    assert np.array_equal(O.fold_parts(h.copy(), P[None].astype(np.int32), sa, sw).view(np.int32), ref.view(np.int32))
+    for S in (2, 3, 5):
+        cut = g.integers(-2 ** 20, 2 ** 20, (S - 1, M, N))
+        parts = np.concatenate([cut, (P - cut.sum(0))[None]]).astype(np.int32)
+        assert np.array_equal(parts.astype(np.int64).sum(0), P)
+        got = O.fold_parts(h.copy(), parts, sa, sw16.view(np.uint16))
+        assert np.array_equal(got.view(np.int32), ref.view(np.int32))
+    part = O.fold_parts(h.copy(), P[None].astype(np.int32), sa, sw, live=4)
+    assert np.array_equal(part[:4].view(np.int32), ref[:4].view(np.int32)) and np.array_equal(part[4:], h[4:])
+
+
 def test_q4k_quantizer_layout_and_torch():
     from prism_amd import gguf_formats as GF
     w = weights_f32(6, 512, seed=21)
