@@ -98,9 +98,10 @@ PRISM_API int prism_q8_0_pack(const int8_t* qs, const uint16_t* d, int8_t* qt, u
                               void* stream);
 
 /*
- * The same chunk permutation for plain int8 weights w [N, K] (per-channel, gk = K): qt int8 [N/16][K/64][64][16] as
- * prism_q8_0_pack's qt.  The load-time repack of the per-channel weights kernels/w8a8.py:274-286 produces.
- * Needs N % 16 == 0, K % 64 == 0.
+ * The chunked layout for plain int8 weights w [N, K] (per-channel, gk = K): qt int8 [N/16][K/64][64][16], lane
+ * slot l of chunk (nt, j) holding inputs 64 j + 16 (l / 16) .. + 15 of row 16 nt + l % 16 (no blocks to keep apart,
+ * so a slot is one MFMA operand as it lies).  The load-time repack of the per-channel weights kernels/w8a8.py:274-286
+ * produces.  Needs N % 16 == 0, K % 64 == 0.
  */
 PRISM_API int prism_i8_pack(const int8_t* w, int8_t* qt, int64_t N, int64_t K, void* stream);
 

@@ -8,6 +8,8 @@
 //       halves are the A operands of v_mfma_i32_16x16x32_i8 for the two blocks, with no re-layout.
 //   dt  fp16 [N/16][K/64][16][2]: the Q8_0 block scales of the chunk, row-major over (row, block of the pair), so a
 //       lane's four output rows 4 (l / 16) .. +3 are one 16-byte load.
+// Per-channel int8 weights (prism_i8_pack, no blocks to keep apart) use the same chunks with lane slot l holding
+// inputs 64 j + 16 q .. + 15 of its row: the 16-byte operand of v_mfma_i32_16x16x64_i8 / 32x32x32_i8 as it lies.
 // Arithmetic: identical to the row-major kernels (kernels/w8a8.py:64-85), every output's fp32 sum over blocks in
 // block order, so both layouts give the same bits.
 #include "common.h"
@@ -29,6 +31,11 @@ __global__ __launch_bounds__(256) void q8_0_pack_kernel(const int8_t* __restrict
     const int l = (int)(e & 63), r = l & 15, q = l >> 4;
     const int64_t c = e >> 6;
     const int j = (int)(c % KP), nt = (int)(c / KP);
+    if (!d) {                                          // per-channel: inputs 16 q .. 16 q + 15 of the chunk
+        reinterpret_cast<v4u*>(qt)[e] =
+            *reinterpret_cast<const v4u*>(qs + (int64_t)(16 * nt + r) * K + 64 * j + 16 * q);
+        return;
+    }
     const int8_t* src = qs + (int64_t)(16 * nt + r) * K + 64 * j + 8 * q;
     v2u lo = *reinterpret_cast<const v2u*>(src), hi = *reinterpret_cast<const v2u*>(src + 32);
     v4u o;

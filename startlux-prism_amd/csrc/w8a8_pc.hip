@@ -47,7 +47,7 @@ __global__ __launch_bounds__(256, 1) void w8a8_pc_tile_kernel(const int8_t* __re
     }
 
     // DMA sources: instruction i of wave wv covers operand rows 16 (4 wv + i) .. + 15; packed weights: the 1 KB
-    // chunk of 16-row tile 4 wv + i as it lies (lane slot l: row l % 16, inputs {8 q .. +7, 32 + 8 q .. +7}, q = l / 16)
+    // chunk of 16-row tile 4 wv + i as it lies (lane slot l: row l % 16, inputs 16 q .. + 15, q = l / 16)
     const int8_t* asrc[4];
     const int8_t* wsrc[4];
 #pragma unroll
@@ -71,23 +71,17 @@ __global__ __launch_bounds__(256, 1) void w8a8_pc_tile_kernel(const int8_t* __re
 
     const int wm = wv >> 1, wn = wv & 1;
     const int r = lane & 31, h = lane >> 5;
-    // fragment byte offsets within an operand stage, for the two 32-input steps s.  Row-major weights: both
-    // operands' lanes hold inputs 16 (2 s + h) .. + 15.  Packed weights: the chunk's lane slot (q = 2 s + h, row)
-    // holds inputs {8 q .. +7, 32 + 8 q .. +7}, and the activation fragment takes the same two 8-byte pieces.
+    // fragment byte offsets within an operand stage, for the two 32-input steps s: both operands' lanes hold inputs
+    // 16 (2 s + h) .. + 15 (packed weights: the chunk's lane slot q = 2 s + h of the row).
     int aoff[2][4], woff[2][4];
 #pragma unroll
     for (int s = 0; s < 2; s++)
 #pragma unroll
         for (int t = 0; t < 4; t++) {
             const int ra = 128 * wm + 32 * t + r, rw = 128 * wn + 32 * t + r;
-            if (WPACK) {
-                const int q = 2 * s + h;
-                aoff[s][t] = ra * PCK + 16 * ((q >> 1) ^ pc_swz(ra)) + 8 * (q & 1);
-                woff[s][t] = (rw >> 4) * 1024 + (16 * q + (rw & 15)) * 16;
-            } else {
-                aoff[s][t] = ra * PCK + 16 * ((2 * s + h) ^ pc_swz(ra));
-                woff[s][t] = rw * PCK + 16 * ((2 * s + h) ^ pc_swz(rw));
-            }
+            aoff[s][t] = ra * PCK + 16 * ((2 * s + h) ^ pc_swz(ra));
+            woff[s][t] = WPACK ? (rw >> 4) * 1024 + (16 * (2 * s + h) + (rw & 15)) * 16
+                               : rw * PCK + 16 * ((2 * s + h) ^ pc_swz(rw));
         }
 
     v16i acc[4][4];
@@ -115,15 +109,7 @@ __global__ __launch_bounds__(256, 1) void w8a8_pc_tile_kernel(const int8_t* __re
             v4i fa[4], fw[4];
 #pragma unroll
             for (int t = 0; t < 4; t++) {
-                if (WPACK) {
-                    // inputs 8 q .. (chunk q / 2) and 32 + 8 q .. (chunk 2 + q / 2 = (q / 2) ^ 2: its swizzled slot
-                    // is the first one's ^ 2, 32 bytes away)
-                    const v2u p0 = *reinterpret_cast<const v2u*>(b + aoff[s][t]);
-                    const v2u p1 = *reinterpret_cast<const v2u*>(b + (aoff[s][t] ^ 32));
-                    fa[t] = v4i{(int)p0.x, (int)p0.y, (int)p1.x, (int)p1.y};
-                } else {
-                    fa[t] = *reinterpret_cast<const v4i*>(b + aoff[s][t]);
-                }
+                fa[t] = *reinterpret_cast<const v4i*>(b + aoff[s][t]);
                 fw[t] = *reinterpret_cast<const v4i*>(b + PC_OPER + woff[s][t]);
             }
             // D = W x A: lane l holds activation row l % 32 of the m-subtile and weight rows
@@ -170,9 +156,9 @@ __global__ __launch_bounds__(256, 1) void w8a8_pc_tile_kernel(const int8_t* __re
 // few 256 x 256 tiles leave the tile kernel's CUs idle, the weight tiles then come from L2 / MALL once per 64 rows).
 // One workgroup per G 16-row weight tiles; wave w takes the 64-input chunks w, w + NW, ... of every
 // tile (the int32 sums are exact in any order), PD chunks in flight in registers.  Per chunk a lane loads 16 bytes
-// of each tile's weights (packed: the chunk's lane slot, 1 KB per wave instruction; row-major: row l % 16, inputs
-// 16 q .. + 15) and the matching 2 x 8 activation bytes of its row per m-tile, reused across the G tiles; two
-// v_mfma_i32_16x16x32_i8 per (tile, m-tile) accumulate into int32.  The waves' sums meet in LDS, and the epilogue
+// of each tile's weights (row l % 16, inputs 16 q .. + 15: packed, the chunk's lane slot, 1 KB per wave
+// instruction) and the same 16 inputs of its activation row per m-tile, reused across the G tiles; one
+// v_mfma_i32_16x16x64_i8 per (tile, m-tile) accumulates into int32.  The waves' sums meet in LDS, and the epilogue
 // applies the two roundings.
 template <int G, int MT, bool WPACK, bool WS16, int EPI>
 __global__ __launch_bounds__(1024) void w8a8_pc_decode_kernel(const int8_t* __restrict__ a,
@@ -201,22 +187,20 @@ __global__ __launch_bounds__(1024) void w8a8_pc_decode_kernel(const int8_t* __re
     }
     const int8_t* ab[MT];
 #pragma unroll
-    for (int u = 0; u < MT; u++) ab[u] = a + (int64_t)min(r0 + 16 * u + lm, M - 1) * K + (WPACK ? 8 * q : 16 * q);
+    for (int u = 0; u < MT; u++) ab[u] = a + (int64_t)min(r0 + 16 * u + lm, M - 1) * K + 16 * q;
 
+    // both layouts give lane (lm, q) the 16 inputs 64 j + 16 q .. + 15 of its weight row and of its activation row:
+    // one v_mfma_i32_16x16x64_i8 per (tile, m-tile) and chunk
     struct Chunk {
         v4i w[G];
-        v2u x0[MT], x1[MT];
+        v4i x[MT];
     };
     auto load = [&](int j, Chunk& c) {
         const int jj = kc0 + min(j, KC - 1);
 #pragma unroll
         for (int g = 0; g < G; g++) c.w[g] = *reinterpret_cast<const v4i*>(wb[g] + (int64_t)jj * (WPACK ? 1024 : 64));
 #pragma unroll
-        for (int u = 0; u < MT; u++) {
-            const int8_t* p = ab[u] + (int64_t)jj * 64;
-            c.x0[u] = *reinterpret_cast<const v2u*>(p);
-            c.x1[u] = *reinterpret_cast<const v2u*>(p + (WPACK ? 32 : 8));
-        }
+        for (int u = 0; u < MT; u++) c.x[u] = *reinterpret_cast<const v4i*>(ab[u] + (int64_t)jj * 64);
     };
     v4i acc[G][MT];
 #pragma unroll
@@ -225,17 +209,9 @@ __global__ __launch_bounds__(1024) void w8a8_pc_decode_kernel(const int8_t* __re
         for (int u = 0; u < MT; u++) acc[g][u] = v4i{0, 0, 0, 0};
     auto mma = [&](const Chunk& c) {
 #pragma unroll
-        for (int g = 0; g < G; g++) {
-            const int64_t w0 = (int64_t)(uint32_t)c.w[g].x | ((int64_t)c.w[g].y << 32);
-            const int64_t w1 = (int64_t)(uint32_t)c.w[g].z | ((int64_t)c.w[g].w << 32);
+        for (int g = 0; g < G; g++)
 #pragma unroll
-            for (int u = 0; u < MT; u++) {
-                const int64_t x0 = (int64_t)c.x0[u].x | ((int64_t)c.x0[u].y << 32);
-                const int64_t x1 = (int64_t)c.x1[u].x | ((int64_t)c.x1[u].y << 32);
-                acc[g][u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(w0, x0, acc[g][u], 0, 0, 0);
-                acc[g][u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(w1, x1, acc[g][u], 0, 0, 0);
-            }
-        }
+            for (int u = 0; u < MT; u++) acc[g][u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(c.w[g], c.x[u], acc[g][u], 0, 0, 0);
     };
     // this wave's chunks: j = wv + NW i, i < cnt; branch-free body over whole rings of PD
     const int cnt = wv < KC ? (KC - wv + NW - 1) / NW : 0;

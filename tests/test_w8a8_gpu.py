@@ -175,19 +175,15 @@ def test_per_channel_gk_equals_k(dev, M, N, K, live):
 
 
 def test_pack_i8_layout(dev):
-    """prism_i8_pack is prism_q8_0_pack's chunk permutation: lane slot l of chunk (t, j) holds row 16 t + l % 16,
-    inputs 64 j + 8 q .. +8 then 64 j + 32 + 8 q .. +8 (q = l / 16)."""
+    """prism_i8_pack: lane slot l of chunk (t, j) holds row 16 t + l % 16, inputs 64 j + 16 q .. + 15 (q = l / 16),
+    checked over the whole tensor against a numpy reshape."""
     from prism_amd import w8a8 as KW
     N, K = 32, 256
     w = rng(4).integers(-127, 128, (N, K), dtype=np.int8)
     pw = KW.pack_i8(_t(w, dev), torch.ones(N, device=dev))
     torch.cuda.synchronize()
-    qt = pw.qt.cpu().numpy()
-    for t, j, l in [(0, 0, 0), (1, 3, 63), (0, 2, 17), (1, 1, 40)]:
-        r, q = l % 16, l // 16
-        want = np.concatenate([w[16 * t + r, 64 * j + 8 * q:64 * j + 8 * q + 8],
-                               w[16 * t + r, 64 * j + 32 + 8 * q:64 * j + 32 + 8 * q + 8]])
-        assert np.array_equal(qt[t, j, l], want)
+    want = w.reshape(N // 16, 16, K // 64, 4, 16).transpose(0, 2, 3, 1, 4).reshape(N // 16, K // 64, 64, 16)
+    assert np.array_equal(pw.qt.cpu().numpy(), want)
 
 
 def test_repeat_runs_identical(dev):
