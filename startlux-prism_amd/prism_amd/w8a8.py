@@ -190,12 +190,12 @@ def _gemm_pc_packed(a, a_s, w, out, n_rows, gk, epi, kernel):
 
 # When a per-channel epilogue-1 product defers (the reference takes the split from its dispatch table,
 # kernels/w8a8.py:199-204): measured on MI355X with the norm that finishes the add, splitting the decode kernel's K
-# pays only for long K at 16-64 rows (5120 x 17408 at 64 rows: 79.6 -> 64.5 us for projection plus norm_q8; 2% at 16
-# rows; 10-40% slower at 1-4 rows or K <= 6144, where the slots' extra traffic and launch outweigh the spread).  The
-# count keeps the workgroups (two 16-row weight tiles each) within two per CU: 512.
+# pays only for long K at 32-64 rows (5120 x 17408 at 64 rows: 57.4 -> 47.4 us for projection plus norm_q8; a tie at
+# 16 rows; 10-40% slower at 1-4 rows or K <= 6144, where the slots' extra traffic and launch outweigh the spread).
+# The count keeps the workgroups (two 16-row weight tiles each) within two per CU: 512.
 def defer_split(M, N, K, S):
     """The number of K parts a deferred per-channel product uses with S slots available (1: do not defer)."""
-    if M < 16 or M > 64 or K < 12288 or S < 2:
+    if M < 32 or M > 64 or K < 12288 or S < 2:
         return 1
     wgs = N // 32 if N % 32 == 0 else N // 16
     return max(1, min(4, S, 512 // max(1, wgs), K // (64 * 16)))

@@ -107,11 +107,11 @@ def test_norm_q8_finishes_the_deferred_add(dev, M, HID, K, live, alias, monkeypa
 
 
 def test_deferral_policy(dev):
-    """The measured rule: long K at 16-64 rows defers (three parts for a 5120-wide projection), everything else runs
+    """The measured rule: long K at 32-64 rows defers (three parts for a 5120-wide projection), everything else runs
     unsplit and returns None with the residual updated."""
     from prism_amd import w8a8 as KW
-    assert KW.defer_split(64, 5120, 17408, 4) == 3 and KW.defer_split(16, 5120, 17408, 8) == 3
-    assert KW.defer_split(4, 5120, 17408, 4) == 1 and KW.defer_split(64, 5120, 5120, 4) == 1
+    assert KW.defer_split(64, 5120, 17408, 4) == 3 and KW.defer_split(32, 5120, 17408, 8) == 3
+    assert KW.defer_split(16, 5120, 17408, 4) == 1 and KW.defer_split(64, 5120, 5120, 4) == 1
     assert KW.defer_split(96, 5120, 17408, 4) == 1 and KW.defer_split(64, 5120, 17408, 1) == 1
     a, w, sa, sw, h, pw = _case(dev, 96, 256, 1024, 5)
     slots = torch.zeros(4, 96, 256, dtype=torch.int32, device=dev)
