@@ -233,7 +233,7 @@ def bench_mxfp4(dev, iters=40):
 
 
 def bench_per_channel(dev, iters=40):
-    """The engine's per-channel (gk = K) W8A8 projections, SURVEY's first "next" row: packed int8 weights
+    """The engine's per-channel (gk = K) W8A8 projections (its production path): packed int8 weights
     (weight_from_q8(q8, K)), one activation scale per token; prefill at config 1's shape (against the int8 MFMA peak)
     and the decode sizes of config 2 (GB/s of the int8 weight bytes)."""
     import torch

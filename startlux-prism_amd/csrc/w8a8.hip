@@ -20,11 +20,6 @@
 //           owner thread adds the round's terms in block order.  HBM-bound on the weight stream.
 #include "common.h"
 
-// Timeline probes for profiling builds (empty in the library).
-#ifndef PRISM_PROBE
-#define PRISM_PROBE(tag)
-#endif
-
 namespace prism {
 
 // ============================================================================================== decode kernel
@@ -63,7 +58,6 @@ __global__ __launch_bounds__(NW * 64) void w8a8_decode_kernel(const int8_t* __re
     const int tstride = R * M * 16;
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    PRISM_PROBE(0);
     const int n0 = blockIdx.x * 16;
     const int live = min(M, __ldg(n_rows));
     const int G = K / 32;
@@ -185,26 +179,18 @@ __global__ __launch_bounds__(NW * 64) void w8a8_decode_kernel(const int8_t* __re
 #pragma unroll
         for (int d = 0; d < D; d++) {
             const int r = r0 + d, rb = r * R;
-            PRISM_PROBE(6);
             load(rb + (D - 1) * R, st[(d + D - 1) % D]);
-            PRISM_PROBE(7);
             store(st[d]);
-            PRISM_PROBE(8);
             lds_barrier();
-            PRISM_PROBE(1);
             if (r < nr) {
                 compute(rb, terms + (r & 1) * tstride);
-                PRISM_PROBE(4);
                 if (r > 0) fold(rb - R, terms + ((r - 1) & 1) * tstride);
-                PRISM_PROBE(5);
             }
             lds_barrier();
-            PRISM_PROBE(2);
         }
     }
     const int last = ((G - 1) / R) * R;
     fold(last, terms + ((last / R) & 1) * tstride);
-    PRISM_PROBE(3);
 #pragma unroll
     for (int jo = 0; jo < OPT; jo++) {
         const int o = tid + jo * NT;

@@ -14,9 +14,6 @@
 // block order, so both layouts give the same bits.
 #include "common.h"
 
-#ifndef PRISM_PROBE
-#define PRISM_PROBE(tag)
-#endif
 
 namespace prism {
 
@@ -87,7 +84,6 @@ __global__ __launch_bounds__((NW + FW) * 64) void w8a8_packed_decode_kernel(cons
     const int tstride = R * M * 16, xstride = M * LDA;
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    PRISM_PROBE(0);
     const int nt = blockIdx.x;
     const int live = min(M, __ldg(n_rows));
     const int KP = K / 64, G = K / 32;
@@ -227,7 +223,6 @@ __global__ __launch_bounds__((NW + FW) * 64) void w8a8_packed_decode_kernel(cons
         }
     }
     if (nr % D == 0 && folder) fold(nr - 1);
-    PRISM_PROBE(3);
     const int m = fo >> 4, n = 16 * nt + (fo & 15);
     if (folder && fo < M * 16 && m < live) {
         if (EPI == 0) {
