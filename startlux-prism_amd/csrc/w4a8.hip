@@ -766,8 +766,11 @@ extern "C" int prism_w4a8_q4k_gemm(const int8_t* xq, const float* a, int64_t a_s
     if (kernel == 1) {
         dim3 grid(Ni / 16);
 #define W4DEC(NW, R, MX, D, E)                                                                                      \
-    hipLaunchKernelGGL((w4a8_decode_kernel<0, NW, R, MX, D, E>), grid, dim3(NW * 64), w4a8_decode_lds(0, R, Mi), st, xq, a, \
-                       a_sb, xs, qv, meta, out, ldo, n_rows, Mi, Ni, Ki)
+    do {                                                                                                           \
+        allow_lds(w4a8_decode_kernel<0, NW, R, MX, D, E>, w4a8_decode_lds(0, R, Mi));                               \
+        hipLaunchKernelGGL((w4a8_decode_kernel<0, NW, R, MX, D, E>), grid, dim3(NW * 64), w4a8_decode_lds(0, R, Mi), \
+                           st, xq, a, a_sb, xs, qv, meta, out, ldo, n_rows, Mi, Ni, Ki);                           \
+    } while (0)
 // decode configurations (waves, super-blocks per round, rows, rounds of weights in flight), measured on MI355X at
 // the 27B's shapes (M <= 4, M <= 16); overridable at build time
 #ifndef W4V_SMALL
@@ -825,8 +828,11 @@ extern "C" int prism_w4a8_q6k_gemm(const int8_t* xq, const float* a, int64_t a_s
     if (kernel == 1) {
         dim3 grid(Ni / 16);
 #define Q6DEC(NW, R, MX, D, E)                                                                                      \
-    hipLaunchKernelGGL((w4a8_decode_kernel<1, NW, R, MX, D, E>), grid, dim3(NW * 64), w4a8_decode_lds(1, R, Mi), st, xq, \
-                       a, a_sb, nullptr, qv, meta, out, ldo, n_rows, Mi, Ni, Ki)
+    do {                                                                                                           \
+        allow_lds(w4a8_decode_kernel<1, NW, R, MX, D, E>, w4a8_decode_lds(1, R, Mi));                               \
+        hipLaunchKernelGGL((w4a8_decode_kernel<1, NW, R, MX, D, E>), grid, dim3(NW * 64), w4a8_decode_lds(1, R, Mi), \
+                           st, xq, a, a_sb, nullptr, qv, meta, out, ldo, n_rows, Mi, Ni, Ki);                      \
+    } while (0)
 // as W4V_SMALL / W4V_BIG, for Q6_K's twice larger weight chunks
 #ifndef W6V_SMALL
 #define W6V_SMALL 4, 4, 4, 2

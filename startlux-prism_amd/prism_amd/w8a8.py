@@ -218,6 +218,25 @@ def _gemm_pc_deferred(a, a_s, w, slots, n_rows, kernel):
     return Deferred(split, a_s, w.ws, slots)
 
 
+def gemm_i32(a, a_s, w, w_s, slots, n_rows, max_split=4, pdl=False):
+    """The int32 products a w^T without the scales (kernels/w8a8.py:234-262): split z's sums in slots[z] (int32
+    [S, >= M, N]), returns the number of slots written.  On one GPU this is the deferred split's first half, used
+    where the caller adds the parts itself; the reference's tensor-parallel callers add other ranks' parts too.
+    w: per-channel packed weights (PackedPC).  a_s / w_s / pdl are accepted as the reference's and not used."""
+    M, K = a.shape
+    if not isinstance(w, PackedPC) or w.k != K:
+        raise TypeError("gemm_i32 takes per-channel packed weights (PackedPC) matching a's K")
+    if slots.dtype != torch.int32 or slots.dim() != 3 or slots.shape[1] < M or slots.shape[2] < w.n \
+            or slots.stride(2) != 1:
+        raise ValueError("slots must be int32 [S, >= M, >= N] with unit column stride")
+    if a.dtype != torch.int8 or not a.is_contiguous():
+        raise ValueError("a must be contiguous int8 [M, K]")
+    split = max(1, min(max_split, slots.shape[0], defer_split(M, w.n, K, slots.shape[0])))
+    L.call("prism_w8a8_pc_packed_gemm_split", L.ptr(a), L.ptr(w.qt), L.ptr(slots), slots.stride(0), slots.stride(1),
+           L.ptr(n_rows), M, w.n, K, split, L.stream_of(a))
+    return split
+
+
 def weight_from_q8(q8, gk, smooth=None, packed=True):
     """Q8_0 matrix -> the GEMM's weight operands (kernels/w8a8.py:274-286).  gk == 32 keeps the Q8_0 values: by
     default as PackedQ8 (the MFMA-native layout; returned as (PackedQ8, None)), or with packed=False as the planes

@@ -120,3 +120,18 @@ def test_deferral_policy(dev):
     torch.cuda.synchronize()
     want = O.w8a8_gemm(a, sa, w, sw.reshape(-1, 1), 1024, epi=1, out=h.copy())
     assert np.array_equal(out.cpu().numpy().view(np.int32), want.view(np.int32))
+
+
+def test_gemm_i32_slots(dev):
+    """gemm_i32: the written slots add up to the exact int32 products (numpy int64), one slot where the deferral rule
+    does not split."""
+    from prism_amd import w8a8 as KW
+    for M, K in ((64, 17408), (8, 2048)):
+        a, w, sa, sw, h, pw = _case(dev, M, 5120 if M == 64 else 256, K, M + K)
+        N = w.shape[0]
+        slots = torch.zeros(4, M, N, dtype=torch.int32, device=dev)
+        n = KW.gemm_i32(_t(a, dev), _t(sa, dev), pw, pw.ws, slots, _n(M, dev))
+        torch.cuda.synchronize()
+        assert n == KW.defer_split(M, N, K, 4) or (n == 1 and KW.defer_split(M, N, K, 4) == 1)
+        got = slots.cpu().numpy().astype(np.int64)[:n].sum(0)
+        assert np.array_equal(got, a.astype(np.int64) @ w.astype(np.int64).T)
