@@ -163,7 +163,8 @@ PRISM_API int prism_q4k_pack(const uint8_t* raw, uint8_t* qv, uint8_t* meta, int
  *   epi 0: bf16(y); epi 1: out = RN(out + y).
  * xq int8 [M, K]; a fp32, element (b, m) at a[b * a_sb + m] (a_sb = 0: one scale per token); xs int8 [K/256, M, 16]
  * (per super-block eight S & 63 then eight S >> 6); qv / meta from prism_q4k_pack; out row stride ldo.
- * kernel: -1 picks by M; 0 the prefill tile kernel; 1 the decode kernel (M <= 16).  Needs K % 256 == 0, N % 16 == 0.
+ * kernel: -1 picks by M; 0 the prefill tile kernel; 1 the decode kernel (M <= 16; the tile kernel when its per-
+ * super-block terms, K/256 x M x 64 bytes, exceed the 160 KB of LDS).  Needs K % 256 == 0, N % 16 == 0.
  */
 PRISM_API int prism_w4a8_q4k_gemm(const int8_t* xq, const float* a, int64_t a_sb, const int8_t* xs, const uint8_t* qv,
                                   const uint8_t* meta, void* out, int64_t ldo, const int32_t* n_rows, int64_t M,

@@ -143,23 +143,22 @@ __global__ __launch_bounds__(256) void q6k_pack_kernel(const uint8_t* __restrict
     }
 }
 
-// ---------------------------------------------------------------------------------------------- decode
-// KIND 0: Q4_K (qv / meta of prism_q4k_pack); KIND 1: Q6_K (prism_q6k_pack).
-// A workgroup of NW waves owns one 16-row tile and every activation row (M <= 16).  Round r covers R super-blocks;
-// wave w computes super-blocks r R + w CB .. + CB - 1.  Per round the per-wave global loads are the weight chunks
-// (2 KB per super-block for Q4_K, 4 KB for Q6_K: two or four dwordx4 per lane, requested D - 1 rounds ahead).  The round's meta (unpacked once per row and
-// super-block by a staging thread), activation rows, activation sums and activation scales are fetched with
-// 16-byte loads a round ahead and staged in one of two LDS buffers.  Each super-block's term t of each output goes
-// to one of two LDS term buffers; the owner thread of each output folds round r - 1's terms,
+// ---------------------------------------------------------------------------------------------- Q6_K decode
+// Q6_K (prism_q6k_pack).  A workgroup of NW waves owns one 16-row tile and every activation row (M <= 16).  Round r
+// covers R super-blocks; wave w computes super-blocks r R + w CB .. + CB - 1.  Per round the per-wave global loads
+// are the weight chunks (4 KB per super-block: four dwordx4 per lane, requested D - 1 rounds ahead).  The round's
+// scales (unpacked once per row and super-block by a staging thread), activation rows and activation scales are
+// fetched with 16-byte loads a round ahead and staged in one of two LDS buffers.  Each super-block's term t of each
+// output goes to one of two LDS term buffers; the owner thread of each output folds round r - 1's terms,
 // y = fma(a[b, m], t, y) in super-block order, while round r is computed; one barrier per round.
-template <int KIND, int NW, int R, int MX, int D, int EPI>
-__global__ __launch_bounds__(NW * 64, KIND == 0 ? 1 : 2) void w4a8_decode_kernel(const int8_t* __restrict__ xq,
-                                                              const float* __restrict__ a, int64_t a_sb,
-                                                              const int8_t* __restrict__ xs,
-                                                              const uint8_t* __restrict__ qv,
-                                                              const uint8_t* __restrict__ meta,
-                                                              void* __restrict__ out, int64_t ldo,
-                                                              const int32_t* __restrict__ n_rows, int M, int N, int K) {
+template <int NW, int R, int MX, int D, int EPI>
+__global__ __launch_bounds__(NW * 64, 2) void w4a8_q6k_decode_kernel(const int8_t* __restrict__ xq,
+                                                                  const float* __restrict__ a, int64_t a_sb,
+                                                                  const uint8_t* __restrict__ qv,
+                                                                  const uint8_t* __restrict__ meta,
+                                                                  void* __restrict__ out, int64_t ldo,
+                                                                  const int32_t* __restrict__ n_rows, int M, int N,
+                                                                  int K) {
     constexpr int NT = NW * 64;
     constexpr int CB = R / NW;                     // super-blocks per wave per round
     static_assert(CB >= 1 && CB * NW == R, "R must be a multiple of NW");
@@ -168,18 +167,15 @@ __global__ __launch_bounds__(NW * 64, KIND == 0 ? 1 : 2) void w4a8_decode_kernel
     constexpr int LDA = RB + 16;
     constexpr int CPR = RB / 16;
     constexpr int XPT = (MX * CPR + NT - 1) / NT;
-    constexpr int WCH = KIND == 0 ? 2 : 4;        // 16-byte weight chunks per lane and super-block
+    constexpr int WCH = 4;                         // 16-byte weight chunks per lane and super-block
     extern __shared__ __attribute__((aligned(16))) int8_t dsm[];
-    // LDS (w4a8_decode_lds): terms, then the unpacked meta, activations and activation scales
+    // LDS (q6k_decode_lds): terms, per window the second scale and the first minus the second, d, activations and
+    // activation scales
     float* terms = reinterpret_cast<float*>(dsm);                 // [2][R][M][16]
-    uint32_t* scl = reinterpret_cast<uint32_t*>(terms + 2 * R * M * 16);  // [2][R][8][16], [g or window][row]: Q4_K
-                                                                  // split scales; Q6_K the window's second scale
-    float* dl = reinterpret_cast<float*>(scl + 2 * R * 128);      // [2][R][16] d
-    float* dml = dl + 2 * R * 16;                                 // Q4_K [2][R][16] dmin; Q6_K [2][R][8][16] the
-                                                                  // window's first scale minus its second
-    int8_t* xsb = reinterpret_cast<int8_t*>(dml + (KIND == 0 ? 2 * R * 16 : 2 * R * 128));  // Q4_K [2][R][M][16]
-    uint8_t* mnb = reinterpret_cast<uint8_t*>(xsb + (KIND == 0 ? 2 * R * M * 16 : 0));        // Q4_K [2][R][16][8]
-    int8_t* xl = reinterpret_cast<int8_t*>(mnb + (KIND == 0 ? 2 * R * 128 : 0));  // [2][M][LDA] activations
+    int* sca = reinterpret_cast<int*>(terms + 2 * R * M * 16);    // [2][R][8][16] [window][row]
+    int* scb = sca + 2 * R * 128;                                 // [2][R][8][16]
+    float* dl = reinterpret_cast<float*>(scb + 2 * R * 128);      // [2][R][16]
+    int8_t* xl = reinterpret_cast<int8_t*>(dl + 2 * R * 16);      // [2][M][LDA]
     float* al = reinterpret_cast<float*>(xl + 2 * M * LDA);       // [3][R][M] activation scales: read by the fold of
                                                                   // round r - 1 while round r + 1 is staged
     const int tstride = R * M * 16, xstride = M * LDA;
@@ -193,29 +189,22 @@ __global__ __launch_bounds__(NW * 64, KIND == 0 ? 1 : 2) void w4a8_decode_kernel
     const int xch = M * CPR;
 
     const v4u* cw = reinterpret_cast<const v4u*>(qv) + (int64_t)nt * NB * 64 * WCH + lane;
-    const v4u* cm = reinterpret_cast<const v4u*>(meta) + (int64_t)nt * NB * 16;
     const uint8_t* cm6 = meta + (int64_t)nt * NB * Q6_META;
 
     struct Staged {
-        v4u m;        // meta row (thread < 16 R: super-block tid / 16, row tid % 16); Q6_K: its 16 scales
-        uint32_t dh;  // Q6_K: the row's fp16 d
-        v4i s;        // split sums (thread < R M: super-block tid / M, activation row tid % M)
-        float as;     // activation scale of the same (super-block, row)
+        v4u m;        // thread < 16 R: super-block tid / 16, row tid % 16: its 16 scales
+        uint32_t dh;  // the row's fp16 d
+        float as;     // thread < R M: activation scale of (super-block tid / M, row tid % M)
         v4i x[XPT];
     };
     auto stage_load = [&](int r, Staged& sg) {
         const int b0 = r * R;
         const int c = min(tid, 16 * R - 1);
-        if (KIND == 0) {
-            sg.m = cm[(int64_t)min(b0 + c / 16, NB - 1) * 16 + (c & 15)];
-        } else {
-            const uint8_t* mp = cm6 + (int64_t)min(b0 + c / 16, NB - 1) * Q6_META;
-            sg.m = reinterpret_cast<const v4u*>(mp)[c & 15];
-            sg.dh = reinterpret_cast<const uint16_t*>(mp + 256)[c & 15];
-        }
+        const uint8_t* mp = cm6 + (int64_t)min(b0 + c / 16, NB - 1) * Q6_META;
+        sg.m = reinterpret_cast<const v4u*>(mp)[c & 15];
+        sg.dh = reinterpret_cast<const uint16_t*>(mp + 256)[c & 15];
         const int e = min(tid, R * M - 1);
         const int bb = min(b0 + e / M, NB - 1), mm = e % M;
-        if (KIND == 0) sg.s = *reinterpret_cast<const v4i*>(xs + ((int64_t)bb * M + mm) * 16);
         sg.as = a[(int64_t)bb * a_sb + mm];
         const int64_t k0 = (int64_t)r * RB;
 #pragma unroll
@@ -229,33 +218,17 @@ __global__ __launch_bounds__(NW * 64, KIND == 0 ? 1 : 2) void w4a8_decode_kernel
         const int buf = rr & 1;
         if (tid < 16 * R) {
             const int lb = tid >> 4, row = tid & 15;
-            if (KIND == 0) {
-                float d, dm;
-                int sc[8], mn[8];
-                row_meta(sg.m, d, dm, sc, mn);
+            int* pa = sca + (buf * R + lb) * 128 + row;
+            int* pb = scb + (buf * R + lb) * 128 + row;
 #pragma unroll
-                for (int g = 0; g < 8; g++) scl[((buf * R + lb) * 8 + g) * 16 + row] = split_scale(sc[g]);
-                *reinterpret_cast<v2u*>(&mnb[((buf * R + lb) * 16 + row) * 8]) =
-                    v2u{(uint32_t)(mn[0] | (mn[1] << 8) | (mn[2] << 16) | (mn[3] << 24)),
-                        (uint32_t)(mn[4] | (mn[5] << 8) | (mn[6] << 16) | (mn[7] << 24))};
-                dl[(buf * R + lb) * 16 + row] = d;
-                dml[(buf * R + lb) * 16 + row] = dm;
-            } else {
-                int* sa = reinterpret_cast<int*>(scl) + (buf * R + lb) * 128 + row;
-                int* sb = reinterpret_cast<int*>(dml) + (buf * R + lb) * 128 + row;
-#pragma unroll
-                for (int w = 0; w < 8; w++) {
-                    const int s0 = sbyte(sg.m, 2 * w), s1 = sbyte(sg.m, 2 * w + 1);
-                    sa[16 * w] = s1;
-                    sb[16 * w] = s0 - s1;
-                }
-                dl[(buf * R + lb) * 16 + row] = f16_to_f32(sg.dh);
+            for (int w = 0; w < 8; w++) {
+                const int s0 = sbyte(sg.m, 2 * w), s1 = sbyte(sg.m, 2 * w + 1);
+                pa[16 * w] = s1;
+                pb[16 * w] = s0 - s1;
             }
+            dl[(buf * R + lb) * 16 + row] = f16_to_f32(sg.dh);
         }
-        if (tid < R * M) {
-            if (KIND == 0) *reinterpret_cast<v4i*>(&xsb[(buf * R * M + tid) * 16]) = sg.s;     // tid = lb M + m
-            al[(rr % 3) * R * M + tid] = sg.as;
-        }
+        if (tid < R * M) al[(rr % 3) * R * M + tid] = sg.as;
 #pragma unroll
         for (int i = 0; i < XPT; i++) {
             const int cc = tid + i * NT;
@@ -277,11 +250,11 @@ __global__ __launch_bounds__(NW * 64, KIND == 0 ? 1 : 2) void w4a8_decode_kernel
 #pragma unroll
         for (int i = 0; i < CB; i++) {
             const int lb = wv * CB + i;
-            if (KIND == 1 && r * R + lb < NB) {
+            if (r * R + lb < NB) {
                 // per 32-input window: P over both sub-blocks, Pl over the first (activations of lanes q >= 2,
                 // which hold the second, zeroed): acc += sc1 P + (sc0 - sc1) Pl
-                const int* sa = reinterpret_cast<const int*>(scl) + (buf * R + lb) * 128 + 4 * q;
-                const int* sb = reinterpret_cast<const int*>(dml) + (buf * R + lb) * 128 + 4 * q;
+                const int* pa = sca + (buf * R + lb) * 128 + 4 * q;
+                const int* pb = scb + (buf * R + lb) * 128 + 4 * q;
                 v4i acc = {0, 0, 0, 0};
                 const v4i zero = {0, 0, 0, 0};
 #pragma unroll
@@ -291,7 +264,7 @@ __global__ __launch_bounds__(NW * 64, KIND == 0 ? 1 : 2) void w4a8_decode_kernel
                     const int64_t af = *reinterpret_cast<const int64_t*>(xrow + lb * 256 + 32 * wn + 8 * q);
                     const v4i P = __builtin_amdgcn_mfma_i32_16x16x32_i8(wf, af, zero, 0, 0, 0);
                     const v4i Pl = __builtin_amdgcn_mfma_i32_16x16x32_i8(wf, q < 2 ? af : 0, zero, 0, 0, 0);
-                    const v4i A = *reinterpret_cast<const v4i*>(sa + 16 * wn), B = *reinterpret_cast<const v4i*>(sb + 16 * wn);
+                    const v4i A = *reinterpret_cast<const v4i*>(pa + 16 * wn), B = *reinterpret_cast<const v4i*>(pb + 16 * wn);
 #pragma unroll
                     for (int e = 0; e < 4; e++) acc[e] += __mul24(A[e], P[e]) + __mul24(B[e], Pl[e]);
                 }
@@ -299,30 +272,6 @@ __global__ __launch_bounds__(NW * 64, KIND == 0 ? 1 : 2) void w4a8_decode_kernel
                 v4f t;
 #pragma unroll
                 for (int e = 0; e < 4; e++) t[e] = mul_rn(d[e], (float)acc[e]);
-                if (lm < M) *reinterpret_cast<v4f*>(&tb[(lb * M + lm) * 16 + 4 * q]) = t;
-            }
-            if (KIND == 0 && r * R + lb < NB) {
-                const uint32_t* scp = scl + (buf * R + lb) * 128;
-                v4i alo = {0, 0, 0, 0}, ahi = {0, 0, 0, 0};
-#pragma unroll
-                for (int p = 0; p < 4; p++) {
-                    v4i wl, wh;
-                    two_plane(w[i][p >> 1][2 * (p & 1)], w[i][p >> 1][2 * (p & 1) + 1],
-                              scp[(2 * p + (q >> 1)) * 16 + lm], wl, wh);
-                    const v4i af = *reinterpret_cast<const v4i*>(xrow + lb * 256 + 64 * p + 16 * q);
-                    alo = __builtin_amdgcn_mfma_i32_16x16x64_i8(wl, af, alo, 0, 0, 0);
-                    ahi = __builtin_amdgcn_mfma_i32_16x16x64_i8(wh, af, ahi, 0, 0, 0);
-                }
-                const int8_t* xp = xsb + ((buf * R + lb) * M + mrow) * 16;
-                const int64_t mn8 = q == 0 ? *reinterpret_cast<const int64_t*>(&mnb[((buf * R + lb) * 16 + lm) * 8]) : 0;
-                const int64_t slo = q == 0 ? *reinterpret_cast<const int64_t*>(xp) : 0;
-                const int64_t shi = q == 0 ? *reinterpret_cast<const int64_t*>(xp + 8) : 0;
-                const v4i mins = mins_mfma(mn8, slo, shi);
-                const v4f d = *reinterpret_cast<const v4f*>(&dl[(buf * R + lb) * 16 + 4 * q]);
-                const v4f dm = *reinterpret_cast<const v4f*>(&dml[(buf * R + lb) * 16 + 4 * q]);
-                v4f t;
-#pragma unroll
-                for (int e = 0; e < 4; e++) t[e] = q4k_term(d[e], dm[e], alo[e] + 8 * ahi[e], mins[e]);
                 if (lm < M) *reinterpret_cast<v4f*>(&tb[(lb * M + lm) * 16 + 4 * q]) = t;
             }
         }
@@ -372,11 +321,111 @@ __global__ __launch_bounds__(NW * 64, KIND == 0 ? 1 : 2) void w4a8_decode_kernel
     }
 }
 
-static size_t w4a8_decode_lds(int kind, int R, int M) {
-    const size_t base = 2 * (size_t)R * M * 16 * 4 + 2 * (size_t)R * 128 * 4 + 2 * (size_t)R * 16 * 4 +
-                        2 * (size_t)M * (R * 256 + 16) + 3 * (size_t)R * M * 4;
-    return kind == 0 ? base + 2 * (size_t)R * 16 * 4 + 2 * (size_t)R * M * 16 + 2 * (size_t)R * 128
-                     : base + 2 * (size_t)R * 128 * 4;
+static size_t q6k_decode_lds(int R, int M) {
+    return 2 * (size_t)R * M * 16 * 4 + 2 * 2 * (size_t)R * 128 * 4 + 2 * (size_t)R * 16 * 4 +
+           2 * (size_t)M * (R * 256 + 16) + 3 * (size_t)R * M * 4;
+}
+
+// ---------------------------------------------------------------------------------------------- Q4_K stream decode
+// Up to 16 activation rows; one workgroup per 16-row weight tile and all of K.  Wave w computes super-blocks
+// w, w + NW, ... with PD of them in flight in a register ring, each holding what its lane needs from memory: the
+// tile's 2 KB of weights (two 16-byte slots), the 16 meta bytes of the lane's weight row, the lane's activation row
+// (four 16-byte pieces) and its split activation sums.  A super-block's term t of each output (the two-plane MFMA
+// sums, the mins on the MFMA, q4k_term) goes to LDS [b][m][n]; after one barrier each output's thread adds the terms
+// in super-block order, y = fma(a[b, m], t, y), as the reference's sequential chain does.
+template <int NW, int PD, int EPI>
+__global__ __launch_bounds__(NW * 64) void w4a8_q4k_stream_kernel(const int8_t* __restrict__ xq,
+                                                                 const float* __restrict__ a, int64_t a_sb,
+                                                                 const int8_t* __restrict__ xs,
+                                                                 const uint8_t* __restrict__ qv,
+                                                                 const uint8_t* __restrict__ meta,
+                                                                 void* __restrict__ out, int64_t ldo,
+                                                                 const int32_t* __restrict__ n_rows, int M, int K) {
+    extern __shared__ __attribute__((aligned(16))) float tl[];          // [NB][M][16]
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int nt = blockIdx.x;
+    const int live = min(M, __ldg(n_rows));
+    const int NB = K / 256;
+    const int lm = lane & 15, q = lane >> 4;
+    const int m = min(lm, M - 1);
+
+    const v4u* cw = reinterpret_cast<const v4u*>(qv) + (int64_t)nt * NB * 128 + lane;
+    const v4u* cm = reinterpret_cast<const v4u*>(meta) + (int64_t)nt * NB * 16 + lm;
+    const int8_t* cx = xq + (int64_t)m * K + 16 * q;
+    struct SB {
+        v4u w[2];
+        v4u mt;
+        v4i x[4];
+        v4i s;
+    };
+    auto load = [&](int i, SB& c) {
+        const int b = min(wv + NW * i, NB - 1);
+        c.w[0] = __builtin_nontemporal_load(cw + (int64_t)b * 128);
+        c.w[1] = __builtin_nontemporal_load(cw + (int64_t)b * 128 + 64);
+        c.mt = cm[(int64_t)b * 16];
+#pragma unroll
+        for (int p = 0; p < 4; p++) c.x[p] = *reinterpret_cast<const v4i*>(cx + (int64_t)b * 256 + 64 * p);
+        c.s = *reinterpret_cast<const v4i*>(xs + ((int64_t)b * M + m) * 16);
+    };
+    auto term = [&](int i, const SB& c) {
+        const int b = wv + NW * i;
+        float d, dm;
+        int sc[8], mn[8];
+        row_meta(c.mt, d, dm, sc, mn);                    // this lane's weight row lm
+        v4i alo = {0, 0, 0, 0}, ahi = {0, 0, 0, 0};
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            v4i wl, wh;
+            const int g = 2 * p + (q >> 1);
+            int scg = sc[0];
+#pragma unroll
+            for (int j = 1; j < 8; j++) scg = g == j ? sc[j] : scg;
+            two_plane(c.w[p >> 1][2 * (p & 1)], c.w[p >> 1][2 * (p & 1) + 1], split_scale(scg), wl, wh);
+            alo = __builtin_amdgcn_mfma_i32_16x16x64_i8(wl, c.x[p], alo, 0, 0, 0);
+            ahi = __builtin_amdgcn_mfma_i32_16x16x64_i8(wh, c.x[p], ahi, 0, 0, 0);
+        }
+        const int64_t mn8 = q == 0 ? (int64_t)(uint32_t)(mn[0] | (mn[1] << 8) | (mn[2] << 16) | (mn[3] << 24)) |
+                                         ((int64_t)(uint32_t)(mn[4] | (mn[5] << 8) | (mn[6] << 16) | (mn[7] << 24)) << 32)
+                                   : 0;
+        const int64_t slo = q == 0 ? ((int64_t)(uint32_t)c.s[0] | ((int64_t)(uint32_t)c.s[1] << 32)) : 0;
+        const int64_t shi = q == 0 ? ((int64_t)(uint32_t)c.s[2] | ((int64_t)(uint32_t)c.s[3] << 32)) : 0;
+        const v4i mins = mins_mfma(mn8, slo, shi);
+        v4f t;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float de = __shfl(d, 4 * q + e, kWave), dme = __shfl(dm, 4 * q + e, kWave);   // row 4 q + e
+            t[e] = q4k_term(de, dme, alo[e] + 8 * ahi[e], mins[e]);
+        }
+        if (lm < M && b < NB) *reinterpret_cast<v4f*>(&tl[((int64_t)b * M + lm) * 16 + 4 * q]) = t;
+    };
+    const int cnt = wv < NB ? (NB - wv + NW - 1) / NW : 0;
+    SB ring[PD];
+#pragma unroll
+    for (int d = 0; d < PD; d++) load(d, ring[d]);
+    const int full = cnt / PD * PD;
+    for (int i0 = 0; i0 < full; i0 += PD) {
+#pragma unroll
+        for (int d = 0; d < PD; d++) {
+            term(i0 + d, ring[d]);
+            load(i0 + d + PD, ring[d]);
+        }
+    }
+#pragma unroll
+    for (int d = 0; d < PD; d++)
+        if (full + d < cnt) term(full + d, ring[d]);
+    __syncthreads();
+    for (int fo = tid; fo < M * 16; fo += NW * 64) {
+        const int mo = fo >> 4, n = 16 * nt + (fo & 15);
+        if (mo >= live) continue;
+        float y = 0.f;
+        for (int b = 0; b < NB; b++) y = fmaf(a[(int64_t)b * a_sb + mo], tl[((int64_t)b * M + mo) * 16 + (fo & 15)], y);
+        if (EPI == 0) {
+            reinterpret_cast<uint16_t*>(out)[(int64_t)mo * ldo + n] = (uint16_t)f32_to_bf16(y);
+        } else {
+            float* op = reinterpret_cast<float*>(out) + (int64_t)mo * ldo + n;
+            *op = add_rn(*op, y);
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------------------------- prefill tile
@@ -764,29 +813,21 @@ extern "C" int prism_w4a8_q4k_gemm(const int8_t* xq, const float* a, int64_t a_s
     hipStream_t st = (hipStream_t)stream;
     const int Mi = (int)M, Ni = (int)N, Ki = (int)K;
     if (kernel == 1) {
-        dim3 grid(Ni / 16);
-#define W4DEC(NW, R, MX, D, E)                                                                                      \
-    do {                                                                                                           \
-        allow_lds(w4a8_decode_kernel<0, NW, R, MX, D, E>, w4a8_decode_lds(0, R, Mi));                               \
-        hipLaunchKernelGGL((w4a8_decode_kernel<0, NW, R, MX, D, E>), grid, dim3(NW * 64), w4a8_decode_lds(0, R, Mi), \
-                           st, xq, a, a_sb, xs, qv, meta, out, ldo, n_rows, Mi, Ni, Ki);                           \
+        // Q4_K decode: the stream kernel, 8 waves for long K or narrow projections (few workgroups), else 4
+        const size_t lds = (size_t)(K / 256) * M * 16 * 4;
+        if (lds > 160 * 1024) kernel = 0;                 // the terms of every super-block do not fit: tile kernel
+    }
+    if (kernel == 1) {
+        const size_t lds = (size_t)(K / 256) * M * 16 * 4;
+        const bool wide = K >= 6144 || N <= 2048;
+#define W4S(NW, E) do {                                                                                            \
+        allow_lds(w4a8_q4k_stream_kernel<NW, 2, E>, lds);                                                         \
+        hipLaunchKernelGGL((w4a8_q4k_stream_kernel<NW, 2, E>), dim3(Ni / 16), dim3(64 * NW), lds, st, xq, a, a_sb,  \
+                           xs, qv, meta, out, ldo, n_rows, Mi, Ki);                                                \
     } while (0)
-// decode configurations (waves, super-blocks per round, rows, rounds of weights in flight), measured on MI355X at
-// the 27B's shapes (M <= 4, M <= 16); overridable at build time
-#ifndef W4V_SMALL
-#define W4V_SMALL 8, 8, 4, 2
-#endif
-#ifndef W4V_BIG
-#define W4V_BIG 4, 4, 16, 2
-#endif
-#define W4DEC_(...) W4DEC(__VA_ARGS__)
-        if (M <= 4) {
-            if (epi == 0) W4DEC_(W4V_SMALL, 0); else W4DEC_(W4V_SMALL, 1);
-        } else {
-            if (epi == 0) W4DEC_(W4V_BIG, 0); else W4DEC_(W4V_BIG, 1);
-        }
-#undef W4DEC_
-#undef W4DEC
+        if (wide) { if (epi == 0) W4S(8, 0); else W4S(8, 1); }
+        else { if (epi == 0) W4S(4, 0); else W4S(4, 1); }
+#undef W4S
     } else {
         const int tiles_m = (Mi + QBM - 1) / QBM, tiles_n = (Ni + QBN - 1) / QBN;
         if (epi == 0)
@@ -829,11 +870,12 @@ extern "C" int prism_w4a8_q6k_gemm(const int8_t* xq, const float* a, int64_t a_s
         dim3 grid(Ni / 16);
 #define Q6DEC(NW, R, MX, D, E)                                                                                      \
     do {                                                                                                           \
-        allow_lds(w4a8_decode_kernel<1, NW, R, MX, D, E>, w4a8_decode_lds(1, R, Mi));                               \
-        hipLaunchKernelGGL((w4a8_decode_kernel<1, NW, R, MX, D, E>), grid, dim3(NW * 64), w4a8_decode_lds(1, R, Mi), \
-                           st, xq, a, a_sb, nullptr, qv, meta, out, ldo, n_rows, Mi, Ni, Ki);                      \
+        allow_lds(w4a8_q6k_decode_kernel<NW, R, MX, D, E>, q6k_decode_lds(R, Mi));                                  \
+        hipLaunchKernelGGL((w4a8_q6k_decode_kernel<NW, R, MX, D, E>), grid, dim3(NW * 64), q6k_decode_lds(R, Mi),    \
+                           st, xq, a, a_sb, qv, meta, out, ldo, n_rows, Mi, Ni, Ki);                               \
     } while (0)
-// as W4V_SMALL / W4V_BIG, for Q6_K's twice larger weight chunks
+// decode configurations (waves, super-blocks per round, rows, rounds of weights in flight), measured on MI355X at
+// the 27B's shapes (M <= 4, M <= 16); overridable at build time
 #ifndef W6V_SMALL
 #define W6V_SMALL 4, 4, 4, 2
 #endif

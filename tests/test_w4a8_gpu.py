@@ -93,6 +93,9 @@ def _gemm(dev, w, xq, a, xs, epi, kernel, live=None, out0=None):
 CASES = [  # (M, N, K, live, group)
     (1, 16, 256, 1, 256), (4, 64, 1024, 3, 256), (16, 128, 5120, 16, 256), (16, 256, 5120, 16, 5120),
     (7, 48, 2560, 5, 256), (64, 128, 1024, 64, 256), (100, 272, 768, 77, 256), (130, 128, 2048, 130, 2048),
+    # the decode kernel's two wave counts (4 waves: N > 2048 and K < 6144), a long K with several ring trips per
+    # wave, and K beyond the decode kernel's LDS for 16 rows (the tile kernel runs)
+    (16, 2576, 1024, 13, 256), (2, 2064, 512, 2, 256), (4, 32, 12288, 4, 256), (16, 16, 41216, 16, 256),
 ]
 
 
