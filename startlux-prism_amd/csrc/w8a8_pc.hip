@@ -4,8 +4,9 @@
 // epilogue 1 out = RN(out + y).  With a single group there is no per-block fp32 work, so this is a plain int8 MFMA
 // GEMM with an epilogue, and the int32 sum is exact in any order.
 //
-// Tile: 256 x 256 outputs per 256-thread workgroup, 4 waves of 128 x 128 (4 x 4 v_mfma_i32_32x32x32_i8 per 32
-// inputs, 256 int32 accumulators per lane).  Operands go global -> LDS by LDS-DMA (global_load_lds_dwordx4), NS
+// Tile: 256 x 256 outputs per 512-thread workgroup, 8 waves of 128 x 64 (4 x 2 v_mfma_i32_32x32x32_i8 per 32
+// inputs, 128 int32 accumulators per lane; two waves per SIMD: 4 waves of 128 x 128, one per SIMD, ran 6-13% slower,
+// 16 waves of 128 x 32 no faster).  Operands go global -> LDS by LDS-DMA (global_load_lds_dwordx4), NS
 // stages of 64 inputs: per stage and operand 256 rows x 64 bytes, each DMA instruction 16 rows x 64 bytes (lane L:
 // row L / 4, 16-byte chunk L % 4 XOR-swizzled by row so that the fragment reads of 8 consecutive rows hit distinct
 // banks).  MFMA operand mapping: lane l holds row l % 32 and the 16 inputs of chunk 2 s + l / 32 for the stage's
@@ -22,8 +23,8 @@ constexpr int PC_STAGE = 2 * PC_OPER;
 __device__ __forceinline__ int pc_swz(int row) { return (row >> 1) & 3; }
 
 
-template <bool WPACK, bool WS16, int EPI, int NS>
-__global__ __launch_bounds__(256, 1) void w8a8_pc_tile_kernel(const int8_t* __restrict__ a,
+template <bool WPACK, bool WS16, int EPI, int NS, int NWV>
+__global__ __launch_bounds__(64 * NWV, 1) void w8a8_pc_tile_kernel(const int8_t* __restrict__ a,
                                                               const float* __restrict__ a_s, int64_t as_sm,
                                                               const int8_t* __restrict__ w,
                                                               const void* __restrict__ w_s, void* __restrict__ out,
@@ -38,57 +39,65 @@ __global__ __launch_bounds__(256, 1) void w8a8_pc_tile_kernel(const int8_t* __re
     const int live = min(M, __ldg(n_rows));
     if (m0 >= live) return;
     const int KS = K / PCK;
+    constexpr int DI = 16 / NWV;                    // DMA instructions per operand, wave and stage
+    constexpr int WNC = NWV / 2;                    // wave columns: 2 waves of 128 rows by WNC of 256 / WNC columns
+    constexpr int CW = PCT / WNC, TN = CW / 32;
 
     // epilogue scales of the tile
-    sal[tid] = a_s[(int64_t)min(m0 + tid, M - 1) * as_sm];
-    {
+    if (tid < PCT) {
+        sal[tid] = a_s[(int64_t)min(m0 + tid, M - 1) * as_sm];
         const int n = min(n0 + tid, N - 1);
         swl[tid] = WS16 ? f16_to_f32(static_cast<const uint16_t*>(w_s)[n]) : static_cast<const float*>(w_s)[n];
     }
 
-    // DMA sources: instruction i of wave wv covers operand rows 16 (4 wv + i) .. + 15; packed weights: the 1 KB
-    // chunk of 16-row tile 4 wv + i as it lies (lane slot l: row l % 16, inputs 16 q .. + 15, q = l / 16)
-    const int8_t* asrc[4];
-    const int8_t* wsrc[4];
+    // DMA sources: instruction i of wave wv covers operand rows 16 (DI wv + i) .. + 15; packed weights: the 1 KB
+    // chunk of 16-row tile DI wv + i as it lies (lane slot l: row l % 16, inputs 16 q .. + 15, q = l / 16)
+    const int8_t* asrc[DI];
+    const int8_t* wsrc[DI];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int row = 16 * (4 * wv + i) + (lane >> 2);
+    for (int i = 0; i < DI; i++) {
+        const int row = 16 * (DI * wv + i) + (lane >> 2);
         const int c = (lane & 3) ^ pc_swz(row);
         asrc[i] = a + (int64_t)min(m0 + row, M - 1) * K + 16 * c;
         if (WPACK)
-            wsrc[i] = w + ((int64_t)min(n0 / 16 + 4 * wv + i, N / 16 - 1) * (K / 64)) * 1024 + 16 * lane;
+            wsrc[i] = w + ((int64_t)min(n0 / 16 + DI * wv + i, N / 16 - 1) * (K / 64)) * 1024 + 16 * lane;
         else
             wsrc[i] = w + (int64_t)min(n0 + row, N - 1) * K + 16 * c;
     }
     auto issue = [&](int st, int buf) {
         uint8_t* b = lds + buf * PC_STAGE;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            dma16(asrc[i] + (int64_t)st * PCK, b + (4 * wv + i) * 1024);
-            dma16(wsrc[i] + (int64_t)st * (WPACK ? 1024 : PCK), b + PC_OPER + (4 * wv + i) * 1024);
+        for (int i = 0; i < DI; i++) {
+            dma16(asrc[i] + (int64_t)st * PCK, b + (DI * wv + i) * 1024);
+            dma16(wsrc[i] + (int64_t)st * (WPACK ? 1024 : PCK), b + PC_OPER + (DI * wv + i) * 1024);
         }
     };
 
-    const int wm = wv >> 1, wn = wv & 1;
+    const int wm = wv / WNC, wn = wv % WNC;
     const int r = lane & 31, h = lane >> 5;
     // fragment byte offsets within an operand stage, for the two 32-input steps s: both operands' lanes hold inputs
     // 16 (2 s + h) .. + 15 (packed weights: the chunk's lane slot q = 2 s + h of the row).
-    int aoff[2][4], woff[2][4];
+    int aoff[2][4], woff[2][TN];
 #pragma unroll
-    for (int s = 0; s < 2; s++)
+    for (int s = 0; s < 2; s++) {
 #pragma unroll
         for (int t = 0; t < 4; t++) {
-            const int ra = 128 * wm + 32 * t + r, rw = 128 * wn + 32 * t + r;
+            const int ra = 128 * wm + 32 * t + r;
             aoff[s][t] = ra * PCK + 16 * ((2 * s + h) ^ pc_swz(ra));
-            woff[s][t] = WPACK ? (rw >> 4) * 1024 + (16 * (2 * s + h) + (rw & 15)) * 16
+        }
+#pragma unroll
+        for (int u = 0; u < TN; u++) {
+            const int rw = CW * wn + 32 * u + r;
+            woff[s][u] = WPACK ? (rw >> 4) * 1024 + (16 * (2 * s + h) + (rw & 15)) * 16
                                : rw * PCK + 16 * ((2 * s + h) ^ pc_swz(rw));
         }
+    }
 
-    v16i acc[4][4];
+    v16i acc[4][TN];
 #pragma unroll
     for (int t = 0; t < 4; t++)
 #pragma unroll
-        for (int u = 0; u < 4; u++)
+        for (int u = 0; u < TN; u++)
 #pragma unroll
             for (int e = 0; e < 16; e++) acc[t][u][e] = 0;
 
@@ -98,26 +107,25 @@ __global__ __launch_bounds__(256, 1) void w8a8_pc_tile_kernel(const int8_t* __re
 
     for (int st = 0; st < KS; st++) {
         const int pend = min(KS - 1, st + NS - 2) - st;     // stages issued after this one
-        if (NS >= 4 && pend >= 2) vm_wait<16>();
-        else if (pend >= 1) vm_wait<8>();
+        if (NS >= 4 && pend >= 2) vm_wait<4 * DI>();
+        else if (pend >= 1) vm_wait<2 * DI>();
         else vm_wait<0>();
         lds_barrier();
         if (st + NS - 1 < KS) issue(st + NS - 1, (st + NS - 1) % NS);
         const uint8_t* b = lds + (st % NS) * PC_STAGE;
 #pragma unroll
         for (int s = 0; s < 2; s++) {
-            v4i fa[4], fw[4];
+            v4i fa[4], fw[TN];
 #pragma unroll
-            for (int t = 0; t < 4; t++) {
-                fa[t] = *reinterpret_cast<const v4i*>(b + aoff[s][t]);
-                fw[t] = *reinterpret_cast<const v4i*>(b + PC_OPER + woff[s][t]);
-            }
+            for (int t = 0; t < 4; t++) fa[t] = *reinterpret_cast<const v4i*>(b + aoff[s][t]);
+#pragma unroll
+            for (int u = 0; u < TN; u++) fw[u] = *reinterpret_cast<const v4i*>(b + PC_OPER + woff[s][u]);
             // D = W x A: lane l holds activation row l % 32 of the m-subtile and weight rows
             // 8 (e / 4) + 4 (l / 32) + e % 4 of the n-subtile
 #pragma unroll
             for (int t = 0; t < 4; t++)
 #pragma unroll
-                for (int u = 0; u < 4; u++)
+                for (int u = 0; u < TN; u++)
                     acc[t][u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fw[u], fa[t], acc[t][u], 0, 0, 0);
         }
     }
@@ -129,10 +137,10 @@ __global__ __launch_bounds__(256, 1) void w8a8_pc_tile_kernel(const int8_t* __re
         if (m >= live) continue;
         const float sa = sal[ml];
 #pragma unroll
-        for (int u = 0; u < 4; u++)
+        for (int u = 0; u < TN; u++)
 #pragma unroll
             for (int g = 0; g < 4; g++) {
-                const int nl = 128 * wn + 32 * u + 8 * g + 4 * h;
+                const int nl = CW * wn + 32 * u + 8 * g + 4 * h;
                 const int n = n0 + nl;
                 if (n >= N) continue;
                 float y[4];
@@ -303,13 +311,17 @@ int launch_w8a8_pc(int kernel, bool wpack, const int8_t* a, const float* a_s, in
         PRISM_LAUNCH_CHECK();
         return PRISM_OK;
     }
+#ifndef PC_NWV
+#define PC_NWV 8                                  // waves per workgroup: 4, 8 or 16
+#endif
     constexpr int NS = 4;
     const int tiles_m = (M + PCT - 1) / PCT, tiles_n = (N + PCT - 1) / PCT;
     const size_t lds = (size_t)NS * PC_STAGE;
 #define PCL(WP, W16, E)                                                                                            \
     do {                                                                                                           \
-        allow_lds(w8a8_pc_tile_kernel<WP, W16, E, NS>, lds);                                                        \
-        hipLaunchKernelGGL((w8a8_pc_tile_kernel<WP, W16, E, NS>), dim3(tiles_m * tiles_n), dim3(256), lds, st, a,   \
+        allow_lds(w8a8_pc_tile_kernel<WP, W16, E, NS, PC_NWV>, lds);                                                \
+        hipLaunchKernelGGL((w8a8_pc_tile_kernel<WP, W16, E, NS, PC_NWV>), dim3(tiles_m * tiles_n), dim3(64 * PC_NWV),  \
+                           lds, st, a,                                                                             \
                            a_s, as_sm, w, w_s, out, ldo, n_rows, M, N, K, tiles_m, tiles_n);                        \
     } while (0)
 #define PCL_WP(W16, E) do { if (wpack) PCL(true, W16, E); else PCL(false, W16, E); } while (0)
