@@ -1,0 +1,108 @@
+"""The headline configurations at their full sizes (3 and 4), checked through properties that do
+not depend on the size: rows sampled from every 128-row tile (and the last row) equal the CPU oracle bit for bit
+(MXFP4: within its fp32 bound), and the decode kernel run on a 16-row batch of the same rows gives the same bits as the
+full prefill (batch invariance, kernels/w8a8.py:14-17)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from _inputs import acts_bf16, rng, weights_f32
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(x, dev):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+
+
+def _rows(M, seed):
+    g = rng(seed)
+    r = [128 * t + int(g.integers(0, 128)) for t in range(M // 128)] + [0, M - 1]
+    return np.array(sorted(set(min(x, M - 1) for x in r)), np.int64)
+
+
+def _bits(out):
+    return out.view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def test_config1_q8_0_prefill_full_size(dev):
+    """Config 1: M = 8192, K = 5120, N = 27648, Q8_0 gk = 32, bf16 out."""
+    from prism_amd import gguf_formats as GF
+    from prism_amd import quant as KQ
+    from prism_amd import w8a8 as KW
+    M, K, N = 8192, 5120, 27648
+    g = torch.Generator(device=dev)
+    g.manual_seed(101)
+    q8 = GF.quantize_q8_0(torch.randn(N, K, generator=g, device=dev) * 0.02)
+    pw, _ = KW.weight_from_q8(q8, 32)
+    x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+    q = torch.empty(M, K, dtype=torch.int8, device=dev)
+    s = torch.empty(M, dtype=torch.float32, device=dev)
+    n = torch.tensor([M], dtype=torch.int32, device=dev)
+    KQ.rows_q8(x, None, q, s, n, M)
+    out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    KW.gemm(q, s, pw, None, out, n, 32, kernel="tile")
+    torch.cuda.synchronize()
+    rows = _rows(M, 1)
+    qs, d = q8.qs.cpu().numpy(), q8.d.view(torch.int16).cpu().numpy().view(np.uint16)
+    qa, sa = q.cpu().numpy()[rows], s.cpu().numpy()[rows]
+    want = O.w8a8_gemm(qa, sa, qs, d, 32, epi=0, nthreads=16)
+    assert np.array_equal(_bits(out)[rows], want)
+    sub = rows[:16]
+    o16 = torch.empty(16, N, dtype=torch.bfloat16, device=dev)
+    KW.gemm(_t(qa[:16], dev), _t(sa[:16], dev), pw, None, o16, torch.tensor([16], dtype=torch.int32, device=dev),
+            32, kernel="decode")
+    torch.cuda.synchronize()
+    assert np.array_equal(_bits(o16), _bits(out)[sub])
+
+
+def test_config3_q4k_prefill_full_size(dev):
+    """Config 3: M = 2048, K = 5120, N = 13824, Q4_K W4A8, one activation scale per token."""
+    from prism_amd import gguf_formats as GF
+    from prism_amd import w4a8 as KW4
+    M, K, N = 2048, 5120, 13824
+    blocks = O.q4k_quantize(weights_f32(N, K, seed=103), nthreads=16)
+    xq, a, xs = O.quant_rows_g(O.bf16_to_f32(acts_bf16(M, K, seed=104)), K, nthreads=16)
+    w = KW4.repack(GF.KQuant(_t(blocks, dev), K))
+    out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    n = torch.tensor([M], dtype=torch.int32, device=dev)
+    KW4.gemm(_t(xq, dev), _t(a, dev), _t(xs, dev), w, out, n, kernel="tile")
+    torch.cuda.synchronize()
+    rows = _rows(M, 3)
+    W = O.q4k_repack(blocks)
+    want = O.w4a8_gemm(xq[rows], a[0][rows].copy(), xs[:, rows], W, nthreads=16)
+    assert np.array_equal(_bits(out)[rows], want)
+    sub = rows[:16]
+    o16 = torch.empty(16, N, dtype=torch.bfloat16, device=dev)
+    KW4.gemm(_t(xq[sub], dev), _t(a[:, sub], dev), _t(xs[:, sub], dev), w, o16,
+             torch.tensor([16], dtype=torch.int32, device=dev), kernel="decode")
+    torch.cuda.synchronize()
+    assert np.array_equal(_bits(o16), _bits(out)[sub])
+
+
+def test_config4_mxfp4_prefill_full_size(dev):
+    """Config 4: M = 4096, K = N = 5120, e2m1 weights (OCP scales) x e4m3 activations; within the fp32 bound of the
+    exact value, and the decode kernel's 16 rows equal the tile kernel's."""
+    from prism_amd import mxfp4 as MX
+    M, K, N = 4096, 5120, 5120
+    g = torch.Generator(device=dev)
+    g.manual_seed(105)
+    mw = MX.pack(torch.randn(N, K, generator=g, device=dev) * 0.02, "ocp")
+    x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+    aq = torch.empty(M, K, dtype=torch.uint8, device=dev)
+    asc = torch.empty(M, K // 32, dtype=torch.uint8, device=dev)
+    MX.quantize_act_fp8(x, aq, asc)
+    out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    MX.gemm(aq, asc, mw, out, M, kernel="tile")
+    torch.cuda.synchronize()
+    rows = _rows(M, 5)
+    wq, ws = (t.cpu().numpy() for t in MX.to_rows(mw))
+    y64, yabs = O.mx_gemm(aq.cpu().numpy()[rows], asc.cpu().numpy()[rows], wq, ws)
+    got = out.float().cpu().numpy()[rows].astype(np.float64)
+    assert (np.abs(got - y64) <= 2.0 ** -8 * np.abs(y64) + 2.0 ** -16 * yabs + 1e-30).all()
+    sub = rows[:16]
+    o16 = torch.empty(16, N, dtype=torch.bfloat16, device=dev)
+    MX.gemm(aq[_t(sub, dev)].contiguous(), asc[_t(sub, dev)].contiguous(), mw, o16, 16, kernel="decode")
+    torch.cuda.synchronize()
+    assert np.array_equal(_bits(o16), _bits(out)[sub])
