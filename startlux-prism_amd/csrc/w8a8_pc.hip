@@ -32,6 +32,7 @@ __global__ __launch_bounds__(64 * NWV, 1) void w8a8_pc_tile_kernel(const int8_t*
                                                               int N, int K, int tiles_m, int tiles_n) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];   // NS x [A 256 x 64 | W 256 x 64]
     __shared__ float sal[PCT], swl[PCT];
+    static_assert(NS * PC_STAGE + 2 * PCT * sizeof(float) <= 160 * 1024, "the stages and scales exceed a CU's LDS");
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     int pm, pn;
     xcd_tile_coords(blockIdx.x, tiles_m, tiles_n, pm, pn);
