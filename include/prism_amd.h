@@ -184,7 +184,8 @@ PRISM_API int prism_q6k_pack(const uint8_t* raw, uint8_t* qv, uint8_t* meta, int
  * startlux_prism::w4a8_gemm (csrc/w4a8_gemm.cu); arithmetic of kernels/w4a8.py:19-20 / gemm_ref (:193-197), per
  * super-block b in increasing b: acc = sum_h sc[n,b,h] (xq . q)_h over its 16 sub-blocks of 16 (int32, exact),
  * y = fma(a[b,m], RN(d[n,b] float(acc)), y); epi 0: bf16(y); epi 1: out = RN(out + y).  xq, a, a_sb, out, ldo,
- * n_rows and kernel as prism_w4a8_q4k_gemm (Q6_K has no mins: no activation sums).
+ * n_rows and kernel as prism_w4a8_q4k_gemm (Q6_K has no mins: no activation sums), plus kernel 2: the stream decode
+ * kernel (M <= 16), which the MI355X dispatch table picks for the shapes where it measured faster.
  */
 PRISM_API int prism_w4a8_q6k_gemm(const int8_t* xq, const float* a, int64_t a_sb, const uint8_t* qv,
                                   const uint8_t* meta, void* out, int64_t ldo, const int32_t* n_rows, int64_t M,

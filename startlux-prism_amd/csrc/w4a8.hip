@@ -428,6 +428,102 @@ __global__ __launch_bounds__(NW * 64) void w4a8_q4k_stream_kernel(const int8_t* 
     }
 }
 
+// ---------------------------------------------------------------------------------------------- Q6_K stream decode
+// The Q4_K stream kernel's structure on Q6_K weights (prism_q6k_pack): per super-block a lane holds the tile's 4 KB
+// of weights (four 16-byte slots), the 16 int8 scales of its four output rows 4 q .. 4 q + 3, their fp16 d, and the
+// eight 8-byte activation pieces of its row.  Per 32-input window, P over both sub-blocks and Pl over the first
+// (activations of lanes q >= 2, which hold the second, zeroed): acc += sc1 P + (sc0 - sc1) Pl, exact; then
+// t = RN(d float(acc)) to LDS, and the ordered fold y = fma(a[b, m], t, y) after one barrier.  About three times the
+// staged kernel's loads per weight byte: faster only for some shapes at a few rows, so the dispatch table picks it
+// ("stream") where it measured faster.
+template <int NW, int PD, int EPI>
+__global__ __launch_bounds__(NW * 64) void w4a8_q6k_stream_kernel(const int8_t* __restrict__ xq,
+                                                                 const float* __restrict__ a, int64_t a_sb,
+                                                                 const uint8_t* __restrict__ qv,
+                                                                 const uint8_t* __restrict__ meta,
+                                                                 void* __restrict__ out, int64_t ldo,
+                                                                 const int32_t* __restrict__ n_rows, int M, int K) {
+    extern __shared__ __attribute__((aligned(16))) float tl[];          // [NB][M][16]
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int nt = blockIdx.x;
+    const int live = min(M, __ldg(n_rows));
+    const int NB = K / 256;
+    const int lm = lane & 15, q = lane >> 4;
+    const int m = min(lm, M - 1);
+
+    const v4u* cw = reinterpret_cast<const v4u*>(qv) + (int64_t)nt * NB * 256 + lane;
+    const uint8_t* cm = meta + (int64_t)nt * NB * Q6_META;
+    const int8_t* cx = xq + (int64_t)m * K + 8 * q;
+    struct SB {
+        v4u w[4];
+        v4u sc[4];
+        v2u dh;
+        v2u x[8];
+    };
+    auto load = [&](int i, SB& c) {
+        const int b = min(wv + NW * i, NB - 1);
+#pragma unroll
+        for (int j = 0; j < 4; j++) c.w[j] = __builtin_nontemporal_load(cw + (int64_t)b * 256 + 64 * j);
+        const uint8_t* mp = cm + (int64_t)b * Q6_META;
+#pragma unroll
+        for (int e = 0; e < 4; e++) c.sc[e] = reinterpret_cast<const v4u*>(mp)[4 * q + e];
+        c.dh = *reinterpret_cast<const v2u*>(mp + 256 + 8 * q);
+#pragma unroll
+        for (int wn = 0; wn < 8; wn++) c.x[wn] = *reinterpret_cast<const v2u*>(cx + (int64_t)b * 256 + 32 * wn);
+    };
+    auto term = [&](int i, const SB& c) {
+        const int b = wv + NW * i;
+        const v4i zero = {0, 0, 0, 0};
+        v4i acc = {0, 0, 0, 0};
+#pragma unroll
+        for (int wn = 0; wn < 8; wn++) {
+            const v4u& c16 = c.w[wn >> 1];
+            const int64_t wf = (int64_t)c16[2 * (wn & 1)] | ((int64_t)c16[2 * (wn & 1) + 1] << 32);
+            const int64_t af = (int64_t)(uint32_t)c.x[wn][0] | ((int64_t)c.x[wn][1] << 32);
+            const v4i P = __builtin_amdgcn_mfma_i32_16x16x32_i8(wf, af, zero, 0, 0, 0);
+            const v4i Pl = __builtin_amdgcn_mfma_i32_16x16x32_i8(wf, q < 2 ? af : 0, zero, 0, 0, 0);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int s0 = sbyte(c.sc[e], 2 * wn), s1 = sbyte(c.sc[e], 2 * wn + 1);
+                acc[e] += __mul24(s1, P[e]) + __mul24(s0 - s1, Pl[e]);
+            }
+        }
+        v4f t;
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            t[e] = mul_rn(f16_to_f32((e & 1) ? (c.dh[e >> 1] >> 16) : (c.dh[e >> 1] & 0xffffu)), (float)acc[e]);
+        if (lm < M && b < NB) *reinterpret_cast<v4f*>(&tl[((int64_t)b * M + lm) * 16 + 4 * q]) = t;
+    };
+    const int cnt = wv < NB ? (NB - wv + NW - 1) / NW : 0;
+    SB ring[PD];
+#pragma unroll
+    for (int d = 0; d < PD; d++) load(d, ring[d]);
+    const int full = cnt / PD * PD;
+    for (int i0 = 0; i0 < full; i0 += PD) {
+#pragma unroll
+        for (int d = 0; d < PD; d++) {
+            term(i0 + d, ring[d]);
+            load(i0 + d + PD, ring[d]);
+        }
+    }
+#pragma unroll
+    for (int d = 0; d < PD; d++)
+        if (full + d < cnt) term(full + d, ring[d]);
+    __syncthreads();
+    for (int fo = tid; fo < M * 16; fo += NW * 64) {
+        const int mo = fo >> 4, n = 16 * nt + (fo & 15);
+        if (mo >= live) continue;
+        float y = 0.f;
+        for (int b = 0; b < NB; b++) y = fmaf(a[(int64_t)b * a_sb + mo], tl[((int64_t)b * M + mo) * 16 + (fo & 15)], y);
+        if (EPI == 0) {
+            reinterpret_cast<uint16_t*>(out)[(int64_t)mo * ldo + n] = (uint16_t)f32_to_bf16(y);
+        } else {
+            float* op = reinterpret_cast<float*>(out) + (int64_t)mo * ldo + n;
+            *op = add_rn(*op, y);
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------------------------- prefill tile
 // 128 (n) x 64 (m) output tile per 256-thread workgroup: 4 waves, each 32 n x 64 m (2 x 4 MFMA tiles of 16 x 16),
 // one super-block per stage, two stage buffers in LDS.  The stage's weight chunks (8 row tiles x 2 KB) and activation
@@ -860,13 +956,23 @@ extern "C" int prism_w4a8_q6k_gemm(const int8_t* xq, const float* a, int64_t a_s
     if (M < 0 || N <= 0 || K <= 0 || N % 16 || K % 256 || ldo < N || M > (1 << 30) || N > (1 << 30) || K > (1 << 30))
         return PRISM_ERR_SHAPE;
     if (!PRISM_ALIGNED(xq, 16) || !PRISM_ALIGNED(qv, 16) || !PRISM_ALIGNED(meta, 16)) return PRISM_ERR_ALIGN;
-    if (kernel < -1 || kernel > 1) return PRISM_ERR_ARG;
+    if (kernel < -1 || kernel > 2) return PRISM_ERR_ARG;
     if (kernel == -1) kernel = M <= 16 ? 1 : 0;
-    if (kernel == 1 && M > 16) return PRISM_ERR_ARG;
+    if (kernel >= 1 && M > 16) return PRISM_ERR_ARG;
     if (M == 0) return PRISM_OK;
     hipStream_t st = (hipStream_t)stream;
     const int Mi = (int)M, Ni = (int)N, Ki = (int)K;
-    if (kernel == 1) {
+    if (kernel == 2 && (size_t)(K / 256) * M * 16 * 4 > 160 * 1024) kernel = 1;   // terms beyond the LDS: staged
+    if (kernel == 2) {
+        const size_t lds = (size_t)(K / 256) * M * 16 * 4;
+#define Q6S(E) do {                                                                                                \
+        allow_lds(w4a8_q6k_stream_kernel<4, 2, E>, lds);                                                          \
+        hipLaunchKernelGGL((w4a8_q6k_stream_kernel<4, 2, E>), dim3(Ni / 16), dim3(256), lds, st, xq, a, a_sb, qv,   \
+                           meta, out, ldo, n_rows, Mi, Ki);                                                        \
+    } while (0)
+        if (epi == 0) Q6S(0); else Q6S(1);
+#undef Q6S
+    } else if (kernel == 1) {
         dim3 grid(Ni / 16);
 #define Q6DEC(NW, R, MX, D, E)                                                                                      \
     do {                                                                                                           \

@@ -129,7 +129,7 @@ def tune_w4(shapes, Ms, dev, log):
             xs = torch.randint(-64, 64, (K // 256, M, 16), generator=g, dtype=torch.int8, device=dev)
             out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
             n = torch.tensor([M], dtype=torch.int32, device=dev)
-            cands = ["decode", "tile"] if M <= 16 else ["tile"]
+            cands = (["decode", "stream", "tile"] if kind == "q6k" else ["decode", "tile"]) if M <= 16 else ["tile"]
             best, us = _pick(cands, lambda c: (lambda i: KW4.gemm(xq, a, xs, ws[i], out, n, kernel=c)), len(ws), M)
             row[str(M)] = [best]
             if us:

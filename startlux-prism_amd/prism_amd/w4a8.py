@@ -25,7 +25,7 @@ from . import dispatch
 from .gguf_formats import KQuant, Q4_K_BYTES, Q6_K_BYTES
 
 QK_K = 256
-KERNELS = {"auto": -1, "tile": 0, "decode": 1}
+KERNELS = {"auto": -1, "tile": 0, "decode": 1, "stream": 2}   # "stream": Q6_K only
 
 
 class W4(NamedTuple):
@@ -135,7 +135,10 @@ def gemm(xq, a, xs, w: W4, out, n_rows, epi=0, cfg=None, pdl=0, kernel="auto"):
         raise ValueError(f"out must be {want} [>= {M}, >= {w.n}] with unit column stride")
     if kernel == "auto":             # the MI355X table's choice for the shape, where valid (dispatch.w4a8_kernel)
         c = dispatch.w4a8_kernel(w.kind, w.n, K, M)
-        kernel = c if c == "tile" or (c == "decode" and M <= 16) else "auto"
+        ok = c == "tile" or (c == "decode" and M <= 16) or (c == "stream" and M <= 16 and w.kind == "q6k")
+        kernel = c if ok else "auto"
+    if kernel == "stream" and w.kind != "q6k":
+        raise ValueError("the stream decode kernel is Q6_K's; Q4_K's decode kernel is already of that form")
     if w.kind == "q6k":              # no mins: xs is not read
         L.call("prism_w4a8_q6k_gemm", L.ptr(xq), L.ptr(a), a_sb, L.ptr(w.qv), L.ptr(w.meta), L.ptr(out),
                out.stride(0), L.ptr(n_rows), M, w.n, K, epi, KERNELS[kernel], L.stream_of(xq))

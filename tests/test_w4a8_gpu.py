@@ -146,3 +146,11 @@ def test_integer_sums_exact(dev):
     for kernel in ("decode", "tile"):
         got = _gemm(dev, w, x, a, xs, 1, kernel, out0=np.zeros((M, N), np.float32)).cpu().numpy()
         assert np.array_equal(got.astype(np.int64), want), kernel
+
+
+def test_stream_kernel_is_q6k_only(dev):
+    """kernel="stream" names Q6_K's stream decode; asking it of Q4_K weights is an error, not a silent fallback."""
+    from prism_amd import w4a8 as KW4
+    blocks, xq, a, xs = _case(32, 512, 2, seed=77)
+    with pytest.raises(ValueError):
+        _gemm(dev, _w4(dev, blocks), xq, a, xs, 0, "stream")

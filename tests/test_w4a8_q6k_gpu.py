@@ -80,7 +80,7 @@ def test_gemm_bit_exact(dev, M, N, K, live, group, rand):
     base = rng(M + N).standard_normal((M, N)).astype(np.float32)
     want1 = O.w4a8_gemm_q6k(xq, ao, W, epi=1, out=base.copy(), live=live)
     w = _w6(dev, blocks)
-    for kernel in ["tile"] + (["decode"] if M <= 16 else []):
+    for kernel in ["tile"] + (["decode", "stream"] if M <= 16 else []):
         got0 = _gemm(dev, w, xq, a, 0, kernel, live=live).view(torch.int16).cpu().numpy().view(np.uint16)
         assert np.array_equal(got0[:live], want0[:live]), kernel
         assert (got0[live:] == 7).all(), kernel
@@ -102,7 +102,7 @@ def test_integer_sums_exact(dev):
     want = acc.astype(np.int64).sum(-1)
     assert np.abs(want).max() < 2 ** 24
     w = _w6(dev, blocks)
-    for kernel in ("decode", "tile"):
+    for kernel in ("decode", "stream", "tile"):
         got = _gemm(dev, w, x, a, 1, kernel, out0=np.zeros((M, N), np.float32)).cpu().numpy()
         assert np.array_equal(got.astype(np.int64), want), kernel
 
