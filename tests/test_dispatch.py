@@ -50,7 +50,7 @@ def test_off(tables, monkeypatch):
 
 
 LIMITS = {"gemm_table": {"decode": 1 << 20, "tile": 1 << 30}, "q8_table": {"decode": 64, "mid": 1 << 20, "tile": 1 << 30},
-          "w4a8_table": {"decode": 16, "tile": 1 << 30}}
+          "w4a8_table": {"decode": 16, "stream": 16, "tile": 1 << 30}}
 
 
 @pytest.mark.parametrize("path", sorted(glob.glob(os.path.join(dispatch.HERE, "*_table_*.json"))))
@@ -66,3 +66,4 @@ def test_committed_tables_well_formed(path):
             assert len(parts) == 2 and int(parts[0]) % 16 == 0
         for m, choice in row.items():
             assert choice[0] in LIMITS[prefix] and int(m) <= LIMITS[prefix][choice[0]], (key, m, choice)
+            assert choice[0] != "stream" or parts[0] == "q6k", (key, m, choice)       # Q6_K's kernel only
