@@ -137,7 +137,10 @@ PRISM_API int prism_w8a8_pc_packed_gemm_split(const int8_t* a, const int8_t* qt,
  * a int8 [M, K]; a_s fp32, row m at a_s[m * as_sm]; qt / dt from prism_q8_0_pack; out as prism_w8a8_gemm.
  * kernel: -1 picks by M; 0 the prefill tile kernel; 1 the decode kernels (M <= 64: M <= 16 folds through LDS,
  * larger M as kernel 2); 2 the register-fold kernel, one wave per 16 x 16 output tile (any M up to 65535 x 16: the
- * choice for narrow projections, whose few 256 x 256 tiles leave CUs idle).
+ * choice for narrow projections, whose few 128 x 128 tiles leave CUs idle); 3 the prefill tile kernel in a
+ * reassociated order that is not the reference's: per block y = fma(float(P), sw, y), then y = RN(y a_s[m]) (the
+ * per-token scale factored out of the block sum), half the epilogue's vector work.  Kernel 3's bf16 outputs equal
+ * kernel 0's on all but a few in 10^4 outputs and are within 1 bf16 ulp plus 2 (K/32 + 2) 2^-24 sum |terms| of them.
  * Needs K % 128 == 0.
  */
 PRISM_API int prism_w8a8_q8_0_packed_gemm(const int8_t* a, const float* a_s, int64_t as_sm, const int8_t* qt,

@@ -70,6 +70,8 @@ def lib():
             "orc_w8a8_block_sums": (None, [_p, _p, _i64, _i64, _i64, _i64, _p]),
             "orc_w8a8_gemm": (None, [_p, _p, _i64, _i64, _p, _p, ctypes.c_int, _i64, _i64, _i64, _i64,
                                      ctypes.c_int, _p, _i64, _i64, ctypes.c_int]),
+            "orc_w8a8_gemm_reassoc": (None, [_p, _p, _i64, _p, _p, ctypes.c_int, _i64, _i64, _i64, ctypes.c_int, _p,
+                                             _i64, _i64, ctypes.c_int]),
             "orc_fold_parts": (None, [_p, _i64, _p, _i64, _i64, ctypes.c_int, _p, _i64, _p, ctypes.c_int, _i64,
                                       _i64]),
             "orc_q4k_quantize": (None, [_p, _i64, _i64, _p, ctypes.c_int]),
@@ -209,6 +211,27 @@ def w8a8_gemm(a, a_s, w, w_s, gk, epi=0, out=None, live=None, nthreads=0):
     assert out.dtype == (np.uint16 if epi == 0 else np.float32) and out.flags["C_CONTIGUOUS"]
     lib().orc_w8a8_gemm(_ptr(a), _ptr(a_s), as_sm, as_sg, _ptr(w), _ptr(w_s), int(ws16), M, N, K, gk, epi,
                         _ptr(out), out.shape[1], live, nthreads)
+    return out
+
+
+def w8a8_gemm_reassoc(a, a_s, w, w_s, gk, epi=0, out=None, live=None, nthreads=0):
+    """w8a8_gemm's reassociated order (one activation scale per token, a_s fp32 [M]): per block y = fmaf(float(P),
+    sw, y), then y = RN(y a_s[m]); not the reference's rounding sequence (the "reassoc" kernel's arithmetic)."""
+    a = _c(np.ascontiguousarray(a), np.int8)
+    w = _c(np.ascontiguousarray(w), np.int8)
+    M, K = a.shape
+    N = w.shape[0]
+    a_s = _c(np.ascontiguousarray(a_s, np.float32).reshape(-1), np.float32)
+    assert a_s.shape[0] >= M
+    ws16 = w_s.dtype == np.uint16
+    w_s = np.ascontiguousarray(w_s)
+    assert w_s.shape == (N, K // gk)
+    live = M if live is None else live
+    if out is None:
+        out = np.zeros((M, N), np.uint16 if epi == 0 else np.float32)
+    assert out.dtype == (np.uint16 if epi == 0 else np.float32) and out.flags["C_CONTIGUOUS"]
+    lib().orc_w8a8_gemm_reassoc(_ptr(a), _ptr(a_s), 1, _ptr(w), _ptr(w_s), int(ws16), N, K, gk, epi, _ptr(out),
+                                out.shape[1], live, nthreads)
     return out
 
 

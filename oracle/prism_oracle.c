@@ -200,6 +200,36 @@ EXPORT void orc_w8a8_gemm(const int8_t* a, const float* a_s, int64_t as_sm, int6
 }
 
 /*
+ * The reassociated form of orc_w8a8_gemm for one activation scale per token (this build's "reassoc" kernel choice,
+ * not the reference's order): the per-token scale factors out of the block sum, so per block g in increasing g
+ * y = fmaf(float(P), sw, y) (one rounding), then y = RN(y sa[m]), then the same epilogues.  P is the same exact int32
+ * block sum; only the fp32 rounding sequence differs from kernels/w8a8.py:64-85.
+ */
+EXPORT void orc_w8a8_gemm_reassoc(const int8_t* a, const float* a_s, int64_t as_sm, const int8_t* w, const void* w_s,
+                                  int ws_fp16, int64_t N, int64_t K, int64_t gk, int epi, void* out, int64_t ldo,
+                                  int64_t live, int nthreads) {
+    int64_t G = K / gk;
+#pragma omp parallel for num_threads(nthreads_or(nthreads)) schedule(dynamic, 1)
+    for (int64_t m = 0; m < live; m++) {
+        for (int64_t n = 0; n < N; n++) {
+            float y = 0.f;
+            for (int64_t g = 0; g < G; g++) {
+                int32_t p = dot_i8(a + m * K + g * gk, w + n * K + g * gk, gk);
+                float sw = ws_fp16 ? orc_half_to_float(((const uint16_t*)w_s)[n * G + g]) : ((const float*)w_s)[n * G + g];
+                y = fmaf((float)p, sw, y);
+            }
+            y = y * a_s[m * as_sm];
+            if (epi == 0)
+                ((uint16_t*)out)[m * ldo + n] = orc_float_to_bf16(y);
+            else {
+                float* o = (float*)out + m * ldo + n;
+                *o = *o + y;
+            }
+        }
+    }
+}
+
+/*
  * The residual add deferred by a split-K per-channel projection (kernels/quant.py:129-141 _fold_parts, run by norm_q8
  * :160-166 and fold :435-457): tot = the sum over the np slots of parts[p][r][c] (int32: the splits' sums add up to
  * the unsplit product's exact sum), then h[r][c] = RN(h + RN(RN(float(tot) psa[r]) psw[c])), the epilogue 1 of the

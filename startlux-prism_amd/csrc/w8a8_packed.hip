@@ -242,7 +242,9 @@ constexpr int PBM = 128, PBN = 128;
 constexpr int PLDA = 128 + 16;          // activation tile row (bytes), padded
 constexpr int PLDB = 2048 + 64;         // one 16-row tile's two chunks, padded
 
-template <int EPI>
+// RA: the reassociated order (one activation scale per token, factored out of the block sum): per block
+// y = fma(float(P), sw, y), then y = RN(y sa) once; 2 VALU operations per output and block instead of 4.
+template <int EPI, bool RA>
 __global__ __launch_bounds__(256, 2) void w8a8_packed_tile_kernel(const int8_t* __restrict__ a,
                                                                   const float* __restrict__ a_s, int64_t as_sm,
                                                                   const int8_t* __restrict__ qt,
@@ -294,13 +296,16 @@ __global__ __launch_bounds__(256, 2) void w8a8_packed_tile_kernel(const int8_t* 
 
     const int lrow = 4 * (lane >> 5);
     float sa[2][16];
+    auto load_sa = [&]() {
 #pragma unroll
-    for (int mt = 0; mt < 2; mt++)
+        for (int mt = 0; mt < 2; mt++)
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int m = min(m0 + wm * 64 + mt * 32 + 8 * (r >> 2) + lrow + (r & 3), M - 1);
-            sa[mt][r] = a_s[(int64_t)m * as_sm];
-        }
+            for (int r = 0; r < 16; r++) {
+                const int m = min(m0 + wm * 64 + mt * 32 + 8 * (r >> 2) + lrow + (r & 3), M - 1);
+                sa[mt][r] = a_s[(int64_t)m * as_sm];
+            }
+    };
+    if (!RA) load_sa();                              // RA applies the scales once, after the K loop
     float y[2][2][16];
 #pragma unroll
     for (int mt = 0; mt < 2; mt++)
@@ -358,11 +363,16 @@ __global__ __launch_bounds__(256, 2) void w8a8_packed_tile_kernel(const int8_t* 
                 for (int nt = 0; nt < 2; nt++) {
                     const v16i acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[mt], fb[nt], zero, 0, 0, 0);
 #pragma unroll
-                    for (int r = 0; r < 16; r++)
-                        y[mt][nt][r] = add_rn(y[mt][nt][r], mul_rn(mul_rn((float)acc[r], sa[mt][r]), sw[nt]));
+                    for (int r = 0; r < 16; r++) {
+                        if (RA)
+                            y[mt][nt][r] = __builtin_fmaf((float)acc[r], sw[nt], y[mt][nt][r]);
+                        else
+                            y[mt][nt][r] = add_rn(y[mt][nt][r], mul_rn(mul_rn((float)acc[r], sa[mt][r]), sw[nt]));
+                    }
                 }
         }
     }
+    if (RA) load_sa();
 #pragma unroll
     for (int mt = 0; mt < 2; mt++)
 #pragma unroll
@@ -373,6 +383,7 @@ __global__ __launch_bounds__(256, 2) void w8a8_packed_tile_kernel(const int8_t* 
             for (int r = 0; r < 16; r++) {
                 const int m = m0 + wm * 64 + mt * 32 + 8 * (r >> 2) + lrow + (r & 3);
                 if (m < live) {
+                    if (RA) y[mt][nt][r] = mul_rn(y[mt][nt][r], sa[mt][r]);
                     if (EPI == 0) {
                         reinterpret_cast<uint16_t*>(out)[(int64_t)m * ldo + n] = (uint16_t)f32_to_bf16(y[mt][nt][r]);
                     } else {
@@ -518,10 +529,14 @@ static void launch_packed(int kernel, const int8_t* a, const float* a_s, int64_t
         const int mt = (M + 15) / 16;
         hipLaunchKernelGGL((w8a8_packed_mid_kernel<8, EPI>), dim3(N / 16, mt), dim3(64), 0, st, a, a_s, as_sm,
                            qt, dt, out, ldo, n_rows, M, N, K);
-    } else if (kernel == 0) {
+    } else if (kernel == 0 || kernel == 3) {
         const int tiles_m = (M + PBM - 1) / PBM, tiles_n = (N + PBN - 1) / PBN;
-        hipLaunchKernelGGL((w8a8_packed_tile_kernel<EPI>), dim3(tiles_m * tiles_n), dim3(256), 0, st, a, a_s, as_sm,
-                           qt, dt, out, ldo, n_rows, M, N, K, tiles_m, tiles_n);
+        if (kernel == 0)
+            hipLaunchKernelGGL((w8a8_packed_tile_kernel<EPI, false>), dim3(tiles_m * tiles_n), dim3(256), 0, st, a,
+                               a_s, as_sm, qt, dt, out, ldo, n_rows, M, N, K, tiles_m, tiles_n);
+        else
+            hipLaunchKernelGGL((w8a8_packed_tile_kernel<EPI, true>), dim3(tiles_m * tiles_n), dim3(256), 0, st, a,
+                               a_s, as_sm, qt, dt, out, ldo, n_rows, M, N, K, tiles_m, tiles_n);
     }
 }
 
@@ -560,7 +575,7 @@ extern "C" int prism_w8a8_q8_0_packed_gemm(const int8_t* a, const float* a_s, in
     if (M < 0 || N <= 0 || K <= 0 || N % 16 || K % 128 || ldo < N || M > (1 << 30) || N > (1 << 30) || K > (1 << 30))
         return PRISM_ERR_SHAPE;
     if (!PRISM_ALIGNED(a, 16) || !PRISM_ALIGNED(qt, 16) || !PRISM_ALIGNED(dt, 16)) return PRISM_ERR_ALIGN;
-    if (kernel < -1 || kernel > 2) return PRISM_ERR_ARG;
+    if (kernel < -1 || kernel > 3) return PRISM_ERR_ARG;
     if (kernel == -1) kernel = M <= 64 ? 1 : 0;
     if (kernel == 1 && M > 64) return PRISM_ERR_ARG;
     if (kernel == 2 && M > 65535 * 16) return PRISM_ERR_SHAPE;         // grid rows: one per 16 activation rows

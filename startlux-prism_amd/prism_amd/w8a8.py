@@ -24,7 +24,11 @@ from . import _lib as L
 from . import dispatch
 from .quant import quant_rows  # noqa: F401  (re-exported: kernels/w8a8.py:264)
 
-KERNELS = {"auto": -1, "tile": 0, "decode": 1, "mid": 2}
+KERNELS = {"auto": -1, "tile": 0, "decode": 1, "mid": 2, "reassoc": 3}
+# "reassoc" (packed Q8_0 only, by request, never chosen by "auto"): the prefill tile kernel with the per-token
+# activation scale factored out of the block sum (y = fma(float(P), sw, y) per block, then y * a_s once), half the
+# exact epilogue's vector work; not the reference's rounding order, so its bf16 outputs differ from the exact kernels'
+# on a few outputs in 10^4, by at most 1 bf16 ulp plus 2 (K/32 + 2) 2^-24 sum |terms|.
 
 
 class PackedQ8(NamedTuple):
@@ -119,6 +123,8 @@ def gemm(a, a_s, w, w_s, out, n_rows, gk, epi=0, outs=None, cfg=None, slots=None
             if d is not None:
                 return d
         return _gemm_pc_packed(a, a_s, w, out, n_rows, gk, epi, kernel)
+    if kernel == "reassoc":
+        raise ValueError('kernel "reassoc" is the packed Q8_0 prefill tile kernel\'s (PackedQ8 weights)')
     M, K = a.shape
     N = w.shape[0]
     if w.shape[1] != K or a.dtype != torch.int8 or w.dtype != torch.int8:
@@ -142,8 +148,10 @@ def gemm(a, a_s, w, w_s, out, n_rows, gk, epi=0, outs=None, cfg=None, slots=None
     return None
 
 
-def _tabled(kernel, N, K, M, gk):
+def _tabled(kernel, N, K, M, gk, packed_q8=False):
     """kernel "auto": the MI355X table's choice for the shape (dispatch.w8a8_kernel) where it is valid at M."""
+    if kernel == "reassoc" and not packed_q8:
+        raise ValueError('kernel "reassoc" is the packed Q8_0 prefill tile kernel\'s; not for these weights')
     if kernel != "auto":
         return kernel
     c = dispatch.w8a8_kernel(N, K, M, gk)
@@ -153,7 +161,7 @@ def _tabled(kernel, N, K, M, gk):
 
 def _gemm_packed(a, a_s, w, out, n_rows, gk, epi, kernel):
     M, K = a.shape
-    kernel = _tabled(kernel, w.n, K, M, gk)
+    kernel = _tabled(kernel, w.n, K, M, gk, packed_q8=True)
     if gk != 32 or (w.n, w.k) != (w.n, K) or w.k != K:
         raise ValueError("packed Q8_0 weights: gk must be 32 and K must match")
     if a.dtype != torch.int8 or not a.is_contiguous():

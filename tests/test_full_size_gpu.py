@@ -49,6 +49,13 @@ def test_config1_q8_0_prefill_full_size(dev):
     qa, sa = q.cpu().numpy()[rows], s.cpu().numpy()[rows]
     want = O.w8a8_gemm(qa, sa, qs, d, 32, epi=0, nthreads=16)
     assert np.array_equal(_bits(out)[rows], want)
+    # the reassociated kernel at the same size: its own order's bits, and the exact kernel's on nearly every output
+    ora = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    KW.gemm(q, s, pw, None, ora, n, 32, kernel="reassoc")
+    torch.cuda.synchronize()
+    got = _bits(ora)[rows]
+    assert np.array_equal(got, O.w8a8_gemm_reassoc(qa, sa, qs, d, 32, epi=0, nthreads=16))
+    assert (got == want).mean() > 0.999
     sub = rows[:16]
     o16 = torch.empty(16, N, dtype=torch.bfloat16, device=dev)
     KW.gemm(_t(qa[:16], dev), _t(sa[:16], dev), pw, None, o16, torch.tensor([16], dtype=torch.int32, device=dev),

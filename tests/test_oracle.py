@@ -172,6 +172,37 @@ def test_w8a8_gemm_error_bound_and_epilogues():
     assert np.array_equal(r0d[:5], r0[:5]) and np.all(r0d[5:] == 0)
 
 
+def test_w8a8_reassoc_order_replayed_and_bounded():
+    """The reassociated order (not the reference's): one element replayed with the pinned fmaf and numpy's fp32
+    multiply; every output within the rounding bound of the float64 value; the bf16 results equal the reference
+    order's on all but a few outputs in 10^4 and are within 1 bf16 ulp plus the two orders' fp32 bounds of them."""
+    M, N, K = 40, 96, 2048
+    qs, d = q8_weights(N, K, seed=16)
+    a, s = O.quant_rows_i8(acts_bf16(M, K, seed=17))
+    sw = d.view(np.float16).astype(np.float32)
+    exact, mag, G = _w8a8_f64(a, s[:, None], qs, sw, 32)
+    y = O.w8a8_gemm_reassoc(a, s, qs, d, 32, epi=1, out=np.zeros((M, N), np.float32))
+    u = 2.0 ** -24
+    assert np.all(np.abs(y - exact) <= (G + 3) * u * mag + 1e-30)
+    P = O.w8a8_block_sums(a, qs, 32)
+    m, n = 7, 33
+    r = np.float32(0)
+    for g in range(G):
+        r = np.float32(O.fmaf(np.float32(P[m, n, g]), sw[n, g], r))
+    assert y[m, n] == np.float32(r * s[m])
+    base = rng(18).standard_normal((M, N)).astype(np.float32)
+    assert np.array_equal(O.w8a8_gemm_reassoc(a, s, qs, d, 32, epi=1, out=base.copy()), (base + y).astype(np.float32))
+    r0 = O.w8a8_gemm_reassoc(a, s, qs, d, 32, epi=0)
+    assert np.array_equal(r0, O.bf16_bits(y))
+    ref = O.w8a8_gemm(a, s, qs, d, 32, epi=0)
+    assert (r0 == ref).mean() > 0.999
+    yr, yq = O.bf16_to_f32(ref).astype(np.float64), O.bf16_to_f32(r0).astype(np.float64)
+    ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(yr), 1e-38))) - 7)
+    assert np.all(np.abs(yr - yq) <= ulp + 2 * (G + 3) * u * mag)
+    live = O.w8a8_gemm_reassoc(a, s, qs, d, 32, epi=0, live=5)
+    assert np.array_equal(live[:5], r0[:5]) and np.all(live[5:] == 0)
+
+
 def test_w8a8_group_order_is_sequential():
     """Three blocks with terms 2^24, 1, -2^24: in block order the 1 is lost to round-to-even (result 0); any other
     order or an exact sum gives 1."""

@@ -270,3 +270,32 @@ def test_packed_cases_bit_exact(dev, M, N, K, live):
         assert (got0[live:] == 7).all(), kernel
         got1 = _packed_gemm(dev, a, s, qs, d, 1, kernel, live=live, out0=base).cpu().numpy()
         assert np.array_equal(got1, want1), kernel
+
+
+@pytest.mark.parametrize("M,N,K,live", [(1, 16, 128, 1), (33, 96, 1280, 33), (130, 272, 640, 100),
+                                         (256, 384, 5120, 256), (300, 528, 2048, 290)])
+def test_packed_reassoc_bit_exact(dev, M, N, K, live):
+    """The reassociated prefill kernel ("reassoc", not the reference's order) equals the oracle's restatement of its
+    order bit for bit, in both epilogues and with live rows."""
+    qs, d = q8_weights(N, K, seed=N + 7 * K)
+    a, s = O.quant_rows_i8(acts_bf16(M, K, seed=M + 9 * K))
+    want0 = O.w8a8_gemm_reassoc(a, s, qs, d, 32, epi=0, live=live)
+    base = rng(M * N + 3).standard_normal((M, N)).astype(np.float32)
+    want1 = O.w8a8_gemm_reassoc(a, s, qs, d, 32, epi=1, out=base.copy(), live=live)
+    got0 = _packed_gemm(dev, a, s, qs, d, 0, "reassoc", live=live).view(torch.int16).cpu().numpy().view(np.uint16)
+    assert np.array_equal(got0[:live], want0[:live]) and (got0[live:] == 7).all()
+    got1 = _packed_gemm(dev, a, s, qs, d, 1, "reassoc", live=live, out0=base).cpu().numpy()
+    assert np.array_equal(got1, want1)
+
+
+def test_reassoc_only_for_packed_q8(dev):
+    from prism_amd import w8a8 as KW
+    a = torch.zeros(4, 128, dtype=torch.int8, device=dev)
+    w = torch.zeros(16, 128, dtype=torch.int8, device=dev)
+    out = torch.empty(4, 16, dtype=torch.bfloat16, device=dev)
+    with pytest.raises(ValueError):
+        KW.gemm(a, torch.ones(4, device=dev), w, torch.ones(16, 4, device=dev), out, _live(4, dev), 32,
+                kernel="reassoc")
+    pw = KW.pack_i8(w, torch.ones(16, device=dev))
+    with pytest.raises(ValueError):
+        KW.gemm(a, torch.ones(4, device=dev), pw, None, out, _live(4, dev), 128, kernel="reassoc")
