@@ -324,37 +324,44 @@ __global__ __launch_bounds__(MT == 1 ? 1024 : 512) void mx_decode_kernel(const u
 }
 
 // ------------------------------------------------------------------------------------------------ tile kernel
-// Workgroup tile: WM x WN waves of 64 x 64 outputs (4 x 4 MFMAs per step), 64 WM activation rows by 64 WN weight
-// rows; by default 128 x 256 (8 waves, one workgroup per CU), which halves the operand traffic per MFMA of a
-// 128 x 128 tile.  Operands move global -> LDS by LDS-DMA (global_load_lds_dwordx4 / _ubyte), NS stages deep,
+// Workgroup tile: WM x WN waves of 16 AR x 64 outputs (4 x AR MFMAs per step), 16 AR WM activation rows by 64 WN
+// weight rows.  Default: 64 x 256 (4 waves of 64 x 64), two LDS stages of 29 KB, two workgroups per CU.  Every step
+// ends in a workgroup barrier, so the waves of one workgroup read their fragments from LDS and then run their MFMAs
+// in the same phase.  Two workgroups per CU drift apart, and one's LDS reads overlap the other's MFMAs.  The 64 x 256
+// tile ran 4-6% faster than one 128 x 256 workgroup of 8 waves per CU with three stages.  Operands move global -> LDS by LDS-DMA (global_load_lds_dwordx4 / _ubyte), NS stages deep,
 // already in MFMA operand order, so each wave reads its fragments with contiguous ds_read_b128 and no VGPR staging.
-template <int AF, int WM, int WN>
+template <int AF, int WM, int WN, int AR>
 struct MxStage {
-    static constexpr int TW = 4 * WN, TA = 4 * WM;                // 16-row weight / activation tiles
+    static constexpr int TW = 4 * WN, TA = AR * WM;               // 16-row weight / activation tiles
     static constexpr int WQ = 0;                                  // TW tiles x 1 KB
     static constexpr int AQ = TW * 1024;                          // TA tiles x (2 KB e4m3 | 1 KB e2m1)
     static constexpr int WS = AQ + TA * (AF == 0 ? 2048 : 1024);  // TW tiles x 64 lanes x 4 B
     static constexpr int AS = WS + TW * 256;                      // TA tiles x 64 lanes x 4 B
-    static constexpr int BYTES = AS + TA * 256;
+    static constexpr int DUMMY = AS + TA * 256;                   // 1 KB sink for surplus copies (below)
+    static constexpr int BYTES = DUMMY + (TA < WM * WN || TA * (AF == 0 ? 2 : 1) < WM * WN ? 1024 : 0);
     // DMA instructions per wave per stage: weights, activations, weight scales, activation scales
-    static constexpr int W_PW = TW / (WM * WN), A_PW = TA * (AF == 0 ? 2 : 1) / (WM * WN);
-    static constexpr int WS_PW = W_PW, AS_PW = TA / (WM * WN);
-    static_assert(W_PW >= 1 && A_PW >= 1 && AS_PW >= 1, "every wave copies a share of each operand");
+    // (activation shares below one per wave: every wave still issues one copy, so each wave's count of copies in
+    // flight, which the stage waits name, is the same; the surplus copies land in the DUMMY sink)
+    static constexpr int A_N = TA * (AF == 0 ? 2 : 1), W_PW = TW / (WM * WN);
+    static constexpr int A_PW = A_N >= WM * WN ? A_N / (WM * WN) : 1;
+    static constexpr int WS_PW = W_PW, AS_PW = TA >= WM * WN ? TA / (WM * WN) : 1;
+    static_assert(W_PW >= 1 && W_PW * WM * WN == TW, "every wave copies a share of the weights");
+    static_assert(A_N % (WM * WN) == 0 || A_N < WM * WN, "activation shares");
     static constexpr int LOADS = W_PW + A_PW + WS_PW + AS_PW;
 };
 
-template <int AF, int EPI, int NS, int WM, int WN>
+template <int AF, int EPI, int NS, int WM, int WN, int AR>
 __global__ __launch_bounds__(64 * WM * WN, WM * WN <= 4 ? 2 : 1) void mx_tile_kernel(const uint8_t* __restrict__ aq, const uint8_t* __restrict__ as,
                                                          const uint8_t* __restrict__ wq,
                                                          const uint8_t* __restrict__ ws, void* __restrict__ out,
                                                          int64_t ldo, const int32_t* __restrict__ n_rows, int M,
                                                          int N, int K, int tiles_m, int tiles_n) {
-    using S = MxStage<AF, WM, WN>;
+    using S = MxStage<AF, WM, WN, AR>;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     int pm, pn;
     xcd_tile_coords(blockIdx.x, tiles_m, tiles_n, pm, pn);
-    const int m0 = pm * 64 * WM, n0 = pn * 64 * WN;
+    const int m0 = pm * 16 * AR * WM, n0 = pn * 64 * WN;
     const int live = n_rows ? min(M, __ldg(n_rows)) : M;
     if (m0 >= live) return;
     const int KS = K / kMxStep, NT = N / 16;
@@ -393,26 +400,31 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN <= 4 ? 2 : 1) void mx_tile_ke
 #pragma unroll
         for (int i = 0; i < S::A_PW; i++) {
             const int idx = S::A_PW * w + i;
-            dma16(asrc[i] + (int64_t)st * (AF == 0 ? 128 : 64), b + S::AQ + idx * 1024);
+            dma16(asrc[i] + (int64_t)st * (AF == 0 ? 128 : 64), b + (idx < S::A_N ? S::AQ + idx * 1024 : S::DUMMY));
         }
 #pragma unroll
         for (int i = 0; i < S::WS_PW; i++) dma1(wssrc[i] + (int64_t)st * 64, b + S::WS + (S::WS_PW * w + i) * 256);
 #pragma unroll
-        for (int i = 0; i < S::AS_PW; i++) dma1(assrc[i] + st * 4, b + S::AS + (S::AS_PW * w + i) * 256);
+        for (int i = 0; i < S::AS_PW; i++)
+            dma1(assrc[i] + st * 4, b + (S::AS_PW * w + i < S::TA ? S::AS + (S::AS_PW * w + i) * 256 : S::DUMMY));
     };
 
     const int wn = w % WN, wm = w / WN;
-    v4f acc[4][4], tot[4][4];
+    v4f acc[4][AR], tot[4][AR];
 #pragma unroll
     for (int a = 0; a < 4; a++)
 #pragma unroll
-        for (int c = 0; c < 4; c++) acc[a][c] = tot[a][c] = v4f{0.f, 0.f, 0.f, 0.f};
+        for (int c = 0; c < AR; c++) acc[a][c] = tot[a][c] = v4f{0.f, 0.f, 0.f, 0.f};
 
 #pragma unroll
     for (int i = 0; i < NS - 1; i++)
         if (i < KS) issue(i, i);
 
-    for (int st = 0; st < KS; st++) {
+    // segments of kMxSegSteps steps as an outer loop, so the fold below runs once per segment (as a conditional
+    // inside the step loop the compiler executes it every step, predicated)
+    for (int s0 = 0; s0 < KS; s0 += kMxSegSteps) {
+    const int s1 = min(KS, s0 + kMxSegSteps);
+    for (int st = s0; st < s1; st++) {
         const int pend = min(KS - 1, st + NS - 2) - st;
         if (NS >= 4 && pend >= 2) vm_wait<2 * S::LOADS>();
         else if (NS >= 3 && pend >= 1) vm_wait<S::LOADS>();
@@ -422,16 +434,16 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN <= 4 ? 2 : 1) void mx_tile_ke
 
         const uint8_t* b = lds + (st % NS) * S::BYTES;
         v4i wf[4];
-        uint32_t wsf[4], asf[4];
-        v8i af[4];
+        uint32_t wsf[4], asf[AR];
+        v8i af[AR];
 #pragma unroll
         for (int a = 0; a < 4; a++) {
             wf[a] = *reinterpret_cast<const v4i*>(b + S::WQ + (4 * wn + a) * 1024 + lane * 16);
             wsf[a] = *reinterpret_cast<const uint32_t*>(b + S::WS + (4 * wn + a) * 256 + lane * 4);
         }
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const int u = 4 * wm + c;
+        for (int c = 0; c < AR; c++) {
+            const int u = AR * wm + c;
             if (AF == 0) {
                 const v4i lo = *reinterpret_cast<const v4i*>(b + S::AQ + u * 2048 + lane * 16);
                 const v4i hi = *reinterpret_cast<const v4i*>(b + S::AQ + u * 2048 + 1024 + lane * 16);
@@ -445,26 +457,24 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN <= 4 ? 2 : 1) void mx_tile_ke
 #pragma unroll
         for (int a = 0; a < 4; a++)
 #pragma unroll
-            for (int c = 0; c < 4; c++) acc[a][c] = mx_mfma<AF>(wf[a], af[c], acc[a][c], wsf[a], asf[c]);
-
-        if ((st % kMxSegSteps) == kMxSegSteps - 1 || st == KS - 1) {
-            const bool first = st < kMxSegSteps;
+            for (int c = 0; c < AR; c++) acc[a][c] = mx_mfma<AF>(wf[a], af[c], acc[a][c], wsf[a], asf[c]);
+    }
+    // segment sum into the running total, left to right (the first segment's sum is the total)
 #pragma unroll
-            for (int a = 0; a < 4; a++)
+    for (int a = 0; a < 4; a++)
 #pragma unroll
-                for (int c = 0; c < 4; c++) {
-                    const v4f z = acc[a][c];
-                    tot[a][c] = first ? z
-                                      : v4f{add_rn(tot[a][c].x, z.x), add_rn(tot[a][c].y, z.y),
-                                            add_rn(tot[a][c].z, z.z), add_rn(tot[a][c].w, z.w)};
-                    acc[a][c] = v4f{0.f, 0.f, 0.f, 0.f};
-                }
+        for (int c = 0; c < AR; c++) {
+            const v4f z = acc[a][c];
+            tot[a][c] = s0 == 0 ? z
+                                : v4f{add_rn(tot[a][c].x, z.x), add_rn(tot[a][c].y, z.y), add_rn(tot[a][c].z, z.z),
+                                      add_rn(tot[a][c].w, z.w)};
+            acc[a][c] = v4f{0.f, 0.f, 0.f, 0.f};
         }
     }
 
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
-        const int m = m0 + 16 * (4 * wm + c) + r;
+    for (int c = 0; c < AR; c++) {
+        const int m = m0 + 16 * (AR * wm + c) + r;
         if (m >= live) continue;
 #pragma unroll
         for (int a = 0; a < 4; a++) {
@@ -686,22 +696,22 @@ extern "C" int prism_mxfp4_gemm(const uint8_t* aq, const uint8_t* as, int a_fmt,
 #undef DEC_MT
 #undef DEC
     } else {
-        // tile configuration: LDS stages in flight, waves along M, waves along N (64 x 64 outputs each)
+        // tile configuration: LDS stages, waves along M, waves along N, 16-row activation tiles per wave
 #ifndef MXV_TILE
-#define MXV_TILE 3, 2, 4
+#define MXV_TILE 2, 1, 4, 4
 #endif
-#define MXT_(NS, WM, WN) constexpr int kNS = NS, kWM = WM, kWN = WN;
+#define MXT_(NS, WM, WN, AR) constexpr int kNS = NS, kWM = WM, kWN = WN, kAR = AR;
 #define MXT(...) MXT_(__VA_ARGS__)
         MXT(MXV_TILE)
 #undef MXT
 #undef MXT_
-        const int tiles_m = (int)((M + 64 * kWM - 1) / (64 * kWM)), tiles_n = (int)((N + 64 * kWN - 1) / (64 * kWN));
+        const int tiles_m = (int)((M + 16 * kAR * kWM - 1) / (16 * kAR * kWM)), tiles_n = (int)((N + 64 * kWN - 1) / (64 * kWN));
         dim3 grid((unsigned)(tiles_m * tiles_n));
 #define TILE(AF, E)                                                                                                  \
     do {                                                                                                             \
-        const size_t lds = (size_t)kNS * MxStage<AF, kWM, kWN>::BYTES;                                               \
-        allow_lds(mx_tile_kernel<AF, E, kNS, kWM, kWN>, lds);                                                        \
-        hipLaunchKernelGGL((mx_tile_kernel<AF, E, kNS, kWM, kWN>), grid, dim3(64 * kWM * kWN), lds, st, aq, as, wq,  \
+        const size_t lds = (size_t)kNS * MxStage<AF, kWM, kWN, kAR>::BYTES;                                          \
+        allow_lds(mx_tile_kernel<AF, E, kNS, kWM, kWN, kAR>, lds);                                                   \
+        hipLaunchKernelGGL((mx_tile_kernel<AF, E, kNS, kWM, kWN, kAR>), grid, dim3(64 * kWM * kWN), lds, st, aq, as, wq,  \
                            ws, out, ldo, n_rows, (int)M, (int)N, (int)K, tiles_m, tiles_n);                          \
     } while (0)
         if (a_fmt == PRISM_MX_E4M3) { if (epi) TILE(0, 1); else TILE(0, 0); }
