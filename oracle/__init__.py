@@ -11,6 +11,9 @@ Pinning (each function is checked by tests/test_oracle.py against something othe
   quant_rows_i8 / _groups    special cases (zero row -> scale 1e-10/127, absmax -> +-127), numpy IEEE division
   w8a8_gemm                  int32 block sums vs brute-force int64 (numpy), fp32 result vs float64 within the
                              rounding bound, gk == K reducing to the per-channel formula, epi 1 = out + epi 0 value
+  w8a8_gemm_reassoc          (this build's opt-in order, not the reference's) one element replayed with the pinned
+                             fmaf, the float64 rounding bound, epilogues as w8a8_gemm's, and agreement with
+                             w8a8_gemm's bf16 bits on all but a few outputs in 10^4
   fold_parts                 one slot holding numpy's int64 sums gives w8a8_gemm's gk = K, epi 1 residual bit for
                              bit; any split of those sums into slots gives the same bits
   q4k_quantize / dequant     an independent numpy decoder of the GGUF block_q4_K layout (ggml get_scale_min_k4)
