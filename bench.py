@@ -2,7 +2,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-sweep] [--no-cpu]
 
-Workload: Q8_0 W8A8 prefill GEMM, fused gate|up, M = 8192 tokens, K = 5120, N = 27648.  One step
+Workload (benchmark config 1): Q8_0 W8A8 prefill GEMM, fused gate|up, M = 8192 tokens, K = 5120, N = 27648.  One step
 is the hot path over one batch: per-token int8 quantization of the bf16 activations (its own kernel), then the
 W8A8 GEMM on the Q8_0 weights (int8 values + fp16 block scales, gk = 32) into bf16.  Inputs are synthetic with the
 config's distributions (weights N(0, 0.02^2) quantized to Q8_0 on the GPU, activations N(0, 1) in bf16) and are

@@ -1,4 +1,4 @@
-"""The headline configurations at their full sizes (3 and 4), checked through properties that do
+"""The headline configurations at their full sizes (benchmark configs 1, 3 and 4), checked through properties that do
 not depend on the size: rows sampled from every 128-row tile (and the last row) equal the CPU oracle bit for bit
 (MXFP4: within its fp32 bound), and the decode kernel run on a 16-row batch of the same rows gives the same bits as the
 full prefill (batch invariance, kernels/w8a8.py:14-17)."""

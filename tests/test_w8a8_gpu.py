@@ -75,7 +75,7 @@ def _gemm(dev, a, s, qs, d, gk, epi, kernel, live=None, out0=None, ldo=None, as_
 
 @pytest.mark.parametrize("kernel", ["decode", "tile"])
 def test_config0_bit_exact(dev, kernel):
-    """M = 16, K = N = 4096, Q8_0 gk = 32, per-token scales, bf16 out."""
+    """Benchmark config 0: M = 16, K = N = 4096, Q8_0 gk = 32, per-token scales, bf16 out."""
     qs, d = q8_weights(4096, 4096, seed=0)
     a, s = O.quant_rows_i8(acts_bf16(16, 4096, seed=100))
     want = O.w8a8_gemm(a, s, qs, d, 32, epi=0)
