@@ -14,8 +14,10 @@ Also measured (key "configs", not the headline; GEMM kernels alone, graph-replay
 K = N = 4096) and config 2 (Q8_0 decode, M in 1, 4, 16, 64; (K, N) = (5120, 5120), (17408, 5120)) as GB/s of packed
 Q8_0 weight bytes; config 3 (Q4_K W4A8, M = 16 and 2048; and the same shape on Q6_K weights) and config 4 (MXFP4,
 M = 16 and 4096), each against its roof (HBM for the decode sizes, the int8 or fp8 MFMA peak for the prefill
-sizes); the engine's per-channel (gk = K) projections at config 1's shape and config 2's decode sizes; and the fused
-producers.  Memory-bound shapes rotate weight
+sizes); the engine's per-channel (gk = K) projections at config 1's shape and config 2's decode sizes; the fused
+producers; and "c1_reassoc", the opt-in reassociated Q8_0 prefill kernel on config 1's operands (timed with HIP
+events, not the headline: its rounding order is not the reference's; it reports the share of its bf16 outputs equal
+to the exact kernel's).  Memory-bound shapes rotate weight
 copies through more than 3 x the 256 MB MALL so that every launch streams its weights from HBM.
 
 cpu_baseline: the CPU oracle (oracle/, the exact restatement of the reference's arithmetic, OpenMP) on a bounded
