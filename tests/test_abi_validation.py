@@ -1,0 +1,76 @@
+"""The C ABI's argument checks, run on the CPU: every entry point validates its pointers, sizes, alignment and kernel
+choice before it touches the GPU, and answers with the documented code (PRISM_ERR_ARG / _SHAPE / _ALIGN), or
+PRISM_OK with nothing launched for zero rows.  The pointers here are placeholders that are never dereferenced."""
+import os
+
+import pytest
+
+OK, SHAPE, ALIGN, ARG = 0, 1, 2, 3
+P = 0x100000          # a 16-byte-aligned placeholder address
+U = 0x100001          # a misaligned one
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from prism_amd import _lib as L
+    if not os.path.exists(L.LIB_PATH):
+        pytest.skip("libprism_amd.so not built (run __graft_entry__.build())")
+    return L.lib()
+
+
+def test_q8_0_packed_gemm_checks(lib):
+    f = lib.prism_w8a8_q8_0_packed_gemm
+
+    def call(a=P, qt=P, out=P, M=16, N=64, K=256, epi=0, kernel=-1):
+        return f(a, P, 1, qt, P, out, N, P, M, N, K, epi, kernel, None)
+    assert call(a=None) == ARG
+    assert call(epi=2) == ARG
+    assert call(K=192) == SHAPE                  # K % 128
+    assert call(N=40) == SHAPE                   # N % 16
+    assert call(a=U) == ALIGN
+    assert call(qt=U) == ALIGN
+    assert call(kernel=4) == ARG
+    assert call(kernel=1, M=65) == ARG           # the decode kernels hold up to 64 rows
+    assert call(M=0) == OK
+    assert call(M=0, kernel=3) == OK             # the reassociated prefill kernel is a valid choice
+
+
+def test_w4a8_q4k_gemm_checks(lib):
+    f = lib.prism_w4a8_q4k_gemm
+
+    def call(xq=P, qv=P, M=16, N=64, K=512, epi=0, kernel=-1):
+        return f(xq, P, 0, P, qv, P, P, N, P, M, N, K, epi, kernel, None)
+    assert call(xq=None) == ARG
+    assert call(K=384) == SHAPE                  # K % 256
+    assert call(qv=U) == ALIGN
+    assert call(epi=3) == ARG
+    assert call(kernel=2) == ARG                 # the stream kernel is Q6_K's
+    assert call(kernel=1, M=17) == ARG
+    assert call(M=0) == OK
+
+
+def test_mxfp4_gemm_checks(lib):
+    f = lib.prism_mxfp4_gemm
+
+    def call(aq=P, fmt=0, M=16, N=64, K=256, epi=0, out=P):
+        return f(aq, P, fmt, P, P, out, N, P, M, N, K, epi, -1, None)
+    assert call(aq=None) == ARG
+    assert call(fmt=1) == ARG                    # neither e4m3 (0) nor e2m1 (4)
+    assert call(K=192) == SHAPE                  # K % 128
+    assert call(aq=U) == ALIGN
+    assert call(epi=1, out=P + 8) == ALIGN       # the fp32 residual needs 16-byte rows
+    assert call(M=0) == OK
+
+
+def test_quant_and_split_checks(lib):
+    q = lib.prism_quant_rows_i8
+    assert q(None, 64, None, P, P, P, 4, 64, None) == ARG
+    assert q(P, 64, None, P, P, P, 4, 60, None) == SHAPE     # K % 8
+    assert q(U, 64, None, P, P, P, 4, 64, None) == ALIGN
+    assert q(P, 64, None, P, P, P, 0, 64, None) == OK
+    s = lib.prism_w8a8_pc_packed_gemm_split
+    assert s(P, P, P, 64 * 64, 64, P, 64, 64, 1024, 0, None) == ARG           # split < 1
+    assert s(P, P, P, 10, 64, P, 64, 64, 1024, 2, None) == SHAPE              # the slots would overlap
+    assert s(P, P, P, 64 * 64, 64, P, 64, 64, 64, 2, None) == SHAPE           # fewer 64-input chunks than parts
+    assert s(P, P, U, 64 * 64, 64, P, 64, 64, 1024, 2, None) == ALIGN
+    assert s(P, P, P, 64 * 64, 64, P, 0, 64, 1024, 2, None) == OK
