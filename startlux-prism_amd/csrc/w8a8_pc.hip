@@ -15,7 +15,7 @@
 
 namespace prism {
 
-constexpr int PCT = 256;                        // tile rows and columns
+constexpr int PCT = 256;                        // tile columns (and the default tile rows)
 constexpr int PCK = 64;                         // inputs per stage
 constexpr int PC_OPER = PCT * PCK;              // bytes per operand per stage (16 KB)
 constexpr int PC_STAGE = 2 * PC_OPER;
@@ -23,55 +23,62 @@ constexpr int PC_STAGE = 2 * PC_OPER;
 __device__ __forceinline__ int pc_swz(int row) { return (row >> 1) & 3; }
 
 
-template <bool WPACK, bool WS16, int EPI, int NS, int NWV>
-__global__ __launch_bounds__(64 * NWV, 1) void w8a8_pc_tile_kernel(const int8_t* __restrict__ a,
+template <bool WPACK, bool WS16, int EPI, int NS, int NWV, int TM>
+__global__ __launch_bounds__(64 * NWV, TM == 128 ? 2 : 1) void w8a8_pc_tile_kernel(const int8_t* __restrict__ a,
                                                               const float* __restrict__ a_s, int64_t as_sm,
                                                               const int8_t* __restrict__ w,
                                                               const void* __restrict__ w_s, void* __restrict__ out,
                                                               int64_t ldo, const int32_t* __restrict__ n_rows, int M,
                                                               int N, int K, int tiles_m, int tiles_n) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];   // NS x [A 256 x 64 | W 256 x 64]
-    __shared__ float sal[PCT], swl[PCT];
-    static_assert(NS * PC_STAGE + 2 * PCT * sizeof(float) <= 160 * 1024, "the stages and scales exceed a CU's LDS");
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];   // NS x [A TM x 64 | W 256 x 64]
+    __shared__ float sal[TM], swl[PCT];
+    constexpr int AOPER = TM * PCK, STAGE = AOPER + PC_OPER;        // A operand bytes, stage bytes
+    static_assert(TM == 128 || TM == 256, "tile rows");
+    static_assert(NS * STAGE + (TM + PCT) * sizeof(float) <= (TM == 128 ? 80 : 160) * 1024,
+                  "the stages and scales exceed the LDS share of a workgroup");
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     int pm, pn;
     xcd_tile_coords(blockIdx.x, tiles_m, tiles_n, pm, pn);
-    const int m0 = pm * PCT, n0 = pn * PCT;
+    const int m0 = pm * TM, n0 = pn * PCT;
     const int live = min(M, __ldg(n_rows));
     if (m0 >= live) return;
     const int KS = K / PCK;
-    constexpr int DI = 16 / NWV;                    // DMA instructions per operand, wave and stage
-    constexpr int WNC = NWV / 2;                    // wave columns: 2 waves of 128 rows by WNC of 256 / WNC columns
+    constexpr int DIA = TM / 16 / NWV, DIW = 16 / NWV;   // DMA instructions per wave and stage: A, W
+    static_assert(DIA >= 1 && DIW >= 1, "every wave copies a share of each operand");
+    constexpr int WNC = NWV / (TM / 128);           // wave columns: TM / 128 waves of 128 rows by WNC of 256 / WNC
     constexpr int CW = PCT / WNC, TN = CW / 32;
 
     // epilogue scales of the tile
-    if (tid < PCT) {
-        sal[tid] = a_s[(int64_t)min(m0 + tid, M - 1) * as_sm];
-        const int n = min(n0 + tid, N - 1);
-        swl[tid] = WS16 ? f16_to_f32(static_cast<const uint16_t*>(w_s)[n]) : static_cast<const float*>(w_s)[n];
+    if (tid < TM) sal[tid] = a_s[(int64_t)min(m0 + tid, M - 1) * as_sm];
+    for (int t = tid; t < PCT; t += 64 * NWV) {
+        const int n = min(n0 + t, N - 1);
+        swl[t] = WS16 ? f16_to_f32(static_cast<const uint16_t*>(w_s)[n]) : static_cast<const float*>(w_s)[n];
     }
 
-    // DMA sources: instruction i of wave wv covers operand rows 16 (DI wv + i) .. + 15; packed weights: the 1 KB
-    // chunk of 16-row tile DI wv + i as it lies (lane slot l: row l % 16, inputs 16 q .. + 15, q = l / 16)
-    const int8_t* asrc[DI];
-    const int8_t* wsrc[DI];
+    // DMA sources: instruction i of wave wv covers operand rows 16 (D wv + i) .. + 15 (D = DIA, DIW); packed
+    // weights: the 1 KB chunk of 16-row tile DIW wv + i as it lies (lane slot l: row l % 16, inputs 16 q .. + 15, q = l / 16)
+    const int8_t* asrc[DIA];
+    const int8_t* wsrc[DIW];
 #pragma unroll
-    for (int i = 0; i < DI; i++) {
-        const int row = 16 * (DI * wv + i) + (lane >> 2);
-        const int c = (lane & 3) ^ pc_swz(row);
-        asrc[i] = a + (int64_t)min(m0 + row, M - 1) * K + 16 * c;
+    for (int i = 0; i < DIA; i++) {
+        const int row = 16 * (DIA * wv + i) + (lane >> 2);
+        asrc[i] = a + (int64_t)min(m0 + row, M - 1) * K + 16 * ((lane & 3) ^ pc_swz(row));
+    }
+#pragma unroll
+    for (int i = 0; i < DIW; i++) {
+        const int row = 16 * (DIW * wv + i) + (lane >> 2);
         if (WPACK)
-            wsrc[i] = w + ((int64_t)min(n0 / 16 + DI * wv + i, N / 16 - 1) * (K / 64)) * 1024 + 16 * lane;
+            wsrc[i] = w + ((int64_t)min(n0 / 16 + DIW * wv + i, N / 16 - 1) * (K / 64)) * 1024 + 16 * lane;
         else
-            wsrc[i] = w + (int64_t)min(n0 + row, N - 1) * K + 16 * c;
+            wsrc[i] = w + (int64_t)min(n0 + row, N - 1) * K + 16 * ((lane & 3) ^ pc_swz(row));
     }
     auto issue = [&](int st, int buf) {
-        uint8_t* b = lds + buf * PC_STAGE;
+        uint8_t* b = lds + buf * STAGE;
 #pragma unroll
-        for (int i = 0; i < DI; i++) {
-            dma16(asrc[i] + (int64_t)st * PCK, b + (DI * wv + i) * 1024);
-            dma16(wsrc[i] + (int64_t)st * (WPACK ? 1024 : PCK), b + PC_OPER + (DI * wv + i) * 1024);
-        }
+        for (int i = 0; i < DIA; i++) dma16(asrc[i] + (int64_t)st * PCK, b + (DIA * wv + i) * 1024);
+#pragma unroll
+        for (int i = 0; i < DIW; i++)
+            dma16(wsrc[i] + (int64_t)st * (WPACK ? 1024 : PCK), b + AOPER + (DIW * wv + i) * 1024);
     };
 
     const int wm = wv / WNC, wn = wv % WNC;
@@ -108,19 +115,19 @@ __global__ __launch_bounds__(64 * NWV, 1) void w8a8_pc_tile_kernel(const int8_t*
 
     for (int st = 0; st < KS; st++) {
         const int pend = min(KS - 1, st + NS - 2) - st;     // stages issued after this one
-        if (NS >= 4 && pend >= 2) vm_wait<4 * DI>();
-        else if (pend >= 1) vm_wait<2 * DI>();
+        if (NS >= 4 && pend >= 2) vm_wait<2 * (DIA + DIW)>();
+        else if (pend >= 1) vm_wait<DIA + DIW>();
         else vm_wait<0>();
         lds_barrier();
         if (st + NS - 1 < KS) issue(st + NS - 1, (st + NS - 1) % NS);
-        const uint8_t* b = lds + (st % NS) * PC_STAGE;
+        const uint8_t* b = lds + (st % NS) * STAGE;
 #pragma unroll
         for (int s = 0; s < 2; s++) {
             v4i fa[4], fw[TN];
 #pragma unroll
             for (int t = 0; t < 4; t++) fa[t] = *reinterpret_cast<const v4i*>(b + aoff[s][t]);
 #pragma unroll
-            for (int u = 0; u < TN; u++) fw[u] = *reinterpret_cast<const v4i*>(b + PC_OPER + woff[s][u]);
+            for (int u = 0; u < TN; u++) fw[u] = *reinterpret_cast<const v4i*>(b + AOPER + woff[s][u]);
             // D = W x A: lane l holds activation row l % 32 of the m-subtile and weight rows
             // 8 (e / 4) + 4 (l / 32) + e % 4 of the n-subtile
 #pragma unroll
@@ -312,16 +319,21 @@ int launch_w8a8_pc(int kernel, bool wpack, const int8_t* a, const float* a_s, in
         PRISM_LAUNCH_CHECK();
         return PRISM_OK;
     }
-#ifndef PC_NWV
-#define PC_NWV 8                                  // waves per workgroup: 4, 8 or 16
+#ifndef PC_TILE
+#define PC_TILE 2, 4, 128                         // LDS stages, waves per workgroup, tile rows (tile columns: 256)
 #endif
-    constexpr int NS = 4;
-    const int tiles_m = (M + PCT - 1) / PCT, tiles_n = (N + PCT - 1) / PCT;
-    const size_t lds = (size_t)NS * PC_STAGE;
+#define PCT_(A, B, C) constexpr int NS = A, PC_NWV = B, PC_TM = C;
+#define PCT__(...) PCT_(__VA_ARGS__)
+    PCT__(PC_TILE)
+#undef PCT__
+#undef PCT_
+    const int tiles_m = (M + PC_TM - 1) / PC_TM, tiles_n = (N + PCT - 1) / PCT;
+    const size_t lds = (size_t)NS * (PC_TM * PCK + PC_OPER);
 #define PCL(WP, W16, E)                                                                                            \
     do {                                                                                                           \
-        allow_lds(w8a8_pc_tile_kernel<WP, W16, E, NS, PC_NWV>, lds);                                                \
-        hipLaunchKernelGGL((w8a8_pc_tile_kernel<WP, W16, E, NS, PC_NWV>), dim3(tiles_m * tiles_n), dim3(64 * PC_NWV),  \
+        allow_lds(w8a8_pc_tile_kernel<WP, W16, E, NS, PC_NWV, PC_TM>, lds);                                         \
+        hipLaunchKernelGGL((w8a8_pc_tile_kernel<WP, W16, E, NS, PC_NWV, PC_TM>), dim3(tiles_m * tiles_n),          \
+                           dim3(64 * PC_NWV),                                                                      \
                            lds, st, a,                                                                             \
                            a_s, as_sm, w, w_s, out, ldo, n_rows, M, N, K, tiles_m, tiles_n);                        \
     } while (0)
