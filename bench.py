@@ -139,7 +139,7 @@ def _graph_us(launch, copies, iters):
         with torch.cuda.graph(g, stream=st):
             for i in range(iters):
                 launch(i % copies)
-    g.replay()
+    g.replay()                       # warm-up replay: clocks settle before the timed one
     torch.cuda.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()
@@ -218,7 +218,7 @@ def bench_w4a8(dev, iters=20, kind="q4k"):
         n = torch.tensor([M], dtype=torch.int32, device=dev)
         KQ.rows_g(x, q, s, xs, n, M, group=K)
         out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
-        us = _graph_us(lambda i: KW4.gemm(q, s, xs, ws[i], out, n), copies, iters if M <= 64 else 5)
+        us = _graph_us(lambda i: KW4.gemm(q, s, xs, ws[i], out, n), copies, iters if M <= 64 else 20)
         rows.append(_row(M, K, N, us, wbytes, "hbm" if M <= 64 else "mfma", PEAK_INT8_TOPS))
         del ws
         torch.cuda.empty_cache()
@@ -244,7 +244,7 @@ def bench_mxfp4(dev, iters=40):
         s = torch.empty(M, K // 32, dtype=torch.uint8, device=dev)
         MX.quantize_act_fp8(x, q, s)
         out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
-        us = _graph_us(lambda i: MX.gemm(q, s, ws[i], out, M), copies, iters if M <= 64 else 10)
+        us = _graph_us(lambda i: MX.gemm(q, s, ws[i], out, M), copies, iters if M <= 64 else 40)
         rows.append(_row(M, K, N, us, wbytes, "hbm" if M <= 64 else "mfma", PEAK_FP8_TFLOPS))
         del ws
         torch.cuda.empty_cache()
@@ -276,7 +276,7 @@ def bench_per_channel(dev, iters=40):
         n = torch.tensor([M], dtype=torch.int32, device=dev)
         KQ.rows_q8(x, None, q, s, n, M)
         out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
-        us = _graph_us(lambda i: KW.gemm(q, s, ws[i], None, out, n, K), copies, iters if M <= 64 else 3)
+        us = _graph_us(lambda i: KW.gemm(q, s, ws[i], None, out, n, K), copies, iters if M <= 64 else 10)
         rows.append(_row(M, K, N, us, wbytes, "hbm" if M <= 64 else "mfma", PEAK_INT8_TOPS))
         del ws, base, out, x, q
         torch.cuda.empty_cache()
