@@ -396,7 +396,7 @@ __global__ __launch_bounds__(256, 2) void w8a8_packed_tile_kernel(const int8_t* 
 }
 
 // ---------------------------------------------------------------------------------------------- mid
-// From 17 rows (and for narrow projections at any row count, where the tile kernel's 256 x 256 tiles leave most CUs
+// From 17 rows (and for narrow projections at any row count, where the tile kernel's 128 x 128 tiles leave most CUs
 // idle): one wave (one workgroup) per (16 activation rows, 16-row weight tile), walking every block pair in order; the
 // m-tiles of one weight tile are grid rows blockIdx.y of the same XCD, so their weight chunks come from HBM once.  Per pair a lane
 // loads its weight chunk slot (16 bytes), the two 8-byte activation pieces of its row and the block scales of its 4

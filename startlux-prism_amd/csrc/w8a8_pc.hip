@@ -4,10 +4,12 @@
 // epilogue 1 out = RN(out + y).  With a single group there is no per-block fp32 work, so this is a plain int8 MFMA
 // GEMM with an epilogue, and the int32 sum is exact in any order.
 //
-// Tile: 256 x 256 outputs per 512-thread workgroup, 8 waves of 128 x 64 (4 x 2 v_mfma_i32_32x32x32_i8 per 32
-// inputs, 128 int32 accumulators per lane; two waves per SIMD: 4 waves of 128 x 128, one per SIMD, ran 6-13% slower,
-// 16 waves of 128 x 32 no faster).  Operands go global -> LDS by LDS-DMA (global_load_lds_dwordx4), NS
-// stages of 64 inputs: per stage and operand 256 rows x 64 bytes, each DMA instruction 16 rows x 64 bytes (lane L:
+// Tile: TM x 256 outputs (TM = 128 by default, or 256), waves of 128 x 64 (4 x 2 v_mfma_i32_32x32x32_i8 per 32
+// inputs, 128 int32 accumulators per lane).  Default: 128 x 256 tiles of 4 waves in two LDS stages, three
+// workgroups per CU, whose phases drift apart so that one's LDS fragment reads overlap another's MFMAs; one
+// 256 x 256 workgroup of 8 waves per CU ran 4-6% slower, 4 waves of 128 x 128 6-13% slower, 16 waves of 128 x 32 no
+// faster.  Operands go global -> LDS by LDS-DMA (global_load_lds_dwordx4), NS
+// stages of 64 inputs: per stage and operand TM or 256 rows x 64 bytes, each DMA instruction 16 rows x 64 bytes (lane L:
 // row L / 4, 16-byte chunk L % 4 XOR-swizzled by row so that the fragment reads of 8 consecutive rows hit distinct
 // banks).  MFMA operand mapping: lane l holds row l % 32 and the 16 inputs of chunk 2 s + l / 32 for the stage's
 // 32-input step s, the same for both operands.
@@ -169,7 +171,7 @@ __global__ __launch_bounds__(64 * NWV, TM == 128 ? 2 : 1) void w8a8_pc_tile_kern
 
 // ---------------------------------------------------------------------------------------------- decode
 // Rows r0 .. r0 + 16 MT - 1 with r0 = 16 MT blockIdx.y (grid rows cover M beyond 64: for narrow projections, whose
-// few 256 x 256 tiles leave the tile kernel's CUs idle, the weight tiles then come from L2 / MALL once per 64 rows).
+// few 128 x 256 tiles leave the tile kernel's CUs idle, the weight tiles then come from L2 / MALL once per 64 rows).
 // One workgroup per G 16-row weight tiles; wave w takes the 64-input chunks w, w + NW, ... of every
 // tile (the int32 sums are exact in any order), PD chunks in flight in registers.  Per chunk a lane loads 16 bytes
 // of each tile's weights (row l % 16, inputs 16 q .. + 15: packed, the chunk's lane slot, 1 KB per wave
