@@ -17,6 +17,16 @@ QK_K = 256         # k-quant super-block
 Q8_0_BYTES = 34
 Q4_K_BYTES = 144
 Q6_K_BYTES = 210
+GGML_Q8_0, GGML_Q4_K, GGML_Q6_K = 8, 12, 14        # ggml type ids (gguf.py:13-15)
+_KIND = {GGML_Q4_K: "q4k", GGML_Q6_K: "q6k", "q4k": "q4k", "q6k": "q6k"}
+
+
+def kquant_kind(t):
+    """A k-quant type, as the reference's ggml id (12, 14) or this build's name ("q4k", "q6k") -> the name."""
+    try:
+        return _KIND[int(t) if not isinstance(t, str) else t]
+    except (KeyError, TypeError, ValueError):
+        raise ValueError(f"k-quant type {t!r}: Q4_K (12) and Q6_K (14) are supported") from None
 
 
 @dataclasses.dataclass
@@ -79,22 +89,32 @@ def scale_min_k4(s):
 @dataclasses.dataclass
 class KQuant:
     """A k-quant matrix [n, k] as its raw super-blocks: raw uint8 [n, k / 256, 144] for Q4_K, [n, k / 256, 210]
-    for Q6_K (gguf_weights.py:100-119)."""
+    for Q6_K.  Fields and their positional order are the reference's (gguf_weights.py:100-112): type is the ggml id
+    (GGML_Q4_K = 12, GGML_Q6_K = 14); the names "q4k" / "q6k" are accepted too."""
     raw: torch.Tensor
+    type: int
     k: int
-    type: str = "q4k"
+
+    def __post_init__(self):
+        kquant_kind(self.type)
+        if isinstance(self.k, str) or int(self.k) % QK_K:
+            raise ValueError(f"KQuant(raw, type, k): k = {self.k!r} must be a multiple of {QK_K}")
+
+    @property
+    def kind(self):
+        return kquant_kind(self.type)
 
     @property
     def shape(self):
         return (self.raw.shape[0], self.k)
 
     def to(self, device):
-        return KQuant(self.raw.to(device), self.k, self.type)
+        return KQuant(self.raw.to(device), self.type, self.k)
 
     def dequant(self, dtype=torch.float32):
         """Q4_K: y = (d sc) q - (dmin m) in fp32, ggml's order of products (gguf_weights.py:63-70).  Q6_K:
         y = (d sc) (q - 32) (:85-97)."""
-        if self.type == "q6k":
+        if self.kind == "q6k":
             b = self.raw.reshape(-1, Q6_K_BYTES)
             sc = b[:, 192:208].contiguous().view(torch.int8).float()
             d = b[:, 208:210].contiguous().view(torch.float16).float()
@@ -142,7 +162,7 @@ def quantize_q4k(w):
     raw = torch.cat([dh.view(torch.uint8).reshape(n, k // QK_K, 2).to(torch.int32),
                      dmh.view(torch.uint8).reshape(n, k // QK_K, 2).to(torch.int32),
                      s12, qs.reshape(n, k // QK_K, 128)], -1).to(torch.uint8)
-    return KQuant(raw.contiguous(), k)
+    return KQuant(raw.contiguous(), GGML_Q4_K, k)
 
 
 def q6k_values(b):
@@ -158,7 +178,7 @@ def q6k_values(b):
 
 
 def quantize_q6k(w):
-    """fp32 [n, k] -> KQuant (type "q6k"): this build's Q6_K quantizer.  Per sub-block j of 16: scale_j =
+    """fp32 [n, k] -> KQuant (type GGML_Q6_K): this build's Q6_K quantizer.  Per sub-block j of 16: scale_j =
     max|x| / 31; d = fp16(max scale / 127); sc_j = clamp(rint(scale_j / d), -128, 127);
     q = clamp(rint(x / (d sc_j)), -32, 31); stored as q + 32 in ggml's block_q6_K layout."""
     n, k = w.shape
@@ -176,4 +196,4 @@ def quantize_q6k(w):
     qh = (Q[:, :, :, 0] >> 4) | ((Q[:, :, :, 1] >> 4) << 2) | ((Q[:, :, :, 2] >> 4) << 4) | ((Q[:, :, :, 3] >> 4) << 6)
     raw = torch.cat([ql.reshape(n, nb, 128), qh.reshape(n, nb, 64), sc.to(torch.int32) & 0xFF,
                      dh.view(torch.uint8).reshape(n, nb, 2).to(torch.int32)], -1).to(torch.uint8)
-    return KQuant(raw.contiguous(), k, "q6k")
+    return KQuant(raw.contiguous(), GGML_Q6_K, k)

@@ -22,7 +22,7 @@ import torch
 
 from . import _lib as L
 from . import dispatch
-from .gguf_formats import KQuant, Q4_K_BYTES, Q6_K_BYTES
+from .gguf_formats import KQuant, Q4_K_BYTES, Q6_K_BYTES, kquant_kind
 
 QK_K = 256
 KERNELS = {"auto": -1, "tile": 0, "decode": 1, "stream": 2}   # "stream": Q6_K only
@@ -49,13 +49,25 @@ class W4(NamedTuple):
         return self.qv.numel() + self.meta.numel()
 
 
-def repack(kq: KQuant) -> W4:
-    """A KQuant (raw uint8 [n, k/256, 144] Q4_K or [n, k/256, 210] Q6_K, on the GPU) -> W4."""
-    if kq.type not in ("q4k", "q6k"):
-        raise ValueError(f"k-quant type {kq.type}: Q4_K and Q6_K are supported")
+def _is_kquant(kq):
+    """Duck type of a k-quant matrix: this build's gguf_formats.KQuant or the reference engine's own
+    gguf_weights.KQuant (gguf_weights.py:100-112), both (raw uint8 [n, k/256, bytes], type, k)."""
+    return all(hasattr(kq, f) for f in ("raw", "type", "k")) and isinstance(getattr(kq, "raw"), torch.Tensor)
+
+
+def repack(kq) -> W4:
+    """A KQuant (raw uint8 [n, k/256, 144] Q4_K or [n, k/256, 210] Q6_K, on the GPU; type the ggml id 12 / 14 as
+    the reference's, or "q4k" / "q6k") -> W4."""
+    if not _is_kquant(kq):
+        raise ValueError(f"repack takes a k-quant matrix (raw, type, k), not {type(kq).__name__}")
+    kind = kquant_kind(kq.type)
     raw = kq.raw.contiguous()
-    n, k = raw.shape[0], kq.k
-    if kq.type == "q6k":
+    n, k = raw.shape[0], int(kq.k)
+    if raw.dim() != 3 or raw.shape[1] * QK_K != k:
+        raise ValueError(f"raw must be [n, k/256, block bytes] with k = {k}")
+    if n % 16:
+        raise ValueError(f"{n} rows: the W4 device layout takes whole 16-row tiles")
+    if kind == "q6k":
         if raw.dtype != torch.uint8 or raw.shape[-1] != Q6_K_BYTES:
             raise ValueError("raw Q6_K blocks expected")
         qv = torch.empty(n // 16, k // 256, 4, 64, 16, dtype=torch.int8, device=raw.device)
@@ -79,12 +91,13 @@ def concat(ws):
 
 
 def segments(kqs, device):
-    """The KQuant matrices of a fused projection -> [(W4, first output column)], neighbours fused."""
+    """The KQuant matrices of a fused projection -> [(W4, first output column)], neighbours of one kind fused
+    (kernels/w4a8.py:107-120).  Takes the reference engine's gguf_weights.KQuant as it is (engine/model.py:287)."""
     out, off = [], 0
     for kq in kqs:
-        if not isinstance(kq, KQuant):
+        if not _is_kquant(kq):
             raise ValueError(f"the W4A8 path needs k-quant projections, not {type(kq).__name__}")
-        w = repack(kq.to(device))
+        w = repack(KQuant(kq.raw.to(device), kq.type, kq.k))
         if out and out[-1][0].kind == w.kind:
             out[-1] = (concat([out[-1][0], w]), out[-1][1])
         else:

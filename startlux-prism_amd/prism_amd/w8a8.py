@@ -135,6 +135,8 @@ def gemm(a, a_s, w, w_s, out, n_rows, gk, epi=0, outs=None, cfg=None, slots=None
         raise ValueError("gk must divide K")
     G = K // gk
     a_s, as_sm, as_sg = _scales_a(a_s, M, G)
+    if G == 1 and w_s.dim() == 1 and w_s.shape[0] == N:
+        w_s = w_s.view(N, 1)        # the engine's per-channel row scales, fp32 [N] (engine/model.py:72-82)
     if w_s.dtype not in (torch.float16, torch.float32) or tuple(w_s.shape) != (N, G) or not w_s.is_contiguous():
         raise ValueError(f"w_s must be contiguous fp16/fp32 [{N}, {G}]")
     want = torch.bfloat16 if epi == 0 else torch.float32

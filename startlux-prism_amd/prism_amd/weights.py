@@ -12,7 +12,7 @@ from . import gguf_formats as GF
 from . import w4a8 as KW4
 from . import w8a8 as KW
 
-GGML_Q8_0, GGML_Q4_K, GGML_Q6_K = 8, 12, 14        # ggml type ids (gguf.py:13-15)
+GGML_Q8_0, GGML_Q4_K, GGML_Q6_K = GF.GGML_Q8_0, GF.GGML_Q4_K, GF.GGML_Q6_K
 BLOCKS = {GGML_Q8_0: (32, GF.Q8_0_BYTES), GGML_Q4_K: (256, GF.Q4_K_BYTES), GGML_Q6_K: (256, GF.Q6_K_BYTES)}
 
 
@@ -32,4 +32,4 @@ def from_gguf(raw, ggml_type, dims, device, gk=32):
     t = t.reshape(n, k // per, nb).to(device)
     if ggml_type == GGML_Q8_0:
         return KW.weight_from_q8(GF.q8_0_from_gguf_bytes(t, n, k), gk)
-    return KW4.repack(GF.KQuant(t, k, "q4k" if ggml_type == GGML_Q4_K else "q6k"))
+    return KW4.repack(GF.KQuant(t, ggml_type, k))

@@ -71,7 +71,7 @@ def test_config3_q4k_prefill_full_size(dev):
     M, K, N = 2048, 5120, 13824
     blocks = O.q4k_quantize(weights_f32(N, K, seed=103), nthreads=16)
     xq, a, xs = O.quant_rows_g(O.bf16_to_f32(acts_bf16(M, K, seed=104)), K, nthreads=16)
-    w = KW4.repack(GF.KQuant(_t(blocks, dev), K))
+    w = KW4.repack(GF.KQuant(_t(blocks, dev), GF.GGML_Q4_K, K))
     out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
     n = torch.tensor([M], dtype=torch.int32, device=dev)
     KW4.gemm(_t(xq, dev), _t(a, dev), _t(xs, dev), w, out, n, kernel="tile")

@@ -58,7 +58,7 @@ def test_gpu_reproduces_fixtures(dev):
         f = _load(name)
         M, K = f["xq"].shape
         n = torch.tensor([M], dtype=torch.int32, device=dev)
-        w4 = KW4.repack(GF.KQuant(torch.from_numpy(f["blocks"]).to(dev), K))
+        w4 = KW4.repack(GF.KQuant(torch.from_numpy(f["blocks"]).to(dev), GF.GGML_Q4_K, K))
         for kernel in ("decode", "tile"):
             out = torch.empty(M, w4.n, dtype=torch.bfloat16, device=dev)
             KW4.gemm(torch.from_numpy(f["xq"]).to(dev), torch.from_numpy(f["a"]).to(dev), torch.from_numpy(f["xs"]).to(dev),

@@ -41,3 +41,19 @@ def test_library_has_no_cpu_fallback_symbols():
         pytest.skip("libprism_amd.so not built")
     lib = ctypes.CDLL(L.LIB_PATH)
     assert not hasattr(lib, "orc_w8a8_gemm")
+
+
+def test_kquant_reference_field_order():
+    """KQuant(raw, type, k) in the reference's positional order with ggml ids (gguf_weights.py:100-112); the old
+    (raw, k, type) order or an unknown type raises instead of silently taking k = 12."""
+    import torch
+    from prism_amd import gguf_formats as GF
+    raw = torch.zeros(16, 2, 144, dtype=torch.uint8)
+    kq = GF.KQuant(raw, 12, 512)
+    assert kq.kind == "q4k" and kq.shape == (16, 512)
+    assert GF.KQuant(torch.zeros(16, 2, 210, dtype=torch.uint8), GF.GGML_Q6_K, 512).kind == "q6k"
+    assert GF.KQuant(raw, "q4k", 512).kind == "q4k"
+    with pytest.raises(ValueError):
+        GF.KQuant(raw, 512, 12)
+    with pytest.raises(ValueError):
+        GF.KQuant(raw, 8, 512)

@@ -92,7 +92,7 @@ def test_w4a8_q4k_random(dev, case):
     ao = a if group == 256 else a[0].copy()
     base = g.standard_normal((M, N)).astype(np.float32)
     want = O.w4a8_gemm(xq, ao, xs, O.q4k_repack(blocks), epi=epi, out=None if epi == 0 else base.copy(), live=live)
-    w = KW4.repack(GF.KQuant(_t(blocks, dev), K))
+    w = KW4.repack(GF.KQuant(_t(blocks, dev), GF.GGML_Q4_K, K))
     out = _out(dev, M, N, epi, base)
     KW4.gemm(_t(xq, dev), _t(a, dev), _t(xs, dev), w, out, _n(live, dev), epi=epi, kernel=kernel)
     torch.cuda.synchronize()
@@ -110,7 +110,7 @@ def test_w4a8_q6k_random(dev, case):
     xq, a, _ = O.quant_rows_g(O.bf16_to_f32(acts_bf16(M, K, seed=case + 10)), 256)
     base = g.standard_normal((M, N)).astype(np.float32)
     want = O.w4a8_gemm_q6k(xq, a, O.q6k_repack(blocks), epi=epi, out=None if epi == 0 else base.copy(), live=live)
-    w = KW4.repack(GF.KQuant(_t(blocks, dev), K, "q6k"))
+    w = KW4.repack(GF.KQuant(_t(blocks, dev), GF.GGML_Q6_K, K))
     out = _out(dev, M, N, epi, base)
     xs = torch.zeros(K // 256, M, 16, dtype=torch.int8, device=dev)
     KW4.gemm(_t(xq, dev), _t(a, dev), xs, w, out, _n(live, dev), epi=epi, kernel=kernel)

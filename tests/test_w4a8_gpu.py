@@ -41,7 +41,7 @@ def _w4(dev, blocks):
     from prism_amd import gguf_formats as GF
     from prism_amd import w4a8 as KW4
     N, NB, _ = blocks.shape
-    return KW4.repack(GF.KQuant(_t(blocks, dev), NB * 256))
+    return KW4.repack(GF.KQuant(_t(blocks, dev), GF.GGML_Q4_K, NB * 256))
 
 
 def test_pack_layout(dev):

@@ -37,7 +37,7 @@ def _np_pack(blocks):
 def _w6(dev, blocks):
     from prism_amd import gguf_formats as GF
     from prism_amd import w4a8 as KW4
-    return KW4.repack(GF.KQuant(_t(blocks, dev), blocks.shape[1] * 256, "q6k"))
+    return KW4.repack(GF.KQuant(_t(blocks, dev), GF.GGML_Q6_K, blocks.shape[1] * 256))
 
 
 def test_pack_layout(dev):
@@ -116,7 +116,7 @@ def test_mixed_segments(dev):
     parts = [("q4k", 64), ("q6k", 32), ("q4k", 48)]
     raws = [O.q4k_quantize(weights_f32(n, K, seed=70 + i)) if kind == "q4k" else
             O.q6k_quantize(weights_f32(n, K, seed=70 + i)) for i, (kind, n) in enumerate(parts)]
-    kqs = [GF.KQuant(_t(r, dev), K, kind) for r, (kind, _) in zip(raws, parts)]
+    kqs = [GF.KQuant(_t(r, dev), kind, K) for r, (kind, _) in zip(raws, parts)]
     segs = KW4.segments(kqs, dev)
     assert [w.kind for w, _ in segs] == ["q4k", "q6k", "q4k"]
     xq, a, xs = O.quant_rows_g(O.bf16_to_f32(acts_bf16(M, K, seed=75)), 256)
