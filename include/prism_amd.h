@@ -141,11 +141,23 @@ PRISM_API int prism_w8a8_pc_packed_gemm_split(const int8_t* a, const int8_t* qt,
  * reassociated order that is not the reference's: per block y = fma(float(P), sw, y), then y = RN(y a_s[m]) (the
  * per-token scale factored out of the block sum), half the epilogue's vector work.  Kernel 3's bf16 outputs equal
  * kernel 0's on all but a few in 10^4 outputs and are within 1 bf16 ulp plus 2 (K/32 + 2) 2^-24 sum |terms| of them.
+ * 4 the balanced decode kernel (1 <= M <= 16): min(N/16, 256) workgroups take equal shares of the projection's
+ * 1 KB weight chunks, so every CU streams the same bytes; a 16-row tile split between two workgroups hands its
+ * running fp32 sums from the first to the second through `workspace` (bits identical to kernels 0-2).  kernel -1
+ * takes kernel 4 when M <= 16 and a workspace is given.
+ * workspace: device memory of at least prism_w8a8_q8_0_packed_workspace_bytes(N, K) bytes, zeroed once before its
+ * first use (every launch leaves it zeroed), or NULL (kernel 4 is then unavailable).  Launches that share a
+ * workspace must not run concurrently.  This argument is the reference schema's `workspace`
+ * (csrc/w8a8_gemm.cu:794-797), which its engine allocates once per device (kernels/cuda_ext.py:432-437).
  * Needs K % 128 == 0.
  */
 PRISM_API int prism_w8a8_q8_0_packed_gemm(const int8_t* a, const float* a_s, int64_t as_sm, const int8_t* qt,
                                           const uint16_t* dt, void* out, int64_t ldo, const int32_t* n_rows,
-                                          int64_t M, int64_t N, int64_t K, int epi, int kernel, void* stream);
+                                          int64_t M, int64_t N, int64_t K, int epi, int kernel, void* workspace,
+                                          int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes prism_w8a8_q8_0_packed_gemm's kernel 4 needs for N x K weights (0 for an unsupported shape). */
+PRISM_API int64_t prism_w8a8_q8_0_packed_workspace_bytes(int64_t N, int64_t K);
 
 /*
  * Repack Q4_K weights into the MFMA-native layout the W4A8 kernels read: a byte permutation of the GGUF block_q4_K

@@ -13,6 +13,7 @@
 // Arithmetic: identical to the row-major kernels (kernels/w8a8.py:64-85), every output's fp32 sum over blocks in
 // block order, so both layouts give the same bits.
 #include "common.h"
+#include "q8_stream.h"
 
 
 namespace prism {
@@ -567,24 +568,48 @@ extern "C" int prism_i8_pack(const int8_t* w, int8_t* qt, int64_t N, int64_t K, 
     return PRISM_OK;
 }
 
-extern "C" int prism_w8a8_q8_0_packed_gemm(const int8_t* a, const float* a_s, int64_t as_sm, const int8_t* qt,
-                                           const uint16_t* dt, void* out, int64_t ldo, const int32_t* n_rows,
-                                           int64_t M, int64_t N, int64_t K, int epi, int kernel, void* stream) {
+static int packed_gemm(const int8_t* a, const float* a_s, int64_t as_sm, const int8_t* qt, const uint16_t* dt,
+                       void* out, int64_t ldo, const int32_t* n_rows, int64_t M, int64_t N, int64_t K, int epi,
+                       int kernel, void* workspace, int64_t workspace_bytes, void* stream) {
     if (!a || !a_s || !qt || !dt || !out || !n_rows) return PRISM_ERR_ARG;
     if (epi != 0 && epi != 1) return PRISM_ERR_ARG;
     if (M < 0 || N <= 0 || K <= 0 || N % 16 || K % 128 || ldo < N || M > (1 << 30) || N > (1 << 30) || K > (1 << 30))
         return PRISM_ERR_SHAPE;
     if (!PRISM_ALIGNED(a, 16) || !PRISM_ALIGNED(qt, 16) || !PRISM_ALIGNED(dt, 16)) return PRISM_ERR_ALIGN;
-    if (kernel < -1 || kernel > 3) return PRISM_ERR_ARG;
-    if (kernel == -1) kernel = M <= 64 ? 1 : 0;
+    if (kernel < -1 || kernel > 4) return PRISM_ERR_ARG;
+    const bool can_stream = M >= 1 && M <= 16 && workspace && workspace_bytes >= q8_stream_workspace_bytes(N, K);
+    // by default: the balanced kernel from 5 to 16 rows (where its even spread over the CUs pays for its per-round
+    // work), the row-round decode kernel below and up to 64 rows, the tile kernel beyond
+    if (kernel == -1) kernel = M >= 5 && M <= 16 && can_stream ? 4 : M <= 64 ? 1 : 0;
     if (kernel == 1 && M > 64) return PRISM_ERR_ARG;
+    if (kernel == 4 && !can_stream) return M > 16 ? PRISM_ERR_SHAPE : PRISM_ERR_ARG;
     if (kernel == 2 && M > 65535 * 16) return PRISM_ERR_SHAPE;         // grid rows: one per 16 activation rows
     if (M == 0) return PRISM_OK;
     hipStream_t st = (hipStream_t)stream;
+    if (kernel == 4) {
+        const int rc = q8_stream_launch(a, a_s, as_sm, qt, dt, out, ldo, n_rows, M, N, K, epi, workspace,
+                                        workspace_bytes, st);
+        if (rc != PRISM_OK) return rc;
+        PRISM_LAUNCH_CHECK();
+        return PRISM_OK;
+    }
     if (epi == 0)
         launch_packed<0>(kernel, a, a_s, as_sm, qt, dt, out, ldo, n_rows, (int)M, (int)N, (int)K, st);
     else
         launch_packed<1>(kernel, a, a_s, as_sm, qt, dt, out, ldo, n_rows, (int)M, (int)N, (int)K, st);
     PRISM_LAUNCH_CHECK();
     return PRISM_OK;
+}
+
+extern "C" int prism_w8a8_q8_0_packed_gemm(const int8_t* a, const float* a_s, int64_t as_sm, const int8_t* qt,
+                                           const uint16_t* dt, void* out, int64_t ldo, const int32_t* n_rows,
+                                           int64_t M, int64_t N, int64_t K, int epi, int kernel, void* workspace,
+                                           int64_t workspace_bytes, void* stream) {
+    return packed_gemm(a, a_s, as_sm, qt, dt, out, ldo, n_rows, M, N, K, epi, kernel, workspace, workspace_bytes,
+                       stream);
+}
+
+extern "C" int64_t prism_w8a8_q8_0_packed_workspace_bytes(int64_t N, int64_t K) {
+    if (N <= 0 || K <= 0 || N % 16) return 0;
+    return q8_stream_workspace_bytes(N, K);
 }

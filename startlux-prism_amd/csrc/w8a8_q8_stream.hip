@@ -1,0 +1,309 @@
+// Q8_0 W8A8 decode (M <= 16) on the packed layout, streamed from HBM by a balanced grid (gfx950).
+//
+// The work of a projection is its (16-row weight tile, block pair) chunks, tiles * K / 64 of them, 1 KB each.  W
+// workgroups (one per CU at most: W <= 256 and W <= tiles) take equal contiguous ranges of that sequence, so every CU
+// streams the same number of bytes whatever N / 16 is (320 tiles at N = 5120 would otherwise leave 64 CUs with two
+// tiles and the rest with one).  A range therefore starts and ends inside tiles: its first tile's chunks continue a
+// tile whose first chunks belong to the previous workgroup (a "tail"), its last tile's chunks start a tile the next
+// workgroup finishes (a "head").  Every output's fp32 sum over blocks runs in block order (kernels/w8a8.py:74-76), so a
+// tail's fold has to start from the head's running sums.  The workgroup walks its tiles last to first: the head comes
+// first and its running sums are handed to the next workgroup through the workspace (one 64-bit word per output:
+// a "valid" tag and the fp32 bits), and the tail comes last, by when the previous workgroup has long published its
+// head.  Whole tiles in between fold from zero and store their outputs.
+//
+// Inside a workgroup, as the row-round decode kernel: NW compute waves take the round's block pairs (CP each), one
+// MFMA per block gives the 16 x 16 int32 sums, every term RN(RN(float(P) sa) sw) goes to an LDS term buffer, and FW
+// fold waves add the previous round's terms of one output per thread in block order while the compute waves run the
+// next round.  Weights are requested D - 1 rounds ahead in a register ring; a round's block scales and activation
+// pieces are staged in LDS one round ahead from a ring loaded D rounds ahead.
+//
+// Handoff protocol (per output word, never leaves a word set after a launch): the producer writes (1 << 32) | bits
+// with a compare-and-swap from 0; the consumer polls for the tag, takes the bits and clears the word.  A consumer that
+// polls past its bound (a predecessor that never ran: not expected, every predecessor is dispatched first and
+// publishes before it waits on anything) swaps in an "abandoned" tag and takes its value if the producer had just
+// finished, or yields NaN outputs (loud, never silently wrong); a producer that finds "abandoned" clears the word.
+#include "common.h"
+#include "q8_stream.h"
+
+namespace prism {
+
+constexpr unsigned long long kTagValid = 1ull << 32, kTagAbandoned = 2ull << 32;
+
+__device__ __forceinline__ unsigned long long hand_load(unsigned long long* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void hand_store(unsigned long long* p, unsigned long long v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Publishes y for the next workgroup.
+__device__ __forceinline__ void hand_publish(unsigned long long* p, float y) {
+    unsigned long long expect = 0;
+    const unsigned long long v = kTagValid | __float_as_uint(y);
+    if (!__hip_atomic_compare_exchange_strong(p, &expect, v, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT) &&
+        expect == kTagAbandoned)
+        hand_store(p, 0);
+}
+
+// Takes the previous workgroup's y (bounded wait).
+__device__ __forceinline__ float hand_take(unsigned long long* p) {
+    for (int it = 0; it < (1 << 22); it++) {
+        const unsigned long long v = hand_load(p);
+        if ((v >> 32) == 1) {
+            hand_store(p, 0);
+            return __uint_as_float((uint32_t)v);
+        }
+        __builtin_amdgcn_s_sleep(2);
+    }
+    const unsigned long long old = __hip_atomic_exchange(p, kTagAbandoned, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if ((old >> 32) == 1) {
+        hand_store(p, 0);
+        return __uint_as_float((uint32_t)old);
+    }
+    return __uint_as_float(0x7fc00000u);
+}
+
+// One round of a workgroup's walk: tile nt, block pairs p0 .. p0 + np - 1 of it; `first` / `last`: the round opens /
+// closes a fragment (the tile's part inside this workgroup's range), whose pairs are ps .. pe - 1.
+struct Round {
+    int nt, p0, np, ps, pe;
+    bool first, last;
+};
+
+// Bounded wait on an LDS counter (workgroup scope): every wave of the workgroup is resident, so the counter's
+// producers always progress; the bound only keeps a broken launch from spinning forever.
+__device__ __forceinline__ void lds_wait_ge(unsigned* c, unsigned target) {
+    for (int it = 0; it < (1 << 24); it++) {
+        if (__hip_atomic_load(c, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) return;
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+template <int NW, int R, int MX, int D, int RD, int EPI>
+__global__ __launch_bounds__((NW + (MX * 16 + 63) / 64) * 64) void w8a8_q8_stream_kernel(
+    const int8_t* __restrict__ a, const float* __restrict__ a_s, int64_t as_sm, const int8_t* __restrict__ qt,
+    const uint16_t* __restrict__ dt, void* __restrict__ out, int64_t ldo, const int32_t* __restrict__ n_rows, int M,
+    int N, int K, unsigned long long* __restrict__ hand) {
+    constexpr int FW = (MX * 16 + 63) / 64;
+    constexpr int NT = NW * 64;                    // compute threads; NT .. NT + 64 FW - 1 fold
+    constexpr int RP = R / 2;                      // block pairs per round
+    constexpr int CP = RP / NW;                    // block pairs per compute wave per round
+    static_assert(CP >= 1 && CP * NW == RP, "R must be a multiple of 2 NW");
+    static_assert(MX <= 16, "one 16-row activation tile");
+    extern __shared__ __attribute__((aligned(16))) int8_t dsm[];
+    float* terms = reinterpret_cast<float*>(dsm);                              // [RD][R][M][16]
+    unsigned* wdone = reinterpret_cast<unsigned*>(terms + RD * R * M * 16);   // [RD]: compute waves done
+    unsigned* fdone = wdone + RD;                                              // [RD]: fold waves done
+    const int tstride = R * M * 16;
+
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int live = min(M, __ldg(n_rows));
+    const int KP = K / 64;
+    const int lm = lane & 15, q = lane >> 4;
+    if (tid < 2 * RD) wdone[tid] = 0;
+    __syncthreads();
+
+    // this workgroup's range of chunks and its fragments, walked from the last tile to the first
+    const int W = gridDim.x, v = blockIdx.x;
+    const int64_t total = (int64_t)(N / 16) * KP;
+    const int64_t c0 = total * v / W, c1 = total * (v + 1) / W;
+    const int nt_lo = (int)(c0 / KP), nt_hi = (int)((c1 - 1) / KP);
+    const int ps_lo = (int)(c0 - (int64_t)nt_lo * KP), pe_hi = (int)(c1 - (int64_t)nt_hi * KP);
+    const int RT = (KP + RP - 1) / RP;
+    const int ps_hi = nt_hi == nt_lo ? ps_lo : 0;
+    const int r_hi = (pe_hi - ps_hi + RP - 1) / RP;
+    const int nmid = max(0, nt_hi - nt_lo - 1);
+    const int r_lo = nt_lo < nt_hi ? (KP - ps_lo + RP - 1) / RP : 0;
+    const int NR = r_hi + nmid * RT + r_lo;
+    auto round_of = [&](int rho) -> Round {
+        Round d;
+        int lr;
+        if (rho < r_hi) {
+            d.nt = nt_hi, d.ps = ps_hi, d.pe = pe_hi, lr = rho;
+        } else if (rho - r_hi < nmid * RT) {
+            const int x = rho - r_hi;
+            d.nt = nt_hi - 1 - x / RT, d.ps = 0, d.pe = KP, lr = x % RT;
+        } else {
+            d.nt = nt_lo, d.ps = ps_lo, d.pe = KP, lr = rho - r_hi - nmid * RT;
+        }
+        d.p0 = d.ps + lr * RP;
+        d.np = max(0, min(RP, d.pe - d.p0));
+        d.first = lr == 0;
+        d.last = d.p0 + RP >= d.pe;
+        if (rho >= NR) d.np = 0, d.first = d.last = false;     // prefetch past the end: clamped, unused
+        return d;
+    };
+
+    if (wv < NW) {
+        // Compute wave: per round its CP block pairs; per lane and pair the weight chunk's 16-byte slot, the four
+        // output rows' scales of both blocks (16 bytes of dt) and the two 8-byte pieces of the lane's activation row,
+        // requested D - 1 rounds ahead.  Each block's int32 sums come from one MFMA (zero accumulator); the terms
+        // RN(RN(float(P) sa) sw) go to ring slot r % RD once the fold waves have released it, then the wave counts
+        // itself done for the round.  Waves run ahead of one another up to the ring's depth: no barriers.
+        const int mc = min(lm, M - 1);
+        const float sa = a_s[(int64_t)mc * as_sm];
+        const v4i* cw = reinterpret_cast<const v4i*>(qt) + lane;
+        const v4u* cs = reinterpret_cast<const v4u*>(dt) + q;
+        const int8_t* xa = a + (int64_t)mc * K + 8 * q;
+        struct Pair {
+            v4i w;
+            v4u s;
+            v2u x0, x1;
+        };
+        auto load = [&](int rho, Pair* pr) {
+            const Round d = round_of(rho);
+            const int64_t tb = (int64_t)d.nt * KP;
+#pragma unroll
+            for (int i = 0; i < CP; i++) {
+                const int p = min(d.p0 + wv * CP + i, KP - 1);
+                pr[i].w = __builtin_nontemporal_load(cw + (tb + p) * 64);
+                pr[i].s = cs[(tb + p) * 4];
+                pr[i].x0 = *reinterpret_cast<const v2u*>(xa + 64 * p);
+                pr[i].x1 = *reinterpret_cast<const v2u*>(xa + 64 * p + 32);
+            }
+        };
+        auto compute = [&](int rho, const Pair* pr) {
+            v4i acc[CP][2];
+#pragma unroll
+            for (int i = 0; i < CP; i++)
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const int64_t wf = h ? ((int64_t)(uint32_t)pr[i].w[2] | ((int64_t)pr[i].w[3] << 32))
+                                         : ((int64_t)(uint32_t)pr[i].w[0] | ((int64_t)pr[i].w[1] << 32));
+                    const v2u xv = h ? pr[i].x1 : pr[i].x0;
+                    const int64_t xf = (int64_t)xv[0] | ((int64_t)xv[1] << 32);
+                    const v4i zero = {0, 0, 0, 0};
+                    acc[i][h] = __builtin_amdgcn_mfma_i32_16x16x32_i8(wf, xf, zero, 0, 0, 0);
+                }
+            v4f t[CP][2];
+#pragma unroll
+            for (int i = 0; i < CP; i++)
+#pragma unroll
+                for (int h = 0; h < 2; h++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const float x = mul_rn((float)acc[i][h][e], sa);
+                        t[i][h][e] = h ? mul_f16_rn<1>(x, pr[i].s[e]) : mul_f16_rn<0>(x, pr[i].s[e]);
+                    }
+            const int slot = rho % RD;
+            lds_wait_ge(&fdone[slot], (unsigned)(FW * (rho / RD)));      // slot released by the fold
+            float* tb = terms + slot * tstride;
+#pragma unroll
+            for (int i = 0; i < CP; i++)
+#pragma unroll
+                for (int h = 0; h < 2; h++)
+                    if (lm < M) *reinterpret_cast<v4f*>(&tb[((2 * (wv * CP + i) + h) * M + lm) * 16 + 4 * q]) = t[i][h];
+            if (lane == 0) __hip_atomic_fetch_add(&wdone[slot], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        };
+        Pair ring[D][CP];
+#pragma unroll
+        for (int d = 0; d < D - 1; d++) load(d, ring[d]);
+        for (int r0 = 0; r0 < NR; r0 += D) {
+#pragma unroll
+            for (int d = 0; d < D; d++) {
+                const int r = r0 + d;
+                if (r < NR) {
+                    load(r + D - 1, ring[(d + D - 1) % D]);   // past the end: clamped addresses, never used
+                    compute(r, ring[d]);
+                }
+            }
+        }
+    } else {
+        // Fold wave: one output per thread (m = fo / 16, row fo % 16 of the tile), round by round in block order.
+        const int fo = tid - NT;
+        const int st = M * 16;
+        float y = 0.f;
+        for (int r = 0; r < NR; r++) {
+            const Round d = round_of(r);
+            const int slot = r % RD;
+            lds_wait_ge(&wdone[slot], (unsigned)(NW * (r / RD + 1)));
+            if (fo < M * 16) {
+                if (d.first) y = d.ps == 0 ? 0.f : hand_take(hand + (int64_t)(v - 1) * (MX * 16) + fo);
+                const float* tp = terms + slot * tstride + fo;
+                const int nb = 2 * d.np;
+                float acc = y;
+                if (nb == R) {
+                    float u[R];
+#pragma unroll
+                    for (int j = 0; j < R; j++) u[j] = tp[j * st];
+#pragma unroll
+                    for (int j = 0; j < R; j++) acc = add_rn(acc, u[j]);
+                } else {
+                    for (int j = 0; j < nb; j++) acc = add_rn(acc, tp[j * st]);
+                }
+                y = acc;
+                if (d.last) {
+                    if (d.pe < KP) {
+                        hand_publish(hand + (int64_t)v * (MX * 16) + fo, y);
+                    } else {
+                        const int m = fo >> 4, n = 16 * d.nt + (fo & 15);
+                        if (m < live) {
+                            if (EPI == 0) {
+                                reinterpret_cast<uint16_t*>(out)[(int64_t)m * ldo + n] = (uint16_t)f32_to_bf16(y);
+                            } else {
+                                float* op = reinterpret_cast<float*>(out) + (int64_t)m * ldo + n;
+                                *op = add_rn(*op, y);
+                            }
+                        }
+                    }
+                }
+            }
+            // the wave's reads of the slot are complete before it is counted released
+            if (lane == 0) __hip_atomic_fetch_add(&fdone[slot], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+    }
+}
+
+static size_t stream_lds(int R, int RD, int M) { return (size_t)RD * R * M * 16 * 4 + 2 * RD * 4; }
+
+int q8_stream_workgroups(int64_t N, int64_t K) {
+    const int64_t tiles = N / 16;
+    (void)K;
+    return (int)(tiles < kQ8StreamMaxWG ? tiles : kQ8StreamMaxWG);
+}
+
+template <int EPI>
+static void launch(const int8_t* a, const float* a_s, int64_t as_sm, const int8_t* qt, const uint16_t* dt, void* out,
+                   int64_t ldo, const int32_t* n_rows, int M, int N, int K, unsigned long long* hand, int W,
+                   hipStream_t st) {
+#define QS(NW, R, MX, D, RD)                                                                                        \
+    do {                                                                                                            \
+        auto fn = w8a8_q8_stream_kernel<NW, R, MX, D, RD, EPI>;                                                     \
+        allow_lds(fn, stream_lds(R, RD, M));                                                                        \
+        hipLaunchKernelGGL(fn, dim3(W), dim3((NW + (MX * 16 + 63) / 64) * 64), stream_lds(R, RD, M), st, a, a_s,     \
+                           as_sm,                                                                                   \
+                           qt, dt, out, ldo, n_rows, M, N, K, hand);                                                \
+    } while (0)
+#ifndef Q8S_SMALL
+#define Q8S_SMALL 8, 32, 4, 2, 4
+#endif
+#ifndef Q8S_BIG
+#define Q8S_BIG 8, 32, 16, 2, 3
+#endif
+#define QS_(...) QS(__VA_ARGS__)
+    if (M <= 4) QS_(Q8S_SMALL);
+    else QS_(Q8S_BIG);
+#undef QS_
+#undef QS
+}
+
+int q8_stream_launch(const int8_t* a, const float* a_s, int64_t as_sm, const int8_t* qt, const uint16_t* dt,
+                     void* out, int64_t ldo, const int32_t* n_rows, int64_t M, int64_t N, int64_t K, int epi,
+                     void* hand, int64_t hand_bytes, hipStream_t st) {
+    if (M < 1 || M > 16) return PRISM_ERR_SHAPE;
+    const int W = q8_stream_workgroups(N, K);
+    if (!hand || !PRISM_ALIGNED(hand, 8) || hand_bytes < q8_stream_workspace_bytes(N, K)) return PRISM_ERR_ARG;
+    auto* h = reinterpret_cast<unsigned long long*>(hand);
+    if (epi == 0)
+        launch<0>(a, a_s, as_sm, qt, dt, out, ldo, n_rows, (int)M, (int)N, (int)K, h, W, st);
+    else
+        launch<1>(a, a_s, as_sm, qt, dt, out, ldo, n_rows, (int)M, (int)N, (int)K, h, W, st);
+    return PRISM_OK;
+}
+
+int64_t q8_stream_workspace_bytes(int64_t N, int64_t K) {
+    return (int64_t)q8_stream_workgroups(N, K) * 16 * 16 * 8;
+}
+
+}  // namespace prism

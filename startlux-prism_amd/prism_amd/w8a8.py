@@ -24,7 +24,9 @@ from . import _lib as L
 from . import dispatch
 from .quant import quant_rows  # noqa: F401  (re-exported: kernels/w8a8.py:264)
 
-KERNELS = {"auto": -1, "tile": 0, "decode": 1, "mid": 2, "reassoc": 3}
+KERNELS = {"auto": -1, "tile": 0, "decode": 1, "mid": 2, "reassoc": 3, "stream": 4}
+# "stream" (packed Q8_0, 1..16 rows): the balanced decode kernel, whose workgroups take equal shares of the weight
+# chunks and hand a split tile's running sums on through a small per-device workspace (workspace()).
 # "reassoc" (packed Q8_0 only, by request, never chosen by "auto"): the prefill tile kernel with the per-token
 # activation scale factored out of the block sum (y = fma(float(P), sw, y) per block, then y * a_s once), half the
 # exact epilogue's vector work; not the reference's rounding order, so its bf16 outputs differ from the exact kernels'
@@ -157,8 +159,31 @@ def _tabled(kernel, N, K, M, gk, packed_q8=False):
     if kernel != "auto":
         return kernel
     c = dispatch.w8a8_kernel(N, K, M, gk)
-    ok = c == "tile" or (c == "decode" and (M <= 64 or gk == K)) or (c == "mid" and gk == 32)
+    if packed_q8 and c == "decode" and 5 <= M <= 16:
+        return "auto"               # the library's rule: the balanced "stream" kernel at 5..16 rows
+    ok = c == "tile" or (c == "decode" and (M <= 64 or gk == K)) or (c == "mid" and gk == 32) or \
+        (c == "stream" and packed_q8 and 1 <= M <= 16)
     return c if ok else "auto"
+
+
+_WS = {}
+
+
+def workspace(dev):
+    """The per-device workspace of the packed Q8_0 "stream" kernel (the reference schema's `workspace`, allocated once
+    per device as kernels/cuda_ext.py:432-437 does): zeroed once, left zeroed by every launch.  None while a graph is
+    being captured on a device that has none yet (its zero fill would be a graph node): "auto" then picks another
+    kernel and "stream" raises."""
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    ws = _WS.get(idx)
+    if ws is None:
+        if torch.cuda.is_current_stream_capturing():
+            return None
+        nbytes = int(L.lib().prism_w8a8_q8_0_packed_workspace_bytes(1 << 20, 128))   # the most any shape needs
+        ws = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=torch.device("cuda", idx))
+        torch.cuda.current_stream(idx).synchronize()
+        _WS[idx] = ws
+    return ws
 
 
 def _gemm_packed(a, a_s, w, out, n_rows, gk, epi, kernel):
@@ -173,8 +198,13 @@ def _gemm_packed(a, a_s, w, out, n_rows, gk, epi, kernel):
     want = torch.bfloat16 if epi == 0 else torch.float32
     if out.dtype != want or out.shape[0] < M or out.shape[1] < w.n or out.stride(1) != 1:
         raise ValueError(f"out must be {want} [>= {M}, >= {w.n}] with unit column stride")
+    ws = workspace(a.device) if M <= 16 and kernel in ("auto", "decode", "stream") else None
+    if kernel == "stream" and ws is None:
+        raise L.PrismError('kernel "stream" needs the device workspace, made outside graph capture: run one eager '
+                           'call first')
     L.call("prism_w8a8_q8_0_packed_gemm", L.ptr(a), L.ptr(a_s), a_s.stride(0), L.ptr(w.qt), L.ptr(w.dt), L.ptr(out),
-           out.stride(0), L.ptr(n_rows), M, w.n, K, epi, KERNELS[kernel], L.stream_of(a))
+           out.stride(0), L.ptr(n_rows), M, w.n, K, epi, KERNELS[kernel], L.ptr(ws), 0 if ws is None else ws.numel(),
+           L.stream_of(a))
     return None
 
 

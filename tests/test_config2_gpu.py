@@ -1,7 +1,8 @@
 """Benchmark config 2 (the Q8_0 decode sweep) at its real shapes, and the decode rows of configs 3 and 4 at full N.
 
 Config 2: M in {1, 4, 16, 64} x (K, N) in {(5120, 5120), (17408, 5120)}, Q8_0 gk = 32, full N.  Every packed kernel
-("auto" -- the MI355X table's choice, the one bench.py times --, "decode", "mid", "tile") must give the oracle's bits
+("auto" -- the MI355X table's choice, the one bench.py times --, "decode", "mid", "tile", and "stream" up to 16
+rows) must give the oracle's bits
 in both epilogues, and one live-row count below M per K leaves the rows past it untouched, as the reference's
 tests/test_cuda_gemm.py:24-29 runs its every-config matrix on the real projection shapes.  Configs 3 and 4 at M = 16:
 the whole N (13824 Q4_K rows, 5120 MXFP4 rows), through the kernel "auto" picks and the decode kernel."""
@@ -50,7 +51,7 @@ def test_config2_every_kernel_bit_exact(dev, M, K):
     base = rng(M + K).standard_normal((M, N2)).astype(np.float32)
     want1 = O.w8a8_gemm(a, s, qs, d, 32, epi=1, out=base.copy(), live=live, nthreads=16)
     ad, sd, n = _t(a, dev), _t(s, dev), torch.tensor([live], dtype=torch.int32, device=dev)
-    for kernel in ("auto", "decode", "mid", "tile"):
+    for kernel in ("auto", "decode", "mid", "tile") + (("stream",) if M <= 16 else ()):
         print(f"config 2 M={M} K={K} live={live} kernel={kernel}", flush=True)
         out = torch.full((M, N2), 7, dtype=torch.int16, device=dev).view(torch.bfloat16)
         KW.gemm(ad, sd, pw, None, out, n, 32, epi=0, kernel=kernel)

@@ -58,18 +58,20 @@ def test_q8_0_packed_and_quantizer(dev):
     n = torch.tensor([M], dtype=torch.int32, device=dev)
     rq, rs = O.quant_rows_i8(xb)
     want = O.w8a8_gemm(rq, rs, qs, d, 32, epi=0)
-    for kernel in ("auto", "decode", "mid", "tile"):
+    for kernel in ("auto", "decode", "mid", "tile", "stream"):
+        rows = 16 if kernel == "stream" else M          # the balanced decode kernel serves up to 16 rows
         out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
         sentinel = torch.full((M, N), 7, dtype=torch.int16, device=dev).view(torch.bfloat16)
 
-        def run():
+        def run(rows=rows, kernel=kernel, out=out):
             KQ.rows_q8(x, None, q, s, n, M)
-            KW.gemm(q, s, pw, None, out, n, 32, kernel=kernel)
+            KW.gemm(q[:rows], s[:rows], pw, None, out, n, 32, kernel=kernel)
 
-        def check(live):
+        def check(live, rows=rows, kernel=kernel, out=out):
             got = _bits(out)
-            assert np.array_equal(got[:live], want[:live]), (kernel, live)
-            assert (got[live:] == 7).all(), (kernel, live)
+            lv = min(live, rows)
+            assert np.array_equal(got[:lv], want[:lv]), (kernel, live)
+            assert (got[lv:] == 7).all(), (kernel, live)
 
         _replay(dev, run, out, n, check, sentinel)
 

@@ -299,3 +299,31 @@ def test_reassoc_only_for_packed_q8(dev):
     pw = KW.pack_i8(w, torch.ones(16, device=dev))
     with pytest.raises(ValueError):
         KW.gemm(a, torch.ones(4, device=dev), pw, None, out, _live(4, dev), 128, kernel="reassoc")
+
+
+SCASES = [  # (M, N, K, live): tiles below, at and above the 256-workgroup grid; ragged shares of a tile
+    (1, 16, 128, 1), (3, 80, 640, 2), (4, 4096, 1024, 4), (16, 4112, 256, 16), (9, 5120, 5120, 7),
+    (16, 5120, 384, 12), (5, 8192, 2048, 5), (2, 27648, 640, 2), (16, 1360, 17408, 16),
+]
+
+
+@pytest.mark.parametrize("M,N,K,live", SCASES)
+def test_packed_stream_bit_exact(dev, M, N, K, live):
+    """The balanced decode kernel ("stream"): a tile split between two workgroups gets its running sums handed over,
+    so every output equals the oracle bit for bit, in both epilogues, on repeated launches, and the workspace is left
+    zeroed for the next launch."""
+    from prism_amd import w8a8 as KW
+    qs, d = q8_weights(N, K, seed=N + 11 * K)
+    a, s = O.quant_rows_i8(acts_bf16(M, K, seed=M + 13 * K))
+    want0 = O.w8a8_gemm(a, s, qs, d, 32, epi=0, live=live, nthreads=16)
+    base = rng(M * N + 5).standard_normal((M, N)).astype(np.float32)
+    want1 = O.w8a8_gemm(a, s, qs, d, 32, epi=1, out=base.copy(), live=live, nthreads=16)
+    for rep in range(2):
+        got0 = _packed_gemm(dev, a, s, qs, d, 0, "stream", live=live).view(torch.int16).cpu().numpy().view(np.uint16)
+        assert np.array_equal(got0[:live], want0[:live]), rep
+        assert (got0[live:] == 7).all(), rep
+        got1 = _packed_gemm(dev, a, s, qs, d, 1, "stream", live=live, out0=base).cpu().numpy()
+        assert np.array_equal(got1, want1), rep
+    ws = KW.workspace(dev)
+    torch.cuda.synchronize()
+    assert int(ws.count_nonzero()) == 0
