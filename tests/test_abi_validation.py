@@ -21,15 +21,19 @@ def lib():
 def test_q8_0_packed_gemm_checks(lib):
     f = lib.prism_w8a8_q8_0_packed_gemm
 
-    def call(a=P, qt=P, out=P, M=16, N=64, K=256, epi=0, kernel=-1):
-        return f(a, P, 1, qt, P, out, N, P, M, N, K, epi, kernel, None)
+    def call(a=P, qt=P, out=P, M=16, N=64, K=256, epi=0, kernel=-1, ws=None, wsb=0):
+        return f(a, P, 1, qt, P, out, N, P, M, N, K, epi, kernel, ws, wsb, None)
     assert call(a=None) == ARG
     assert call(epi=2) == ARG
     assert call(K=192) == SHAPE                  # K % 128
     assert call(N=40) == SHAPE                   # N % 16
     assert call(a=U) == ALIGN
     assert call(qt=U) == ALIGN
-    assert call(kernel=4) == ARG
+    assert call(kernel=5) == ARG
+    assert call(kernel=4) == ARG                 # the balanced decode kernel needs a workspace
+    assert call(kernel=4, ws=P, wsb=16) == ARG   # ... of prism_w8a8_q8_0_packed_workspace_bytes
+    assert call(kernel=4, M=17, ws=P, wsb=1 << 20) == SHAPE      # it holds up to 16 rows
+    assert lib.prism_w8a8_q8_0_packed_workspace_bytes(64, 256) == 4 * 16 * 16 * 8
     assert call(kernel=1, M=65) == ARG           # the decode kernels hold up to 64 rows
     assert call(M=0) == OK
     assert call(M=0, kernel=3) == OK             # the reassociated prefill kernel is a valid choice
