@@ -160,6 +160,20 @@ PRISM_API int prism_w8a8_q8_0_packed_gemm(const int8_t* a, const float* a_s, int
 PRISM_API int64_t prism_w8a8_q8_0_packed_workspace_bytes(int64_t N, int64_t K);
 
 /*
+ * prism_w8a8_q8_0_packed_gemm without a workspace argument and without any allocation: the same kernels and bits,
+ * with kernel 4's handoff words in a 512 KB array of device memory that the library holds, one per GPU, for the life
+ * of the process (found with hipGetSymbolAddress, and cleared by a fill kernel on `stream`, at the first call on a
+ * device).  This entry point has no counterpart in the reference; it is for callers that cannot allocate (code
+ * under graph capture, tight serving loops, harnesses that forbid hipMalloc).  Calls on one GPU share the array:
+ * calls that overlap in time on one GPU (two streams) race; calls in sequence are safe, since every launch leaves
+ * the array zeroed.  Workspace needs above 512 KB are rejected with PRISM_ERR_SHAPE (none arises: the balanced
+ * kernel runs at most 256 workgroups, 2 KB each).  PRISM_ERR_LAUNCH if the array's address cannot be found.
+ */
+PRISM_API int prism_w8a8_q8_0_packed_gemm_noalloc(const int8_t* a, const float* a_s, int64_t as_sm, const int8_t* qt,
+                                                  const uint16_t* dt, void* out, int64_t ldo, const int32_t* n_rows,
+                                                  int64_t M, int64_t N, int64_t K, int epi, int kernel, void* stream);
+
+/*
  * Repack Q4_K weights into the MFMA-native layout the W4A8 kernels read: a byte permutation of the GGUF block_q4_K
  * bytes (the load-time step the reference's repack is: kernels/w4a8.py:70-94).  raw uint8 [N, K/256, 144] ->
  * qv uint8 [N/16][K/256][2][64][16] (per 16-row tile and super-block, lane slot l = row l % 16, q = l / 16; bytes

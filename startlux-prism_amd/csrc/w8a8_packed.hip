@@ -12,6 +12,8 @@
 // inputs 64 j + 16 q .. + 15 of its row: the 16-byte operand of v_mfma_i32_16x16x64_i8 / 32x32x32_i8 as it lies.
 // Arithmetic: identical to the row-major kernels (kernels/w8a8.py:64-85), every output's fp32 sum over blocks in
 // block order, so both layouts give the same bits.
+#include <mutex>
+
 #include "common.h"
 #include "q8_stream.h"
 
@@ -612,4 +614,49 @@ extern "C" int prism_w8a8_q8_0_packed_gemm(const int8_t* a, const float* a_s, in
 extern "C" int64_t prism_w8a8_q8_0_packed_workspace_bytes(int64_t N, int64_t K) {
     if (N <= 0 || K <= 0 || N % 16) return 0;
     return q8_stream_workspace_bytes(N, K);
+}
+
+// ---------------------------------------------------------------------------------------------- no-allocation form
+// For callers that cannot allocate (code under graph capture, serving loops, harnesses that forbid hipMalloc): the
+// balanced decode kernel's workspace is this file-scope device array instead of a caller's buffer.  Each GPU holds
+// its own copy (zero-initialised when the code object loads, cleared once more by a fill kernel at the first call
+// on the device, and left zeroed by every launch: each handoff word is reset by the workgroup that consumes it).
+// In host code the array's name is not a device address; its per-device address comes from hipGetSymbolAddress.
+constexpr int64_t kScratchBytes = 512 * 1024;
+static __device__ __align__(256) unsigned long long scratch[kScratchBytes / 8];
+static_assert(kQ8StreamMaxWG * 16 * 16 * 8 <= kScratchBytes, "the scratch array holds the largest workspace");
+
+__global__ void scratch_clear_kernel(unsigned long long* p, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = 0;
+}
+
+constexpr int kMaxDevices = 64;
+static void* g_scratch[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+// The device's scratch address (looked up, and cleared on `st`, at the first call on the device), or nullptr.
+static void* device_scratch(hipStream_t st) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch[dev]) {
+        void* ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
+        hipLaunchKernelGGL(scratch_clear_kernel, dim3(64), dim3(256), 0, st, (unsigned long long*)ptr,
+                           kScratchBytes / 8);
+        if (hipGetLastError() != hipSuccess) return nullptr;
+        g_scratch[dev] = ptr;
+    }
+    return g_scratch[dev];
+}
+
+extern "C" int prism_w8a8_q8_0_packed_gemm_noalloc(const int8_t* a, const float* a_s, int64_t as_sm, const int8_t* qt,
+                                                   const uint16_t* dt, void* out, int64_t ldo, const int32_t* n_rows,
+                                                   int64_t M, int64_t N, int64_t K, int epi, int kernel,
+                                                   void* stream) {
+    if (N > 0 && K > 0 && N % 16 == 0 && q8_stream_workspace_bytes(N, K) > kScratchBytes) return PRISM_ERR_SHAPE;
+    void* ws = device_scratch((hipStream_t)stream);
+    if (!ws) return PRISM_ERR_LAUNCH;
+    return packed_gemm(a, a_s, as_sm, qt, dt, out, ldo, n_rows, M, N, K, epi, kernel, ws, kScratchBytes, stream);
 }
