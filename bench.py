@@ -21,7 +21,12 @@ to the exact kernel's).  Memory-bound shapes rotate weight
 copies through more than 3 x the 256 MB MALL so that every launch streams its weights from HBM.
 
 cpu_baseline: the CPU oracle (oracle/, the exact restatement of the reference's arithmetic, OpenMP) on a bounded
-row sample of the same workload, on this host's cores.
+row sample of the same workload, on this host's cores; beside it, "reference_cpu_path": the reference's own CPU
+emulation of this GEMM (tests/int8_sim.py:75-81, fp32 fake quantization and matmul in torch, 16 threads).
+
+peaks_measured: the library's probes on this GPU (dense int8 / fp8 / fp4 / bf16 MFMA chains, and HBM reads of 1 GiB
+and of the decode weight sizes, graph-replayed as the decode lines are); roofline.peak stays MI355X's published
+figure, roofline.peak_measured is the probe's.
 """
 import argparse
 import json
@@ -122,7 +127,7 @@ def bench_prefill(steps, warmup, dev):
                           frac=round(ops / (ra_ms * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4),
                           bf16_equal_to_exact=round(same, 6))
     del ora
-    sample = dict(q=q, s=s, qs=q8.qs, d=q8.d)
+    sample = dict(q=q, s=s, qs=q8.qs, d=q8.d, x=x[:M1])
     return res, sample
 
 
@@ -399,6 +404,80 @@ def cpu_baseline(sample, rows):
                        f"{dt:.1f} s")
 
 
+def cpu_reference_path(sample, rows_max=M1, budget_s=5.0):
+    """The reference's own CPU path for this GEMM (tests/int8_sim.py:75-81, torch.set_num_threads(16) at :41): fp32
+    fake quantization of the activations per token (scale amax / 127, round, rescale) and an fp32 matmul against the
+    dequantized weights (Q8_0 values times their fp16 block scales), timed on a row sample of config 1's operands.
+    The weights' dequantization is set-up, not timed (the reference caches it, :63-72)."""
+    import torch
+    threads = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    qs, d = sample["qs"].cpu(), sample["d"].cpu()
+    w = (qs.view(N1, K1 // 32, 32).float() * d.float().view(N1, K1 // 32, 1)).view(N1, K1)
+    x = sample["x"].cpu().float()
+    rows = 64
+    while True:
+        xs = x[:rows]
+        t0 = time.perf_counter()
+        sc = xs.abs().amax(1, keepdim=True).clamp_min(1e-10) / 127
+        xq = torch.round(xs / sc) * sc
+        _ = xq @ w.T
+        dt = time.perf_counter() - t0
+        if dt > budget_s / 4 or rows >= rows_max:
+            break
+        rows = min(rows_max, rows * 4)
+    ops = 2.0 * rows * N1 * K1
+    return dict(value=round(ops / dt / 1e12, 4), unit="TOPS", threads=threads, os_cpu_count=os.cpu_count(),
+                torch_threads=torch.get_num_threads(),
+                sample=f"{rows} of {M1} rows of config 1, fp32 fake-quant matmul (tests/int8_sim.py:75-81), "
+                       f"{dt:.2f} s")
+
+
+def measure_peaks(dev):
+    """The roofline denominators measured on this GPU with the library's probes: dense MFMA rates (int8, fp8, fp4,
+    bf16; independent MFMA chains in registers) and the HBM read rate (a 1 GiB stream, and the decode GEMMs' sizes
+    streamed back to back from a HIP graph with copies rotated past the MALL, as the decode lines are timed)."""
+    import ctypes
+    import torch
+    from prism_amd import _lib as L
+    st = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)   # noqa: E731
+    sink = torch.zeros(1 << 16, dtype=torch.float32, device=dev)
+    out = {}
+    wgs, iters = 256 * 8, 256
+    for kind, name in ((0, "int8_tops"), (1, "fp8_tflops"), (2, "fp4_tflops"), (3, "bf16_tflops")):
+        best = 1e30
+        for _ in range(4):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            L.call("prism_probe_mfma", kind, wgs, iters, L.ptr(sink), st())
+            e1.record()
+            torch.cuda.synchronize()
+            best = min(best, e0.elapsed_time(e1))
+        ops = wgs * 4 * iters * 4 * L.lib().prism_probe_mfma_ops(kind)
+        out[name] = round(ops / (best * 1e-3) / 1e12, 1)
+    buf = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    buf.fill_(1)
+    best = 1e30
+    for _ in range(5):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        L.call("prism_probe_read", L.ptr(buf), buf.numel(), 2048, L.ptr(sink), st())
+        e1.record()
+        torch.cuda.synchronize()
+        best = min(best, e0.elapsed_time(e1))
+    out["hbm_gbs_1gib"] = round(buf.numel() / (best * 1e-3) / 1e9, 1)
+    for nbytes in (q8_bytes(5120, 5120), q8_bytes(5120, 17408)):
+        copies = _copies(nbytes, 1)
+        views = [buf[i * nbytes:(i + 1) * nbytes] for i in range(min(copies, (1 << 30) // nbytes))]
+        us = _graph_us(lambda i: L.call("prism_probe_read", L.ptr(views[i]), nbytes, 256, L.ptr(sink), st()),
+                       len(views), 40)
+        out[f"read_{nbytes}_bytes_us"] = round(us, 2)
+        out[f"read_{nbytes}_bytes_gbs"] = round(nbytes / us / 1e3, 1)
+    del buf
+    torch.cuda.empty_cache()
+    return out
+
+
 def traffic_from_profiles():
     """HBM bytes per launch of the GEMM from the committed rocprofv3 --pmc summary, if present."""
     p = os.path.join(ROOT, "profiles", "w8a8_tile_prefill_traffic.json")
@@ -439,7 +518,12 @@ def main():
         return
     res, sample = bench_prefill(a.steps, a.warmup, dev)
     configs = None if a.no_sweep else bench_configs(dev)
-    cpu = None if a.no_cpu else cpu_baseline(sample, a.cpu_rows)
+    peaks = measure_peaks(dev)
+    cpu = None
+    if not a.no_cpu:
+        cpu = cpu_baseline(sample, a.cpu_rows)
+        cpu["reference_cpu_path"] = cpu_reference_path(sample)
+        cpu["os_cpu_count"] = os.cpu_count()
     achieved = res["ops"] / (res["gemm_ms"] * 1e-3) / 1e12
     line = {
         "metric": "W8A8/W4A8 GEMM TOPS and GB/s vs MI355X roofline, prefill M=8192 and decode M=1..64",
@@ -458,7 +542,10 @@ def main():
                    "M": M1, "K": K1, "N": N1, "gemm_ms": round(res["gemm_ms"], 4),
                    "quant_ms": round(res["quant_ms"], 4)},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": traffic_from_profiles()},
+                     "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": traffic_from_profiles(),
+                     "peak_measured": peaks["int8_tops"],
+                     "frac_of_measured": round(achieved / peaks["int8_tops"], 4)},
+        "peaks_measured": peaks,
         "cpu_baseline": cpu,
         "configs": dict(configs or {}, c1_reassoc=res["reassoc"]),
     }

@@ -325,6 +325,20 @@ PRISM_API int prism_mxfp4_gemm(const uint8_t* aq, const uint8_t* as, int a_fmt, 
                                void* out, int64_t ldo, const int32_t* n_rows, int64_t M, int64_t N, int64_t K,
                                int epi, int kernel, void* stream);
 
+/*
+ * Peak probes (measurement tooling: the reference's bench/csrc/mma_peak.cu:14-70 and bench/csrc/l2_bw.cu:8 for
+ * this GPU, no counterpart on the engine's path).  prism_probe_mfma launches `workgroups` workgroups of 4 waves,
+ * each wave issuing `iters` x 4 independent MFMAs of one kind on register operands: 0 int8
+ * (v_mfma_i32_32x32x32_i8), 1 fp8 e4m3 and 2 fp4 e2m1 (v_mfma_scale_f32_16x16x128_f8f6f4, unit scales), 3 bf16
+ * (v_mfma_f32_32x32x16_bf16); prism_probe_mfma_ops gives one instruction's operations (2 M N K).  prism_probe_read
+ * streams `bytes` of `buf` (16-byte aligned) with `workgroups` workgroups of 512 threads, each a contiguous slice, 8
+ * nontemporal 16-byte loads per lane in flight.  `sink` (device, >= workgroups elements) is written only on a value
+ * the probes never produce.
+ */
+PRISM_API int prism_probe_mfma(int kind, int64_t workgroups, int64_t iters, float* sink, void* stream);
+PRISM_API int64_t prism_probe_mfma_ops(int kind);
+PRISM_API int prism_probe_read(const void* buf, int64_t bytes, int64_t workgroups, uint32_t* sink, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

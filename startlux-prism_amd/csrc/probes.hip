@@ -1,0 +1,111 @@
+// Peak probes: the measured denominators of the rooflines bench.py reports beside MI355X's published peaks.
+//
+//   MFMA: every wave issues independent MFMAs on register operands (no memory traffic), CH accumulator chains per
+//         wave so an instruction never waits on the one before it; one kind per launch: int8
+//         (v_mfma_i32_32x32x32_i8, 65536 ops), fp8 and fp4 (v_mfma_scale_f32_16x16x128_f8f6f4 with unit e8m0 scales,
+//         65536 flops) and bf16 (v_mfma_f32_32x32x16_bf16, 32768 flops).  The same idea as the reference's
+//         bench/csrc/mma_peak.cu:14-70 (mma.sync chains per warp), written for CDNA4's MFMA.
+//   HBM:  each workgroup streams a contiguous slice of a buffer with 16-byte nontemporal loads, U per lane in flight
+//         (the reference's bench/csrc/l2_bw.cu:8 reader, at the sizes the decode GEMMs stream).
+// The results are folded into a sink the host never reads, so the compiler keeps the work.
+#include "common.h"
+
+namespace prism {
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
+constexpr int kChains = 4;
+
+template <int KIND>
+__global__ __launch_bounds__(256) void mfma_peak_kernel(int iters, float* __restrict__ sink) {
+    const int t = threadIdx.x;
+    float s = 0.f;
+    if (KIND == 0) {
+        const v4i a = {t, t * 3, t * 5, t * 7};
+        v16i c[kChains] = {};
+        for (int i = 0; i < iters; i++)
+#pragma unroll
+            for (int j = 0; j < kChains; j++) c[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, a, c[j], 0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < kChains; j++) s += (float)c[j][0];
+    } else if (KIND == 1 || KIND == 2) {
+        const v8i a = {0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x22222222, 0x22222222, 0x22222222,
+                       0x22222222};
+        v4f c[kChains] = {};
+        constexpr int fmt = KIND == 1 ? 0 : 4;            // e4m3 / e2m1 operands
+        for (int i = 0; i < iters; i++)
+#pragma unroll
+            for (int j = 0; j < kChains; j++)
+                c[j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, a, c[j], fmt, fmt, 0, 127, 0, 127);
+#pragma unroll
+        for (int j = 0; j < kChains; j++) s += c[j][0];
+    } else {
+        v8bf a;
+#pragma unroll
+        for (int e = 0; e < 8; e++) a[e] = (__bf16)(float)(t + e);
+        v16f c[kChains] = {};
+        for (int i = 0; i < iters; i++)
+#pragma unroll
+            for (int j = 0; j < kChains; j++) c[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, a, c[j], 0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < kChains; j++) s += c[j][0];
+    }
+    if (s == 1.2345f) sink[blockIdx.x] = s;
+}
+
+template <int U>
+__global__ __launch_bounds__(512) void read_probe_kernel(const v4u* __restrict__ p, int64_t per16,
+                                                         uint32_t* __restrict__ sink) {
+    const v4u* b = p + (int64_t)blockIdx.x * per16;
+    uint32_t acc = 0;
+    for (int64_t i = threadIdx.x; i < per16; i += 512 * U) {
+        v4u v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int64_t j = i + (int64_t)u * 512;
+            v[u] = j < per16 ? __builtin_nontemporal_load(b + j) : v4u{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) acc ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
+    }
+    if (acc == 0x9e3779b9u) sink[blockIdx.x] = acc;
+}
+
+}  // namespace prism
+
+using namespace prism;
+
+extern "C" int prism_probe_mfma(int kind, int64_t workgroups, int64_t iters, float* sink, void* stream) {
+    if (!sink || workgroups < 1 || workgroups > (1 << 20) || iters < 1 || iters > (1 << 24)) return PRISM_ERR_ARG;
+    hipStream_t st = (hipStream_t)stream;
+    const dim3 g((unsigned)workgroups), b(256);
+    switch (kind) {
+        case 0: hipLaunchKernelGGL(mfma_peak_kernel<0>, g, b, 0, st, (int)iters, sink); break;
+        case 1: hipLaunchKernelGGL(mfma_peak_kernel<1>, g, b, 0, st, (int)iters, sink); break;
+        case 2: hipLaunchKernelGGL(mfma_peak_kernel<2>, g, b, 0, st, (int)iters, sink); break;
+        case 3: hipLaunchKernelGGL(mfma_peak_kernel<3>, g, b, 0, st, (int)iters, sink); break;
+        default: return PRISM_ERR_ARG;
+    }
+    PRISM_LAUNCH_CHECK();
+    return PRISM_OK;
+}
+
+extern "C" int64_t prism_probe_mfma_ops(int kind) {
+    switch (kind) {
+        case 0: case 1: case 2: return 65536;
+        case 3: return 32768;
+        default: return 0;
+    }
+}
+
+extern "C" int prism_probe_read(const void* buf, int64_t bytes, int64_t workgroups, uint32_t* sink, void* stream) {
+    if (!buf || !sink || workgroups < 1 || workgroups > (1 << 20) || bytes < 16 * workgroups) return PRISM_ERR_ARG;
+    if (!PRISM_ALIGNED(buf, 16)) return PRISM_ERR_ALIGN;
+    const int64_t per16 = bytes / 16 / workgroups;
+    hipLaunchKernelGGL(read_probe_kernel<8>, dim3((unsigned)workgroups), dim3(512), 0, (hipStream_t)stream,
+                       reinterpret_cast<const v4u*>(buf), per16, sink);
+    PRISM_LAUNCH_CHECK();
+    return PRISM_OK;
+}

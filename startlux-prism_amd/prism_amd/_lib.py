@@ -44,6 +44,9 @@ _SIGS = {
     "prism_mxfp4_pack": (_int, [_p, _i64, _p, _p, _i64, _i64, _int, _p]),
     "prism_mxfp4_repack": (_int, [_p, _p, _p, _p, _i64, _i64, _p]),
     "prism_mxfp4_quant_act": (_int, [_p, _int, _i64, _p, _p, _p, _p, _i64, _i64, _int, _p]),
+    "prism_probe_mfma": (_int, [_int, _i64, _i64, _p, _p]),
+    "prism_probe_mfma_ops": (_i64, [_int]),
+    "prism_probe_read": (_int, [_p, _i64, _i64, _p, _p]),
     "prism_mxfp4_gemm": (_int, [_p, _p, _int, _p, _p, _p, _i64, _p, _i64, _i64, _i64, _int, _int, _p]),
 }
 
