@@ -256,7 +256,7 @@ def bench_mxfp4(dev, iters=40):
     return rows
 
 
-def bench_per_channel(dev, iters=40):
+def bench_per_channel(dev, iters=40, decode_only=False):
     """The engine's per-channel (gk = K) W8A8 projections (its production path): packed int8 weights
     (weight_from_q8(q8, K)), one activation scale per token; prefill at config 1's shape (against the int8 MFMA peak)
     and the decode sizes of config 2 (GB/s of the int8 weight bytes)."""
@@ -264,8 +264,9 @@ def bench_per_channel(dev, iters=40):
     from prism_amd import gguf_formats as GF
     from prism_amd import w8a8 as KW
     rows = []
-    for (M, K, N) in ((M1, K1, N1), (1, 5120, 5120), (16, 5120, 5120), (64, 5120, 5120), (1, 17408, 5120),
-                      (16, 17408, 5120), (64, 17408, 5120)):
+    shapes = ((M1, K1, N1), (1, 5120, 5120), (16, 5120, 5120), (64, 5120, 5120), (1, 17408, 5120),
+              (16, 17408, 5120), (64, 17408, 5120))
+    for (M, K, N) in shapes[1:] if decode_only else shapes:
         g = torch.Generator(device=dev)
         g.manual_seed(9)
         q8 = GF.quantize_q8_0(torch.randn(N, K, generator=g, device=dev) * 0.02)
@@ -372,17 +373,24 @@ def bench_producers(dev, iters=20):
     return rows
 
 
-def bench_configs(dev):
-    return {
-        "producers": bench_producers(dev),
-        "per_channel": bench_per_channel(dev),
-        "per_channel_deferred": bench_deferred(dev),
-        "c0": bench_q8_decode(dev, [(4096, 4096)], (16,)),
-        "c2": bench_q8_decode(dev, [(5120, 5120), (17408, 5120)], (1, 4, 16, 64)),
-        "c3": bench_w4a8(dev),
-        "c3_q6k": bench_w4a8(dev, kind="q6k"),
-        "c4": bench_mxfp4(dev),
-    }
+CONFIG_LINES = {
+    "producers": bench_producers,
+    "per_channel": bench_per_channel,
+    "per_channel_deferred": bench_deferred,
+    "c0": lambda dev: bench_q8_decode(dev, [(4096, 4096)], (16,)),
+    "c2": lambda dev: bench_q8_decode(dev, [(5120, 5120), (17408, 5120)], (1, 4, 16, 64)),
+    "c3": bench_w4a8,
+    "c3_q6k": lambda dev: bench_w4a8(dev, kind="q6k"),
+    "c4": bench_mxfp4,
+}
+# Lines that --only accepts besides the keys above: the per-channel decode sizes without the prefill.
+EXTRA_LINES = {"per_channel_decode": lambda dev: bench_per_channel(dev, decode_only=True)}
+
+
+def bench_configs(dev, only=None):
+    table = dict(CONFIG_LINES, **EXTRA_LINES) if only else CONFIG_LINES
+    names = only or list(CONFIG_LINES)
+    return {k: table[k](dev) for k in names}
 
 
 def cpu_baseline(sample, rows):
@@ -497,6 +505,10 @@ def main():
     ap.add_argument("--no-sweep", action="store_true", help="skip the per-config measurements")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=M1)
+    ap.add_argument("--only", default=None,
+                    help="comma-separated config lines (c0, c2, c3, c3_q6k, c4, per_channel, per_channel_decode, "
+                         "per_channel_deferred, producers): run just those and print them as one JSON line, "
+                         "without the headline (for profiling one kernel family)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 1 GiB device copy (3 times): the calibration kernel for rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE, whose true traffic is known")
@@ -505,6 +517,11 @@ def main():
         print("bench.py measures one GPU only: this build has no multi-GPU path (the hot path shards by output "
               "columns with no exchange; see the sharding notes).  Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
+    if a.only:
+        unknown = [k for k in a.only.split(",") if k not in CONFIG_LINES and k not in EXTRA_LINES]
+        if unknown:
+            raise SystemExit(f"bench.py: unknown --only line(s) {unknown}; known: "
+                             f"{sorted(list(CONFIG_LINES) + list(EXTRA_LINES))}")
     import torch
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -515,6 +532,9 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes_read": src.numel() * 4, "copy_bytes_written": dst.numel() * 4}))
+        return
+    if a.only:
+        print(json.dumps({"configs": bench_configs(dev, a.only.split(","))}), flush=True)
         return
     res, sample = bench_prefill(a.steps, a.warmup, dev)
     configs = None if a.no_sweep else bench_configs(dev)

@@ -400,12 +400,18 @@ __global__ __launch_bounds__(256, 2) void w8a8_packed_tile_kernel(const int8_t* 
 
 // ---------------------------------------------------------------------------------------------- mid
 // From 17 rows (and for narrow projections at any row count, where the tile kernel's 128 x 128 tiles leave most CUs
-// idle): one wave (one workgroup) per (16 activation rows, 16-row weight tile), walking every block pair in order; the
-// m-tiles of one weight tile are grid rows blockIdx.y of the same XCD, so their weight chunks come from HBM once.  Per pair a lane
-// loads its weight chunk slot (16 bytes), the two 8-byte activation pieces of its row and the block scales of its 4
-// output rows, PD pairs ahead; each block's int32 sums come from one v_mfma_i32_16x16x32_i8 with a zero accumulator
-// and the lane folds RN(RN(float(P) sa) sw) into its 4 outputs in block order, in registers.
-template <int PD, int EPI>
+// idle): one wave (one workgroup) per (MT x 16 activation rows, 16-row weight tile), walking every block pair in
+// order; the m-tiles of one weight tile are grid rows blockIdx.y of the same XCD, so their weight chunks come from
+// HBM once.  The activations are the MFMA's A operand, so lane (i, q) = (lane % 16, lane / 16) ends with the sums of
+// activation rows 4q..4q+3 of each m-tile against weight row i: its weight scales are one 4-byte word per pair (both
+// blocks of row i) and its activation scales four constants per m-tile.  Per pair a lane loads its weight chunk slot
+// as it lies (16 bytes), one 16-byte piece of its activation row per m-tile and that word, PD pairs ahead.  The piece
+// is bytes 16 s(q)..+15 of the pair with s = (0, 2, 1, 3), and one v_permlane16_swap_b32 per dword pair turns the four
+// lanes' pieces into the operand layout of the weight chunk (lane q: bytes 8q..8q+7 of each block).  Loading the
+// activation rows in 64-byte runs instead of eight-byte pieces halved this kernel's time.  Each block's int32 sums
+// come from one v_mfma_i32_16x16x32_i8 with a zero accumulator and the lane folds RN(RN(float(P) sa) sw) into its
+// outputs in block order, in registers.
+template <int PD, int MT, int EPI>
 __global__ __launch_bounds__(64) void w8a8_packed_mid_kernel(const int8_t* __restrict__ a,
                                                               const float* __restrict__ a_s, int64_t as_sm,
                                                               const int8_t* __restrict__ qt,
@@ -413,62 +419,75 @@ __global__ __launch_bounds__(64) void w8a8_packed_mid_kernel(const int8_t* __res
                                                               void* __restrict__ out, int64_t ldo,
                                                               const int32_t* __restrict__ n_rows, int M, int N,
                                                               int K) {
-    const int lane = threadIdx.x & 63, mt = blockIdx.y;
+    const int lane = threadIdx.x & 63, m0 = blockIdx.y * MT * 16;
     const int nt = blockIdx.x;
     const int live = min(M, __ldg(n_rows));
-    if (mt * 16 >= live) return;
+    if (m0 >= live) return;
     const int KP = K / 64;
-    const int lm = lane & 15, q = lane >> 4;
-    const int m = min(mt * 16 + lm, M - 1);
-    const float sa = a_s[(int64_t)m * as_sm];
+    const int li = lane & 15, q = lane >> 4;
+    float sa[MT][4];
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) sa[t][e] = a_s[(int64_t)min(m0 + 16 * t + 4 * q + e, M - 1) * as_sm];
     const v4i* cw = reinterpret_cast<const v4i*>(qt) + (int64_t)nt * KP * 64 + lane;
-    const v4u* cs = reinterpret_cast<const v4u*>(dt) + (int64_t)nt * KP * 4 + q;
-    const int8_t* xa = a + (int64_t)m * K + 8 * q;
+    const uint32_t* cs = reinterpret_cast<const uint32_t*>(dt) + (int64_t)nt * KP * 16 + li;
+    const int sq = ((q & 1) << 1) | (q >> 1);
+    const int8_t* xa[MT];
+#pragma unroll
+    for (int t = 0; t < MT; t++) xa[t] = a + (int64_t)min(m0 + 16 * t + li, M - 1) * K + 16 * sq;
 
     struct Pair {
         v4i w;
-        v4u s;
-        v2u x0, x1;
+        v4u x[MT];
+        uint32_t s;
     };
     auto load = [&](int j, Pair& p) {
         const int jj = min(j, KP - 1);
         p.w = cw[(int64_t)jj * 64];
-        p.s = cs[(int64_t)jj * 4];
-        p.x0 = *reinterpret_cast<const v2u*>(xa + 64 * jj);
-        p.x1 = *reinterpret_cast<const v2u*>(xa + 64 * jj + 32);
-    };
-    float y[4] = {0.f, 0.f, 0.f, 0.f};
-    const v4i zero = {0, 0, 0, 0};
-    // the int32 sums of a pair's two blocks (one MFMA each, zero accumulator)
-    auto sums = [&](const Pair& p, v4i* acc) {
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const int64_t wf = h ? ((int64_t)(uint32_t)p.w[2] | ((int64_t)p.w[3] << 32))
-                                 : ((int64_t)(uint32_t)p.w[0] | ((int64_t)p.w[1] << 32));
-            const v2u xv = h ? p.x1 : p.x0;
-            const int64_t xf = (int64_t)xv[0] | ((int64_t)xv[1] << 32);
-            acc[h] = __builtin_amdgcn_mfma_i32_16x16x32_i8(wf, xf, zero, 0, 0, 0);
+        for (int t = 0; t < MT; t++) p.x[t] = *reinterpret_cast<const v4u*>(xa[t] + 64 * jj);
+        p.s = cs[(int64_t)jj * 16];
+    };
+    float y[MT][4] = {};
+    const v4i zero = {0, 0, 0, 0};
+    // the int32 sums of a pair's two blocks (one MFMA each per m-tile, zero accumulator)
+    auto sums = [&](const Pair& p, v4i (*acc)[2]) {
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+            // lane q holds 8-byte units (u(2s), u(2s+1)) of the pair; after the swap it holds (u(q), u(4 + q)):
+            // block 0's bytes 8q..8q+7 and block 1's
+            const auto lo = __builtin_amdgcn_permlane16_swap(p.x[t][0], p.x[t][2], false, false);
+            const auto hi = __builtin_amdgcn_permlane16_swap(p.x[t][1], p.x[t][3], false, false);
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const int64_t wf = h ? ((int64_t)(uint32_t)p.w[2] | ((int64_t)p.w[3] << 32))
+                                     : ((int64_t)(uint32_t)p.w[0] | ((int64_t)p.w[1] << 32));
+                const int64_t xf = (int64_t)(uint32_t)lo[h] | ((int64_t)hi[h] << 32);
+                acc[t][h] = __builtin_amdgcn_mfma_i32_16x16x32_i8(xf, wf, zero, 0, 0, 0);
+            }
         }
     };
-    // fold the pair's terms into the 4 outputs, block 2j before 2j + 1
-    auto fold = [&](const v4i* acc, const Pair& p) {
+    // fold the pair's terms into the outputs, block 2j before 2j + 1
+    auto fold = [&](v4i (*acc)[2], const Pair& p) {
 #pragma unroll
         for (int h = 0; h < 2; h++)
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                // scales of this lane's row 4 q + e: chunk row-major over (row, block of the pair), block h in half h
-                const float x = mul_rn((float)acc[h][e], sa);
-                y[e] = add_rn(y[e], h ? mul_f16_rn<1>(x, p.s[e]) : mul_f16_rn<0>(x, p.s[e]));
-            }
+            for (int t = 0; t < MT; t++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float x = mul_rn((float)acc[t][h][e], sa[t][e]);
+                    y[t][e] = add_rn(y[t][e], h ? mul_f16_rn<1>(x, p.s) : mul_f16_rn<0>(x, p.s));
+                }
     };
     Pair ring[PD];
 #pragma unroll
     for (int d = 0; d < PD; d++) load(d, ring[d]);
-    // branch-free body, so the compiler's wait counts let the later pairs stay in flight; pairs go two at a time (four
+    // branch-free body, so the compiler's wait counts let the later pairs stay in flight; pairs go two at a time (their
     // MFMAs, then the two folds in order), so the VALU fold of one waits on MFMAs issued before the other's
     static_assert(PD % 2 == 0, "pairs are taken two at a time");
     const int full = KP / PD * PD;
-    v4i acc0[2], acc1[2];
+    v4i acc0[MT][2], acc1[MT][2];
     for (int j0 = 0; j0 < full; j0 += PD) {
 #pragma unroll
         for (int d = 0; d < PD; d += 2) {
@@ -478,6 +497,8 @@ __global__ __launch_bounds__(64) void w8a8_packed_mid_kernel(const int8_t* __res
             fold(acc1, ring[d + 1]);
             load(j0 + d + PD, ring[d]);          // past the end: the last pair again (a cache hit)
             load(j0 + d + 1 + PD, ring[d + 1]);
+            // keep each step's work in place: hoisted across steps, the MFMAs would wait for the whole ring
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
 #pragma unroll
@@ -486,19 +507,21 @@ __global__ __launch_bounds__(64) void w8a8_packed_mid_kernel(const int8_t* __res
             sums(ring[d], acc0);
             fold(acc0, ring[d]);
         }
-    const int row = mt * 16 + lm;
-    if (row < live) {
+    const int n = 16 * nt + li;
+#pragma unroll
+    for (int t = 0; t < MT; t++)
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            const int n = 16 * nt + 4 * q + e;
-            if (EPI == 0) {
-                reinterpret_cast<uint16_t*>(out)[(int64_t)row * ldo + n] = (uint16_t)f32_to_bf16(y[e]);
-            } else {
-                float* o = reinterpret_cast<float*>(out) + (int64_t)row * ldo + n;
-                *o = add_rn(*o, y[e]);
+            const int row = m0 + 16 * t + 4 * q + e;
+            if (row < live) {
+                if (EPI == 0) {
+                    reinterpret_cast<uint16_t*>(out)[(int64_t)row * ldo + n] = (uint16_t)f32_to_bf16(y[t][e]);
+                } else {
+                    float* o = reinterpret_cast<float*>(out) + (int64_t)row * ldo + n;
+                    *o = add_rn(*o, y[t][e]);
+                }
             }
         }
-    }
 }
 
 static size_t packed_decode_lds(int R, int M) {
@@ -529,9 +552,14 @@ static void launch_packed(int kernel, const int8_t* a, const float* a_s, int64_t
 #undef PDEC
     }
     if (kernel == 2) {
-        const int mt = (M + 15) / 16;
-        hipLaunchKernelGGL((w8a8_packed_mid_kernel<8, EPI>), dim3(N / 16, mt), dim3(64), 0, st, a, a_s, as_sm,
-                           qt, dt, out, ldo, n_rows, M, N, K);
+        // from 33 rows each wave takes two m-tiles: the shared weight loads and the doubled independent work per pair
+        // outweigh the halved wave count (M = 64, 5120 x 17408: 58 us against 60-65 us)
+        if (M > 32)
+            hipLaunchKernelGGL((w8a8_packed_mid_kernel<6, 2, EPI>), dim3(N / 16, (M + 31) / 32), dim3(64), 0, st,
+                               a, a_s, as_sm, qt, dt, out, ldo, n_rows, M, N, K);
+        else
+            hipLaunchKernelGGL((w8a8_packed_mid_kernel<8, 1, EPI>), dim3(N / 16, (M + 15) / 16), dim3(64), 0, st,
+                               a, a_s, as_sm, qt, dt, out, ldo, n_rows, M, N, K);
     } else if (kernel == 0 || kernel == 3) {
         const int tiles_m = (M + PBM - 1) / PBM, tiles_n = (N + PBN - 1) / PBN;
         if (kernel == 0)

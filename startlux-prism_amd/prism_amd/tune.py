@@ -96,7 +96,8 @@ def tune_w8(kind, shapes, Ms, dev, log):
             out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
             n = torch.tensor([M], dtype=torch.int32, device=dev)
             if kind == "q8":
-                cands = ["decode", "mid", "tile"] if M <= 64 else ["mid", "tile"]
+                # "decode" hands 17..64 rows to the "mid" kernel, so it is a candidate up to 16 rows only
+                cands = ["decode", "stream", "mid", "tile"] if M <= 16 else ["mid", "tile"]
             else:
                 cands = ["decode", "tile"]
             best, us = _pick(cands, lambda c: (lambda i: KW.gemm(a, s, ws[i], None, out, n, gk, kernel=c)),

@@ -159,8 +159,6 @@ def _tabled(kernel, N, K, M, gk, packed_q8=False):
     if kernel != "auto":
         return kernel
     c = dispatch.w8a8_kernel(N, K, M, gk)
-    if packed_q8 and c == "decode" and 5 <= M <= 16:
-        return "auto"               # the library's rule: the balanced "stream" kernel at 5..16 rows
     ok = c == "tile" or (c == "decode" and (M <= 64 or gk == K)) or (c == "mid" and gk == 32) or \
         (c == "stream" and packed_q8 and 1 <= M <= 16)
     return c if ok else "auto"
@@ -188,6 +186,7 @@ def workspace(dev):
 
 def _gemm_packed(a, a_s, w, out, n_rows, gk, epi, kernel):
     M, K = a.shape
+    asked = kernel
     kernel = _tabled(kernel, w.n, K, M, gk, packed_q8=True)
     if gk != 32 or (w.n, w.k) != (w.n, K) or w.k != K:
         raise ValueError("packed Q8_0 weights: gk must be 32 and K must match")
@@ -199,6 +198,8 @@ def _gemm_packed(a, a_s, w, out, n_rows, gk, epi, kernel):
     if out.dtype != want or out.shape[0] < M or out.shape[1] < w.n or out.stride(1) != 1:
         raise ValueError(f"out must be {want} [>= {M}, >= {w.n}] with unit column stride")
     ws = workspace(a.device) if M <= 16 and kernel in ("auto", "decode", "stream") else None
+    if kernel == "stream" and ws is None and asked == "auto":
+        kernel = "auto"             # the table's pick needs the workspace; the library then picks without it
     if kernel == "stream" and ws is None:
         raise L.PrismError('kernel "stream" needs the device workspace, made outside graph capture: run one eager '
                            'call first')
