@@ -49,7 +49,8 @@ def test_off(tables, monkeypatch):
     assert dispatch.w4a8_kernel("q4k", 13824, 5120, 1) == "auto"
 
 
-LIMITS = {"gemm_table": {"decode": 1 << 20, "tile": 1 << 30}, "q8_table": {"decode": 64, "mid": 1 << 20, "tile": 1 << 30},
+LIMITS = {"gemm_table": {"decode": 1 << 20, "tile": 1 << 30}, "q8_table": {"decode": 64, "stream": 16, "mid": 1 << 20,
+                                                                                   "tile": 1 << 30},
           "w4a8_table": {"decode": 16, "stream": 16, "tile": 1 << 30}}
 
 
@@ -66,4 +67,5 @@ def test_committed_tables_well_formed(path):
             assert len(parts) == 2 and int(parts[0]) % 16 == 0
         for m, choice in row.items():
             assert choice[0] in LIMITS[prefix] and int(m) <= LIMITS[prefix][choice[0]], (key, m, choice)
-            assert choice[0] != "stream" or parts[0] == "q6k", (key, m, choice)       # Q6_K's kernel only
+            # W4A8: the stream kernel is Q6_K's only
+            assert prefix != "w4a8_table" or choice[0] != "stream" or parts[0] == "q6k", (key, m, choice)
