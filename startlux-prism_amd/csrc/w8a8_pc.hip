@@ -172,20 +172,20 @@ __global__ __launch_bounds__(64 * NWV, TM == 128 ? 2 : 1) void w8a8_pc_tile_kern
 // ---------------------------------------------------------------------------------------------- decode
 // Rows r0 .. r0 + 16 MT - 1 with r0 = 16 MT blockIdx.y (grid rows cover M beyond 64: for narrow projections, whose
 // few 128 x 256 tiles leave the tile kernel's CUs idle, the weight tiles then come from L2 / MALL once per 64 rows).
-// One workgroup per G 16-row weight tiles; wave w takes the 64-input chunks w, w + NW, ... of every
-// tile (the int32 sums are exact in any order), PD chunks in flight in registers.  Per chunk a lane loads 16 bytes
-// of each tile's weights (row l % 16, inputs 16 q .. + 15: packed, the chunk's lane slot, 1 KB per wave
+// One workgroup per G 16-row weight tiles; wave w takes the 64-input chunks w, w + NW, ... of every tile (the int32
+// sums are exact in any order), PD = 4 chunks in flight in registers (at most 8 waves, so up to 256 VGPRs).  Per
+// chunk a lane loads 16 bytes of each tile's weights (row l % 16, inputs 16 q .. + 15: packed, the chunk's lane slot, 1 KB per wave
 // instruction) and the same 16 inputs of its activation row per m-tile, reused across the G tiles; one
 // v_mfma_i32_16x16x64_i8 per (tile, m-tile) accumulates into int32.  The waves' sums meet in LDS, and the epilogue
 // applies the two roundings.
 template <int G, int MT, bool WPACK, bool WS16, int EPI>
-__global__ __launch_bounds__(1024) void w8a8_pc_decode_kernel(const int8_t* __restrict__ a,
+__global__ __launch_bounds__(512) void w8a8_pc_decode_kernel(const int8_t* __restrict__ a,
                                                               const float* __restrict__ a_s, int64_t as_sm,
                                                               const int8_t* __restrict__ w,
                                                               const void* __restrict__ w_s, void* __restrict__ out,
                                                               int64_t ldo, const int32_t* __restrict__ n_rows, int M,
                                                               int N, int K, int64_t zstride) {
-    constexpr int PD = MT <= 2 ? 4 : 2;
+    constexpr int PD = 4;
     extern __shared__ __attribute__((aligned(16))) v4i red[];          // [NW][G][MT][64]
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, NW = blockDim.x >> 6;
     const int nt0 = blockIdx.x * G, r0 = 16 * MT * blockIdx.y;
@@ -242,6 +242,8 @@ __global__ __launch_bounds__(1024) void w8a8_pc_decode_kernel(const int8_t* __re
         for (int d = 0; d < PD; d++) {
             mma(ring[d]);
             load(wv + NW * (i0 + d + PD), ring[d]);
+            // keep each chunk's MFMAs in place: hoisted across chunks, they would wait for the whole ring
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
 #pragma unroll
@@ -298,7 +300,7 @@ int launch_w8a8_pc(int kernel, bool wpack, const int8_t* a, const float* a_s, in
         const int MT = min(4, (M + 15) / 16);
         const int G = (N % 32 == 0) ? 2 : 1;
         const int KP = K / 64 / split;
-        int nw = min(8, max(1, KP / 4));               // 8 waves: 64 KB in flight per workgroup (16 measured slower)
+        int nw = min(8, max(1, KP / 4));  // 8 waves (the launch bound), 4 chunks each in flight (16 waves measured slower)
         const size_t lds = (size_t)nw * G * MT * 64 * sizeof(v4i);
         dim3 grid((unsigned)(N / (16 * G)), (unsigned)((M + 16 * MT - 1) / (16 * MT)), (unsigned)split);
 #define PDL(GV, MTV, WP, W16, E)                                                                                   \
