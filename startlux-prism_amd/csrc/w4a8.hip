@@ -718,30 +718,33 @@ __global__ __launch_bounds__(256, 2) void w4a8_tile_kernel(const int8_t* __restr
 }
 
 // ---------------------------------------------------------------------------------------------- Q6_K prefill tile
-// 64 (n) x 64 (m) output tile per 256-thread workgroup: wave wv owns weight row tile wv (16 rows) and all 64
-// activation rows (4 MFMA tiles of 16 x 16).  Staging as the Q4_K tile kernel: per stage (one super-block) the 4 row
-// tiles' 4 KB of weights and the 64 activation rows by LDS-DMA into the free buffer, the scales through registers.
-// Per 32-input window two MFMAs: P over both of its sub-blocks and Pl over the first (lanes q >= 2, which hold the
-// second, give zeros): acc += sc1 P + (sc0 - sc1) Pl, exact.
 constexpr int Q6BN = 64;
 
+// The Q6_K prefill tile on v_mfma_i32_32x32x16_i8, whose 16 inputs are one Q6_K sub-block: no masked second MFMA.
+// 64 (m) x 64 (n) per 256-thread workgroup; wave wv owns the 32 x 32 block (m rows 32 (wv & 1) .., n rows
+// 32 (wv >> 1) ..).  A stage is half a super-block (8 sub-blocks): the 4 row tiles' 2 KB of packed weights and the 64
+// activation rows' 128 bytes by LDS-DMA, double-buffered, 33 KB of LDS per workgroup so that four fit a CU (four
+// waves per SIMD hide the MFMA-to-VALU chain).  The activations are the A operand and the weights the B operand, so
+// lane l's 16 sums are all of weight row n = l % 32 (activation rows 8 i + 4 (l / 32) + e, e < 4): its sub-block scale
+// is one int per sub-block, and acc += sc_h P_h is one v_mad_i32_i24 per sum and sub-block (exact: |P_h| < 2^16).
+// The B operand of sub-block h is gathered from the packed chunks: lane l's 8 bytes are inputs 16 h + 8 (l / 32) ..
+// + 7 of row n, which the pack keeps in chunk h / 4, lane slot 16 (2 (h & 1) + l / 32) + n % 16, half (h / 2) & 1.
+// The super-block's d, scales and activation scales come through registers into LDS once per super-block.
 template <int EPI>
-__global__ __launch_bounds__(256, 2) void w4a8_q6k_tile_kernel(const int8_t* __restrict__ xq,
-                                                               const float* __restrict__ a, int64_t a_sb,
-                                                               const uint8_t* __restrict__ qv,
-                                                               const uint8_t* __restrict__ meta,
-                                                               void* __restrict__ out, int64_t ldo,
-                                                               const int32_t* __restrict__ n_rows, int M, int N,
-                                                               int K, int tiles_m, int tiles_n) {
-    __shared__ __attribute__((aligned(16))) uint8_t Bs[2][4 * 4096];   // 4 row tiles x (4 chunks x 64 lanes x 16 B)
-    __shared__ __attribute__((aligned(16))) int8_t As[2][QBM * 256];   // swizzled activation rows
-    __shared__ __attribute__((aligned(16))) int sca[2][8][Q6BN];       // per window: second scale
-    __shared__ __attribute__((aligned(16))) int scb[2][8][Q6BN];       // per window: first scale - second
+__global__ __launch_bounds__(256, 4) void w4a8_q6k_tile32_kernel(const int8_t* __restrict__ xq,
+                                                                 const float* __restrict__ a, int64_t a_sb,
+                                                                 const uint8_t* __restrict__ qv,
+                                                                 const uint8_t* __restrict__ meta,
+                                                                 void* __restrict__ out, int64_t ldo,
+                                                                 const int32_t* __restrict__ n_rows, int M, int N,
+                                                                 int K, int tiles_m, int tiles_n) {
+    __shared__ __attribute__((aligned(16))) uint8_t Bs[2][4 * 2048];   // 4 row tiles x (2 chunks x 64 lanes x 16 B)
+    __shared__ __attribute__((aligned(16))) int8_t As[2][QBM * 128];   // activation rows, 8 swizzled granules each
+    __shared__ __attribute__((aligned(16))) v4u scs[2][Q6BN];          // per weight row: its 16 int8 scales
     __shared__ __attribute__((aligned(16))) float dl[2][Q6BN];
-    __shared__ float al[2][QBM];
+    __shared__ __attribute__((aligned(16))) float al[2][QBM];
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int lm = lane & 15, q = lane >> 4;
     int pm, pn;
     {
         const int total = tiles_m * tiles_n;
@@ -754,23 +757,26 @@ __global__ __launch_bounds__(256, 2) void w4a8_q6k_tile_kernel(const int8_t* __r
     const int m0 = pm * QBM, n0 = pn * Q6BN;
     const int live = min(M, __ldg(n_rows));
     if (m0 >= live) return;
-    const int NB = K / 256, ntiles = N / 16;
+    const int NB = K / 256, ntiles = N / 16, NS = 2 * NB;
 
-    const uint8_t* wsrc[4];
-    const int8_t* xsrc[4];
+    // stage s = (super-block s / 2, half s % 2): thread c = tid + 256 i (i < 2) copies weight tile c / 128's
+    // 16 bytes (c % 128) of the half's 2 KB, and activation row c / 8's granule (c % 8) ^ (row % 8)
+    const uint8_t* wsrc[2];
+    const int8_t* xsrc[2];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
+    for (int i = 0; i < 2; i++) {
         const int c = tid + 256 * i;
-        wsrc[i] = qv + ((int64_t)min(n0 / 16 + (c >> 8), ntiles - 1) * NB * 256 + (c & 255)) * 16;
-        const int r = c >> 4;
-        xsrc[i] = xq + (int64_t)min(m0 + r, M - 1) * K + (((c & 15) ^ (r & 15)) * 16);
+        wsrc[i] = qv + ((int64_t)min(n0 / 16 + (c >> 7), ntiles - 1) * NB * 256 + (c & 127)) * 16;
+        const int r = c >> 3;
+        xsrc[i] = xq + (int64_t)min(m0 + r, M - 1) * K + (((c & 7) ^ (r & 7)) * 16);
     }
-    auto dma = [&](int b, int buf) {
+    auto dma = [&](int st, int buf) {
+        const int64_t wo = (int64_t)(st >> 1) * 4096 + (st & 1) * 2048, xo = (int64_t)st * 128;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
+        for (int i = 0; i < 2; i++) {
             const int base = (256 * i + 64 * wv) * 16;
-            dma16(wsrc[i] + (int64_t)b * 4096, &Bs[buf][base]);
-            dma16(xsrc[i] + (int64_t)b * 256, &As[buf][base]);
+            dma16(wsrc[i] + wo, &Bs[buf][base]);
+            dma16(xsrc[i] + xo, &As[buf][base]);
         }
     };
     // threads < 64: weight row tid's scales and d, activation row tid's scale
@@ -789,91 +795,83 @@ __global__ __launch_bounds__(256, 2) void w4a8_q6k_tile_kernel(const int8_t* __r
     };
     auto smeta = [&](int buf) {
         if (tid < 64) {
-#pragma unroll
-            for (int w = 0; w < 8; w++) {
-                const int s0 = sbyte(rm, 2 * w), s1 = sbyte(rm, 2 * w + 1);
-                sca[buf][w][tid] = s1;
-                scb[buf][w][tid] = s0 - s1;
-            }
+            scs[buf][tid] = rm;
             dl[buf][tid] = f16_to_f32(rd);
             al[buf][tid] = ra;
         }
     };
 
-    float y[4][4];
+    const int mb = wv & 1, nbk = wv >> 1;
+    const int col = lane & 31, kh = lane >> 5;
+    const int nr = 32 * nbk + col;                                     // this lane's weight row in the tile
+    const int mr = 32 * mb + col;                                      // this lane's A-operand activation row
+    const int bofs = (nr >> 4) * 2048 + (16 * kh + (nr & 15)) * 16;    // + chunk, slot pair and half per sub-block
+    const int aofs = mr * 128 + 8 * kh;
+
+    float y[16];
 #pragma unroll
-    for (int j = 0; j < 4; j++)
-#pragma unroll
-        for (int e = 0; e < 4; e++) y[j][e] = 0.f;
+    for (int e = 0; e < 16; e++) y[e] = 0.f;
+    v16i acc;
 
     gmeta(0);
     dma(0, 0);
     smeta(0);
     vm_wait<0>();
     lds_barrier();
-    for (int b = 0; b < NB; b++) {
-        const int cb = b & 1;
-        if (b + 1 < NB) {
-            gmeta(b + 1);
-            dma(b + 1, cb ^ 1);
+    for (int st = 0; st < NS; st++) {
+        const int cb = st & 1, b = st >> 1, mbuf = b & 1;
+        if (st + 1 < NS) dma(st + 1, cb ^ 1);
+        if (cb == 1 && b + 1 < NB) gmeta(b + 1);
+        if (cb == 0) {
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[e] = 0;
         }
-        v4i acc[4];
+        const v4u scv = scs[mbuf][nr];
+        const uint32_t sw0 = cb ? scv[2] : scv[0], sw1 = cb ? scv[3] : scv[1];   // this half's 8 scales
+        const uint8_t* bp = &Bs[cb][bofs];
+        const int8_t* ap = &As[cb][aofs];
+        const v16i zero = {};
 #pragma unroll
-        for (int j = 0; j < 4; j++) acc[j] = v4i{0, 0, 0, 0};
-        const v4i zero = {0, 0, 0, 0};
-#pragma unroll 1
-        for (int jj = 0; jj < 4; jj++) {
-            const v4u wq = *reinterpret_cast<const v4u*>(&Bs[cb][wv * 4096 + jj * 1024 + lane * 16]);
+        for (int h = 0; h < 8; h++) {
+            // local sub-block h: chunk h / 4 of the half, lane slot pair h & 1, half (h / 2) & 1
+            const int64_t bf = *reinterpret_cast<const int64_t*>(bp + (h >> 2) * 1024 + (h & 1) * 512 +
+                                                                 ((h >> 1) & 1) * 8);
+            const int64_t af = *reinterpret_cast<const int64_t*>(ap + ((h ^ (mr & 7)) * 16));
+            const v16i P = __builtin_amdgcn_mfma_i32_32x32x16_i8(af, bf, zero, 0, 0, 0);
+            const int sc = (int)(int8_t)((h < 4 ? sw0 : sw1) >> (8 * (h & 3)));
 #pragma unroll
-            for (int u = 0; u < 2; u++) {
-                const int wn = 2 * jj + u;
-                const int64_t wf = (int64_t)wq[2 * u] | ((int64_t)wq[2 * u + 1] << 32);
-                const v4i A = *reinterpret_cast<const v4i*>(&sca[cb][wn][16 * wv + 4 * q]);
-                const v4i B = *reinterpret_cast<const v4i*>(&scb[cb][wn][16 * wv + 4 * q]);
+            for (int e = 0; e < 16; e++) acc[e] += __mul24(sc, P[e]);
+        }
+        if (cb == 1) {
+            const float d = dl[mbuf][nr];
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const int8_t* ap = &As[cb][(16 * j + lm) * 256 + (((2 * wn + (q >> 1)) ^ lm) * 16) + 8 * (q & 1)];
-                    const int64_t af = *reinterpret_cast<const int64_t*>(ap);
-                    const v4i P = __builtin_amdgcn_mfma_i32_16x16x32_i8(wf, af, zero, 0, 0, 0);
-                    const v4i Pl = __builtin_amdgcn_mfma_i32_16x16x32_i8(wf, q < 2 ? af : 0, zero, 0, 0, 0);
+            for (int i = 0; i < 4; i++) {
+                const v4f am = *reinterpret_cast<const v4f*>(&al[mbuf][32 * mb + 8 * i + 4 * kh]);
 #pragma unroll
-                    for (int e = 0; e < 4; e++) acc[j][e] += __mul24(A[e], P[e]) + __mul24(B[e], Pl[e]);
-                }
+                for (int e = 0; e < 4; e++) y[4 * i + e] = fmaf(am[e], mul_rn(d, (float)acc[4 * i + e]), y[4 * i + e]);
             }
+            if (b + 1 < NB) smeta(mbuf ^ 1);
         }
-        const v4f d = *reinterpret_cast<const v4f*>(&dl[cb][16 * wv + 4 * q]);
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const float am = al[cb][16 * j + lm];
-#pragma unroll
-            for (int e = 0; e < 4; e++) y[j][e] = fmaf(am, mul_rn(d[e], (float)acc[j][e]), y[j][e]);
-        }
-        if (b + 1 < NB) smeta(cb ^ 1);
         vm_wait<0>();
         lds_barrier();
     }
-    // D element (j, e): n = n0 + 16 wv + 4 q + e, m = m0 + 16 j + lm
+    // register 4 i + e: m = m0 + 32 mb + 8 i + 4 kh + e, n = n0 + nr
+    const int n = n0 + nr;
+    if (n < N) {
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int m = m0 + 16 * j + lm;
-        const int nb = n0 + 16 * wv + 4 * q;
-        if (m < live && nb < N) {
-            if (EPI == 0) {
-                const uint32_t lo = f32_to_bf16(y[j][0]) | (f32_to_bf16(y[j][1]) << 16);
-                const uint32_t hi = f32_to_bf16(y[j][2]) | (f32_to_bf16(y[j][3]) << 16);
-                uint16_t* o = reinterpret_cast<uint16_t*>(out) + (int64_t)m * ldo + nb;
-                if ((((uintptr_t)o) & 7) == 0) {
-                    *reinterpret_cast<v2u*>(o) = v2u{lo, hi};
-                } else {
+        for (int i = 0; i < 4; i++)
 #pragma unroll
-                    for (int e = 0; e < 4; e++) o[e] = (uint16_t)f32_to_bf16(y[j][e]);
+            for (int e = 0; e < 4; e++) {
+                const int m = m0 + 32 * mb + 8 * i + 4 * kh + e;
+                if (m < live) {
+                    if (EPI == 0) {
+                        reinterpret_cast<uint16_t*>(out)[(int64_t)m * ldo + n] = (uint16_t)f32_to_bf16(y[4 * i + e]);
+                    } else {
+                        float* o = reinterpret_cast<float*>(out) + (int64_t)m * ldo + n;
+                        *o = add_rn(*o, y[4 * i + e]);
+                    }
                 }
-            } else {
-                float* o = reinterpret_cast<float*>(out) + (int64_t)m * ldo + nb;
-#pragma unroll
-                for (int e = 0; e < 4; e++) o[e] = add_rn(o[e], y[j][e]);
             }
-        }
     }
 }
 
@@ -999,11 +997,11 @@ extern "C" int prism_w4a8_q6k_gemm(const int8_t* xq, const float* a, int64_t a_s
     } else {
         const int tiles_m = (Mi + QBM - 1) / QBM, tiles_n = (Ni + Q6BN - 1) / Q6BN;
         if (epi == 0)
-            hipLaunchKernelGGL((w4a8_q6k_tile_kernel<0>), dim3(tiles_m * tiles_n), dim3(256), 0, st, xq, a, a_sb, qv,
-                               meta, out, ldo, n_rows, Mi, Ni, Ki, tiles_m, tiles_n);
+            hipLaunchKernelGGL((w4a8_q6k_tile32_kernel<0>), dim3(tiles_m * tiles_n), dim3(256), 0, st, xq, a, a_sb,
+                               qv, meta, out, ldo, n_rows, Mi, Ni, Ki, tiles_m, tiles_n);
         else
-            hipLaunchKernelGGL((w4a8_q6k_tile_kernel<1>), dim3(tiles_m * tiles_n), dim3(256), 0, st, xq, a, a_sb, qv,
-                               meta, out, ldo, n_rows, Mi, Ni, Ki, tiles_m, tiles_n);
+            hipLaunchKernelGGL((w4a8_q6k_tile32_kernel<1>), dim3(tiles_m * tiles_n), dim3(256), 0, st, xq, a, a_sb,
+                               qv, meta, out, ldo, n_rows, Mi, Ni, Ki, tiles_m, tiles_n);
     }
     PRISM_LAUNCH_CHECK();
     return PRISM_OK;
