@@ -289,6 +289,35 @@ def bench_per_channel(dev, iters=40, decode_only=False):
     return rows
 
 
+def bench_per_channel_plain(dev, iters=40):
+    """The per-channel GEMM on plain int8 planes (w int8 [N, K], fp32 w_s [N]): the operand an engine holds when it
+    requantizes its weights itself instead of calling weight_from_q8 (which packs them).  Same kernels through the
+    row-major entry point prism_w8a8_gemm, at the shapes of bench_per_channel."""
+    import torch
+    from prism_amd import quant as KQ
+    from prism_amd import w8a8 as KW
+    rows = []
+    for (M, K, N) in ((M1, K1, N1), (1, 5120, 5120), (16, 5120, 5120), (64, 5120, 5120), (1, 17408, 5120),
+                      (16, 17408, 5120), (64, 17408, 5120)):
+        g = torch.Generator(device=dev)
+        g.manual_seed(9)
+        wbytes = N * K
+        copies = _copies(wbytes, M)
+        ws = [torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8, device=dev) for _ in range(copies)]
+        sw = torch.rand(N, generator=g, device=dev)
+        x = make_acts(M, K, 10, dev)
+        q = torch.empty(M, K, dtype=torch.int8, device=dev)
+        s = torch.empty(M, dtype=torch.float32, device=dev)
+        n = torch.tensor([M], dtype=torch.int32, device=dev)
+        KQ.rows_q8(x, None, q, s, n, M)
+        out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+        us = _graph_us(lambda i: KW.gemm(q, s, ws[i], sw, out, n, K), copies, iters if M <= 64 else 10)
+        rows.append(_row(M, K, N, us, wbytes, "hbm" if M <= 64 else "mfma", PEAK_INT8_TOPS))
+        del ws, out, x, q
+        torch.cuda.empty_cache()
+    return rows
+
+
 def bench_deferred(dev, iters=40):
     """The engine's down projection at 64 decode rows (K 17408 -> HID 5120, per channel, residual add) followed by the
     norm_q8 that reads the residual: unsplit (epilogue 1, then norm_q8) against deferred (K in defer_split parts
@@ -376,6 +405,7 @@ def bench_producers(dev, iters=20):
 CONFIG_LINES = {
     "producers": bench_producers,
     "per_channel": bench_per_channel,
+    "per_channel_plain": bench_per_channel_plain,
     "per_channel_deferred": bench_deferred,
     "c0": lambda dev: bench_q8_decode(dev, [(4096, 4096)], (16,)),
     "c2": lambda dev: bench_q8_decode(dev, [(5120, 5120), (17408, 5120)], (1, 4, 16, 64)),
@@ -507,7 +537,7 @@ def main():
     ap.add_argument("--cpu-rows", type=int, default=M1)
     ap.add_argument("--only", default=None,
                     help="comma-separated config lines (c0, c2, c3, c3_q6k, c4, per_channel, per_channel_decode, "
-                         "per_channel_deferred, producers): run just those and print them as one JSON line, "
+                         "per_channel_plain, per_channel_deferred, producers): run just those and print them as one JSON line, "
                          "without the headline (for profiling one kernel family)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 1 GiB device copy (3 times): the calibration kernel for rocprofv3 "

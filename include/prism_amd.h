@@ -92,7 +92,7 @@ PRISM_API int prism_w8a8_gemm(const int8_t* a, const float* a_s, int64_t as_sm, 
  * weight_from_q8 (kernels/w8a8.py:274-286) and repack (kernels/w4a8.py:70-94) are).  qs int8 [N, K], d fp16 [N, K/32]
  * -> qt int8 [N/16][K/64][64][16] (per 16-row tile and block pair a 1 KB chunk; lane slot l: row l % 16,
  * bytes 0..7 = k 8 (l/16) .. +8 of the pair's first block, bytes 8..15 the same of its second), dt fp16
- * [N/16][K/64][16][2].  Needs N % 16 == 0, K % 64 == 0.
+ * [N/16][K/64][16][2].  Needs N % 16 == 0, K % 128 == 0 (the packed GEMM's rule).
  */
 PRISM_API int prism_q8_0_pack(const int8_t* qs, const uint16_t* d, int8_t* qt, uint16_t* dt, int64_t N, int64_t K,
                               void* stream);

@@ -578,7 +578,8 @@ using namespace prism;
 extern "C" int prism_q8_0_pack(const int8_t* qs, const uint16_t* d, int8_t* qt, uint16_t* dt, int64_t N, int64_t K,
                                void* stream) {
     if (!qs || !d || !qt || !dt) return PRISM_ERR_ARG;
-    if (N <= 0 || K <= 0 || N % 16 || K % 64 || N > (1 << 30) || K > (1 << 30)) return PRISM_ERR_SHAPE;
+    // K % 128: the packed GEMM's rule (its prefill tile stages 128 inputs), so a packed operand is always usable
+    if (N <= 0 || K <= 0 || N % 16 || K % 128 || N > (1 << 30) || K > (1 << 30)) return PRISM_ERR_SHAPE;
     if (!PRISM_ALIGNED(qs, 16) || !PRISM_ALIGNED(qt, 16) || !PRISM_ALIGNED(dt, 16)) return PRISM_ERR_ALIGN;
     const int64_t total = N / 16 * (K / 64) * 64;
     hipLaunchKernelGGL(q8_0_pack_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream, qs,

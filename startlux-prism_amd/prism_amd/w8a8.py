@@ -48,7 +48,8 @@ class PackedQ8(NamedTuple):
 
 
 def pack_q8(qs, d):
-    """Q8_0 planes (qs int8 [n, k], d fp16 [n, k/32], on the GPU) -> PackedQ8 (n % 16 == 0, k % 64 == 0)."""
+    """Q8_0 planes (qs int8 [n, k], d fp16 [n, k/32], on the GPU) -> PackedQ8 (n % 16 == 0, k % 128 == 0, the packed
+    GEMM's rule)."""
     n, k = qs.shape
     if qs.dtype != torch.int8 or d.dtype != torch.float16 or tuple(d.shape) != (n, k // 32):
         raise ValueError("pack_q8: qs int8 [n, k], d fp16 [n, k/32]")
@@ -146,6 +147,8 @@ def gemm(a, a_s, w, w_s, out, n_rows, gk, epi=0, outs=None, cfg=None, slots=None
         raise ValueError(f"out must be {want} [>= {M}, >= {N}] with unit column stride")
     if n_rows.dtype != torch.int32:
         raise ValueError("n_rows must be int32")
+    if gk == K:
+        kernel = _tabled(kernel, N, K, M, gk)     # per channel on int8 planes: the same table as PackedPC
     L.call("prism_w8a8_gemm", L.ptr(a), L.ptr(a_s), as_sm, as_sg, L.ptr(w), L.ptr(w_s),
            int(w_s.dtype == torch.float16), L.ptr(out), out.stride(0), L.ptr(n_rows), M, N, K, gk, epi,
            KERNELS[kernel], L.stream_of(a))

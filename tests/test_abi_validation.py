@@ -39,6 +39,16 @@ def test_q8_0_packed_gemm_checks(lib):
     assert call(M=0, kernel=3) == OK             # the reassociated prefill kernel is a valid choice
 
 
+def test_pack_checks_match_the_gemms(lib):
+    """The Q8_0 pack takes the packed GEMM's K rule (K % 128), so every packed operand is usable; the per-channel
+    pack keeps K % 64, its GEMM's rule."""
+    assert lib.prism_q8_0_pack(P, P, P, P, 64, 192, None) == SHAPE
+    assert lib.prism_q8_0_pack(P, P, P, P, 40, 256, None) == SHAPE
+    assert lib.prism_q8_0_pack(U, P, P, P, 64, 256, None) == ALIGN
+    assert lib.prism_i8_pack(P, P, 64, 96, None) == SHAPE
+    assert lib.prism_i8_pack(U, P, 64, 192, None) == ALIGN
+
+
 def test_w4a8_q4k_gemm_checks(lib):
     f = lib.prism_w4a8_q4k_gemm
 
