@@ -11,17 +11,21 @@
 // a "valid" tag and the fp32 bits), and the tail comes last, by when the previous workgroup has long published its
 // head.  Whole tiles in between fold from zero and store their outputs.
 //
-// Inside a workgroup, as the row-round decode kernel: NW compute waves take the round's block pairs (CP each), one
-// MFMA per block gives the 16 x 16 int32 sums, every term RN(RN(float(P) sa) sw) goes to an LDS term buffer, and FW
-// fold waves add the previous round's terms of one output per thread in block order while the compute waves run the
-// next round.  Weights are requested D - 1 rounds ahead in a register ring; a round's block scales and activation
-// pieces are staged in LDS one round ahead from a ring loaded D rounds ahead.
+// Inside a workgroup: NW compute waves take the round's block pairs (CP each); per block one MFMA with the activation
+// rows as its A operand and the weight chunk's slot as its B gives the int32 sums, and every term
+// RN(RN(float(P) sa) sw) goes to an LDS term buffer.  FW fold waves add the previous rounds' terms of one output per
+// thread in block order while the compute waves run ahead (up to RD rounds, counted through LDS counters: no
+// workgroup barriers in the loop).  Weights and their block scales are requested D - 1 rounds ahead in a register
+// ring.  The activation rows sit in LDS, copied whole at the start when they fit (XL), else they travel in the ring.
+// Measured on MI355X: twelve compute waves per workgroup (not eight, nor more) for one to four rows; a ring deeper
+// than one round ahead and rounds of other sizes were slower.
 //
 // Handoff protocol (per output word, never leaves a word set after a launch): the producer writes (1 << 32) | bits
-// with a compare-and-swap from 0; the consumer polls for the tag, takes the bits and clears the word.  A consumer that
-// polls past its bound (a predecessor that never ran: not expected, every predecessor is dispatched first and
-// publishes before it waits on anything) swaps in an "abandoned" tag and takes its value if the producer had just
-// finished, or yields NaN outputs (loud, never silently wrong); a producer that finds "abandoned" clears the word.
+// with a compare-and-swap from 0 (whose result it checks only at its end); the consumer takes the bits, normally read
+// one round ahead, else by polling, and clears the word.  A consumer that polls past its bound (a predecessor that
+// never ran: not expected, every predecessor is dispatched first and publishes before it waits on anything) swaps in
+// an "abandoned" tag and takes its value if the producer had just finished, or yields NaN outputs (loud, never
+// silently wrong); a producer that finds "abandoned" clears the word.
 #include "common.h"
 #include "q8_stream.h"
 
@@ -34,16 +38,6 @@ __device__ __forceinline__ unsigned long long hand_load(unsigned long long* p) {
 }
 __device__ __forceinline__ void hand_store(unsigned long long* p, unsigned long long v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Publishes y for the next workgroup.
-__device__ __forceinline__ void hand_publish(unsigned long long* p, float y) {
-    unsigned long long expect = 0;
-    const unsigned long long v = kTagValid | __float_as_uint(y);
-    if (!__hip_atomic_compare_exchange_strong(p, &expect, v, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                              __HIP_MEMORY_SCOPE_AGENT) &&
-        expect == kTagAbandoned)
-        hand_store(p, 0);
 }
 
 // Takes the previous workgroup's y (bounded wait).
@@ -80,7 +74,7 @@ __device__ __forceinline__ void lds_wait_ge(unsigned* c, unsigned target) {
     }
 }
 
-template <int NW, int R, int MX, int D, int RD, int EPI>
+template <int NW, int R, int MX, int D, int RD, int EPI, bool XL>
 __global__ __launch_bounds__((NW + (MX * 16 + 63) / 64) * 64) void w8a8_q8_stream_kernel(
     const int8_t* __restrict__ a, const float* __restrict__ a_s, int64_t as_sm, const int8_t* __restrict__ qt,
     const uint16_t* __restrict__ dt, void* __restrict__ out, int64_t ldo, const int32_t* __restrict__ n_rows, int M,
@@ -92,24 +86,36 @@ __global__ __launch_bounds__((NW + (MX * 16 + 63) / 64) * 64) void w8a8_q8_strea
     static_assert(CP >= 1 && CP * NW == RP, "R must be a multiple of 2 NW");
     static_assert(MX <= 16, "one 16-row activation tile");
     extern __shared__ __attribute__((aligned(16))) int8_t dsm[];
-    float* terms = reinterpret_cast<float*>(dsm);                              // [RD][R][M][16]
-    unsigned* wdone = reinterpret_cast<unsigned*>(terms + RD * R * M * 16);   // [RD]: compute waves done
+    // terms [RD][M x 16 outputs][TL]: an output's R terms of a round are contiguous, so the fold reads them four at
+    // a time; rows padded by 4 floats so the 16 lanes storing one block's terms hit distinct banks
+    constexpr int TL = R + 4;
+    float* terms = reinterpret_cast<float*>(dsm);
+    unsigned* wdone = reinterpret_cast<unsigned*>(terms + RD * M * 16 * TL);  // [RD]: compute waves done
     unsigned* fdone = wdone + RD;                                              // [RD]: fold waves done
-    const int tstride = R * M * 16;
+    const int tstride = M * 16 * TL;
+    // XL: the M activation rows, copied whole into LDS at the start ([M][K] bytes, as they lie), so the register
+    // ring carries only the weight stream
+    int8_t* xs = dsm + ((RD * M * 16 * TL * 4 + 2 * RD * 4 + 15) & ~15);
 
+    // every argument fetched at once: the compiler would otherwise load each where first used, one scalar memory
+    // round trip after another before the first weight request
+    const int W = gridDim.x, v = blockIdx.x;
+    asm volatile("" ::"s"(a), "s"(a_s), "s"(as_sm), "s"(qt), "s"(dt), "s"(out), "s"(ldo), "s"(n_rows), "s"(M), "s"(N),
+                 "s"(K), "s"(hand), "s"(W));
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int live = min(M, __ldg(n_rows));
     const int KP = K / 64;
     const int lm = lane & 15, q = lane >> 4;
+    // the counters are cleared here and first used after the workgroup barrier that follows the first loads (no
+    // barrier, and no global load the first weight requests would wait behind, before those requests go out)
     if (tid < 2 * RD) wdone[tid] = 0;
-    __syncthreads();
 
-    // this workgroup's range of chunks and its fragments, walked from the last tile to the first
-    const int W = gridDim.x, v = blockIdx.x;
-    const int64_t total = (int64_t)(N / 16) * KP;
-    const int64_t c0 = total * v / W, c1 = total * (v + 1) / W;
-    const int nt_lo = (int)(c0 / KP), nt_hi = (int)((c1 - 1) / KP);
-    const int ps_lo = (int)(c0 - (int64_t)nt_lo * KP), pe_hi = (int)(c1 - (int64_t)nt_hi * KP);
+    // this workgroup's range of chunks and its fragments, walked from the last tile to the first: ranges of
+    // total / W or one more chunks (the host keeps total below 2^31, so the arithmetic is 32-bit)
+    const int total = (N / 16) * KP;
+    const int cq = total / W, cr = total - cq * W;
+    const int c0 = v * cq + min(v, cr), c1 = c0 + cq + (v < cr ? 1 : 0);
+    const int nt_lo = c0 / KP, nt_hi = (c1 - 1) / KP;
+    const int ps_lo = c0 - nt_lo * KP, pe_hi = c1 - nt_hi * KP;
     const int RT = (KP + RP - 1) / RP;
     const int ps_hi = nt_hi == nt_lo ? ps_lo : 0;
     const int r_hi = (pe_hi - ps_hi + RP - 1) / RP;
@@ -141,14 +147,20 @@ __global__ __launch_bounds__((NW + (MX * 16 + 63) / 64) * 64) void w8a8_q8_strea
         // requested D - 1 rounds ahead.  Each block's int32 sums come from one MFMA (zero accumulator); the terms
         // RN(RN(float(P) sa) sw) go to ring slot r % RD once the fold waves have released it, then the wave counts
         // itself done for the round.  Waves run ahead of one another up to the ring's depth: no barriers.
+        // Operands: the activation rows are the MFMA's A (lane l: row m = l % 16, 8-byte piece l / 16) and the weight
+        // chunk's 16-byte slot its B as it lies (column n = l % 16), so lane l holds the sums of outputs
+        // (m = 4 (l / 16) + e, n = l % 16): with MX <= 4 rows only e < MX of the lanes below 16 carry outputs, and the
+        // epilogue works on those values alone; every lane's outputs share one weight row, whose two block scales
+        // are one 4-byte word of dt.
+        constexpr int EV = MX < 4 ? MX : 4;                            // accumulator values per lane in use
         const int mc = min(lm, M - 1);
-        const float sa = a_s[(int64_t)mc * as_sm];
         const v4i* cw = reinterpret_cast<const v4i*>(qt) + lane;
-        const v4u* cs = reinterpret_cast<const v4u*>(dt) + q;
+        const uint32_t* cs = reinterpret_cast<const uint32_t*>(dt) + lm;
         const int8_t* xa = a + (int64_t)mc * K + 8 * q;
+        float sa[EV];
         struct Pair {
             v4i w;
-            v4u s;
+            uint32_t s;
             v2u x0, x1;
         };
         auto load = [&](int rho, Pair* pr) {
@@ -158,12 +170,15 @@ __global__ __launch_bounds__((NW + (MX * 16 + 63) / 64) * 64) void w8a8_q8_strea
             for (int i = 0; i < CP; i++) {
                 const int p = min(d.p0 + wv * CP + i, KP - 1);
                 pr[i].w = __builtin_nontemporal_load(cw + (tb + p) * 64);
-                pr[i].s = cs[(tb + p) * 4];
-                pr[i].x0 = *reinterpret_cast<const v2u*>(xa + 64 * p);
-                pr[i].x1 = *reinterpret_cast<const v2u*>(xa + 64 * p + 32);
+                pr[i].s = cs[(tb + p) * 16];
+                if (!XL) {
+                    pr[i].x0 = *reinterpret_cast<const v2u*>(xa + 64 * p);
+                    pr[i].x1 = *reinterpret_cast<const v2u*>(xa + 64 * p + 32);
+                }
             }
         };
         auto compute = [&](int rho, const Pair* pr) {
+            const Round d = round_of(rho);
             v4i acc[CP][2];
 #pragma unroll
             for (int i = 0; i < CP; i++)
@@ -171,20 +186,26 @@ __global__ __launch_bounds__((NW + (MX * 16 + 63) / 64) * 64) void w8a8_q8_strea
                 for (int h = 0; h < 2; h++) {
                     const int64_t wf = h ? ((int64_t)(uint32_t)pr[i].w[2] | ((int64_t)pr[i].w[3] << 32))
                                          : ((int64_t)(uint32_t)pr[i].w[0] | ((int64_t)pr[i].w[1] << 32));
-                    const v2u xv = h ? pr[i].x1 : pr[i].x0;
-                    const int64_t xf = (int64_t)xv[0] | ((int64_t)xv[1] << 32);
+                    int64_t xf;
+                    if (XL) {
+                        const int p = min(d.p0 + wv * CP + i, KP - 1);
+                        xf = *reinterpret_cast<const int64_t*>(xs + mc * K + 64 * p + 32 * h + 8 * q);
+                    } else {
+                        const v2u xv = h ? pr[i].x1 : pr[i].x0;
+                        xf = (int64_t)xv[0] | ((int64_t)xv[1] << 32);
+                    }
                     const v4i zero = {0, 0, 0, 0};
-                    acc[i][h] = __builtin_amdgcn_mfma_i32_16x16x32_i8(wf, xf, zero, 0, 0, 0);
+                    acc[i][h] = __builtin_amdgcn_mfma_i32_16x16x32_i8(xf, wf, zero, 0, 0, 0);
                 }
-            v4f t[CP][2];
+            float t[CP][2][EV];
 #pragma unroll
             for (int i = 0; i < CP; i++)
 #pragma unroll
                 for (int h = 0; h < 2; h++)
 #pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        const float x = mul_rn((float)acc[i][h][e], sa);
-                        t[i][h][e] = h ? mul_f16_rn<1>(x, pr[i].s[e]) : mul_f16_rn<0>(x, pr[i].s[e]);
+                    for (int e = 0; e < EV; e++) {
+                        const float x = mul_rn((float)acc[i][h][e], sa[e]);
+                        t[i][h][e] = h ? mul_f16_rn<1>(x, pr[i].s) : mul_f16_rn<0>(x, pr[i].s);
                     }
             const int slot = rho % RD;
             lds_wait_ge(&fdone[slot], (unsigned)(FW * (rho / RD)));      // slot released by the fold
@@ -193,13 +214,30 @@ __global__ __launch_bounds__((NW + (MX * 16 + 63) / 64) * 64) void w8a8_q8_strea
             for (int i = 0; i < CP; i++)
 #pragma unroll
                 for (int h = 0; h < 2; h++)
-                    if (lm < M) *reinterpret_cast<v4f*>(&tb[((2 * (wv * CP + i) + h) * M + lm) * 16 + 4 * q]) = t[i][h];
+#pragma unroll
+                    for (int e = 0; e < EV; e++) {
+                        const int m = 4 * q + e;
+                        if (m < M) tb[(m * 16 + lm) * TL + 2 * (wv * CP + i) + h] = t[i][h][e];
+                    }
             if (lane == 0) __hip_atomic_fetch_add(&wdone[slot], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
         };
+        // the first weight requests go out first; then the activation scales and (XL) the activation image, one
+        // wave-wide 1 KB DMA per step, the image's last partial KB by the lanes it covers
         Pair ring[D][CP];
 #pragma unroll
         for (int d = 0; d < D - 1; d++) load(d, ring[d]);
-        for (int r0 = 0; r0 < NR; r0 += D) {
+#pragma unroll
+        for (int e = 0; e < EV; e++) sa[e] = a_s[(int64_t)min(4 * q + e, M - 1) * as_sm];
+        if (XL) {
+            const int nx = (M * K + 1023) / 1024;
+            for (int c = wv; c < nx; c += NW)
+                if (c * 1024 + lane * 16 < M * K) dma16(a + c * 1024 + lane * 16, xs + c * 1024);
+        }
+        __syncthreads();                          // counters cleared; with XL the activation image is in LDS
+        // NR >= 1 (every workgroup has at least one chunk: W <= tiles), so the loop is entered unconditionally and
+        // the prologue's requests are not sunk into a guarded block behind the barrier
+        int r0 = 0;
+        do {
 #pragma unroll
             for (int d = 0; d < D; d++) {
                 const int r = r0 + d;
@@ -208,34 +246,61 @@ __global__ __launch_bounds__((NW + (MX * 16 + 63) / 64) * 64) void w8a8_q8_strea
                     compute(r, ring[d]);
                 }
             }
-        }
+            r0 += D;
+        } while (r0 < NR);
     } else {
         // Fold wave: one output per thread (m = fo / 16, row fo % 16 of the tile), round by round in block order.
         const int fo = tid - NT;
-        const int st = M * 16;
         float y = 0.f;
+        __syncthreads();
+        const int live = min(M, __ldg(n_rows));
+        // the word a tail continues from, read one round ahead (a predecessor publishes its head early, so the value
+        // is normally there and the take costs no round trip); an untagged read falls back to polling
+        unsigned long long pre = 0;
+        // the running sums handed on: the compare-and-swap's result is checked once, at the end
+        unsigned long long* pub = nullptr;
+        unsigned long long pub_old = 0;
         for (int r = 0; r < NR; r++) {
             const Round d = round_of(r);
             const int slot = r % RD;
+            if (r + 1 < NR && fo < M * 16) {
+                const Round dn = round_of(r + 1);
+                if (dn.first && dn.ps > 0) pre = hand_load(hand + (int64_t)(v - 1) * (MX * 16) + fo);
+            }
             lds_wait_ge(&wdone[slot], (unsigned)(NW * (r / RD + 1)));
             if (fo < M * 16) {
-                if (d.first) y = d.ps == 0 ? 0.f : hand_take(hand + (int64_t)(v - 1) * (MX * 16) + fo);
-                const float* tp = terms + slot * tstride + fo;
+                if (d.first) {
+                    if (d.ps == 0) {
+                        y = 0.f;
+                    } else if ((pre >> 32) == 1) {
+                        hand_store(hand + (int64_t)(v - 1) * (MX * 16) + fo, 0);
+                        y = __uint_as_float((uint32_t)pre);
+                    } else {
+                        y = hand_take(hand + (int64_t)(v - 1) * (MX * 16) + fo);
+                    }
+                }
+                const float* tp = terms + slot * tstride + fo * TL;
                 const int nb = 2 * d.np;
                 float acc = y;
                 if (nb == R) {
-                    float u[R];
+                    v4f u[R / 4];
 #pragma unroll
-                    for (int j = 0; j < R; j++) u[j] = tp[j * st];
+                    for (int j = 0; j < R / 4; j++) u[j] = *reinterpret_cast<const v4f*>(tp + 4 * j);
 #pragma unroll
-                    for (int j = 0; j < R; j++) acc = add_rn(acc, u[j]);
+                    for (int j = 0; j < R / 4; j++)
+#pragma unroll
+                        for (int e = 0; e < 4; e++) acc = add_rn(acc, u[j][e]);
                 } else {
-                    for (int j = 0; j < nb; j++) acc = add_rn(acc, tp[j * st]);
+                    for (int j = 0; j < nb; j++) acc = add_rn(acc, tp[j]);
                 }
                 y = acc;
                 if (d.last) {
                     if (d.pe < KP) {
-                        hand_publish(hand + (int64_t)v * (MX * 16) + fo, y);
+                        pub = hand + (int64_t)v * (MX * 16) + fo;
+                        pub_old = 0;
+                        __hip_atomic_compare_exchange_strong(pub, &pub_old, kTagValid | __float_as_uint(y),
+                                                             __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                             __HIP_MEMORY_SCOPE_AGENT);
                     } else {
                         const int m = fo >> 4, n = 16 * d.nt + (fo & 15);
                         if (m < live) {
@@ -252,10 +317,16 @@ __global__ __launch_bounds__((NW + (MX * 16 + 63) / 64) * 64) void w8a8_q8_strea
             // the wave's reads of the slot are complete before it is counted released
             if (lane == 0) __hip_atomic_fetch_add(&fdone[slot], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
+        // a consumer that gave up on this word (never expected) left it tagged abandoned: clear it
+        if (pub && pub_old == kTagAbandoned) hand_store(pub, 0);
     }
 }
 
-static size_t stream_lds(int R, int RD, int M) { return (size_t)RD * R * M * 16 * 4 + 2 * RD * 4; }
+static size_t stream_lds(int R, int RD, int M, int K, bool xl) {
+    const size_t base = (size_t)RD * M * 16 * (R + 4) * 4 + 2 * RD * 4;
+    return xl ? ((base + 15) & ~(size_t)15) + (size_t)M * K : base;
+}
+constexpr size_t kLdsMax = 160 * 1024;
 
 int q8_stream_workgroups(int64_t N, int64_t K) {
     const int64_t tiles = N / 16;
@@ -269,20 +340,34 @@ static void launch(const int8_t* a, const float* a_s, int64_t as_sm, const int8_
                    hipStream_t st) {
 #define QS(NW, R, MX, D, RD)                                                                                        \
     do {                                                                                                            \
-        auto fn = w8a8_q8_stream_kernel<NW, R, MX, D, RD, EPI>;                                                     \
-        allow_lds(fn, stream_lds(R, RD, M));                                                                        \
-        hipLaunchKernelGGL(fn, dim3(W), dim3((NW + (MX * 16 + 63) / 64) * 64), stream_lds(R, RD, M), st, a, a_s,     \
-                           as_sm,                                                                                   \
-                           qt, dt, out, ldo, n_rows, M, N, K, hand);                                                \
+        constexpr int NTH = (NW + (MX * 16 + 63) / 64) * 64;                                                        \
+        if (Q8S_XL && stream_lds(R, RD, M, K, true) <= kLdsMax) {                                                   \
+            auto fn = w8a8_q8_stream_kernel<NW, R, MX, D, RD, EPI, true>;                                           \
+            allow_lds(fn, stream_lds(R, RD, M, K, true));                                                           \
+            hipLaunchKernelGGL(fn, dim3(W), dim3(NTH), stream_lds(R, RD, M, K, true), st, a, a_s, as_sm, qt, dt,    \
+                               out, ldo, n_rows, M, N, K, hand);                                                    \
+        } else {                                                                                                    \
+            auto fn = w8a8_q8_stream_kernel<NW, R, MX, D, RD, EPI, false>;                                          \
+            allow_lds(fn, stream_lds(R, RD, M, K, false));                                                          \
+            hipLaunchKernelGGL(fn, dim3(W), dim3(NTH), stream_lds(R, RD, M, K, false), st, a, a_s, as_sm, qt, dt,   \
+                               out, ldo, n_rows, M, N, K, hand);                                                    \
+        }                                                                                                           \
     } while (0)
+#ifndef Q8S_XL
+#define Q8S_XL 1
+#endif
 #ifndef Q8S_SMALL
-#define Q8S_SMALL 8, 32, 4, 2, 4
+#define Q8S_SMALL 12, 48, 4, 2, 4
+#endif
+#ifndef Q8S_ONE
+#define Q8S_ONE 12, 48, 1, 2, 4
 #endif
 #ifndef Q8S_BIG
 #define Q8S_BIG 8, 32, 16, 2, 3
 #endif
 #define QS_(...) QS(__VA_ARGS__)
-    if (M <= 4) QS_(Q8S_SMALL);
+    if (M == 1) QS_(Q8S_ONE);
+    else if (M <= 4) QS_(Q8S_SMALL);
     else QS_(Q8S_BIG);
 #undef QS_
 #undef QS
@@ -291,7 +376,7 @@ static void launch(const int8_t* a, const float* a_s, int64_t as_sm, const int8_
 int q8_stream_launch(const int8_t* a, const float* a_s, int64_t as_sm, const int8_t* qt, const uint16_t* dt,
                      void* out, int64_t ldo, const int32_t* n_rows, int64_t M, int64_t N, int64_t K, int epi,
                      void* hand, int64_t hand_bytes, hipStream_t st) {
-    if (M < 1 || M > 16) return PRISM_ERR_SHAPE;
+    if (M < 1 || M > 16 || (N / 16) * (K / 64) >= ((int64_t)1 << 31)) return PRISM_ERR_SHAPE;
     const int W = q8_stream_workgroups(N, K);
     if (!hand || !PRISM_ALIGNED(hand, 8) || hand_bytes < q8_stream_workspace_bytes(N, K)) return PRISM_ERR_ARG;
     auto* h = reinterpret_cast<unsigned long long*>(hand);
