@@ -55,6 +55,31 @@ __device__ __forceinline__ float mul_f16_rn(float x, uint32_t word) {
     return r;
 }
 
+// Every listed kernel argument in scalar registers at this point, with one wait: the compiler otherwise loads each
+// argument where it is first used, one scalar memory round trip after another, and a decode-size kernel's first
+// weight request then waits behind several of them.  Up to 14 arguments (all wave-uniform values).
+#define PRISM_S_(x) "s"(x)
+#define PRISM_MAP1(f, x) f(x)
+#define PRISM_MAP2(f, x, ...) f(x), PRISM_MAP1(f, __VA_ARGS__)
+#define PRISM_MAP3(f, x, ...) f(x), PRISM_MAP2(f, __VA_ARGS__)
+#define PRISM_MAP4(f, x, ...) f(x), PRISM_MAP3(f, __VA_ARGS__)
+#define PRISM_MAP5(f, x, ...) f(x), PRISM_MAP4(f, __VA_ARGS__)
+#define PRISM_MAP6(f, x, ...) f(x), PRISM_MAP5(f, __VA_ARGS__)
+#define PRISM_MAP7(f, x, ...) f(x), PRISM_MAP6(f, __VA_ARGS__)
+#define PRISM_MAP8(f, x, ...) f(x), PRISM_MAP7(f, __VA_ARGS__)
+#define PRISM_MAP9(f, x, ...) f(x), PRISM_MAP8(f, __VA_ARGS__)
+#define PRISM_MAP10(f, x, ...) f(x), PRISM_MAP9(f, __VA_ARGS__)
+#define PRISM_MAP11(f, x, ...) f(x), PRISM_MAP10(f, __VA_ARGS__)
+#define PRISM_MAP12(f, x, ...) f(x), PRISM_MAP11(f, __VA_ARGS__)
+#define PRISM_MAP13(f, x, ...) f(x), PRISM_MAP12(f, __VA_ARGS__)
+#define PRISM_MAP14(f, x, ...) f(x), PRISM_MAP13(f, __VA_ARGS__)
+#define PRISM_NARG_(_1, _2, _3, _4, _5, _6, _7, _8, _9, _10, _11, _12, _13, _14, N, ...) N
+#define PRISM_NARG(...) PRISM_NARG_(__VA_ARGS__, 14, 13, 12, 11, 10, 9, 8, 7, 6, 5, 4, 3, 2, 1)
+#define PRISM_CAT_(a, b) a##b
+#define PRISM_CAT(a, b) PRISM_CAT_(a, b)
+#define kernel_args_now(...) \
+    asm volatile("" ::PRISM_CAT(PRISM_MAP, PRISM_NARG(__VA_ARGS__))(PRISM_S_, __VA_ARGS__))
+
 // Workgroup barrier for LDS hand-offs only: waits for this wave's LDS operations, not for its outstanding global
 // loads (__syncthreads() also drains those, which would empty a kernel's prefetch pipeline at every barrier).
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }

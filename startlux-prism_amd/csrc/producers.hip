@@ -85,12 +85,15 @@ __device__ __forceinline__ float row_sum_fixed(float v, float* red) {
 // Back ends.  BACK 0: int8 row + one scale per row (q [M, K], s [M]).  BACK 1: the W4A8 operands with one scale
 // per 256 inputs (xq [M, K], a [K/256, M], xs [K/256, M, 16]); BACK 2: the same with one scale per row (a [M]).
 // TPB: the workgroup size (thread t owns chunks t, t + TPB, ...); every result is independent of it.
+// live: the row is below n_rows (the workgroup computes either way and stores only then: reading n_rows before the
+// row's loads would hold them back by a memory round trip).
 template <int NCH, int BACK, int TPB = kPThreads>
 __device__ __forceinline__ void store_back(float (&y)[NCH][8], float rmax, float* red, int64_t row, int out_row,
                                            int M, int K, int8_t* __restrict__ q, float* __restrict__ s,
-                                           int8_t* __restrict__ xs) {
+                                           int8_t* __restrict__ xs, bool live) {
     const int nch = K / 8;
     if (BACK == 0 || BACK == 2) rmax = row_max<TPB>(rmax, red);
+    if (!live) return;                       // uniform over the workgroup, after its last barrier
     v2u* qr = reinterpret_cast<v2u*>(q + (int64_t)out_row * K);
 #pragma unroll
     for (int c = 0; c < NCH; c++) {
@@ -206,25 +209,44 @@ __global__ __launch_bounds__(kPThreads) void norm_prod_kernel(float* __restrict_
                                                               const int32_t* __restrict__ n_rows, int M, int HID,
                                                               float eps, Fold f) {
     __shared__ float red[4];
+    kernel_args_now(h, ldh, w, rows, q, s, xs, n_rows, M, HID, eps);
     const int i = blockIdx.x;
-    if (i >= __ldg(n_rows)) return;
+    // a gathered row's index is only meaningful below n_rows: that path tests the count first (a dependent load
+    // follows anyway); without a gather every row index below M is a valid address and the count is read later
+    if (rows && i >= __ldg(n_rows)) return;
     const int64_t src = rows ? (int64_t)__ldg(rows + i) : i;
     const int nch = HID / 8;
     v4f* hr = reinterpret_cast<v4f*>(h + src * ldh);
     const v4f* wr = reinterpret_cast<const v4f*>(w);
     float y[NCH][8];
     float ss = 0.f;
+    // the row's and the weights' loads first, all of them, unconditionally (chunk indices clamped into the row): a
+    // load inside a per-chunk branch would wait before the next chunk's went out
+    v4f ha[NCH], hb[NCH], wa[NCH], wb[NCH];
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+        const int idx = min((int)threadIdx.x + c * kPThreads, nch - 1);
+        ha[c] = __builtin_nontemporal_load(hr + 2 * idx);
+        hb[c] = __builtin_nontemporal_load(hr + 2 * idx + 1);
+    }
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+        const int idx = min((int)threadIdx.x + c * kPThreads, nch - 1);
+        wa[c] = wr[2 * idx];
+        wb[c] = wr[2 * idx + 1];
+    }
+    const bool live = i < __ldg(n_rows);
 #pragma unroll
     for (int c = 0; c < NCH; c++) {
         const int idx = threadIdx.x + c * kPThreads;
         if (idx < nch) {
-            const v4f a = __builtin_nontemporal_load(hr + 2 * idx), b = __builtin_nontemporal_load(hr + 2 * idx + 1);
+            const v4f a = ha[c], b = hb[c];
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 y[c][j] = a[j];
                 y[c][j + 4] = b[j];
             }
-            if (FOLD) {
+            if (FOLD && live) {
                 fold8(y[c], f, src, 8 * idx);
                 hr[2 * idx] = v4f{y[c][0], y[c][1], y[c][2], y[c][3]};
                 hr[2 * idx + 1] = v4f{y[c][4], y[c][5], y[c][6], y[c][7]};
@@ -240,7 +262,7 @@ __global__ __launch_bounds__(kPThreads) void norm_prod_kernel(float* __restrict_
     for (int c = 0; c < NCH; c++) {
         const int idx = threadIdx.x + c * kPThreads;
         if (idx < nch) {
-            const v4f a = wr[2 * idx], b = wr[2 * idx + 1];
+            const v4f a = wa[c], b = wb[c];
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 y[c][j] = mul_rn(mul_rn(y[c][j], r), a[j]);
@@ -250,7 +272,7 @@ __global__ __launch_bounds__(kPThreads) void norm_prod_kernel(float* __restrict_
             for (int j = 0; j < 8; j++) amax = fmaxf(amax, fabsf(y[c][j]));
         }
     }
-    store_back<NCH, BACK>(y, amax, red, src, i, M, HID, q, s, xs);
+    store_back<NCH, BACK>(y, amax, red, src, i, M, HID, q, s, xs, live);
 }
 
 // ---------------------------------------------------------------------------------------------- SwiGLU
@@ -263,28 +285,48 @@ __global__ __launch_bounds__(TPB) void swiglu_prod_kernel(const void* __restrict
                                                                 int8_t* __restrict__ xs,
                                                                 const int32_t* __restrict__ n_rows, int M, int FF) {
     __shared__ float red[TPB / 64];
+    kernel_args_now(gu, ldg, inv_s, q, s, xs, n_rows, M, FF);
     const int i = blockIdx.x;
-    if (i >= __ldg(n_rows)) return;
     const int nch = FF / 8;
     float y[NCH][8];
     float amax = 0.f;
+    // every load first, unconditionally (chunk indices clamped into the row; see norm_prod_kernel)
+    v4u raw[NCH][4];
+    v4f isv[NCH][2];
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+        const int idx = min((int)threadIdx.x + c * TPB, nch - 1);
+        if (GU32) {
+            const v4u* row = reinterpret_cast<const v4u*>(static_cast<const float*>(gu) + (int64_t)i * ldg);
+            raw[c][0] = row[2 * idx];
+            raw[c][1] = row[2 * idx + 1];
+            raw[c][2] = row[FF / 4 + 2 * idx];
+            raw[c][3] = row[FF / 4 + 2 * idx + 1];
+        } else {
+            const v4u* row = reinterpret_cast<const v4u*>(static_cast<const uint16_t*>(gu) + (int64_t)i * ldg);
+            raw[c][0] = row[idx];
+            raw[c][1] = row[FF / 8 + idx];
+        }
+        if (inv_s) {
+            isv[c][0] = reinterpret_cast<const v4f*>(inv_s)[2 * idx];
+            isv[c][1] = reinterpret_cast<const v4f*>(inv_s)[2 * idx + 1];
+        }
+    }
+    const bool live = i < __ldg(n_rows);
 #pragma unroll
     for (int c = 0; c < NCH; c++) {
         const int idx = threadIdx.x + c * TPB;
         if (idx < nch) {
             float g[8], u[8];
             if (GU32) {
-                const v4f* row = reinterpret_cast<const v4f*>(static_cast<const float*>(gu) + (int64_t)i * ldg);
-                const v4f g0 = row[2 * idx], g1 = row[2 * idx + 1];
-                const v4f u0 = row[FF / 4 + 2 * idx], u1 = row[FF / 4 + 2 * idx + 1];
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    g[j] = g0[j]; g[j + 4] = g1[j];
-                    u[j] = u0[j]; u[j + 4] = u1[j];
+                    g[j] = __uint_as_float(raw[c][0][j]); g[j + 4] = __uint_as_float(raw[c][1][j]);
+                    u[j] = __uint_as_float(raw[c][2][j]);
+                    u[j + 4] = __uint_as_float(raw[c][3][j]);
                 }
             } else {
-                const v4u* row = reinterpret_cast<const v4u*>(static_cast<const uint16_t*>(gu) + (int64_t)i * ldg);
-                const v4u gv = row[idx], uv = row[FF / 8 + idx];
+                const v4u gv = raw[c][0], uv = raw[c][1];
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
                     g[2 * j] = __uint_as_float(gv[j] << 16);
@@ -295,11 +337,10 @@ __global__ __launch_bounds__(TPB) void swiglu_prod_kernel(const void* __restrict
             }
             float is[8];
             if (inv_s) {
-                const v4f a = reinterpret_cast<const v4f*>(inv_s)[2 * idx], b = reinterpret_cast<const v4f*>(inv_s)[2 * idx + 1];
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    is[j] = a[j];
-                    is[j + 4] = b[j];
+                    is[j] = isv[c][0][j];
+                    is[j + 4] = isv[c][1][j];
                 }
             }
 #pragma unroll
@@ -311,7 +352,7 @@ __global__ __launch_bounds__(TPB) void swiglu_prod_kernel(const void* __restrict
             }
         }
     }
-    store_back<NCH, BACK, TPB>(y, amax, red, i, i, M, FF, q, s, xs);
+    store_back<NCH, BACK, TPB>(y, amax, red, i, i, M, FF, q, s, xs, live);
 }
 
 // ---------------------------------------------------------------------------------------------- gated RMSNorm
@@ -328,19 +369,43 @@ __global__ __launch_bounds__(TPB) void gated_norm_prod_kernel(const float* __res
                                                                     const int32_t* __restrict__ n_rows, int M, int HV,
                                                                     int D, float eps) {
     __shared__ float red[TPB / 64];
+    kernel_args_now(o, ldo, z, ldz, w, inv_s, q, s, xs, n_rows, M, HV, D, eps);
     const int i = blockIdx.x;
-    if (i >= __ldg(n_rows)) return;
     const int K = HV * D, nch = K / 8, cph = D / 8;
     const v4f* orow = reinterpret_cast<const v4f*>(o + (int64_t)i * ldo);
     float y[NCH][8];
     float amax = 0.f;
+    // every load first, unconditionally (chunk indices clamped into the row; see norm_prod_kernel)
+    v4f oa[NCH], ob[NCH], wv0[NCH], wv1[NCH], iv0[NCH], iv1[NCH];
+    v4u zv[NCH][2];
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+        const int idx = min((int)threadIdx.x + c * TPB, nch - 1);
+        oa[c] = __builtin_nontemporal_load(orow + 2 * idx);
+        ob[c] = __builtin_nontemporal_load(orow + 2 * idx + 1);
+        const int d0 = (idx & (cph - 1)) * 8;
+        wv0[c] = reinterpret_cast<const v4f*>(w + d0)[0];
+        wv1[c] = reinterpret_cast<const v4f*>(w + d0)[1];
+        if (Z32) {
+            const v4u* zr = reinterpret_cast<const v4u*>(static_cast<const float*>(z) + (int64_t)i * ldz);
+            zv[c][0] = zr[2 * idx];
+            zv[c][1] = zr[2 * idx + 1];
+        } else {
+            zv[c][0] = reinterpret_cast<const v4u*>(static_cast<const uint16_t*>(z) + (int64_t)i * ldz)[idx];
+        }
+        if (inv_s) {
+            iv0[c] = reinterpret_cast<const v4f*>(inv_s)[2 * idx];
+            iv1[c] = reinterpret_cast<const v4f*>(inv_s)[2 * idx + 1];
+        }
+    }
+    const bool live = i < __ldg(n_rows);
 #pragma unroll
     for (int c = 0; c < NCH; c++) {
         const int idx = threadIdx.x + c * TPB;
         const bool in = idx < nch;
         float ss = 0.f;
         if (in) {
-            const v4f a = __builtin_nontemporal_load(orow + 2 * idx), b = __builtin_nontemporal_load(orow + 2 * idx + 1);
+            const v4f a = oa[c], b = ob[c];
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 y[c][j] = a[j];
@@ -352,19 +417,16 @@ __global__ __launch_bounds__(TPB) void gated_norm_prod_kernel(const float* __res
         for (int off = cph >> 1; off > 0; off >>= 1) ss = add_rn(ss, __shfl_xor(ss, off, kWave));
         if (in) {
             const float r = div_rn(1.0f, sqrt_rn(add_rn(div_rn(ss, (float)D), eps)));
-            const int d0 = (idx & (cph - 1)) * 8;
-            const v4f w0 = reinterpret_cast<const v4f*>(w + d0)[0], w1 = reinterpret_cast<const v4f*>(w + d0)[1];
+            const v4f w0 = wv0[c], w1 = wv1[c];
             float g[8];
             if (Z32) {
-                const v4f* zr = reinterpret_cast<const v4f*>(static_cast<const float*>(z) + (int64_t)i * ldz);
-                const v4f g0 = zr[2 * idx], g1 = zr[2 * idx + 1];
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    g[j] = g0[j];
-                    g[j + 4] = g1[j];
+                    g[j] = __uint_as_float(zv[c][0][j]);
+                    g[j + 4] = __uint_as_float(zv[c][1][j]);
                 }
             } else {
-                const v4u gv = reinterpret_cast<const v4u*>(static_cast<const uint16_t*>(z) + (int64_t)i * ldz)[idx];
+                const v4u gv = zv[c][0];
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
                     g[2 * j] = __uint_as_float(gv[j] << 16);
@@ -373,11 +435,10 @@ __global__ __launch_bounds__(TPB) void gated_norm_prod_kernel(const float* __res
             }
             float is[8];
             if (inv_s) {
-                const v4f a = reinterpret_cast<const v4f*>(inv_s)[2 * idx], b = reinterpret_cast<const v4f*>(inv_s)[2 * idx + 1];
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    is[j] = a[j];
-                    is[j + 4] = b[j];
+                    is[j] = iv0[c][j];
+                    is[j + 4] = iv1[c][j];
                 }
             }
 #pragma unroll
@@ -390,7 +451,7 @@ __global__ __launch_bounds__(TPB) void gated_norm_prod_kernel(const float* __res
             }
         }
     }
-    store_back<NCH, BACK, TPB>(y, amax, red, i, i, M, K, q, s, xs);
+    store_back<NCH, BACK, TPB>(y, amax, red, i, i, M, K, q, s, xs, live);
 }
 
 template <typename KN>

@@ -49,31 +49,44 @@ __global__ __launch_bounds__(kQThreads) void quant_rows_i8_kernel(const uint16_t
                                                                   int8_t* __restrict__ q, float* __restrict__ s,
                                                                   const int32_t* __restrict__ n_rows, int K) {
     __shared__ float red[kQThreads / kWave];
+    kernel_args_now(x, ldx, inv_s, q, s, n_rows, K);
     const int64_t row = blockIdx.x;
-    if (row >= (int64_t)__ldg(n_rows)) return;
     const int nch = K / 8;
     const v4u* xr = reinterpret_cast<const v4u*>(x + row * ldx);
     float v[NCH][8];
     float amax = 0.f;
+    // every chunk's loads first, unconditionally (indices clamped into the row), so they are in flight together;
+    // a load inside a per-chunk branch would wait before the next chunk's went out
+    v4u raw[NCH];
+#pragma unroll
+    for (int c = 0; c < NCH; c++) raw[c] = __builtin_nontemporal_load(xr + min((int)threadIdx.x + c * kQThreads, nch - 1));
+    v4f isc[NCH][2];
+    if (inv_s) {
+#pragma unroll
+        for (int c = 0; c < NCH; c++) {
+            const v4f* ip = reinterpret_cast<const v4f*>(inv_s + min((int)threadIdx.x + c * kQThreads, nch - 1) * 8);
+            isc[c][0] = ip[0];
+            isc[c][1] = ip[1];
+        }
+    }
 #pragma unroll
     for (int c = 0; c < NCH; c++) {
         const int idx = threadIdx.x + c * kQThreads;
-        if (idx < nch) {
-            unpack_bf16x8(__builtin_nontemporal_load(xr + idx), v[c]);
-            if (inv_s) {
-                const v4f* ip = reinterpret_cast<const v4f*>(inv_s + idx * 8);
-                v4f i0 = ip[0], i1 = ip[1];
+        unpack_bf16x8(raw[c], v[c]);
+        if (inv_s) {
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    v[c][j] = mul_rn(v[c][j], i0[j]);
-                    v[c][j + 4] = mul_rn(v[c][j + 4], i1[j]);
-                }
+            for (int j = 0; j < 4; j++) {
+                v[c][j] = mul_rn(v[c][j], isc[c][0][j]);
+                v[c][j + 4] = mul_rn(v[c][j + 4], isc[c][1][j]);
             }
+        }
+        if (idx < nch) {
 #pragma unroll
             for (int j = 0; j < 8; j++) amax = fmaxf(amax, fabsf(v[c][j]));
         }
     }
     amax = block_max(amax, red);
+    if (row >= (int64_t)__ldg(n_rows)) return;                 // read after the row's loads went out (see above)
     const float scale = div_rn(fmaxf(amax, 1e-10f), 127.0f);
     v2u* qr = reinterpret_cast<v2u*>(q + row * K);
 #pragma unroll
@@ -99,8 +112,8 @@ __global__ __launch_bounds__(kQThreads) void quant_rows_groups_kernel(const uint
                                                                       int8_t* __restrict__ q, float* __restrict__ s,
                                                                       const int32_t* __restrict__ n_rows, int K,
                                                                       int gk) {
+    kernel_args_now(x, q, s, n_rows, K, gk);
     const int64_t row = blockIdx.y;
-    if (row >= (int64_t)__ldg(n_rows)) return;
     const int idx = blockIdx.x * kQThreads + threadIdx.x;       // chunk of 8 inputs
     const int nch = K / 8, width = gk / 8;
     const bool live = idx < nch;
@@ -112,7 +125,7 @@ __global__ __launch_bounds__(kQThreads) void quant_rows_groups_kernel(const uint
         for (int j = 0; j < 8; j++) amax = fmaxf(amax, fabsf(v[j]));
     }
     for (int o = width / 2; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, kWave));
-    if (!live) return;
+    if (!live || row >= (int64_t)__ldg(n_rows)) return;        // read after the row's loads went out
     const float scale = div_rn(fmaxf(amax, 1e-10f), 127.0f);
     float r[8];
 #pragma unroll
@@ -152,25 +165,29 @@ __global__ __launch_bounds__(kQThreads) void quant_rows_g_kernel(const uint16_t*
                                                                  int8_t* __restrict__ xs,
                                                                  const int32_t* __restrict__ n_rows, int M, int K) {
     __shared__ float red[kQThreads / kWave];
+    kernel_args_now(x, ldx, xq, a, xs, n_rows, M, K);
     const int64_t row = blockIdx.x;
-    if (row >= (int64_t)__ldg(n_rows)) return;
     const int nch = K / 8;
     const v4u* xr = reinterpret_cast<const v4u*>(x + row * ldx);
     float v[NCH][8];
     float amax[NCH];
     float rmax = 0.f;
+    v4u raw[NCH];                                      // all loads first (see rows_q8)
+#pragma unroll
+    for (int c = 0; c < NCH; c++) raw[c] = __builtin_nontemporal_load(xr + min((int)threadIdx.x + c * kQThreads, nch - 1));
 #pragma unroll
     for (int c = 0; c < NCH; c++) {
         const int idx = threadIdx.x + c * kQThreads;
         amax[c] = 0.f;
+        unpack_bf16x8(raw[c], v[c]);
         if (idx < nch) {
-            unpack_bf16x8(__builtin_nontemporal_load(xr + idx), v[c]);
 #pragma unroll
             for (int j = 0; j < 8; j++) amax[c] = fmaxf(amax[c], fabsf(v[c][j]));
         }
         rmax = fmaxf(rmax, amax[c]);
     }
     if (GROUP_ROW) rmax = block_max(rmax, red);
+    if (row >= (int64_t)__ldg(n_rows)) return;                 // read after the row's loads went out
     v2u* qr = reinterpret_cast<v2u*>(xq + row * K);
 #pragma unroll
     for (int c = 0; c < NCH; c++) {

@@ -419,10 +419,14 @@ __global__ __launch_bounds__(64) void w8a8_packed_mid_kernel(const int8_t* __res
                                                               void* __restrict__ out, int64_t ldo,
                                                               const int32_t* __restrict__ n_rows, int M, int N,
                                                               int K) {
+    // every argument fetched at once (else one scalar round trip per first use before the first weight request)
+    asm volatile("" ::"s"(a), "s"(a_s), "s"(as_sm), "s"(qt), "s"(dt), "s"(out), "s"(ldo), "s"(n_rows), "s"(M), "s"(N),
+                 "s"(K));
     const int lane = threadIdx.x & 63, m0 = blockIdx.y * MT * 16;
     const int nt = blockIdx.x;
-    const int live = min(M, __ldg(n_rows));
-    if (m0 >= live) return;
+    // no row-count read before the first requests (it would hold them back by a round trip): workgroups past the
+    // live rows still run, and the stores skip rows >= n_rows
+    if (m0 >= M) return;
     const int KP = K / 64;
     const int li = lane & 15, q = lane >> 4;
     float sa[MT][4];
@@ -508,6 +512,7 @@ __global__ __launch_bounds__(64) void w8a8_packed_mid_kernel(const int8_t* __res
             fold(acc0, ring[d]);
         }
     const int n = 16 * nt + li;
+    const int live = min(M, __ldg(n_rows));
 #pragma unroll
     for (int t = 0; t < MT; t++)
 #pragma unroll

@@ -187,14 +187,16 @@ __global__ __launch_bounds__(512) void w8a8_pc_decode_kernel(const int8_t* __res
                                                               int N, int K, int64_t zstride) {
     constexpr int PD = 4;
     extern __shared__ __attribute__((aligned(16))) v4i red[];          // [NW][G][MT][64]
+    // every argument fetched at once (else one scalar round trip per first use before the first weight request)
+    const int gz = gridDim.z;
+    asm volatile("" ::"s"(a), "s"(a_s), "s"(as_sm), "s"(w), "s"(w_s), "s"(out), "s"(ldo), "s"(n_rows), "s"(M), "s"(N),
+                 "s"(K), "s"(zstride), "s"(gz));
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, NW = blockDim.x >> 6;
     const int nt0 = blockIdx.x * G, r0 = 16 * MT * blockIdx.y;
     const int KP = K / 64, NT = N / 16;
     // split z of gridDim.z takes the 64-input chunks kc0 .. kc1 - 1 (EPI 2: its int32 sums go to slot z)
     const int z = blockIdx.z;
-    const int kc0 = (int)((int64_t)KP * z / gridDim.z), KC = (int)((int64_t)KP * (z + 1) / gridDim.z) - kc0;
-    const int live = min(M, __ldg(n_rows));
-    if (r0 >= live) return;                                             // the whole workgroup: before any barrier
+    const int kc0 = KP * z / gz, KC = KP * (z + 1) / gz - kc0;        // KP * split < 2^31 (host)
     const int lm = lane & 15, q = lane >> 4;
 
     const int8_t* wb[G];
@@ -255,6 +257,11 @@ __global__ __launch_bounds__(512) void w8a8_pc_decode_kernel(const int8_t* __res
 #pragma unroll
         for (int u = 0; u < MT; u++) red[((wv * G + g) * MT + u) * 64 + lane] = acc[g][u];
     __syncthreads();
+    // the live-row count only here: read before the first requests it would hold them back by a round trip, so
+    // every workgroup computes and the stores skip rows >= n_rows (no early exit either: with one after the first
+    // requests this kernel computed wrong sums on MI355X at 8 x 368 x 3008, epilogue 1, a case the random-shape
+    // test holds)
+    const int live = min(M, __ldg(n_rows));
     for (int idx = tid; idx < G * MT * 64; idx += blockDim.x) {
         const int g = idx / (MT * 64), u = (idx >> 6) % MT, l = idx & 63;
         const int m = r0 + 16 * u + (l & 15), t = nt0 + g;
