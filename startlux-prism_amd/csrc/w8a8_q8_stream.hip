@@ -93,8 +93,9 @@ __global__ __launch_bounds__((NW + (MX * 16 + 63) / 64) * 64) void w8a8_q8_strea
     unsigned* wdone = reinterpret_cast<unsigned*>(terms + RD * M * 16 * TL);  // [RD]: compute waves done
     unsigned* fdone = wdone + RD;                                              // [RD]: fold waves done
     const int tstride = M * 16 * TL;
-    // XL: the M activation rows, copied whole into LDS at the start ([M][K] bytes, as they lie), so the register
-    // ring carries only the weight stream
+    // XL: the M activation rows, copied whole into LDS at the start ([M][K + 32] bytes: rows 32 bytes apart in the
+    // banks, so the pieces of four rows a wave reads at once hit distinct banks), so the register ring carries only
+    // the weight stream
     int8_t* xs = dsm + ((RD * M * 16 * TL * 4 + 2 * RD * 4 + 15) & ~15);
 
     // every argument fetched at once: the compiler would otherwise load each where first used, one scalar memory
@@ -189,7 +190,7 @@ __global__ __launch_bounds__((NW + (MX * 16 + 63) / 64) * 64) void w8a8_q8_strea
                     int64_t xf;
                     if (XL) {
                         const int p = min(d.p0 + wv * CP + i, KP - 1);
-                        xf = *reinterpret_cast<const int64_t*>(xs + mc * K + 64 * p + 32 * h + 8 * q);
+                        xf = *reinterpret_cast<const int64_t*>(xs + mc * (K + 32) + 64 * p + 32 * h + 8 * q);
                     } else {
                         const v2u xv = h ? pr[i].x1 : pr[i].x0;
                         xf = (int64_t)xv[0] | ((int64_t)xv[1] << 32);
@@ -229,9 +230,11 @@ __global__ __launch_bounds__((NW + (MX * 16 + 63) / 64) * 64) void w8a8_q8_strea
 #pragma unroll
         for (int e = 0; e < EV; e++) sa[e] = a_s[(int64_t)min(4 * q + e, M - 1) * as_sm];
         if (XL) {
-            const int nx = (M * K + 1023) / 1024;
-            for (int c = wv; c < nx; c += NW)
-                if (c * 1024 + lane * 16 < M * K) dma16(a + c * 1024 + lane * 16, xs + c * 1024);
+            const int cpr = (K + 1023) / 1024, nx = M * cpr;          // 1 KB copies per row, per image
+            for (int c = wv; c < nx; c += NW) {
+                const int m = c / cpr, k0 = (c - m * cpr) * 1024;
+                if (k0 + lane * 16 < K) dma16(a + (int64_t)m * K + k0 + lane * 16, xs + m * (K + 32) + k0);
+            }
         }
         __syncthreads();                          // counters cleared; with XL the activation image is in LDS
         // NR >= 1 (every workgroup has at least one chunk: W <= tiles), so the loop is entered unconditionally and
@@ -324,7 +327,7 @@ __global__ __launch_bounds__((NW + (MX * 16 + 63) / 64) * 64) void w8a8_q8_strea
 
 static size_t stream_lds(int R, int RD, int M, int K, bool xl) {
     const size_t base = (size_t)RD * M * 16 * (R + 4) * 4 + 2 * RD * 4;
-    return xl ? ((base + 15) & ~(size_t)15) + (size_t)M * K : base;
+    return xl ? ((base + 15) & ~(size_t)15) + (size_t)M * (K + 32) : base;
 }
 constexpr size_t kLdsMax = 160 * 1024;
 
@@ -363,7 +366,7 @@ static void launch(const int8_t* a, const float* a_s, int64_t as_sm, const int8_
 #define Q8S_ONE 12, 48, 1, 2, 4
 #endif
 #ifndef Q8S_BIG
-#define Q8S_BIG 8, 32, 16, 2, 3
+#define Q8S_BIG 8, 32, 16, 2, 2
 #endif
 #define QS_(...) QS(__VA_ARGS__)
     if (M == 1) QS_(Q8S_ONE);
