@@ -485,7 +485,7 @@ int launch_w8a8_pc(int kernel, bool wpack, const int8_t* a, const float* a_s, in
 #undef PCT__
 #undef PCT_
 #ifndef PC_DW_NS
-#define PC_DW_NS 4                                // activation stages of the direct-weight tile kernel (0: off)
+#define PC_DW_NS 0                                // activation stages of the direct-weight tile kernel (0: off)
 #endif
     if (wpack && PC_DW_NS > 0) {
         constexpr int DNS = PC_DW_NS > 0 ? PC_DW_NS : 2;
