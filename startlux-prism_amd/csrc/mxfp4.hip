@@ -248,6 +248,7 @@ __global__ __launch_bounds__(MT == 1 ? 1024 : 512) void mx_decode_kernel(const u
                                                          int64_t ldo, const int32_t* __restrict__ n_rows, int M,
                                                          int K) {
     extern __shared__ __attribute__((aligned(16))) v4f part[];    // [nseg][MT][64]
+    kernel_args_now(aq, as, wq, ws, out, ldo, n_rows, M, K);
     const int t = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6, NW = blockDim.x >> 6;
     const int KS = K / kMxStep, nseg = (KS + kMxSegSteps - 1) / kMxSegSteps;
     const int live = n_rows ? min(M, __ldg(n_rows)) : M;
@@ -512,6 +513,7 @@ __global__ __launch_bounds__(1024) void mx_decode_staged_kernel(const uint8_t* _
     uint8_t* act = lds;                                               // [SL][16][kDecRow]
     uint8_t* asl = lds + SL * kDecActSlot;                            // [SL][16][32]
     v4f* part = reinterpret_cast<v4f*>(asl + SL * kDecScaleSlot);     // [SL][NTG][64]
+    kernel_args_now(aq, as, wq, ws, out, ldo, n_rows, M, K, SL);
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int nt = w % NTG, sl = w / NTG;
     const int t = blockIdx.x * NTG + nt;

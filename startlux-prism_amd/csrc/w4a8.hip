@@ -180,6 +180,7 @@ __global__ __launch_bounds__(NW * 64, 2) void w4a8_q6k_decode_kernel(const int8_
                                                                   // round r - 1 while round r + 1 is staged
     const int tstride = R * M * 16, xstride = M * LDA;
 
+    kernel_args_now(xq, a, a_sb, qv, meta, out, ldo, n_rows, M, N, K);
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int nt = blockIdx.x;
     const int live = min(M, __ldg(n_rows));
@@ -350,6 +351,7 @@ __global__ __launch_bounds__(NW * 64) void w4a8_q4k_stream_kernel(const int8_t* 
     const int m = min(lm, M - 1);
 
     const v4u* cw = reinterpret_cast<const v4u*>(qv) + (int64_t)nt * NB * 128 + lane;
+    kernel_args_now(xq, a, a_sb, xs, qv, meta, out, ldo, n_rows, M, K);
     const v4u* cm = reinterpret_cast<const v4u*>(meta) + (int64_t)nt * NB * 16 + lm;
     const int8_t* cx = xq + (int64_t)m * K + 16 * q;
     struct SB {
@@ -452,6 +454,7 @@ __global__ __launch_bounds__(NW * 64) void w4a8_q6k_stream_kernel(const int8_t* 
     const int m = min(lm, M - 1);
 
     const v4u* cw = reinterpret_cast<const v4u*>(qv) + (int64_t)nt * NB * 256 + lane;
+    kernel_args_now(xq, a, a_sb, qv, meta, out, ldo, n_rows, M, K);
     const uint8_t* cm = meta + (int64_t)nt * NB * Q6_META;
     const int8_t* cx = xq + (int64_t)m * K + 8 * q;
     struct SB {

@@ -86,6 +86,7 @@ __global__ __launch_bounds__((NW + FW) * 64) void w8a8_packed_decode_kernel(cons
     int8_t* xs = reinterpret_cast<int8_t*>(sws + 2 * R * 16);                  // [2][M][LDA]
     const int tstride = R * M * 16, xstride = M * LDA;
 
+    kernel_args_now(a, a_s, as_sm, qt, dt, out, ldo, n_rows, M, N, K);
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int nt = blockIdx.x;
     const int live = min(M, __ldg(n_rows));
