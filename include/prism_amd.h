@@ -192,12 +192,18 @@ PRISM_API int prism_q4k_pack(const uint8_t* raw, uint8_t* qv, uint8_t* meta, int
  *   epi 0: bf16(y); epi 1: out = RN(out + y).
  * xq int8 [M, K]; a fp32, element (b, m) at a[b * a_sb + m] (a_sb = 0: one scale per token); xs int8 [K/256, M, 16]
  * (per super-block eight S & 63 then eight S >> 6); qv / meta from prism_q4k_pack; out row stride ldo.
- * kernel: -1 picks by M; 0 the prefill tile kernel; 1 the decode kernel (M <= 16; the tile kernel when its per-
- * super-block terms, K/256 x M x 64 bytes, exceed the 160 KB of LDS).  Needs K % 256 == 0, N % 16 == 0.
+ * kernel: -1 picks by M (2 up to 16 rows where it applies, else 1, beyond 16 rows 0); 0 the prefill tile kernel;
+ * 1 the per-tile decode kernel (M <= 16; the tile kernel when its per-super-block terms, K/256 x M x 64 bytes, exceed
+ * the 160 KB of LDS); 2 the balanced-grid decode kernel (M <= 16 with M (K + 32) + K M / 8 bytes of activation image
+ * within LDS; equal shares of the weights per CU, running sums handed between workgroups through `workspace`).
+ * workspace: for kernel 2, a zero-initialised device buffer of at least prism_w8a8_q8_0_packed_workspace_bytes(N, K)
+ * bytes (the same size rule as the Q8_0 one), left zeroed by every call; may be null for the other kernels.  Calls
+ * sharing one workspace must not overlap in time.  Needs K % 256 == 0, N % 16 == 0.
  */
 PRISM_API int prism_w4a8_q4k_gemm(const int8_t* xq, const float* a, int64_t a_sb, const int8_t* xs, const uint8_t* qv,
                                   const uint8_t* meta, void* out, int64_t ldo, const int32_t* n_rows, int64_t M,
-                                  int64_t N, int64_t K, int epi, int kernel, void* stream);
+                                  int64_t N, int64_t K, int epi, int kernel, void* workspace, int64_t workspace_bytes,
+                                  void* stream);
 
 /*
  * Repack Q6_K weights for the W4A8 kernels (the load-time step of kernels/w4a8.py:82-90, repack "q6k", which keeps

@@ -19,62 +19,10 @@
 // Activations: xq int8 [M, K] row-major; a fp32, (b, m) at a[b a_sb + m] (a_sb = 0: one scale per token);
 // xs int8 [K/256, M, 16]: per super-block the eight S & 63 then the eight S >> 6 (kernels/quant.py:314-330).
 #include "common.h"
+#include "w4a8_bal.h"
+#include "w4a8_common.h"
 
 namespace prism {
-
-typedef unsigned short us2 __attribute__((ext_vector_type(2)));
-
-// A lane's 8 bytes of a sub-block pair (w0, w1) times its sub-block scale sc = 8 hi + lo (3-bit parts, given packed
-// as split_scale(sc) = lo | hi << 16) as two MFMA weight operands: the 16 nibbles (<= 15) times lo and times hi
-// (<= 105: still int8, no carry between bytes of a packed 16-bit multiply).  acc = (x . lo q) + 8 (x . hi q) exactly.
-__device__ __forceinline__ uint32_t split_scale(int sc) { return (uint32_t)(sc & 7) | ((uint32_t)(sc >> 3) << 16); }
-
-__device__ __forceinline__ void two_plane(uint32_t w0, uint32_t w1, uint32_t sp, v4i& lo, v4i& hi) {
-    const us2 s = __builtin_bit_cast(us2, sp);
-    const us2 sl = __builtin_shufflevector(s, s, 0, 0), sh = __builtin_shufflevector(s, s, 1, 1);
-    const uint32_t n[4] = {w0 & 0x0f0f0f0fu, w1 & 0x0f0f0f0fu, (w0 >> 4) & 0x0f0f0f0fu, (w1 >> 4) & 0x0f0f0f0fu};
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-        lo[e] = (int)__builtin_bit_cast(uint32_t, (us2)(__builtin_bit_cast(us2, n[e]) * sl));
-        hi[e] = (int)__builtin_bit_cast(uint32_t, (us2)(__builtin_bit_cast(us2, n[e]) * sh));
-    }
-}
-
-// mins = sum_g mn[n, g] S[m, g] for a 16 x 16 tile as two MFMAs over k = 0..7 (lanes q > 0 carry zeros): the weight
-// rows' 8 mins (bytes) against the 8 low parts S & 63, then against the 8 high parts S >> 6; mins = lo + 64 hi.
-__device__ __forceinline__ v4i mins_mfma(int64_t mn8, int64_t slo, int64_t shi) {
-    const v4i zero = {0, 0, 0, 0};
-    const v4i lo = __builtin_amdgcn_mfma_i32_16x16x32_i8(mn8, slo, zero, 0, 0, 0);
-    const v4i hi = __builtin_amdgcn_mfma_i32_16x16x32_i8(mn8, shi, zero, 0, 0, 0);
-    v4i r;
-#pragma unroll
-    for (int e = 0; e < 4; e++) r[e] = lo[e] + 64 * hi[e];
-    return r;
-}
-
-// Q6_K meta per (16-row tile, super-block): the 16 rows' 16 int8 scales, then their fp16 d.
-constexpr int Q6_META = 288;
-
-__device__ __forceinline__ int sbyte(v4u m, int j) { return (int)(int8_t)(m[j >> 2] >> (8 * (j & 3))); }
-
-// One row's 16 meta bytes -> d, dmin (fp32) and the 8 scales and 8 mins (ggml get_scale_min_k4).
-__device__ __forceinline__ void row_meta(v4u m, float& d, float& dm, int* sc, int* mn) {
-    d = f16_to_f32(m[0] & 0xffffu);
-    dm = f16_to_f32(m[0] >> 16);
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const uint32_t s0 = (m[1] >> (8 * j)) & 0xff, s4 = (m[2] >> (8 * j)) & 0xff, s8 = (m[3] >> (8 * j)) & 0xff;
-        sc[j] = s0 & 63;
-        mn[j] = s4 & 63;
-        sc[j + 4] = (s8 & 0xf) | ((s0 >> 6) << 4);
-        mn[j + 4] = (s8 >> 4) | ((s4 >> 6) << 4);
-    }
-}
-
-// t = RN(d float(acc)); t = fma(-dm, float(mins), t)   (kernels/w4a8.py:191)
-__device__ __forceinline__ float q4k_term(float d, float dm, int acc, int mins) {
-    return fmaf(-dm, (float)mins, mul_rn(d, (float)acc));
-}
 
 // ---------------------------------------------------------------------------------------------- pack
 // One thread per (nt, b, h, l): gathers 4 sub-blocks x 4 bytes from the GGUF block of row 16 nt + l % 16.
@@ -896,18 +844,31 @@ extern "C" int prism_q4k_pack(const uint8_t* raw, uint8_t* qv, uint8_t* meta, in
 extern "C" int prism_w4a8_q4k_gemm(const int8_t* xq, const float* a, int64_t a_sb, const int8_t* xs,
                                    const uint8_t* qv, const uint8_t* meta, void* out, int64_t ldo,
                                    const int32_t* n_rows, int64_t M, int64_t N, int64_t K, int epi, int kernel,
-                                   void* stream) {
+                                   void* workspace, int64_t workspace_bytes, void* stream) {
     if (!xq || !a || !xs || !qv || !meta || !out || !n_rows) return PRISM_ERR_ARG;
     if (epi != 0 && epi != 1) return PRISM_ERR_ARG;
     if (M < 0 || N <= 0 || K <= 0 || N % 16 || K % 256 || ldo < N || M > (1 << 30) || N > (1 << 30) || K > (1 << 30))
         return PRISM_ERR_SHAPE;
     if (!PRISM_ALIGNED(xq, 16) || !PRISM_ALIGNED(xs, 16) || !PRISM_ALIGNED(qv, 16) || !PRISM_ALIGNED(meta, 16))
         return PRISM_ERR_ALIGN;
-    if (kernel < -1 || kernel > 1) return PRISM_ERR_ARG;
-    if (kernel == -1) kernel = M <= 16 ? 1 : 0;
+    if (kernel < -1 || kernel > 2) return PRISM_ERR_ARG;
+    const bool can_bal = q4k_bal_fits(M, N, K) && workspace && workspace_bytes >= q4k_bal_workspace_bytes(N);
+    // by default up to 16 rows: the balanced kernel for projections of fewer than two 16-row tiles per CU (where a
+    // tile per workgroup leaves CUs with one tile more than others: 5120 x 17408, 16 -> 1 rows 15.96 us against
+    // 18.73 us), given its workspace; the per-tile kernel otherwise (13824 x 5120: 12.9 us against 16.0 us); the tile
+    // kernel beyond 16 rows
+    if (kernel == -1) kernel = M >= 1 && M <= 16 ? (can_bal && N / 16 < 512 ? 2 : 1) : 0;
     if (kernel == 1 && M > 16) return PRISM_ERR_ARG;
+    if (kernel == 2 && !can_bal) return M > 16 || !q4k_bal_fits(M, N, K) ? PRISM_ERR_SHAPE : PRISM_ERR_ARG;
     if (M == 0) return PRISM_OK;
     hipStream_t st = (hipStream_t)stream;
+    if (kernel == 2) {
+        const int rc = q4k_bal_launch(xq, a, a_sb, xs, qv, meta, out, ldo, n_rows, M, N, K, epi, workspace,
+                                      workspace_bytes, st);
+        if (rc != PRISM_OK) return rc;
+        PRISM_LAUNCH_CHECK();
+        return PRISM_OK;
+    }
     const int Mi = (int)M, Ni = (int)N, Ki = (int)K;
     if (kernel == 1) {
         // Q4_K decode: the stream kernel, 8 waves for long K or narrow projections (few workgroups), else 4

@@ -20,59 +20,12 @@
 // Measured on MI355X: twelve compute waves per workgroup (not eight, nor more) for one to four rows; a ring deeper
 // than one round ahead and rounds of other sizes were slower.
 //
-// Handoff protocol (per output word, never leaves a word set after a launch): the producer writes (1 << 32) | bits
-// with a compare-and-swap from 0 (whose result it checks only at its end); the consumer takes the bits, normally read
-// one round ahead, else by polling, and clears the word.  A consumer that polls past its bound (a predecessor that
-// never ran: not expected, every predecessor is dispatched first and publishes before it waits on anything) swaps in
-// an "abandoned" tag and takes its value if the producer had just finished, or yields NaN outputs (loud, never
-// silently wrong); a producer that finds "abandoned" clears the word.
+// The walk over a range and the handoff protocol between neighbouring workgroups are handoff.h's.
 #include "common.h"
+#include "handoff.h"
 #include "q8_stream.h"
 
 namespace prism {
-
-constexpr unsigned long long kTagValid = 1ull << 32, kTagAbandoned = 2ull << 32;
-
-__device__ __forceinline__ unsigned long long hand_load(unsigned long long* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void hand_store(unsigned long long* p, unsigned long long v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Takes the previous workgroup's y (bounded wait).
-__device__ __forceinline__ float hand_take(unsigned long long* p) {
-    for (int it = 0; it < (1 << 22); it++) {
-        const unsigned long long v = hand_load(p);
-        if ((v >> 32) == 1) {
-            hand_store(p, 0);
-            return __uint_as_float((uint32_t)v);
-        }
-        __builtin_amdgcn_s_sleep(2);
-    }
-    const unsigned long long old = __hip_atomic_exchange(p, kTagAbandoned, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if ((old >> 32) == 1) {
-        hand_store(p, 0);
-        return __uint_as_float((uint32_t)old);
-    }
-    return __uint_as_float(0x7fc00000u);
-}
-
-// One round of a workgroup's walk: tile nt, block pairs p0 .. p0 + np - 1 of it; `first` / `last`: the round opens /
-// closes a fragment (the tile's part inside this workgroup's range), whose pairs are ps .. pe - 1.
-struct Round {
-    int nt, p0, np, ps, pe;
-    bool first, last;
-};
-
-// Bounded wait on an LDS counter (workgroup scope): every wave of the workgroup is resident, so the counter's
-// producers always progress; the bound only keeps a broken launch from spinning forever.
-__device__ __forceinline__ void lds_wait_ge(unsigned* c, unsigned target) {
-    for (int it = 0; it < (1 << 24); it++) {
-        if (__hip_atomic_load(c, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) return;
-        __builtin_amdgcn_s_sleep(1);
-    }
-}
 
 template <int NW, int R, int MX, int D, int RD, int EPI, bool XL>
 __global__ __launch_bounds__((NW + (MX * 16 + 63) / 64) * 64) void w8a8_q8_stream_kernel(
@@ -110,37 +63,10 @@ __global__ __launch_bounds__((NW + (MX * 16 + 63) / 64) * 64) void w8a8_q8_strea
     // barrier, and no global load the first weight requests would wait behind, before those requests go out)
     if (tid < 2 * RD) wdone[tid] = 0;
 
-    // this workgroup's range of chunks and its fragments, walked from the last tile to the first: ranges of
-    // total / W or one more chunks (the host keeps total below 2^31, so the arithmetic is 32-bit)
-    const int total = (N / 16) * KP;
-    const int cq = total / W, cr = total - cq * W;
-    const int c0 = v * cq + min(v, cr), c1 = c0 + cq + (v < cr ? 1 : 0);
-    const int nt_lo = c0 / KP, nt_hi = (c1 - 1) / KP;
-    const int ps_lo = c0 - nt_lo * KP, pe_hi = c1 - nt_hi * KP;
-    const int RT = (KP + RP - 1) / RP;
-    const int ps_hi = nt_hi == nt_lo ? ps_lo : 0;
-    const int r_hi = (pe_hi - ps_hi + RP - 1) / RP;
-    const int nmid = max(0, nt_hi - nt_lo - 1);
-    const int r_lo = nt_lo < nt_hi ? (KP - ps_lo + RP - 1) / RP : 0;
-    const int NR = r_hi + nmid * RT + r_lo;
-    auto round_of = [&](int rho) -> Round {
-        Round d;
-        int lr;
-        if (rho < r_hi) {
-            d.nt = nt_hi, d.ps = ps_hi, d.pe = pe_hi, lr = rho;
-        } else if (rho - r_hi < nmid * RT) {
-            const int x = rho - r_hi;
-            d.nt = nt_hi - 1 - x / RT, d.ps = 0, d.pe = KP, lr = x % RT;
-        } else {
-            d.nt = nt_lo, d.ps = ps_lo, d.pe = KP, lr = rho - r_hi - nmid * RT;
-        }
-        d.p0 = d.ps + lr * RP;
-        d.np = max(0, min(RP, d.pe - d.p0));
-        d.first = lr == 0;
-        d.last = d.p0 + RP >= d.pe;
-        if (rho >= NR) d.np = 0, d.first = d.last = false;     // prefetch past the end: clamped, unused
-        return d;
-    };
+    // this workgroup's range of chunks (units: block pairs), walked from the last tile to the first
+    const Walk walk(N / 16, KP, RP, W, v);
+    const int NR = walk.NR;
+    auto round_of = [&](int rho) -> Round { return walk.round(rho); };
 
     if (wv < NW) {
         // Compute wave: per round its CP block pairs; per lane and pair the weight chunk's 16-byte slot, the four
@@ -300,10 +226,7 @@ __global__ __launch_bounds__((NW + (MX * 16 + 63) / 64) * 64) void w8a8_q8_strea
                 if (d.last) {
                     if (d.pe < KP) {
                         pub = hand + (int64_t)v * (MX * 16) + fo;
-                        pub_old = 0;
-                        __hip_atomic_compare_exchange_strong(pub, &pub_old, kTagValid | __float_as_uint(y),
-                                                             __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                                             __HIP_MEMORY_SCOPE_AGENT);
+                        pub_old = hand_publish(pub, y);
                     } else {
                         const int m = fo >> 4, n = 16 * d.nt + (fo & 15);
                         if (m < live) {

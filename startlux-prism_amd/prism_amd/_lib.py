@@ -28,7 +28,8 @@ _SIGS = {
     "prism_w8a8_q8_0_packed_gemm_noalloc": (_int, [_p, _p, _i64, _p, _p, _p, _i64, _p, _i64, _i64, _i64, _int, _int,
                                                    _p]),
     "prism_q4k_pack": (_int, [_p, _p, _p, _i64, _i64, _p]),
-    "prism_w4a8_q4k_gemm": (_int, [_p, _p, _i64, _p, _p, _p, _p, _i64, _p, _i64, _i64, _i64, _int, _int, _p]),
+    "prism_w4a8_q4k_gemm": (_int, [_p, _p, _i64, _p, _p, _p, _p, _i64, _p, _i64, _i64, _i64, _int, _int, _p, _i64,
+                                   _p]),
     "prism_q6k_pack": (_int, [_p, _p, _p, _i64, _i64, _p]),
     "prism_w4a8_q6k_gemm": (_int, [_p, _p, _i64, _p, _p, _p, _i64, _p, _i64, _i64, _i64, _int, _int, _p]),
     "prism_i8_pack": (_int, [_p, _p, _i64, _i64, _p]),

@@ -18,6 +18,7 @@ import time
 
 import torch
 
+from . import _lib as L
 from . import dispatch
 from . import gguf_formats as GF
 from . import w4a8 as KW4
@@ -66,7 +67,12 @@ def _time(launch, copies, iters=20, reps=3):
 def _pick(cands, launch_for, copies, M):
     if len(cands) == 1:
         return cands[0], {}
-    us = {c: _time(launch_for(c), copies if M <= 256 else 1, iters=20 if M <= 256 else 5) for c in cands}
+    us = {}
+    for c in cands:
+        try:
+            us[c] = _time(launch_for(c), copies if M <= 256 else 1, iters=20 if M <= 256 else 5)
+        except L.PrismError:         # not valid at this shape (e.g. an activation image beyond LDS)
+            continue
     return min(us, key=us.get), us
 
 
@@ -130,7 +136,7 @@ def tune_w4(shapes, Ms, dev, log):
             xs = torch.randint(-64, 64, (K // 256, M, 16), generator=g, dtype=torch.int8, device=dev)
             out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
             n = torch.tensor([M], dtype=torch.int32, device=dev)
-            cands = (["decode", "stream", "tile"] if kind == "q6k" else ["decode", "tile"]) if M <= 16 else ["tile"]
+            cands = ["decode", "stream", "tile"] if M <= 16 else ["tile"]
             best, us = _pick(cands, lambda c: (lambda i: KW4.gemm(xq, a, xs, ws[i], out, n, kernel=c)), len(ws), M)
             row[str(M)] = [best]
             if us:

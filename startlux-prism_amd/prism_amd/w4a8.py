@@ -22,10 +22,13 @@ import torch
 
 from . import _lib as L
 from . import dispatch
+from . import w8a8 as KW8
 from .gguf_formats import KQuant, Q4_K_BYTES, Q6_K_BYTES, kquant_kind
 
 QK_K = 256
-KERNELS = {"auto": -1, "tile": 0, "decode": 1, "stream": 2}   # "stream": Q6_K only
+# "stream": on Q6_K the per-tile stream kernel, on Q4_K the balanced-grid kernel (up to 16 rows, its activation image
+# within LDS, with the device workspace of w8a8.workspace)
+KERNELS = {"auto": -1, "tile": 0, "decode": 1, "stream": 2}
 
 
 class W4(NamedTuple):
@@ -148,10 +151,8 @@ def gemm(xq, a, xs, w: W4, out, n_rows, epi=0, cfg=None, pdl=0, kernel="auto"):
         raise ValueError(f"out must be {want} [>= {M}, >= {w.n}] with unit column stride")
     if kernel == "auto":             # the MI355X table's choice for the shape, where valid (dispatch.w4a8_kernel)
         c = dispatch.w4a8_kernel(w.kind, w.n, K, M)
-        ok = c == "tile" or (c == "decode" and M <= 16) or (c == "stream" and M <= 16 and w.kind == "q6k")
+        ok = c == "tile" or (c in ("decode", "stream") and M <= 16)
         kernel = c if ok else "auto"
-    if kernel == "stream" and w.kind != "q6k":
-        raise ValueError("the stream decode kernel is Q6_K's; Q4_K's decode kernel is already of that form")
     if w.kind == "q6k":              # no mins: xs is not read
         L.call("prism_w4a8_q6k_gemm", L.ptr(xq), L.ptr(a), a_sb, L.ptr(w.qv), L.ptr(w.meta), L.ptr(out),
                out.stride(0), L.ptr(n_rows), M, w.n, K, epi, KERNELS[kernel], L.stream_of(xq))
@@ -161,5 +162,10 @@ def gemm(xq, a, xs, w: W4, out, n_rows, epi=0, cfg=None, pdl=0, kernel="auto"):
     Mx = xs.shape[1]
     if Mx != M:
         raise ValueError("xs rows must equal xq rows")
+    ws = KW8.workspace(xq.device) if M <= 16 and kernel in ("auto", "stream") else None
+    if kernel == "stream" and ws is None:
+        raise L.PrismError('kernel "stream" needs the device workspace, made outside graph capture: run one eager '
+                           'call first')
     L.call("prism_w4a8_q4k_gemm", L.ptr(xq), L.ptr(a), a_sb, L.ptr(xs), L.ptr(w.qv), L.ptr(w.meta), L.ptr(out),
-           out.stride(0), L.ptr(n_rows), M, w.n, K, epi, KERNELS[kernel], L.stream_of(xq))
+           out.stride(0), L.ptr(n_rows), M, w.n, K, epi, KERNELS[kernel], L.ptr(ws), 0 if ws is None else ws.numel(),
+           L.stream_of(xq))

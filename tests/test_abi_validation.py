@@ -52,13 +52,17 @@ def test_pack_checks_match_the_gemms(lib):
 def test_w4a8_q4k_gemm_checks(lib):
     f = lib.prism_w4a8_q4k_gemm
 
-    def call(xq=P, qv=P, M=16, N=64, K=512, epi=0, kernel=-1):
-        return f(xq, P, 0, P, qv, P, P, N, P, M, N, K, epi, kernel, None)
+    def call(xq=P, qv=P, M=16, N=64, K=512, epi=0, kernel=-1, ws=None, ws_bytes=0):
+        return f(xq, P, 0, P, qv, P, P, N, P, M, N, K, epi, kernel, ws, ws_bytes, None)
     assert call(xq=None) == ARG
     assert call(K=384) == SHAPE                  # K % 256
     assert call(qv=U) == ALIGN
     assert call(epi=3) == ARG
-    assert call(kernel=2) == ARG                 # the stream kernel is Q6_K's
+    assert call(kernel=3) == ARG
+    assert call(kernel=2) == ARG                 # the balanced kernel needs its workspace
+    assert call(kernel=2, ws=P, ws_bytes=64) == ARG                  # too small: 4 workgroups x 2 KB
+    assert call(kernel=2, M=17, ws=P, ws_bytes=1 << 20) == SHAPE     # at most 16 rows
+    assert call(kernel=2, K=1 << 16, ws=P, ws_bytes=1 << 20) == SHAPE  # the activation image exceeds LDS
     assert call(kernel=1, M=17) == ARG
     assert call(M=0) == OK
 

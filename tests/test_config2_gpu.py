@@ -74,7 +74,7 @@ def test_config3_decode_full_n(dev):
     want = O.w4a8_gemm(xq, a[0].copy(), xs, O.q4k_repack(blocks), nthreads=16)
     w = KW4.repack(GF.KQuant(_t(blocks, dev), GF.GGML_Q4_K, K))
     n = torch.tensor([M], dtype=torch.int32, device=dev)
-    for kernel in ("auto", "decode"):
+    for kernel in ("auto", "decode", "stream"):
         print(f"config 3 M=16 full N kernel={kernel}", flush=True)
         out = torch.full((M, N), 7, dtype=torch.int16, device=dev).view(torch.bfloat16)
         KW4.gemm(_t(xq, dev), _t(a, dev), _t(xs, dev), w, out, n, kernel=kernel)

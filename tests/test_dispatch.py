@@ -67,5 +67,8 @@ def test_committed_tables_well_formed(path):
             assert len(parts) == 2 and int(parts[0]) % 16 == 0
         for m, choice in row.items():
             assert choice[0] in LIMITS[prefix] and int(m) <= LIMITS[prefix][choice[0]], (key, m, choice)
-            # W4A8: the stream kernel is Q6_K's only
-            assert prefix != "w4a8_table" or choice[0] != "stream" or parts[0] == "q6k", (key, m, choice)
+            # W4A8 on Q4_K: the balanced stream kernel needs its activation image in LDS (M (K + 32) bytes and the
+            # sums, scales and terms, within 160 KB)
+            if prefix == "w4a8_table" and choice[0] == "stream" and parts[0] == "q4k":
+                M, K = int(m), int(parts[2])
+                assert M * (K + 32) + K // 16 * M + K // 64 * M + 3 * 12 * M * 64 + 64 <= 160 * 1024, (key, m)

@@ -119,7 +119,7 @@ def test_w4a8(dev, kind):
     rq, ra, rxs = O.quant_rows_g(O.bf16_to_f32(xb), 256)
     want = (O.w4a8_gemm(rq, ra, rxs, O.q4k_repack(blocks)) if kind == "q4k" else
             O.w4a8_gemm_q6k(rq, ra, O.q6k_repack(blocks)))
-    kernels = ("auto", "decode", "tile") + (("stream",) if kind == "q6k" else ())
+    kernels = ("auto", "decode", "tile", "stream")
     for kernel in kernels:
         rows = M if kernel in ("auto", "tile") else 16     # the decode / stream kernels serve up to 16 rows
         xq = torch.zeros(rows, K, dtype=torch.int8, device=dev)

@@ -85,7 +85,7 @@ def test_w4a8_q4k_random(dev, case):
     from prism_amd import w4a8 as KW4
     g = rng(3000 + case)
     M, live, N, K, epi = _draw(g, 256, 6144)
-    kernel = str(g.choice(["tile"] + (["decode"] if M <= 16 else [])))
+    kernel = str(g.choice(["tile"] + (["decode", "stream"] if M <= 16 else [])))
     group = int(g.choice([256, K]))
     blocks = O.q4k_quantize(weights_f32(N, K, seed=case + 7))
     xq, a, xs = O.quant_rows_g(O.bf16_to_f32(acts_bf16(M, K, seed=case + 8)), group)

@@ -90,6 +90,12 @@ def _gemm(dev, w, xq, a, xs, epi, kernel, live=None, out0=None):
     return out
 
 
+def _bal_fits(M, K):
+    """The balanced kernel's LDS rule: activation image M (K + 32), sums K M / 16, scales K M / 64, terms 2.3 KB per
+    row (12 units x 3 rounds x 16 outputs x 4 bytes)."""
+    return M * (K + 32) + K // 16 * M + K // 64 * M + 3 * 12 * M * 64 + 64 <= 160 * 1024
+
+
 CASES = [  # (M, N, K, live, group)
     (1, 16, 256, 1, 256), (4, 64, 1024, 3, 256), (16, 128, 5120, 16, 256), (16, 256, 5120, 16, 5120),
     (7, 48, 2560, 5, 256), (64, 128, 1024, 64, 256), (100, 272, 768, 77, 256), (130, 128, 2048, 130, 2048),
@@ -108,7 +114,7 @@ def test_gemm_bit_exact(dev, M, N, K, live, group):
     base = rng(M + N).standard_normal((M, N)).astype(np.float32)
     want1 = O.w4a8_gemm(xq, ao, xs, W, epi=1, out=base.copy(), live=live)
     w = _w4(dev, blocks)
-    for kernel in ["tile"] + (["decode"] if M <= 16 else []):
+    for kernel in ["tile"] + (["decode", "stream"] if M <= 16 and _bal_fits(M, K) else ["decode"] if M <= 16 else []):
         got0 = _gemm(dev, w, xq, a, xs, 0, kernel, live=live).view(torch.int16).cpu().numpy().view(np.uint16)
         assert np.array_equal(got0[:live], want0[:live]), kernel
         assert (got0[live:] == 7).all(), kernel
@@ -122,7 +128,7 @@ def test_config3_decode_slice_bit_exact(dev):
     W = O.q4k_repack(blocks)
     want = O.w4a8_gemm(xq, a[0].copy(), xs, W, epi=0)
     w = _w4(dev, blocks)
-    for kernel in ("decode", "tile"):
+    for kernel in ("decode", "stream", "tile"):
         got = _gemm(dev, w, xq, a, xs, 0, kernel).view(torch.int16).cpu().numpy().view(np.uint16)
         assert np.array_equal(got, want), kernel
 
@@ -143,14 +149,17 @@ def test_integer_sums_exact(dev):
     _, acc, mins = O.w4a8_gemm(x, a, xs, W, epi=1, out=np.zeros((M, N), np.float32), sums=True)
     want = (acc.astype(np.int64) - mins).sum(-1)
     w = _w4(dev, blocks)
-    for kernel in ("decode", "tile"):
+    for kernel in ("decode", "stream", "tile"):
         got = _gemm(dev, w, x, a, xs, 1, kernel, out0=np.zeros((M, N), np.float32)).cpu().numpy()
         assert np.array_equal(got.astype(np.int64), want), kernel
 
 
-def test_stream_kernel_is_q6k_only(dev):
-    """kernel="stream" names Q6_K's stream decode; asking it of Q4_K weights is an error, not a silent fallback."""
-    from prism_amd import w4a8 as KW4
-    blocks, xq, a, xs = _case(32, 512, 2, seed=77)
-    with pytest.raises(ValueError):
+def test_stream_kernel_limits(dev):
+    """kernel="stream" on Q4_K weights is the balanced-grid kernel: more than 16 rows, or an activation image beyond
+    LDS, is an error rather than a silent fallback."""
+    blocks, xq, a, xs = _case(32, 512, 17, seed=77)
+    with pytest.raises(Exception):
+        _gemm(dev, _w4(dev, blocks), xq, a, xs, 0, "stream")
+    blocks, xq, a, xs = _case(16, 41216, 16, seed=78)
+    with pytest.raises(Exception):
         _gemm(dev, _w4(dev, blocks), xq, a, xs, 0, "stream")
