@@ -169,152 +169,6 @@ __global__ __launch_bounds__(64 * NWV, TM == 128 ? 2 : 1) void w8a8_pc_tile_kern
     }
 }
 
-// ---------------------------------------------------------------------------------------------- tile, direct weights
-// Packed weights only.  The same 128 x 256 tile and 128 x 64 waves (wave w: columns 64 w .. + 63, all 128 rows),
-// but only the activation operand goes through LDS (LDS-DMA, NS stages of 64 inputs, read by all four waves); each
-// wave's weight fragments are its own columns, so they come straight from the packed chunks into registers, NS - 1
-// stages ahead.  For a 32-input step s a lane (r = l % 32, h = l / 32) needs inputs 16 (2 s + h) .. + 15 of weight row
-// r: the chunk's lane slot 2 s + h of that row, sixteen lanes reading 256 contiguous bytes.  Against the kernel
-// above this halves the LDS traffic per MFMA (the DMA writes and fragment reads of the weight operand are gone),
-// which bound it: there a stage moved 72 KB through LDS per 64 MFMAs of the workgroup, here 40 KB.
-template <bool WS16, int EPI, int NS>
-__global__ __launch_bounds__(256, 2) void w8a8_pc_tile_dw_kernel(const int8_t* __restrict__ a,
-                                                                 const float* __restrict__ a_s, int64_t as_sm,
-                                                                 const int8_t* __restrict__ w,
-                                                                 const void* __restrict__ w_s, void* __restrict__ out,
-                                                                 int64_t ldo, const int32_t* __restrict__ n_rows,
-                                                                 int M, int N, int K, int tiles_m, int tiles_n) {
-    constexpr int TM = 128, AOPER = TM * PCK;                       // activation bytes per stage (8 KB)
-    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];   // NS x [A TM x 64]
-    __shared__ float sal[TM], swl[PCT];
-    static_assert(NS >= 2 && NS * AOPER + (TM + PCT) * sizeof(float) <= 80 * 1024, "two workgroups per CU");
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    int pm, pn;
-    xcd_tile_coords(blockIdx.x, tiles_m, tiles_n, pm, pn);
-    const int m0 = pm * TM, n0 = pn * PCT;
-    const int live = min(M, __ldg(n_rows));
-    if (m0 >= live) return;
-    const int KS = K / PCK, NT = N / 16;
-
-    if (tid < TM) sal[tid] = a_s[(int64_t)min(m0 + tid, M - 1) * as_sm];
-    {
-        const int n = min(n0 + tid, N - 1);
-        swl[tid] = WS16 ? f16_to_f32(static_cast<const uint16_t*>(w_s)[n]) : static_cast<const float*>(w_s)[n];
-    }
-
-    // activation DMA: two 16-row x 64-byte instructions per wave and stage (lane L: row L / 4, 16-byte chunk L % 4
-    // XOR-swizzled by row, as the kernel above)
-    const int8_t* asrc[2];
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-        const int row = 16 * (2 * wv + i) + (lane >> 2);
-        asrc[i] = a + (int64_t)min(m0 + row, M - 1) * K + 16 * ((lane & 3) ^ pc_swz(row));
-    }
-    const int r = lane & 31, h = lane >> 5;
-    // weight fragment sources: subtile u's rows 64 wv + 32 u + r, chunk slot 2 s + h
-    const int8_t* wsrc[2];
-#pragma unroll
-    for (int u = 0; u < 2; u++) {
-        const int row = n0 + 64 * wv + 32 * u + r;
-        const int t = min(row >> 4, NT - 1);
-        wsrc[u] = w + (int64_t)t * KS * 1024 + (16 * h + (row & 15)) * 16;
-    }
-    struct WStage {
-        v4i f[2][2];                                                // [step][subtile]
-    };
-    // stage indices past the end are clamped (the copies land in buffers no later stage reads), so every iteration
-    // issues the same number of memory instructions and the waits below are constants
-    auto issue = [&](int st, WStage& ws) {
-        const int sc = min(st, KS - 1);
-        uint8_t* b = lds + (st % NS) * AOPER;
-#pragma unroll
-        for (int i = 0; i < 2; i++) dma16(asrc[i] + (int64_t)sc * PCK, b + (2 * wv + i) * 1024);
-#pragma unroll
-        for (int s = 0; s < 2; s++)
-#pragma unroll
-            for (int u = 0; u < 2; u++)
-                ws.f[s][u] = *reinterpret_cast<const v4i*>(wsrc[u] + (int64_t)sc * 1024 + 512 * s);
-    };
-
-    int aoff[2][4];
-#pragma unroll
-    for (int s = 0; s < 2; s++)
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-            const int ra = 32 * t + r;
-            aoff[s][t] = ra * PCK + 16 * ((2 * s + h) ^ pc_swz(ra));
-        }
-    v16i acc[4][2];
-#pragma unroll
-    for (int t = 0; t < 4; t++)
-#pragma unroll
-        for (int u = 0; u < 2; u++)
-#pragma unroll
-            for (int e = 0; e < 16; e++) acc[t][u][e] = 0;
-
-    WStage ring[NS - 1];
-#pragma unroll
-    for (int i = 0; i < NS - 1; i++) issue(i, ring[i]);
-    // per iteration: wait for stage st (issued NS - 1 iterations ago; (NS - 2) iterations' 6 instructions are
-    // newer), barrier (stage st visible, stage st - 1's buffer free), compute stage st, issue stage st + NS - 1
-    int st = 0;
-    for (int st0 = 0; st0 < KS; st0 += NS - 1) {
-#pragma unroll
-        for (int d = 0; d < NS - 1; d++) {
-            st = st0 + d;
-            if (st < KS) {
-                vm_wait<(NS - 2) * 6>();
-                lds_barrier();
-                const uint8_t* b = lds + (st % NS) * AOPER;
-#pragma unroll
-                for (int s = 0; s < 2; s++) {
-                    v4i fa[4];
-#pragma unroll
-                    for (int t = 0; t < 4; t++) fa[t] = *reinterpret_cast<const v4i*>(b + aoff[s][t]);
-#pragma unroll
-                    for (int t = 0; t < 4; t++)
-#pragma unroll
-                        for (int u = 0; u < 2; u++)
-                            acc[t][u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ring[d].f[s][u], fa[t], acc[t][u], 0, 0,
-                                                                              0);
-                }
-                // the next copy into buffer (st - 1) % NS, whose stage every wave finished before the barrier above,
-                // and the next weights into the slot just consumed
-                issue(st + NS - 1, ring[d]);
-            }
-        }
-    }
-    vm_wait<0>();                                   // the clamped copies past the end land before the workgroup ends
-
-#pragma unroll
-    for (int t = 0; t < 4; t++) {
-        const int ml = 32 * t + r;
-        const int m = m0 + ml;
-        if (m >= live) continue;
-        const float sa = sal[ml];
-#pragma unroll
-        for (int u = 0; u < 2; u++)
-#pragma unroll
-            for (int g = 0; g < 4; g++) {
-                const int nl = 64 * wv + 32 * u + 8 * g + 4 * h;
-                const int n = n0 + nl;
-                if (n >= N) continue;
-                float y[4];
-#pragma unroll
-                for (int e = 0; e < 4; e++) y[e] = mul_rn(mul_rn((float)acc[t][u][4 * g + e], sa), swl[nl + e]);
-                if (EPI == 0) {
-                    uint16_t* o = static_cast<uint16_t*>(out) + (int64_t)m * ldo + n;
-                    *reinterpret_cast<v2u*>(o) = v2u{f32_to_bf16(y[0]) | (f32_to_bf16(y[1]) << 16),
-                                                     f32_to_bf16(y[2]) | (f32_to_bf16(y[3]) << 16)};
-                } else {
-                    float4* o = reinterpret_cast<float4*>(static_cast<float*>(out) + (int64_t)m * ldo + n);
-                    const float4 p = *o;
-                    *o = make_float4(add_rn(p.x, y[0]), add_rn(p.y, y[1]), add_rn(p.z, y[2]), add_rn(p.w, y[3]));
-                }
-            }
-    }
-}
-
 // ---------------------------------------------------------------------------------------------- decode
 // Rows r0 .. r0 + 16 MT - 1 with r0 = 16 MT blockIdx.y (grid rows cover M beyond 64: for narrow projections, whose
 // few 128 x 256 tiles leave the tile kernel's CUs idle, the weight tiles then come from L2 / MALL once per 64 rows).
@@ -484,22 +338,6 @@ int launch_w8a8_pc(int kernel, bool wpack, const int8_t* a, const float* a_s, in
     PCT__(PC_TILE)
 #undef PCT__
 #undef PCT_
-#ifndef PC_DW_NS
-#define PC_DW_NS 0                                // activation stages of the direct-weight tile kernel (0: off)
-#endif
-    if (wpack && PC_DW_NS > 0) {
-        constexpr int DNS = PC_DW_NS > 0 ? PC_DW_NS : 2;
-        const int tiles_m = (M + 127) / 128, tiles_n = (N + PCT - 1) / PCT;
-        const size_t lds = (size_t)DNS * 128 * PCK;
-#define PCD(W16, E)                                                                                                \
-    hipLaunchKernelGGL((w8a8_pc_tile_dw_kernel<W16, E, DNS>), dim3(tiles_m * tiles_n), dim3(256), lds, st, a, a_s,  \
-                       as_sm, w, w_s, out, ldo, n_rows, M, N, K, tiles_m, tiles_n)
-        if (ws16) { if (epi == 0) PCD(true, 0); else PCD(true, 1); }
-        else { if (epi == 0) PCD(false, 0); else PCD(false, 1); }
-#undef PCD
-        PRISM_LAUNCH_CHECK();
-        return PRISM_OK;
-    }
     const int tiles_m = (M + PC_TM - 1) / PC_TM, tiles_n = (N + PCT - 1) / PCT;
     const size_t lds = (size_t)NS * (PC_TM * PCK + PC_OPER);
 #define PCL(WP, W16, E)                                                                                            \
