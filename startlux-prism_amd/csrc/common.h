@@ -93,6 +93,26 @@ __device__ __forceinline__ void dma1(const void* g, void* lds) {
     __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 1, 0, 0);
 }
 
+// Buffer loads: a wave-uniform base in a buffer resource (SGPRs), the uniform part of the offset in soffset (an
+// SGPR) and the lane's fixed part in one VGPR, so a streaming loop computes no per-load addresses in VGPRs.  Streamed
+// that way the compiler has no address temporaries to place in registers still awaiting an earlier load (which makes
+// it wait for the previous requests before issuing the next ones).  Raw buffer (stride 0): the range check compares
+// voffset + soffset with the record count, here the largest, so it never clips a valid offset.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, 0x00020000);
+}
+constexpr int kBufNT = 2;                 // the cache-policy bit of a non-temporal (streaming) load
+template <int AUX = 0>
+__device__ __forceinline__ v4i buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, AUX));
+}
+__device__ __forceinline__ uint32_t buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0);
+}
+__device__ __forceinline__ v2u buf_load8(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(v2u, __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, (int)soff, 0));
+}
+
 // Waits until at most N vector-memory operations of this wave are outstanding.  The compiler does not count LDS-DMA
 // writes as producers of later LDS reads, so every DMA stage is closed by an explicit wait (then a barrier).
 template <int N>

@@ -614,7 +614,8 @@ static int packed_gemm(const int8_t* a, const float* a_s, int64_t as_sm, const i
         return PRISM_ERR_SHAPE;
     if (!PRISM_ALIGNED(a, 16) || !PRISM_ALIGNED(qt, 16) || !PRISM_ALIGNED(dt, 16)) return PRISM_ERR_ALIGN;
     if (kernel < -1 || kernel > 4) return PRISM_ERR_ARG;
-    const bool can_stream = M >= 1 && M <= 16 && (N / 16) * (K / 64) < ((int64_t)1 << 31) && workspace &&
+    const bool can_stream = M >= 1 && M <= 16 && (N / 16) * (K / 64) < ((int64_t)1 << 31) &&
+                            M * K < ((int64_t)1 << 31) && workspace &&
                             workspace_bytes >= q8_stream_workspace_bytes(N, K);
     // by default: the balanced kernel up to 16 rows (given its workspace), the row-round decode kernel up to 64 rows
     // (and up to 16 without a workspace), the tile kernel beyond

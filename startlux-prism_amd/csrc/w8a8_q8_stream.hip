@@ -81,34 +81,57 @@ __global__ __launch_bounds__((NW + (MX * 16 + 63) / 64) * 64) void w8a8_q8_strea
         // are one 4-byte word of dt.
         constexpr int EV = MX < 4 ? MX : 4;                            // accumulator values per lane in use
         const int mc = min(lm, M - 1);
-        const v4i* cw = reinterpret_cast<const v4i*>(qt) + lane;
-        const uint32_t* cs = reinterpret_cast<const uint32_t*>(dt) + lm;
-        const int8_t* xa = a + (int64_t)mc * K + 8 * q;
+        // buffer loads: per round the tile's base in SGPRs, per pair the offset in soffset, per lane one fixed
+        // VGPR offset (weights: its 16-byte slot; scales: its row's 4-byte word; activations: its 8-byte piece)
+        // activations: 16 bytes of the lane's row per pair, bytes 16 s .. 16 s + 15 with s = (0, 2, 1, 3)[q], which
+        // one v_permlane16_swap per dword pair turns into the MFMA operand (lane q: bytes 8 q .. 8 q + 7 of each
+        // block); one 16-byte request per lane instead of two 8-byte ones
+        const int sq = ((q & 1) << 1) | (q >> 1);
+        const uint32_t vw = 16 * lane, vs = 4 * lm, vx = (uint32_t)(mc * K + 16 * sq);
+        const __amdgpu_buffer_rsrc_t ra = buf_rsrc(a);
+        const int wvu = __builtin_amdgcn_readfirstlane(wv);
         float sa[EV];
         struct Pair {
             v4i w;
             uint32_t s;
-            v2u x0, x1;
+            v4i x;
         };
         auto load = [&](int rho, Pair* pr) {
             const Round d = round_of(rho);
             const int64_t tb = (int64_t)d.nt * KP;
+            if (XL) {
+#pragma unroll
+                for (int i = 0; i < CP; i++) {
+                    const int p = min(d.p0 + wv * CP + i, KP - 1);
+                    pr[i].w = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(qt) + (tb + p) * 64 + lane);
+                    pr[i].s = reinterpret_cast<const uint32_t*>(dt)[(tb + p) * 16 + lm];
+                }
+                return;
+            }
+            const __amdgpu_buffer_rsrc_t rw = buf_rsrc(qt + tb * 1024);
+            const __amdgpu_buffer_rsrc_t rs = buf_rsrc(reinterpret_cast<const uint8_t*>(dt) + tb * 64);
 #pragma unroll
             for (int i = 0; i < CP; i++) {
-                const int p = min(d.p0 + wv * CP + i, KP - 1);
-                pr[i].w = __builtin_nontemporal_load(cw + (tb + p) * 64);
-                pr[i].s = cs[(tb + p) * 16];
-                if (!XL) {
-                    pr[i].x0 = *reinterpret_cast<const v2u*>(xa + 64 * p);
-                    pr[i].x1 = *reinterpret_cast<const v2u*>(xa + 64 * p + 32);
-                }
+                const uint32_t p = (uint32_t)min(d.p0 + wvu * CP + i, KP - 1);
+                pr[i].w = buf_load16<kBufNT>(rw, vw, p * 1024);
+                pr[i].s = buf_load4(rs, vs, p * 64);
+                pr[i].x = buf_load16(ra, vx, p * 64);
             }
         };
         auto compute = [&](int rho, const Pair* pr) {
             const Round d = round_of(rho);
             v4i acc[CP][2];
 #pragma unroll
-            for (int i = 0; i < CP; i++)
+            for (int i = 0; i < CP; i++) {
+                // lane q holds 8-byte units (u(2s), u(2s+1)) of the pair; after the swaps it holds (u(q), u(4 + q))
+                uint32_t lo[2] = {0, 0}, hi[2] = {0, 0};
+                if (!XL) {
+                    const auto l2 = __builtin_amdgcn_permlane16_swap((uint32_t)pr[i].x[0], (uint32_t)pr[i].x[2], false,
+                                                                     false);
+                    const auto h2 = __builtin_amdgcn_permlane16_swap((uint32_t)pr[i].x[1], (uint32_t)pr[i].x[3], false,
+                                                                     false);
+                    lo[0] = l2[0], lo[1] = l2[1], hi[0] = h2[0], hi[1] = h2[1];
+                }
 #pragma unroll
                 for (int h = 0; h < 2; h++) {
                     const int64_t wf = h ? ((int64_t)(uint32_t)pr[i].w[2] | ((int64_t)pr[i].w[3] << 32))
@@ -118,12 +141,12 @@ __global__ __launch_bounds__((NW + (MX * 16 + 63) / 64) * 64) void w8a8_q8_strea
                         const int p = min(d.p0 + wv * CP + i, KP - 1);
                         xf = *reinterpret_cast<const int64_t*>(xs + mc * (K + 32) + 64 * p + 32 * h + 8 * q);
                     } else {
-                        const v2u xv = h ? pr[i].x1 : pr[i].x0;
-                        xf = (int64_t)xv[0] | ((int64_t)xv[1] << 32);
+                        xf = (int64_t)lo[h] | ((int64_t)hi[h] << 32);
                     }
                     const v4i zero = {0, 0, 0, 0};
                     acc[i][h] = __builtin_amdgcn_mfma_i32_16x16x32_i8(xf, wf, zero, 0, 0, 0);
                 }
+            }
             float t[CP][2][EV];
 #pragma unroll
             for (int i = 0; i < CP; i++)
@@ -302,7 +325,8 @@ static void launch(const int8_t* a, const float* a_s, int64_t as_sm, const int8_
 int q8_stream_launch(const int8_t* a, const float* a_s, int64_t as_sm, const int8_t* qt, const uint16_t* dt,
                      void* out, int64_t ldo, const int32_t* n_rows, int64_t M, int64_t N, int64_t K, int epi,
                      void* hand, int64_t hand_bytes, hipStream_t st) {
-    if (M < 1 || M > 16 || (N / 16) * (K / 64) >= ((int64_t)1 << 31)) return PRISM_ERR_SHAPE;
+    if (M < 1 || M > 16 || (N / 16) * (K / 64) >= ((int64_t)1 << 31) || M * K >= ((int64_t)1 << 31))
+        return PRISM_ERR_SHAPE;                  // 32-bit chunk and activation offsets
     const int W = q8_stream_workgroups(N, K);
     if (!hand || !PRISM_ALIGNED(hand, 8) || hand_bytes < q8_stream_workspace_bytes(N, K)) return PRISM_ERR_ARG;
     auto* h = reinterpret_cast<unsigned long long*>(hand);
