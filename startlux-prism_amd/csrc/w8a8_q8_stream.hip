@@ -18,7 +18,8 @@
 // workgroup barriers in the loop).  Weights and their block scales are requested D - 1 rounds ahead in a register
 // ring.  The activation rows sit in LDS, copied whole at the start when they fit (XL), else they travel in the ring.
 // Measured on MI355X: twelve compute waves per workgroup (not eight, nor more) for one to four rows; a ring deeper
-// than one round ahead and rounds of other sizes were slower.
+// than one round ahead and rounds of other sizes were slower.  From five rows the form depends on the shape (see the
+// launch below).
 //
 // The walk over a range and the handoff protocol between neighbouring workgroups are handoff.h's.
 #include "common.h"
@@ -314,10 +315,22 @@ static void launch(const int8_t* a, const float* a_s, int64_t as_sm, const int8_
 #ifndef Q8S_BIG
 #define Q8S_BIG 8, 32, 16, 2, 2
 #endif
+#ifndef Q8S_WIDE
+#define Q8S_WIDE 12, 48, 16, 2, 2
+#endif
 #define QS_(...) QS(__VA_ARGS__)
+    // 5..16 rows: twelve compute waves and rounds of 48 blocks (24 pairs) where a workgroup's share is at least four
+    // such rounds and that form's activation image fits LDS, else eight waves and rounds of 32 where their image
+    // fits, else the activations travel in the register ring, with twelve waves up to 12 rows and eight beyond
+    // (measured: 5120 x 17408 at 8 rows 23.7 -> 20.9 us, at 12 rows 24.8 -> 22.8 us, at 16 rows 0.5-0.9 us slower
+    // with twelve; 5120^2 at 8 rows 10.3 -> 9.8 us; on 4096^2, 64 pairs per workgroup, the eight-wave form is
+    // 0.1-0.4 us faster; at 16 rows on 5120^2 its image fits and it ties)
+    const bool wide = (int64_t)(N / 16) * (K / 64) >= 4LL * 24 * W;
     if (M == 1) QS_(Q8S_ONE);
     else if (M <= 4) QS_(Q8S_SMALL);
-    else QS_(Q8S_BIG);
+    else if (Q8S_XL && wide && stream_lds(48, 2, M, K, true) <= kLdsMax) QS_(Q8S_WIDE);
+    else if ((Q8S_XL && stream_lds(32, 2, M, K, true) <= kLdsMax) || M > 12) QS_(Q8S_BIG);
+    else QS_(Q8S_WIDE);
 #undef QS_
 #undef QS
 }
