@@ -192,7 +192,8 @@ PRISM_API int prism_q4k_pack(const uint8_t* raw, uint8_t* qv, uint8_t* meta, int
  *   epi 0: bf16(y); epi 1: out = RN(out + y).
  * xq int8 [M, K]; a fp32, element (b, m) at a[b * a_sb + m] (a_sb = 0: one scale per token); xs int8 [K/256, M, 16]
  * (per super-block eight S & 63 then eight S >> 6); qv / meta from prism_q4k_pack; out row stride ldo.
- * kernel: -1 picks by M (2 up to 16 rows where it applies, else 1, beyond 16 rows 0); 0 the prefill tile kernel;
+ * kernel: -1 picks by M (2 up to 4 rows where it applies and N / 16 < 512, else 1 up to 16 rows, beyond 16 rows 0);
+ * 0 the prefill tile kernel;
  * 1 the per-tile decode kernel (M <= 16; the tile kernel when its per-super-block terms, K/256 x M x 64 bytes, exceed
  * the 160 KB of LDS); 2 the balanced-grid decode kernel (M <= 16 with M (K + 32) + K M / 8 bytes of activation image
  * within LDS; equal shares of the weights per CU, running sums handed between workgroups through `workspace`).

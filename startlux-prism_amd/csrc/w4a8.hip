@@ -22,6 +22,10 @@
 #include "w4a8_bal.h"
 #include "w4a8_common.h"
 
+#ifndef Q4S_TG2_ROWS
+#define Q4S_TG2_ROWS 5
+#endif
+
 namespace prism {
 
 // ---------------------------------------------------------------------------------------------- pack
@@ -276,13 +280,15 @@ static size_t q6k_decode_lds(int R, int M) {
 }
 
 // ---------------------------------------------------------------------------------------------- Q4_K stream decode
-// Up to 16 activation rows; one workgroup per 16-row weight tile and all of K.  Wave w computes super-blocks
-// w, w + NW, ... with PD of them in flight in a register ring, each holding what its lane needs from memory: the
-// tile's 2 KB of weights (two 16-byte slots), the 16 meta bytes of the lane's weight row, the lane's activation row
-// (four 16-byte pieces) and its split activation sums.  A super-block's term t of each output (the two-plane MFMA
-// sums, the mins on the MFMA, q4k_term) goes to LDS [b][m][n]; after one barrier each output's thread adds the terms
-// in super-block order, y = fma(a[b, m], t, y), as the reference's sequential chain does.
-template <int NW, int PD, int EPI>
+// Up to 16 activation rows; one workgroup per TG adjacent 16-row weight tiles and all of K.  Wave w computes
+// super-blocks w, w + NW, ... of every tile with PD of them in flight in a register ring, each holding what its lane
+// needs from memory: per tile the 2 KB of weights (two 16-byte slots) and the 16 meta bytes of the lane's weight row,
+// and once for the TG tiles the lane's activation row (four 16-byte pieces) and its split activation sums.  A
+// super-block's term t of each output (the two-plane MFMA sums, the mins on the MFMA, q4k_term) goes to LDS
+// [tile][b][m][n]; after one barrier each output's thread adds the terms in super-block order, y = fma(a[b, m], t, y),
+// as the reference's sequential chain does.  Two tiles per wave halve the activation requests, which at 16 rows are
+// twice the weight bytes (every tile reads every activation row).
+template <int NW, int PD, int TG, int EPI>
 __global__ __launch_bounds__(NW * 64) void w4a8_q4k_stream_kernel(const int8_t* __restrict__ xq,
                                                                  const float* __restrict__ a, int64_t a_sb,
                                                                  const int8_t* __restrict__ xs,
@@ -290,63 +296,69 @@ __global__ __launch_bounds__(NW * 64) void w4a8_q4k_stream_kernel(const int8_t* 
                                                                  const uint8_t* __restrict__ meta,
                                                                  void* __restrict__ out, int64_t ldo,
                                                                  const int32_t* __restrict__ n_rows, int M, int K) {
-    extern __shared__ __attribute__((aligned(16))) float tl[];          // [NB][M][16]
+    extern __shared__ __attribute__((aligned(16))) float tl[];          // [TG][NB][M][16]
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int nt = blockIdx.x;
-    const int live = min(M, __ldg(n_rows));
+    const int nt0 = blockIdx.x * TG;
     const int NB = K / 256;
     const int lm = lane & 15, q = lane >> 4;
     const int m = min(lm, M - 1);
 
-    const v4u* cw = reinterpret_cast<const v4u*>(qv) + (int64_t)nt * NB * 128 + lane;
+    const v4u* cw = reinterpret_cast<const v4u*>(qv) + (int64_t)nt0 * NB * 128 + lane;
     kernel_args_now(xq, a, a_sb, xs, qv, meta, out, ldo, n_rows, M, K);
-    const v4u* cm = reinterpret_cast<const v4u*>(meta) + (int64_t)nt * NB * 16 + lm;
+    const v4u* cm = reinterpret_cast<const v4u*>(meta) + (int64_t)nt0 * NB * 16 + lm;
     const int8_t* cx = xq + (int64_t)m * K + 16 * q;
     struct SB {
-        v4u w[2];
-        v4u mt;
+        v4u w[TG][2];
+        v4u mt[TG];
         v4i x[4];
         v4i s;
     };
     auto load = [&](int i, SB& c) {
         const int b = min(wv + NW * i, NB - 1);
-        c.w[0] = __builtin_nontemporal_load(cw + (int64_t)b * 128);
-        c.w[1] = __builtin_nontemporal_load(cw + (int64_t)b * 128 + 64);
-        c.mt = cm[(int64_t)b * 16];
+#pragma unroll
+        for (int g = 0; g < TG; g++) {
+            c.w[g][0] = __builtin_nontemporal_load(cw + ((int64_t)g * NB + b) * 128);
+            c.w[g][1] = __builtin_nontemporal_load(cw + ((int64_t)g * NB + b) * 128 + 64);
+            c.mt[g] = cm[((int64_t)g * NB + b) * 16];
+        }
 #pragma unroll
         for (int p = 0; p < 4; p++) c.x[p] = *reinterpret_cast<const v4i*>(cx + (int64_t)b * 256 + 64 * p);
         c.s = *reinterpret_cast<const v4i*>(xs + ((int64_t)b * M + m) * 16);
     };
     auto term = [&](int i, const SB& c) {
         const int b = wv + NW * i;
-        float d, dm;
-        int sc[8], mn[8];
-        row_meta(c.mt, d, dm, sc, mn);                    // this lane's weight row lm
-        v4i alo = {0, 0, 0, 0}, ahi = {0, 0, 0, 0};
-#pragma unroll
-        for (int p = 0; p < 4; p++) {
-            v4i wl, wh;
-            const int g = 2 * p + (q >> 1);
-            int scg = sc[0];
-#pragma unroll
-            for (int j = 1; j < 8; j++) scg = g == j ? sc[j] : scg;
-            two_plane(c.w[p >> 1][2 * (p & 1)], c.w[p >> 1][2 * (p & 1) + 1], split_scale(scg), wl, wh);
-            alo = __builtin_amdgcn_mfma_i32_16x16x64_i8(wl, c.x[p], alo, 0, 0, 0);
-            ahi = __builtin_amdgcn_mfma_i32_16x16x64_i8(wh, c.x[p], ahi, 0, 0, 0);
-        }
-        const int64_t mn8 = q == 0 ? (int64_t)(uint32_t)(mn[0] | (mn[1] << 8) | (mn[2] << 16) | (mn[3] << 24)) |
-                                         ((int64_t)(uint32_t)(mn[4] | (mn[5] << 8) | (mn[6] << 16) | (mn[7] << 24)) << 32)
-                                   : 0;
         const int64_t slo = q == 0 ? ((int64_t)(uint32_t)c.s[0] | ((int64_t)(uint32_t)c.s[1] << 32)) : 0;
         const int64_t shi = q == 0 ? ((int64_t)(uint32_t)c.s[2] | ((int64_t)(uint32_t)c.s[3] << 32)) : 0;
-        const v4i mins = mins_mfma(mn8, slo, shi);
-        v4f t;
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const float de = __shfl(d, 4 * q + e, kWave), dme = __shfl(dm, 4 * q + e, kWave);   // row 4 q + e
-            t[e] = q4k_term(de, dme, alo[e] + 8 * ahi[e], mins[e]);
+        for (int g = 0; g < TG; g++) {
+            float d, dm;
+            int sc[8], mn[8];
+            row_meta(c.mt[g], d, dm, sc, mn);             // this lane's weight row lm of tile g
+            v4i alo = {0, 0, 0, 0}, ahi = {0, 0, 0, 0};
+#pragma unroll
+            for (int p = 0; p < 4; p++) {
+                v4i wl, wh;
+                const int j2 = 2 * p + (q >> 1);
+                int scg = sc[0];
+#pragma unroll
+                for (int j = 1; j < 8; j++) scg = j2 == j ? sc[j] : scg;
+                two_plane(c.w[g][p >> 1][2 * (p & 1)], c.w[g][p >> 1][2 * (p & 1) + 1], split_scale(scg), wl, wh);
+                alo = __builtin_amdgcn_mfma_i32_16x16x64_i8(wl, c.x[p], alo, 0, 0, 0);
+                ahi = __builtin_amdgcn_mfma_i32_16x16x64_i8(wh, c.x[p], ahi, 0, 0, 0);
+            }
+            const int64_t mn8 =
+                q == 0 ? (int64_t)(uint32_t)(mn[0] | (mn[1] << 8) | (mn[2] << 16) | (mn[3] << 24)) |
+                             ((int64_t)(uint32_t)(mn[4] | (mn[5] << 8) | (mn[6] << 16) | (mn[7] << 24)) << 32)
+                       : 0;
+            const v4i mins = mins_mfma(mn8, slo, shi);
+            v4f t;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float de = __shfl(d, 4 * q + e, kWave), dme = __shfl(dm, 4 * q + e, kWave);   // row 4 q + e
+                t[e] = q4k_term(de, dme, alo[e] + 8 * ahi[e], mins[e]);
+            }
+            if (lm < M && b < NB) *reinterpret_cast<v4f*>(&tl[(((int64_t)g * NB + b) * M + lm) * 16 + 4 * q]) = t;
         }
-        if (lm < M && b < NB) *reinterpret_cast<v4f*>(&tl[((int64_t)b * M + lm) * 16 + 4 * q]) = t;
     };
     const int cnt = wv < NB ? (NB - wv + NW - 1) / NW : 0;
     SB ring[PD];
@@ -364,11 +376,15 @@ __global__ __launch_bounds__(NW * 64) void w4a8_q4k_stream_kernel(const int8_t* 
     for (int d = 0; d < PD; d++)
         if (full + d < cnt) term(full + d, ring[d]);
     __syncthreads();
-    for (int fo = tid; fo < M * 16; fo += NW * 64) {
-        const int mo = fo >> 4, n = 16 * nt + (fo & 15);
+    // the live-row count only here (read earlier, its load would precede the first weight requests)
+    const int live = min(M, __ldg(n_rows));
+    for (int fo = tid; fo < TG * M * 16; fo += NW * 64) {
+        const int g = fo / (M * 16), f = fo - g * M * 16;
+        const int mo = f >> 4, n = 16 * (nt0 + g) + (f & 15);
         if (mo >= live) continue;
         float y = 0.f;
-        for (int b = 0; b < NB; b++) y = fmaf(a[(int64_t)b * a_sb + mo], tl[((int64_t)b * M + mo) * 16 + (fo & 15)], y);
+        for (int b = 0; b < NB; b++)
+            y = fmaf(a[(int64_t)b * a_sb + mo], tl[(((int64_t)g * NB + b) * M + mo) * 16 + (f & 15)], y);
         if (EPI == 0) {
             reinterpret_cast<uint16_t*>(out)[(int64_t)mo * ldo + n] = (uint16_t)f32_to_bf16(y);
         } else {
@@ -853,11 +869,12 @@ extern "C" int prism_w4a8_q4k_gemm(const int8_t* xq, const float* a, int64_t a_s
         return PRISM_ERR_ALIGN;
     if (kernel < -1 || kernel > 2) return PRISM_ERR_ARG;
     const bool can_bal = q4k_bal_fits(M, N, K) && workspace && workspace_bytes >= q4k_bal_workspace_bytes(N);
-    // by default up to 16 rows: the balanced kernel for projections of fewer than two 16-row tiles per CU (where a
-    // tile per workgroup leaves CUs with one tile more than others: 5120 x 17408, 16 -> 1 rows 15.96 us against
-    // 18.73 us), given its workspace; the per-tile kernel otherwise (13824 x 5120: 12.9 us against 16.0 us); the tile
-    // kernel beyond 16 rows
-    if (kernel == -1) kernel = M >= 1 && M <= 16 ? (can_bal && N / 16 < 512 ? 2 : 1) : 0;
+    // by default up to 4 rows: the balanced kernel for projections of fewer than two 16-row tiles per CU (where a
+    // tile per workgroup leaves CUs with one tile more than others: 5120 x 17408 at 1 row 15.96 us against
+    // 18.73 us), given its workspace; the per-tile kernel otherwise (13824 x 5120: 12.9 us against 16.0 us) and from
+    // 5 rows, where it takes two tiles per workgroup (5120^2 at 16 rows 8.9 against 9.9 us); the tile kernel beyond 16
+    // rows.  The MI355X table overrides this per shape.
+    if (kernel == -1) kernel = M >= 1 && M <= 16 ? (can_bal && N / 16 < 512 && M <= 4 ? 2 : 1) : 0;
     if (kernel == 1 && M > 16) return PRISM_ERR_ARG;
     if (kernel == 2 && !can_bal) return M > 16 || !q4k_bal_fits(M, N, K) ? PRISM_ERR_SHAPE : PRISM_ERR_ARG;
     if (M == 0) return PRISM_OK;
@@ -876,15 +893,22 @@ extern "C" int prism_w4a8_q4k_gemm(const int8_t* xq, const float* a, int64_t a_s
         if (lds > 160 * 1024) kernel = 0;                 // the terms of every super-block do not fit: tile kernel
     }
     if (kernel == 1) {
-        const size_t lds = (size_t)(K / 256) * M * 16 * 4;
         const bool wide = K >= 6144 || N <= 2048;
-#define W4S(NW, E) do {                                                                                            \
-        allow_lds(w4a8_q4k_stream_kernel<NW, 2, E>, lds);                                                         \
-        hipLaunchKernelGGL((w4a8_q4k_stream_kernel<NW, 2, E>), dim3(Ni / 16), dim3(64 * NW), lds, st, xq, a, a_sb,  \
-                           xs, qv, meta, out, ldo, n_rows, Mi, Ki);                                                \
+        // two tiles per wave (one activation load for both) from 5 rows, below 1024 tiles (at 17408 x 5120 half as
+        // many workgroups lost 1-1.3 us up to 8 rows and tied at 16; C3's 13824 x 5120 at 16 rows: 16.6 -> 14.4 us,
+        // 5120 x 17408: 26.8 -> 20.7 us)
+        const int tg = (M >= Q4S_TG2_ROWS && N % 32 == 0 && N / 16 < 1024 &&
+                        (size_t)(K / 256) * M * 16 * 4 * 2 <= 160 * 1024) ? 2 : 1;
+        const size_t lds = (size_t)tg * (K / 256) * M * 16 * 4;
+#define W4S(NW, TG, E) do {                                                                                        \
+        allow_lds(w4a8_q4k_stream_kernel<NW, 2, TG, E>, lds);                                                     \
+        hipLaunchKernelGGL((w4a8_q4k_stream_kernel<NW, 2, TG, E>), dim3(Ni / (16 * TG)), dim3(64 * NW), lds, st, xq, \
+                           a, a_sb, xs, qv, meta, out, ldo, n_rows, Mi, Ki);                                       \
     } while (0)
-        if (wide) { if (epi == 0) W4S(8, 0); else W4S(8, 1); }
-        else { if (epi == 0) W4S(4, 0); else W4S(4, 1); }
+#define W4S_TG(NW, E) do { if (tg == 2) W4S(NW, 2, E); else W4S(NW, 1, E); } while (0)
+        if (wide) { if (epi == 0) W4S_TG(8, 0); else W4S_TG(8, 1); }
+        else { if (epi == 0) W4S_TG(4, 0); else W4S_TG(4, 1); }
+#undef W4S_TG
 #undef W4S
     } else {
         const int tiles_m = (Mi + QBM - 1) / QBM, tiles_n = (Ni + QBN - 1) / QBN;
