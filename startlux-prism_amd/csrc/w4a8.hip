@@ -96,25 +96,26 @@ __global__ __launch_bounds__(256) void q6k_pack_kernel(const uint8_t* __restrict
 }
 
 // ---------------------------------------------------------------------------------------------- Q6_K decode
-// Q6_K (prism_q6k_pack).  A workgroup of NW waves owns one 16-row tile and every activation row (M <= 16).  Round r
-// covers R super-blocks; wave w computes super-blocks r R + w CB .. + CB - 1.  Per round the per-wave global loads
+// Q6_K (prism_q6k_pack).  A workgroup owns TG adjacent 16-row tiles, NW waves each, and every activation row
+// (M <= 16), staged once for its TG tiles.  Round r covers R super-blocks; wave w of a tile computes super-blocks
+// r R + w CB .. + CB - 1.  Per round the per-wave global loads
 // are the weight chunks (4 KB per super-block: four dwordx4 per lane, requested D - 1 rounds ahead).  The round's
 // scales (unpacked once per row and super-block by a staging thread), activation rows and activation scales are
 // fetched with 16-byte loads a round ahead and staged in one of two LDS buffers.  Each super-block's term t of each
 // output goes to one of two LDS term buffers; the owner thread of each output folds round r - 1's terms,
 // y = fma(a[b, m], t, y) in super-block order, while round r is computed; one barrier per round.
-template <int NW, int R, int MX, int D, int EPI>
-__global__ __launch_bounds__(NW * 64, 2) void w4a8_q6k_decode_kernel(const int8_t* __restrict__ xq,
+template <int NW, int R, int MX, int D, int TG, int EPI>
+__global__ __launch_bounds__(NW * TG * 64, 2) void w4a8_q6k_decode_kernel(const int8_t* __restrict__ xq,
                                                                   const float* __restrict__ a, int64_t a_sb,
                                                                   const uint8_t* __restrict__ qv,
                                                                   const uint8_t* __restrict__ meta,
                                                                   void* __restrict__ out, int64_t ldo,
                                                                   const int32_t* __restrict__ n_rows, int M, int N,
                                                                   int K) {
-    constexpr int NT = NW * 64;
+    constexpr int NT = NW * TG * 64;
     constexpr int CB = R / NW;                     // super-blocks per wave per round
     static_assert(CB >= 1 && CB * NW == R, "R must be a multiple of NW");
-    static_assert(MX <= 16 && R * 16 <= NT && R * MX <= NT, "one staging thread per (row, super-block)");
+    static_assert(MX <= 16 && TG * R * 16 <= NT && R * MX <= NT, "one staging thread per (tile, row, super-block)");
     constexpr int RB = R * 256;                    // activation bytes per row per round
     constexpr int LDA = RB + 16;
     constexpr int CPR = RB / 16;
@@ -123,37 +124,38 @@ __global__ __launch_bounds__(NW * 64, 2) void w4a8_q6k_decode_kernel(const int8_
     extern __shared__ __attribute__((aligned(16))) int8_t dsm[];
     // LDS (q6k_decode_lds): terms, per window the second scale and the first minus the second, d, activations and
     // activation scales
-    float* terms = reinterpret_cast<float*>(dsm);                 // [2][R][M][16]
-    int* sca = reinterpret_cast<int*>(terms + 2 * R * M * 16);    // [2][R][8][16] [window][row]
-    int* scb = sca + 2 * R * 128;                                 // [2][R][8][16]
-    float* dl = reinterpret_cast<float*>(scb + 2 * R * 128);      // [2][R][16]
-    int8_t* xl = reinterpret_cast<int8_t*>(dl + 2 * R * 16);      // [2][M][LDA]
+    float* terms = reinterpret_cast<float*>(dsm);                 // [TG][2][R][M][16]
+    int* sca = reinterpret_cast<int*>(terms + TG * 2 * R * M * 16);  // [TG][2][R][8][16] [window][row]
+    int* scb = sca + TG * 2 * R * 128;                            // [TG][2][R][8][16]
+    float* dl = reinterpret_cast<float*>(scb + TG * 2 * R * 128);  // [TG][2][R][16]
+    int8_t* xl = reinterpret_cast<int8_t*>(dl + TG * 2 * R * 16);  // [2][M][LDA]
     float* al = reinterpret_cast<float*>(xl + 2 * M * LDA);       // [3][R][M] activation scales: read by the fold of
                                                                   // round r - 1 while round r + 1 is staged
     const int tstride = R * M * 16, xstride = M * LDA;
 
     kernel_args_now(xq, a, a_sb, qv, meta, out, ldo, n_rows, M, N, K);
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int nt = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wt = tid >> 6, tg = wt / NW, wv = wt - tg * NW;      // wave wv of tile tg
+    const int nt0 = blockIdx.x * TG;
     const int live = min(M, __ldg(n_rows));
     const int NB = K / 256;
     const int nr = (NB + R - 1) / R;
     const int lm = lane & 15, q = lane >> 4;
     const int xch = M * CPR;
 
-    const v4u* cw = reinterpret_cast<const v4u*>(qv) + (int64_t)nt * NB * 64 * WCH + lane;
-    const uint8_t* cm6 = meta + (int64_t)nt * NB * Q6_META;
+    const v4u* cw = reinterpret_cast<const v4u*>(qv) + (int64_t)(nt0 + tg) * NB * 64 * WCH + lane;
+    const uint8_t* cm6 = meta + (int64_t)nt0 * NB * Q6_META;
 
     struct Staged {
-        v4u m;        // thread < 16 R: super-block tid / 16, row tid % 16: its 16 scales
+        v4u m;        // thread < 16 R TG: tile tid / 16 R, super-block tid / 16 % R, row tid % 16: its 16 scales
         uint32_t dh;  // the row's fp16 d
         float as;     // thread < R M: activation scale of (super-block tid / M, row tid % M)
         v4i x[XPT];
     };
     auto stage_load = [&](int r, Staged& sg) {
         const int b0 = r * R;
-        const int c = min(tid, 16 * R - 1);
-        const uint8_t* mp = cm6 + (int64_t)min(b0 + c / 16, NB - 1) * Q6_META;
+        const int c = min(tid, 16 * R * TG - 1), cg = c / (16 * R), cl = c - cg * 16 * R;
+        const uint8_t* mp = cm6 + ((int64_t)cg * NB + min(b0 + cl / 16, NB - 1)) * Q6_META;
         sg.m = reinterpret_cast<const v4u*>(mp)[c & 15];
         sg.dh = reinterpret_cast<const uint16_t*>(mp + 256)[c & 15];
         const int e = min(tid, R * M - 1);
@@ -169,17 +171,17 @@ __global__ __launch_bounds__(NW * 64, 2) void w4a8_q6k_decode_kernel(const int8_
     };
     auto stage_store = [&](const Staged& sg, int rr) {
         const int buf = rr & 1;
-        if (tid < 16 * R) {
-            const int lb = tid >> 4, row = tid & 15;
-            int* pa = sca + (buf * R + lb) * 128 + row;
-            int* pb = scb + (buf * R + lb) * 128 + row;
+        if (tid < 16 * R * TG) {
+            const int sg_t = tid / (16 * R), lb = (tid >> 4) % R, row = tid & 15;
+            int* pa = sca + ((sg_t * 2 + buf) * R + lb) * 128 + row;
+            int* pb = scb + ((sg_t * 2 + buf) * R + lb) * 128 + row;
 #pragma unroll
             for (int w = 0; w < 8; w++) {
                 const int s0 = sbyte(sg.m, 2 * w), s1 = sbyte(sg.m, 2 * w + 1);
                 pa[16 * w] = s1;
                 pb[16 * w] = s0 - s1;
             }
-            dl[(buf * R + lb) * 16 + row] = f16_to_f32(sg.dh);
+            dl[((sg_t * 2 + buf) * R + lb) * 16 + row] = f16_to_f32(sg.dh);
         }
         if (tid < R * M) al[(rr % 3) * R * M + tid] = sg.as;
 #pragma unroll
@@ -197,7 +199,7 @@ __global__ __launch_bounds__(NW * 64, 2) void w4a8_q6k_decode_kernel(const int8_
         }
     };
     auto compute = [&](int r, v4u (*w)[WCH], int buf) {
-        float* tb = terms + (r & 1) * tstride;
+        float* tb = terms + (tg * 2 + (r & 1)) * tstride;
         const int mrow = min(lm, M - 1);
         const int8_t* xrow = xl + buf * xstride + mrow * LDA;
 #pragma unroll
@@ -206,8 +208,8 @@ __global__ __launch_bounds__(NW * 64, 2) void w4a8_q6k_decode_kernel(const int8_
             if (r * R + lb < NB) {
                 // per 32-input window: P over both sub-blocks, Pl over the first (activations of lanes q >= 2,
                 // which hold the second, zeroed): acc += sc1 P + (sc0 - sc1) Pl
-                const int* pa = sca + (buf * R + lb) * 128 + 4 * q;
-                const int* pb = scb + (buf * R + lb) * 128 + 4 * q;
+                const int* pa = sca + ((tg * 2 + buf) * R + lb) * 128 + 4 * q;
+                const int* pb = scb + ((tg * 2 + buf) * R + lb) * 128 + 4 * q;
                 v4i acc = {0, 0, 0, 0};
                 const v4i zero = {0, 0, 0, 0};
 #pragma unroll
@@ -221,7 +223,7 @@ __global__ __launch_bounds__(NW * 64, 2) void w4a8_q6k_decode_kernel(const int8_
 #pragma unroll
                     for (int e = 0; e < 4; e++) acc[e] += __mul24(A[e], P[e]) + __mul24(B[e], Pl[e]);
                 }
-                const v4f d = *reinterpret_cast<const v4f*>(&dl[(buf * R + lb) * 16 + 4 * q]);
+                const v4f d = *reinterpret_cast<const v4f*>(&dl[((tg * 2 + buf) * R + lb) * 16 + 4 * q]);
                 v4f t;
 #pragma unroll
                 for (int e = 0; e < 4; e++) t[e] = mul_rn(d[e], (float)acc[e]);
@@ -230,10 +232,11 @@ __global__ __launch_bounds__(NW * 64, 2) void w4a8_q6k_decode_kernel(const int8_
         }
     };
     float y = 0.f;
-    const int fo = tid;                                            // output (m = fo / 16, n = 16 nt + fo % 16)
+    // output fo of tile fg (m = fo / 16, n = 16 (nt0 + fg) + fo % 16): thread tid < TG M 16
+    const int fg = tid / (M * 16), fo = tid - fg * M * 16;
     auto fold = [&](int r) {
-        if (fo < M * 16) {
-            const float* tb = terms + (r & 1) * tstride;
+        if (fg < TG) {
+            const float* tb = terms + (fg * 2 + (r & 1)) * tstride;
             const float* ap = al + (r % 3) * R * M + (fo >> 4);
             const int nb = min(R, NB - r * R);
             float acc = y;
@@ -263,8 +266,8 @@ __global__ __launch_bounds__(NW * 64, 2) void w4a8_q6k_decode_kernel(const int8_
         }
     }
     if (nr % D == 0) fold(nr - 1);
-    const int m = fo >> 4, n = 16 * nt + (fo & 15);
-    if (fo < M * 16 && m < live) {
+    const int m = fo >> 4, n = 16 * (nt0 + fg) + (fo & 15);
+    if (fg < TG && m < live) {
         if (EPI == 0) {
             reinterpret_cast<uint16_t*>(out)[(int64_t)m * ldo + n] = (uint16_t)f32_to_bf16(y);
         } else {
@@ -274,8 +277,8 @@ __global__ __launch_bounds__(NW * 64, 2) void w4a8_q6k_decode_kernel(const int8_
     }
 }
 
-static size_t q6k_decode_lds(int R, int M) {
-    return 2 * (size_t)R * M * 16 * 4 + 2 * 2 * (size_t)R * 128 * 4 + 2 * (size_t)R * 16 * 4 +
+static size_t q6k_decode_lds(int R, int M, int TG) {
+    return TG * (2 * (size_t)R * M * 16 * 4 + 2 * 2 * (size_t)R * 128 * 4 + 2 * (size_t)R * 16 * 4) +
            2 * (size_t)M * (R * 256 + 16) + 3 * (size_t)R * M * 4;
 }
 
@@ -959,24 +962,31 @@ extern "C" int prism_w4a8_q6k_gemm(const int8_t* xq, const float* a, int64_t a_s
         if (epi == 0) Q6S(0); else Q6S(1);
 #undef Q6S
     } else if (kernel == 1) {
-        dim3 grid(Ni / 16);
-#define Q6DEC(NW, R, MX, D, E)                                                                                      \
+#define Q6DEC(NW, R, MX, D, TG, E)                                                                                  \
     do {                                                                                                           \
-        allow_lds(w4a8_q6k_decode_kernel<NW, R, MX, D, E>, q6k_decode_lds(R, Mi));                                  \
-        hipLaunchKernelGGL((w4a8_q6k_decode_kernel<NW, R, MX, D, E>), grid, dim3(NW * 64), q6k_decode_lds(R, Mi),    \
-                           st, xq, a, a_sb, qv, meta, out, ldo, n_rows, Mi, Ni, Ki);                               \
+        const size_t lds = q6k_decode_lds(R, Mi, TG);                                                               \
+        allow_lds(w4a8_q6k_decode_kernel<NW, R, MX, D, TG, E>, lds);                                                \
+        hipLaunchKernelGGL((w4a8_q6k_decode_kernel<NW, R, MX, D, TG, E>), dim3(Ni / (16 * TG)), dim3(NW * TG * 64),  \
+                           lds, st, xq, a, a_sb, qv, meta, out, ldo, n_rows, Mi, Ni, Ki);                          \
     } while (0)
-// decode configurations (waves, super-blocks per round, rows, rounds of weights in flight), measured on MI355X at
-// the 27B's shapes (M <= 4, M <= 16); overridable at build time
+// decode configurations (waves per tile, super-blocks per round, rows, rounds of weights in flight, tiles per
+// workgroup), measured on MI355X at the 27B's shapes (M <= 4, M <= 16); overridable at build time.  At 5-8 rows two
+// tiles share each staged activation copy where N allows (C3's 13824 x 5120: 25.1 / 23.9 -> 23.5 / 23.1 us at 5 / 8
+// rows; at 16 rows 0.3-0.8 us slower: this kernel's own VALU, not the activation copy, bounds it there)
 #ifndef W6V_SMALL
-#define W6V_SMALL 4, 4, 4, 2
+#define W6V_SMALL 4, 4, 4, 2, 1
 #endif
 #ifndef W6V_BIG
-#define W6V_BIG 4, 4, 16, 2
+#define W6V_BIG 4, 4, 16, 2, 1
+#endif
+#ifndef W6V_BIG2
+#define W6V_BIG2 4, 4, 16, 2, 2
 #endif
 #define Q6DEC_(...) Q6DEC(__VA_ARGS__)
         if (M <= 4) {
             if (epi == 0) Q6DEC_(W6V_SMALL, 0); else Q6DEC_(W6V_SMALL, 1);
+        } else if (M <= 8 && N % 32 == 0 && N / 16 < 1024) {
+            if (epi == 0) Q6DEC_(W6V_BIG2, 0); else Q6DEC_(W6V_BIG2, 1);
         } else {
             if (epi == 0) Q6DEC_(W6V_BIG, 0); else Q6DEC_(W6V_BIG, 1);
         }

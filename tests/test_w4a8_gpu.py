@@ -102,6 +102,8 @@ CASES = [  # (M, N, K, live, group)
     # the decode kernel's two wave counts (4 waves: N > 2048 and K < 6144), a long K with several ring trips per
     # wave, and K beyond the decode kernel's LDS for 16 rows (the tile kernel runs)
     (16, 2576, 1024, 13, 256), (2, 2064, 512, 2, 256), (4, 32, 12288, 4, 256), (16, 16, 41216, 16, 256),
+    # from 5 rows with N % 32 == 0 the decode kernel takes two tiles per workgroup (4 waves each here)
+    (12, 2560, 1024, 9, 256),
 ]
 
 

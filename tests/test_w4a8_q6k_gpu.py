@@ -66,6 +66,7 @@ CASES = [  # (M, N, K, live, group, random blocks)
     (1, 16, 256, 1, 256, True), (4, 64, 1024, 3, 256, False), (16, 128, 5120, 16, 256, True),
     (16, 256, 5120, 16, 5120, False), (7, 48, 2560, 5, 256, True), (64, 128, 1024, 64, 256, False),
     (100, 272, 768, 77, 256, True), (130, 128, 2048, 130, 2048, False),
+    (8, 96, 2560, 6, 256, True),       # 5-8 rows, N % 32 == 0: the decode kernel's two tiles per workgroup
 ]
 
 
