@@ -401,9 +401,9 @@ __global__ __launch_bounds__(256, 2) void w8a8_packed_tile_kernel(const int8_t* 
 
 // ---------------------------------------------------------------------------------------------- mid
 // From 17 rows (and for narrow projections at any row count, where the tile kernel's 128 x 128 tiles leave most CUs
-// idle): one wave (one workgroup) per (MT x 16 activation rows, 16-row weight tile), walking every block pair in
-// order; the m-tiles of one weight tile are grid rows blockIdx.y of the same XCD, so their weight chunks come from
-// HBM once.  The activations are the MFMA's A operand, so lane (i, q) = (lane % 16, lane / 16) ends with the sums of
+// idle): one wave (one workgroup) per (MT x 16 activation rows, TG adjacent 16-row weight tiles), walking every block
+// pair in order; the m-tiles of one weight tile are grid rows blockIdx.y of the same XCD, so their weight chunks come
+// from HBM once.  The activations are the MFMA's A operand, so lane (i, q) = (lane % 16, lane / 16) ends with the sums of
 // activation rows 4q..4q+3 of each m-tile against weight row i: its weight scales are one 4-byte word per pair (both
 // blocks of row i) and its activation scales four constants per m-tile.  Per pair a lane loads its weight chunk slot
 // as it lies (16 bytes), one 16-byte piece of its activation row per m-tile and that word, PD pairs ahead.  The piece
@@ -412,7 +412,7 @@ __global__ __launch_bounds__(256, 2) void w8a8_packed_tile_kernel(const int8_t* 
 // activation rows in 64-byte runs instead of eight-byte pieces halved this kernel's time.  Each block's int32 sums
 // come from one v_mfma_i32_16x16x32_i8 with a zero accumulator and the lane folds RN(RN(float(P) sa) sw) into its
 // outputs in block order, in registers.
-template <int PD, int MT, int EPI>
+template <int PD, int MT, int TG, int EPI>
 __global__ __launch_bounds__(64) void w8a8_packed_mid_kernel(const int8_t* __restrict__ a,
                                                               const float* __restrict__ a_s, int64_t as_sm,
                                                               const int8_t* __restrict__ qt,
@@ -424,7 +424,7 @@ __global__ __launch_bounds__(64) void w8a8_packed_mid_kernel(const int8_t* __res
     asm volatile("" ::"s"(a), "s"(a_s), "s"(as_sm), "s"(qt), "s"(dt), "s"(out), "s"(ldo), "s"(n_rows), "s"(M), "s"(N),
                  "s"(K));
     const int lane = threadIdx.x & 63, m0 = blockIdx.y * MT * 16;
-    const int nt = blockIdx.x;
+    const int nt0 = blockIdx.x * TG;
     // no row-count read before the first requests (it would hold them back by a round trip): workgroups past the
     // live rows still run, and the stores skip rows >= n_rows
     if (m0 >= M) return;
@@ -435,29 +435,31 @@ __global__ __launch_bounds__(64) void w8a8_packed_mid_kernel(const int8_t* __res
     for (int t = 0; t < MT; t++)
 #pragma unroll
         for (int e = 0; e < 4; e++) sa[t][e] = a_s[(int64_t)min(m0 + 16 * t + 4 * q + e, M - 1) * as_sm];
-    const v4i* cw = reinterpret_cast<const v4i*>(qt) + (int64_t)nt * KP * 64 + lane;
-    const uint32_t* cs = reinterpret_cast<const uint32_t*>(dt) + (int64_t)nt * KP * 16 + li;
+    const v4i* cw = reinterpret_cast<const v4i*>(qt) + (int64_t)nt0 * KP * 64 + lane;
+    const uint32_t* cs = reinterpret_cast<const uint32_t*>(dt) + (int64_t)nt0 * KP * 16 + li;
     const int sq = ((q & 1) << 1) | (q >> 1);
     const int8_t* xa[MT];
 #pragma unroll
     for (int t = 0; t < MT; t++) xa[t] = a + (int64_t)min(m0 + 16 * t + li, M - 1) * K + 16 * sq;
 
     struct Pair {
-        v4i w;
+        v4i w[TG];
         v4u x[MT];
-        uint32_t s;
+        uint32_t s[TG];
     };
     auto load = [&](int j, Pair& p) {
         const int jj = min(j, KP - 1);
-        p.w = cw[(int64_t)jj * 64];
+#pragma unroll
+        for (int g = 0; g < TG; g++) p.w[g] = cw[((int64_t)g * KP + jj) * 64];
 #pragma unroll
         for (int t = 0; t < MT; t++) p.x[t] = *reinterpret_cast<const v4u*>(xa[t] + 64 * jj);
-        p.s = cs[(int64_t)jj * 16];
+#pragma unroll
+        for (int g = 0; g < TG; g++) p.s[g] = cs[((int64_t)g * KP + jj) * 16];
     };
-    float y[MT][4] = {};
+    float y[TG][MT][4] = {};
     const v4i zero = {0, 0, 0, 0};
-    // the int32 sums of a pair's two blocks (one MFMA each per m-tile, zero accumulator)
-    auto sums = [&](const Pair& p, v4i (*acc)[2]) {
+    // the int32 sums of a pair's two blocks (one MFMA each per weight tile and m-tile, zero accumulator)
+    auto sums = [&](const Pair& p, v4i (*acc)[MT][2]) {
 #pragma unroll
         for (int t = 0; t < MT; t++) {
             // lane q holds 8-byte units (u(2s), u(2s+1)) of the pair; after the swap it holds (u(q), u(4 + q)):
@@ -466,24 +468,29 @@ __global__ __launch_bounds__(64) void w8a8_packed_mid_kernel(const int8_t* __res
             const auto hi = __builtin_amdgcn_permlane16_swap(p.x[t][1], p.x[t][3], false, false);
 #pragma unroll
             for (int h = 0; h < 2; h++) {
-                const int64_t wf = h ? ((int64_t)(uint32_t)p.w[2] | ((int64_t)p.w[3] << 32))
-                                     : ((int64_t)(uint32_t)p.w[0] | ((int64_t)p.w[1] << 32));
                 const int64_t xf = (int64_t)(uint32_t)lo[h] | ((int64_t)hi[h] << 32);
-                acc[t][h] = __builtin_amdgcn_mfma_i32_16x16x32_i8(xf, wf, zero, 0, 0, 0);
+#pragma unroll
+                for (int g = 0; g < TG; g++) {
+                    const int64_t wf = h ? ((int64_t)(uint32_t)p.w[g][2] | ((int64_t)p.w[g][3] << 32))
+                                         : ((int64_t)(uint32_t)p.w[g][0] | ((int64_t)p.w[g][1] << 32));
+                    acc[g][t][h] = __builtin_amdgcn_mfma_i32_16x16x32_i8(xf, wf, zero, 0, 0, 0);
+                }
             }
         }
     };
     // fold the pair's terms into the outputs, block 2j before 2j + 1
-    auto fold = [&](v4i (*acc)[2], const Pair& p) {
+    auto fold = [&](v4i (*acc)[MT][2], const Pair& p) {
 #pragma unroll
         for (int h = 0; h < 2; h++)
 #pragma unroll
-            for (int t = 0; t < MT; t++)
+            for (int g = 0; g < TG; g++)
 #pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const float x = mul_rn((float)acc[t][h][e], sa[t][e]);
-                    y[t][e] = add_rn(y[t][e], h ? mul_f16_rn<1>(x, p.s) : mul_f16_rn<0>(x, p.s));
-                }
+                for (int t = 0; t < MT; t++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const float x = mul_rn((float)acc[g][t][h][e], sa[t][e]);
+                        y[g][t][e] = add_rn(y[g][t][e], h ? mul_f16_rn<1>(x, p.s[g]) : mul_f16_rn<0>(x, p.s[g]));
+                    }
     };
     Pair ring[PD];
 #pragma unroll
@@ -492,7 +499,7 @@ __global__ __launch_bounds__(64) void w8a8_packed_mid_kernel(const int8_t* __res
     // MFMAs, then the two folds in order), so the VALU fold of one waits on MFMAs issued before the other's
     static_assert(PD % 2 == 0, "pairs are taken two at a time");
     const int full = KP / PD * PD;
-    v4i acc0[MT][2], acc1[MT][2];
+    v4i acc0[TG][MT][2], acc1[TG][MT][2];
     for (int j0 = 0; j0 < full; j0 += PD) {
 #pragma unroll
         for (int d = 0; d < PD; d += 2) {
@@ -512,22 +519,25 @@ __global__ __launch_bounds__(64) void w8a8_packed_mid_kernel(const int8_t* __res
             sums(ring[d], acc0);
             fold(acc0, ring[d]);
         }
-    const int n = 16 * nt + li;
     const int live = min(M, __ldg(n_rows));
 #pragma unroll
-    for (int t = 0; t < MT; t++)
+    for (int g = 0; g < TG; g++) {
+        const int n = 16 * (nt0 + g) + li;
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const int row = m0 + 16 * t + 4 * q + e;
-            if (row < live) {
-                if (EPI == 0) {
-                    reinterpret_cast<uint16_t*>(out)[(int64_t)row * ldo + n] = (uint16_t)f32_to_bf16(y[t][e]);
-                } else {
-                    float* o = reinterpret_cast<float*>(out) + (int64_t)row * ldo + n;
-                    *o = add_rn(*o, y[t][e]);
+        for (int t = 0; t < MT; t++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int row = m0 + 16 * t + 4 * q + e;
+                if (row < live) {
+                    if (EPI == 0) {
+                        reinterpret_cast<uint16_t*>(out)[(int64_t)row * ldo + n] = (uint16_t)f32_to_bf16(y[g][t][e]);
+                    } else {
+                        float* o = reinterpret_cast<float*>(out) + (int64_t)row * ldo + n;
+                        *o = add_rn(*o, y[g][t][e]);
+                    }
                 }
             }
-        }
+    }
 }
 
 static size_t packed_decode_lds(int R, int M) {
@@ -558,13 +568,21 @@ static void launch_packed(int kernel, const int8_t* a, const float* a_s, int64_t
 #undef PDEC
     }
     if (kernel == 2) {
-        // from 33 rows each wave takes two m-tiles: the shared weight loads and the doubled independent work per pair
-        // outweigh the halved wave count (M = 64, 5120 x 17408: 58 us against 60-65 us)
-        if (M > 32)
-            hipLaunchKernelGGL((w8a8_packed_mid_kernel<6, 2, EPI>), dim3(N / 16, (M + 31) / 32), dim3(64), 0, st,
+        // from 33 rows: each wave one m-tile and two weight tiles (one activation request serves both; the same wave
+        // count and fold work as two m-tiles of one tile, with fewer activation line requests: M = 64 at 5120^2
+        // 21.0 -> 19.0 us, at 5120 x 17408 59.7 -> 59.1 us), else two m-tiles (shared weight and scale loads; one
+        // m-tile per wave with twice the waves ran 60-65 us against 58 us at 64 rows x 5120 x 17408)
+#ifndef Q8M_TG
+#define Q8M_TG 2
+#endif
+        if (M > 32 && Q8M_TG == 2 && N % 32 == 0)
+            hipLaunchKernelGGL((w8a8_packed_mid_kernel<6, 1, 2, EPI>), dim3(N / 32, (M + 15) / 16), dim3(64), 0, st,
+                               a, a_s, as_sm, qt, dt, out, ldo, n_rows, M, N, K);
+        else if (M > 32)
+            hipLaunchKernelGGL((w8a8_packed_mid_kernel<6, 2, 1, EPI>), dim3(N / 16, (M + 31) / 32), dim3(64), 0, st,
                                a, a_s, as_sm, qt, dt, out, ldo, n_rows, M, N, K);
         else
-            hipLaunchKernelGGL((w8a8_packed_mid_kernel<8, 1, EPI>), dim3(N / 16, (M + 15) / 16), dim3(64), 0, st,
+            hipLaunchKernelGGL((w8a8_packed_mid_kernel<8, 1, 1, EPI>), dim3(N / 16, (M + 15) / 16), dim3(64), 0, st,
                                a, a_s, as_sm, qt, dt, out, ldo, n_rows, M, N, K);
     } else if (kernel == 0 || kernel == 3) {
         const int tiles_m = (M + PBM - 1) / PBM, tiles_n = (N + PBN - 1) / PBN;
