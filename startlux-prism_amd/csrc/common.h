@@ -45,6 +45,18 @@ __device__ __forceinline__ float sqrt_rn(float a) { return sqrtf(a); }
 __device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
 __device__ __forceinline__ float add_rn(float a, float b) { return __fadd_rn(a, b); }
 
+// rint(RN(y / s)) for a quantizer: s = RN(max(amax, 1e-10) / 127) of a group holding y (so |y / s| <= 127.0001), and
+// r = RN(1 / s) computed once per scale.  q0 = RN(y r) is within |y / s| (3u + u^2) <= 2^-15.4 of RN(y / s) (u = 2^-24:
+// r, the product and the quotient each round once; an underflowing product only moves values far below 1/2), so
+// rint(q0) is rint(RN(y / s)) unless q0 lies within 2^-15 of a half-integer, where the two could fall on different
+// sides or RN(y / s) could be a tie: those few, and non-finite q0, take the exact division.  Bits equal the division's.
+__device__ __forceinline__ float quant_rint(float y, float s, float r) {
+    const float q0 = __fmul_rn(y, r);
+    const float fr = fabsf(q0 - truncf(q0));                 // exact below 2^23
+    if (__builtin_expect(fabsf(fr - 0.5f) > 0x1p-15f, 1)) return rintf(q0);
+    return rintf(__fdiv_rn(y, s));
+}
+
 // RN(x * float(h)) for the fp16 half H (0 low, 1 high) of word, in one v_fma_mix_f32 (fp16 operand widened exactly,
 // one rounding; the -0.0 addend leaves every product, signed zeros included, as the plain product).
 template <int H>

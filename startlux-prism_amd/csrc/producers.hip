@@ -109,13 +109,13 @@ __device__ __forceinline__ void store_back(float (&y)[NCH][8], float rmax, float
             for (int o = 16; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, kWave));
             gmax = m;
         }
-        const float scale = div_rn(fmaxf(gmax, 1e-10f), 127.0f);
+        const float scale = div_rn(fmaxf(gmax, 1e-10f), 127.0f), rs = div_rn(1.0f, scale);
         int sum = 0;
         if (idx < nch) {
             float r[8];
 #pragma unroll
             for (int j = 0; j < 8; j++) {
-                r[j] = rintf(div_rn(y[c][j], scale));
+                r[j] = quant_rint(y[c][j], scale, rs);
                 sum += (int)r[j];
             }
             qr[idx] = v2u{pack4_i8(r), pack4_i8(r + 4)};

@@ -87,7 +87,7 @@ __global__ __launch_bounds__(kQThreads) void quant_rows_i8_kernel(const uint16_t
     }
     amax = block_max(amax, red);
     if (row >= (int64_t)__ldg(n_rows)) return;                 // read after the row's loads went out (see above)
-    const float scale = div_rn(fmaxf(amax, 1e-10f), 127.0f);
+    const float scale = div_rn(fmaxf(amax, 1e-10f), 127.0f), rs = div_rn(1.0f, scale);
     v2u* qr = reinterpret_cast<v2u*>(q + row * K);
 #pragma unroll
     for (int c = 0; c < NCH; c++) {
@@ -95,7 +95,7 @@ __global__ __launch_bounds__(kQThreads) void quant_rows_i8_kernel(const uint16_t
         if (idx < nch) {
             float r[8];
 #pragma unroll
-            for (int j = 0; j < 8; j++) r[j] = rintf(div_rn(v[c][j], scale));
+            for (int j = 0; j < 8; j++) r[j] = quant_rint(v[c][j], scale, rs);
             v2u o;
             o[0] = pack_i8x4(r);
             o[1] = pack_i8x4(r + 4);
@@ -126,10 +126,10 @@ __global__ __launch_bounds__(kQThreads) void quant_rows_groups_kernel(const uint
     }
     for (int o = width / 2; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, kWave));
     if (!live || row >= (int64_t)__ldg(n_rows)) return;        // read after the row's loads went out
-    const float scale = div_rn(fmaxf(amax, 1e-10f), 127.0f);
+    const float scale = div_rn(fmaxf(amax, 1e-10f), 127.0f), rs = div_rn(1.0f, scale);
     float r[8];
 #pragma unroll
-    for (int j = 0; j < 8; j++) r[j] = rintf(div_rn(v[j], scale));
+    for (int j = 0; j < 8; j++) r[j] = quant_rint(v[j], scale, rs);
     v2u o;
     o[0] = pack_i8x4(r);
     o[1] = pack_i8x4(r + 4);
@@ -151,9 +151,9 @@ __global__ __launch_bounds__(kQThreads) void quant_rows_groups_slow_kernel(const
     float amax = 0.f;
     for (int i = threadIdx.x; i < gk; i += kQThreads) amax = fmaxf(amax, fabsf(bf16_to_f32(xr[i])));
     amax = block_max(amax, red);
-    const float scale = div_rn(fmaxf(amax, 1e-10f), 127.0f);
+    const float scale = div_rn(fmaxf(amax, 1e-10f), 127.0f), rs = div_rn(1.0f, scale);
     for (int i = threadIdx.x; i < gk; i += kQThreads)
-        q[row * K + (int64_t)g * gk + i] = (int8_t)(int)rintf(div_rn(bf16_to_f32(xr[i]), scale));
+        q[row * K + (int64_t)g * gk + i] = (int8_t)(int)quant_rint(bf16_to_f32(xr[i]), scale, rs);
     if (threadIdx.x == 0) s[row * (K / gk) + g] = scale;
 }
 
@@ -198,13 +198,13 @@ __global__ __launch_bounds__(kQThreads) void quant_rows_g_kernel(const uint16_t*
 #pragma unroll
             for (int o = 16; o > 0; o >>= 1) gmax = fmaxf(gmax, __shfl_xor(gmax, o, kWave));
         }
-        const float scale = div_rn(fmaxf(gmax, 1e-10f), 127.0f);
+        const float scale = div_rn(fmaxf(gmax, 1e-10f), 127.0f), rs = div_rn(1.0f, scale);
         int sum = 0;
         if (idx < nch) {
             float r[8];
 #pragma unroll
             for (int j = 0; j < 8; j++) {
-                r[j] = rintf(div_rn(v[c][j], scale));
+                r[j] = quant_rint(v[c][j], scale, rs);
                 sum += (int)r[j];
             }
             v2u o;

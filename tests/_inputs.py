@@ -36,3 +36,18 @@ def q6k_random_blocks(N, NB, seed):
     d = (g.random((N, NB)) * 1e-3 + 1e-5).astype(np.float16)
     b[..., 208:210] = d.view(np.uint8).reshape(N, NB, 2)
     return b
+
+
+def half_integer_rows(K):
+    """bf16 rows whose quotients y / scale sit on and beside half-integers, where the quantizers' rounding is decided:
+    row 0 has amax 127 (scale 1: every k + 1/2 an exact tie, rounded to even), row 1 amax 127 / 32 (scale 2^-5, exact
+    ties again), row 2 amax 381 (scale 3: (k + 1/2) 3 rounded to bf16 lands just beside the half-integers), row 3 the
+    same with a sign flip per element.  K a multiple of 256."""
+    k = np.arange(K) % 254 - 127                               # -127 .. 126
+    rows = np.empty((4, K), np.float32)
+    rows[0] = k + 0.5
+    rows[1] = (k + 0.5) / 32
+    rows[2] = (k + 0.5) * 3
+    rows[3] = -rows[2] * np.where(np.arange(K) % 2, 1, -1)
+    rows[0, 0], rows[1, 0], rows[2, 0], rows[3, 0] = 127.0, 127.0 / 32, 381.0, -381.0   # the row maxima
+    return O.bf16_bits(rows)

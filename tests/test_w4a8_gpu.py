@@ -10,7 +10,7 @@ import pytest
 import torch
 
 import oracle as O
-from _inputs import acts_bf16, rng, weights_f32
+from _inputs import acts_bf16, half_integer_rows, rng, weights_f32
 
 pytestmark = pytest.mark.gpu
 
@@ -67,6 +67,22 @@ def test_rows_g_bit_exact(dev, M, K, group, live):
     assert np.array_equal(q.cpu().numpy()[:live], rq[:live])
     assert np.array_equal(s.cpu().numpy()[:, :live], ra[:, :live])
     assert np.array_equal(xs.cpu().numpy()[:, :live], rxs[:, :live])
+
+
+@pytest.mark.parametrize("group", [256, 1024])
+def test_rows_g_half_integers(dev, group):
+    """The W4A8 quantizer on quotients at and beside half-integers (see _inputs.half_integer_rows)."""
+    from prism_amd import quant as KQ
+    x = half_integer_rows(1024)
+    M, K = x.shape
+    q = torch.zeros((M, K), dtype=torch.int8, device=dev)
+    s = torch.zeros(K // group, M, dtype=torch.float32, device=dev)
+    xs = torch.zeros(K // 256, M, 16, dtype=torch.int8, device=dev)
+    KQ.rows_g(_t(x, dev, torch.bfloat16), q, s, xs, _live(M, dev), M, group=group)
+    rq, ra, rxs = O.quant_rows_g(O.bf16_to_f32(x), group, live=M)
+    torch.cuda.synchronize()
+    assert np.array_equal(q.cpu().numpy(), rq) and np.array_equal(s.cpu().numpy(), ra)
+    assert np.array_equal(xs.cpu().numpy(), rxs)
 
 
 def _case(N, K, M, seed, group=256):

@@ -9,7 +9,7 @@ import pytest
 import torch
 
 import oracle as O
-from _inputs import acts_bf16, q8_weights, rng
+from _inputs import acts_bf16, half_integer_rows, q8_weights, rng
 
 pytestmark = pytest.mark.gpu
 
@@ -43,6 +43,24 @@ def test_rows_q8_bit_exact(dev, M, K, live):
     KQ.rows_q8(xd, _t(inv, dev), q, s, _live(live, dev), M)
     rq, rs = O.quant_rows_i8(x, inv_s=inv, live=live)
     assert np.array_equal(q.cpu().numpy()[:live], rq[:live]) and np.array_equal(s.cpu().numpy()[:live], rs[:live])
+
+
+def test_rows_q8_half_integers(dev):
+    """Quotients on and beside half-integers (exact ties at scales 1 and 2^-5): the quantizer's reciprocal product
+    falls back to the exact division there, and the bits stay the oracle's RN(y / s) rounded to even."""
+    from prism_amd import quant as KQ
+    x = half_integer_rows(1024)
+    M, K = x.shape
+    q = torch.zeros((M, K), dtype=torch.int8, device=dev)
+    s = torch.zeros((M,), dtype=torch.float32, device=dev)
+    KQ.rows_q8(_t(x, dev, torch.bfloat16), None, q, s, _live(M, dev), M)
+    rq, rs = O.quant_rows_i8(x, live=M)
+    torch.cuda.synchronize()
+    assert np.array_equal(q.cpu().numpy(), rq) and np.array_equal(s.cpu().numpy(), rs)
+    assert (np.abs(rq[0, 1:].astype(np.int32)) % 2 == 0).all()       # row 0: every tie went to the even neighbour
+    q2, s2 = KQ.quant_rows(_t(x, dev, torch.bfloat16), 32)
+    rq2, rs2 = O.quant_rows_groups(x, 32)
+    assert np.array_equal(q2.cpu().numpy(), rq2) and np.array_equal(s2.cpu().numpy(), rs2)
 
 
 @pytest.mark.parametrize("gk", [32, 64, 256, 1024, 96])
