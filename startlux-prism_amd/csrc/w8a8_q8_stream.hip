@@ -16,7 +16,10 @@
 // RN(RN(float(P) sa) sw) goes to an LDS term buffer.  FW fold waves add the previous rounds' terms of one output per
 // thread in block order while the compute waves run ahead (up to RD rounds, counted through LDS counters: no
 // workgroup barriers in the loop).  Weights and their block scales are requested D - 1 rounds ahead in a register
-// ring.  The activation rows sit in LDS, copied whole at the start when they fit (XL), else they travel in the ring.
+// ring.  The activation rows travel in the ring with the weights (16 bytes per lane and pair, buffer loads); the
+// build option Q8S_XL=1 copies them whole into LDS at the start where they fit (XL), which measured slower at
+// every row count once the ring's activation loads took 16 bytes (5120^2 at 1 row 8.5 against 8.1 us, 5120 x 17408
+// 18.4 against 17.8 us, 16 rows 11.2 against 10.6 us): the copy costs each workgroup the image's bytes up front.
 // Measured on MI355X: twelve compute waves per workgroup (not eight, nor more) for one to four rows; a ring deeper
 // than one round ahead and rounds of other sizes were slower.  From five rows the form depends on the shape (see the
 // launch below).
@@ -304,7 +307,7 @@ static void launch(const int8_t* a, const float* a_s, int64_t as_sm, const int8_
         }                                                                                                           \
     } while (0)
 #ifndef Q8S_XL
-#define Q8S_XL 1
+#define Q8S_XL 0
 #endif
 #ifndef Q8S_SMALL
 #define Q8S_SMALL 12, 48, 4, 2, 4
@@ -319,12 +322,10 @@ static void launch(const int8_t* a, const float* a_s, int64_t as_sm, const int8_
 #define Q8S_WIDE 12, 48, 16, 2, 2
 #endif
 #define QS_(...) QS(__VA_ARGS__)
-    // 5..16 rows: twelve compute waves and rounds of 48 blocks (24 pairs) where a workgroup's share is at least four
-    // such rounds and that form's activation image fits LDS, else eight waves and rounds of 32 where their image
-    // fits, else the activations travel in the register ring, with twelve waves up to 12 rows and eight beyond
-    // (measured: 5120 x 17408 at 8 rows 23.7 -> 20.9 us, at 12 rows 24.8 -> 22.8 us, at 16 rows 0.5-0.9 us slower
-    // with twelve; 5120^2 at 8 rows 10.3 -> 9.8 us; on 4096^2, 64 pairs per workgroup, the eight-wave form is
-    // 0.1-0.4 us faster; at 16 rows on 5120^2 its image fits and it ties)
+    // 5..16 rows (activations in the ring): twelve compute waves and 24-pair rounds up to 12 rows, eight waves and
+    // 16-pair rounds beyond (measured at 5120 x 17408: 8 rows 23.7 -> 20.9 us and 12 rows 24.8 -> 22.8 us with twelve,
+    // 16 rows 0.5-0.9 us slower with twelve).  With the XL build option the image forms come first where they fit:
+    // twelve waves where a workgroup's share spans four 24-pair rounds, else eight.
     const bool wide = (int64_t)(N / 16) * (K / 64) >= 4LL * 24 * W;
     if (M == 1) QS_(Q8S_ONE);
     else if (M <= 4) QS_(Q8S_SMALL);
