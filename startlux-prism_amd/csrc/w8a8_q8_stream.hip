@@ -336,7 +336,7 @@ static void launch(const int8_t* a, const float* a_s, int64_t as_sm, const int8_
     // 16 rows 0.5-0.9 us slower with twelve).  With the XL build option the image forms come first where they fit:
     // twelve waves where a workgroup's share spans four 24-pair rounds, else eight.
     const bool wide = (int64_t)(N / 16) * (K / 64) >= 4LL * 24 * W;
-    // up to 12 rows: ten compute waves (20-pair rounds) instead of twelve (24) when that takes no more rounds of a
+    // every row count: ten compute waves (20-pair rounds) instead of twelve (24) when that takes no more rounds of a
     // workgroup's share (5120^2, 100 pairs: five full rounds, 8.1 -> 7.7 us at one row; at 4096^2 and 5120 x 17408,
     // where twelve waves need fewer rounds, twelve are 0.3-3 us faster)
     const int64_t share = ((int64_t)(N / 16) * (K / 64) + W - 1) / W;
@@ -346,6 +346,7 @@ static void launch(const int8_t* a, const float* a_s, int64_t as_sm, const int8_
     else if (M <= 4 && ten) QS_(Q8S_SMALL10);
     else if (M <= 4) QS_(Q8S_SMALL);
     else if (Q8S_XL && wide && stream_lds(48, 2, M, K, true) <= kLdsMax) QS_(Q8S_WIDE);
+    else if (ten && M > 12) QS_(Q8S_WIDE10);        // 5120^2 at 16 rows 11.1 -> 10.1 us
     else if ((Q8S_XL && stream_lds(32, 2, M, K, true) <= kLdsMax) || M > 12) QS_(Q8S_BIG);
     else if (ten) QS_(Q8S_WIDE10);                  // as at 1-4 rows (5120^2 at 12 rows 10.3 -> 9.2 us)
     else QS_(Q8S_WIDE);
