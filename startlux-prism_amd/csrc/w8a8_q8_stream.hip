@@ -347,6 +347,7 @@ static void launch(const int8_t* a, const float* a_s, int64_t as_sm, const int8_
     else if (M <= 4) QS_(Q8S_SMALL);
     else if (Q8S_XL && wide && stream_lds(48, 2, M, K, true) <= kLdsMax) QS_(Q8S_WIDE);
     else if (ten && M > 12) QS_(Q8S_WIDE10);        // 5120^2 at 16 rows 11.1 -> 10.1 us
+    else if (M > 12 && wide) QS_(Q8S_WIDE);         // 5120 x 17408 at 13 rows 25.5-26.8 -> 23.8-24.4 us, 16 a tie
     else if ((Q8S_XL && stream_lds(32, 2, M, K, true) <= kLdsMax) || M > 12) QS_(Q8S_BIG);
     else if (ten) QS_(Q8S_WIDE10);                  // as at 1-4 rows (5120^2 at 12 rows 10.3 -> 9.2 us)
     else QS_(Q8S_WIDE);
