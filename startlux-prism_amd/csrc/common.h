@@ -132,6 +132,16 @@ __device__ __forceinline__ void vm_wait() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// The same wait through the compiler's builtin, which the compiler's own wait insertion takes into account: after
+// it, loads older than the last N count as complete (an LDS-DMA among them then needs no further wait before the
+// LDS reads that follow).  gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their
+// maxima.
+template <int N>
+__device__ __forceinline__ void vm_wait_tracked() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
 // Dynamic LDS above the default 64 KB needs the kernel's limit raised (up to the CU's 160 KB) before its launch.
 template <typename F>
 inline void allow_lds(F* fn, size_t bytes) {

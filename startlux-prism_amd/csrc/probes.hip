@@ -3,7 +3,8 @@
 //   MFMA: every wave issues independent MFMAs on register operands (no memory traffic), CH accumulator chains per
 //         wave so an instruction never waits on the one before it; one kind per launch: int8
 //         (v_mfma_i32_32x32x32_i8, 65536 ops), fp8 and fp4 (v_mfma_scale_f32_16x16x128_f8f6f4 with unit e8m0 scales,
-//         65536 flops) and bf16 (v_mfma_f32_32x32x16_bf16, 32768 flops).  The same idea as the reference's
+//         65536 flops), bf16 (v_mfma_f32_32x32x16_bf16, 32768 flops) and int8 again with pseudo-random operands that
+//         change from one MFMA to the next (the power a GEMM's operands draw; kind 4).  The same idea as the reference's
 //         bench/csrc/mma_peak.cu:14-70 (mma.sync chains per warp), written for CDNA4's MFMA.
 //   HBM:  each workgroup streams a contiguous slice of a buffer with 16-byte nontemporal loads, U per lane in flight
 //         (the reference's bench/csrc/l2_bw.cu:8 reader, at the sizes the decode GEMMs stream).
@@ -28,6 +29,27 @@ __global__ __launch_bounds__(256) void mfma_peak_kernel(int iters, float* __rest
         for (int i = 0; i < iters; i++)
 #pragma unroll
             for (int j = 0; j < kChains; j++) c[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, a, c[j], 0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < kChains; j++) s += (float)c[j][0];
+    } else if (KIND == 4) {
+        // int8 with operands that change from one MFMA to the next: four pseudo-random register operands per lane
+        // (uniform bytes, as quantized weights and activations look to the multipliers), rotated across the chains,
+        // so the array toggles as in a GEMM; constant operands draw less power, and under the board's power limit
+        // the clock, and so the rate, then differs
+        v4i a[4];
+        uint32_t x = 0x9e3779b9u * (uint32_t)(t + 1) ^ (uint32_t)blockIdx.x * 0x85ebca6bu;
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                x ^= x << 13; x ^= x >> 17; x ^= x << 5;
+                a[q][e] = (int)x;
+            }
+        v16i c[kChains] = {};
+        for (int i = 0; i < iters; i++)
+#pragma unroll
+            for (int j = 0; j < kChains; j++)
+                c[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[j & 3], a[(j + 1 + (i & 1)) & 3], c[j], 0, 0, 0);
 #pragma unroll
         for (int j = 0; j < kChains; j++) s += (float)c[j][0];
     } else if (KIND == 1 || KIND == 2) {
@@ -86,6 +108,7 @@ extern "C" int prism_probe_mfma(int kind, int64_t workgroups, int64_t iters, flo
         case 1: hipLaunchKernelGGL(mfma_peak_kernel<1>, g, b, 0, st, (int)iters, sink); break;
         case 2: hipLaunchKernelGGL(mfma_peak_kernel<2>, g, b, 0, st, (int)iters, sink); break;
         case 3: hipLaunchKernelGGL(mfma_peak_kernel<3>, g, b, 0, st, (int)iters, sink); break;
+        case 4: hipLaunchKernelGGL(mfma_peak_kernel<4>, g, b, 0, st, (int)iters, sink); break;
         default: return PRISM_ERR_ARG;
     }
     PRISM_LAUNCH_CHECK();
@@ -94,7 +117,7 @@ extern "C" int prism_probe_mfma(int kind, int64_t workgroups, int64_t iters, flo
 
 extern "C" int64_t prism_probe_mfma_ops(int kind) {
     switch (kind) {
-        case 0: case 1: case 2: return 65536;
+        case 0: case 1: case 2: case 4: return 65536;
         case 3: return 32768;
         default: return 0;
     }

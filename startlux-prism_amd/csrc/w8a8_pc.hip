@@ -4,15 +4,16 @@
 // epilogue 1 out = RN(out + y).  With a single group there is no per-block fp32 work, so this is a plain int8 MFMA
 // GEMM with an epilogue, and the int32 sum is exact in any order.
 //
-// Tile: TM x 256 outputs (TM = 128 by default, or 256), waves of 128 x 64 (4 x 2 v_mfma_i32_32x32x32_i8 per 32
-// inputs, 128 int32 accumulators per lane).  Default: 128 x 256 tiles of 4 waves in two LDS stages, three
-// workgroups per CU, whose phases drift apart so that one's LDS fragment reads overlap another's MFMAs; one
-// 256 x 256 workgroup of 8 waves per CU ran 4-6% slower, 4 waves of 128 x 128 6-13% slower, 16 waves of 128 x 32 no
-// faster.  Operands go global -> LDS by LDS-DMA (global_load_lds_dwordx4), NS
-// stages of 64 inputs: per stage and operand TM or 256 rows x 64 bytes, each DMA instruction 16 rows x 64 bytes (lane L:
-// row L / 4, 16-byte chunk L % 4 XOR-swizzled by row so that the fragment reads of 8 consecutive rows hit distinct
-// banks).  MFMA operand mapping: lane l holds row l % 32 and the 16 inputs of chunk 2 s + l / 32 for the stage's
-// 32-input step s, the same for both operands.
+// Packed weights (the engine's operand): w8a8_pc_wd_kernel, 128 x 256 tiles of 4 waves of 128 x 64, the activation
+// rows staged through LDS and each wave's weight fragments loaded straight into registers (below).  Plain int8
+// weights: w8a8_pc_tile_kernel, TM x 256 outputs (TM = 128 by default, or 256), waves of 128 x 64 (4 x 2
+// v_mfma_i32_32x32x32_i8 per 32 inputs, 128 int32 accumulators per lane), 128 x 256 tiles of 4 waves in two LDS
+// stages, three workgroups per CU, whose phases drift apart so that one's LDS fragment reads overlap another's MFMAs;
+// one 256 x 256 workgroup of 8 waves per CU ran 4-6% slower, 4 waves of 128 x 128 6-13% slower, 16 waves of 128 x 32
+// no faster.  Its operands go global -> LDS by LDS-DMA (global_load_lds_dwordx4), NS stages of 64 inputs: per stage
+// and operand TM or 256 rows x 64 bytes, each DMA instruction 16 rows x 64 bytes (lane L: row L / 4, 16-byte chunk
+// L % 4 swizzled by row, pc_swz).  MFMA operand mapping: lane l holds row l % 32 and the 16 inputs of chunk
+// 2 s + l / 32 for the stage's 32-input step s, the same for both operands.
 #include "common.h"
 
 namespace prism {
@@ -22,8 +23,47 @@ constexpr int PCK = 64;                         // inputs per stage
 constexpr int PC_OPER = PCT * PCK;              // bytes per operand per stage (16 KB)
 constexpr int PC_STAGE = 2 * PC_OPER;
 
-__device__ __forceinline__ int pc_swz(int row) { return (row >> 1) & 3; }
+// 16-byte chunk swizzle of a 64-byte operand row in LDS: chunk c of row r lies at slot c ^ ((r / 4) % 4), so the 16
+// lanes a ds_read_b128 serves together (16 consecutive rows, one chunk each) fall on 16 distinct 16-byte bank groups
+// ((r / 2) % 4, conflict-free over 8 rows only, cost 4 conflict cycles per read, measured).
+__device__ __forceinline__ int pc_swz(int row) { return (row >> 2) & 3; }
 
+
+// Epilogue of a wave's 128 x 32 TN outputs at tile rows ml0 .. + 127, columns nl0 .. + 32 TN - 1: y = RN(RN(float(P) sa)
+// sw), stored as bf16 (EPI 0) or added to the fp32 output (EPI 1).  acc[t][u] lane l: row 32 t + l % 32, columns
+// 32 u + 8 g + 4 (l / 32) + e for element 4 g + e.
+template <int EPI, int TN>
+__device__ __forceinline__ void pc_store(const v16i (&acc)[4][TN], const float* sal, const float* swl, int ml0,
+                                         int nl0, int lane, int m0, int n0, int live, int N, void* out, int64_t ldo) {
+    const int r = lane & 31, h = lane >> 5;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const int ml = ml0 + 32 * t + r;
+        const int m = m0 + ml;
+        if (m >= live) continue;
+        const float sa = sal[ml];
+#pragma unroll
+        for (int u = 0; u < TN; u++)
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const int nl = nl0 + 32 * u + 8 * g + 4 * h;
+                const int n = n0 + nl;
+                if (n >= N) continue;
+                float y[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) y[e] = mul_rn(mul_rn((float)acc[t][u][4 * g + e], sa), swl[nl + e]);
+                if (EPI == 0) {
+                    uint16_t* o = static_cast<uint16_t*>(out) + (int64_t)m * ldo + n;
+                    *reinterpret_cast<v2u*>(o) = v2u{f32_to_bf16(y[0]) | (f32_to_bf16(y[1]) << 16),
+                                                     f32_to_bf16(y[2]) | (f32_to_bf16(y[3]) << 16)};
+                } else {
+                    float4* o = reinterpret_cast<float4*>(static_cast<float*>(out) + (int64_t)m * ldo + n);
+                    const float4 p = *o;
+                    *o = make_float4(add_rn(p.x, y[0]), add_rn(p.y, y[1]), add_rn(p.z, y[2]), add_rn(p.w, y[3]));
+                }
+            }
+    }
+}
 
 template <bool WPACK, bool WS16, int EPI, int NS, int NWV, int TM>
 __global__ __launch_bounds__(64 * NWV, TM == 128 ? 2 : 1) void w8a8_pc_tile_kernel(const int8_t* __restrict__ a,
@@ -140,33 +180,131 @@ __global__ __launch_bounds__(64 * NWV, TM == 128 ? 2 : 1) void w8a8_pc_tile_kern
         }
     }
 
+    pc_store<EPI, TN>(acc, sal, swl, 128 * wm, CW * wn, lane, m0, n0, live, N, out, ldo);
+}
+
+// Packed weights straight to registers: 128 x 256 tiles of 4 waves, wave wv computing all 128 rows by columns
+// 64 wv .. + 63.  Only the activation rows, which all four waves read, go through LDS (two buffers); each weight
+// fragment is read by one wave only, so it comes from the packed chunks by buffer loads (lane l: the 16 bytes of lane
+// slot 2 s + l / 32, row l % 16 of a 16-row tile: the MFMA operand as it lies) two stages ahead in a register ring.
+// That takes the weights' LDS writes and fragment reads (44% of the tile kernel's LDS traffic) off the LDS.  The
+// activation rows are staged through registers (buffer loads two stages ahead, then one ds_write per 16 bytes)
+// rather than by LDS-DMA: every request is then a plain load, and those complete in order, so one counted wait
+// covers both operands (an LDS-DMA and later buffer loads were measured to complete out of order).  The rings are
+// indexed by stage mod 6 in a loop unrolled by six, so every slot is a fixed register.
+template <bool WS16, int EPI, int TN>
+__global__ __launch_bounds__(256, TN == 2 ? 2 : 1) void w8a8_pc_wd_kernel(const int8_t* __restrict__ a, const float* __restrict__ a_s,
+                                                            int64_t as_sm, const int8_t* __restrict__ w,
+                                                            const void* __restrict__ w_s, void* __restrict__ out,
+                                                            int64_t ldo, const int32_t* __restrict__ n_rows, int M,
+                                                            int N, int K, int tiles_m, int tiles_n) {
+    constexpr int TM = 128, TW = 128 * TN, DIA = 2, WL = 2 * TN, U = 6;   // tile columns TW; DIA activation and WL
+                                                                          // weight loads per wave and stage
+    constexpr int AOPER = TM * PCK;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * AOPER];
+    __shared__ float sal[TM], swl[TW];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    int pm, pn;
+    xcd_tile_coords(blockIdx.x, tiles_m, tiles_n, pm, pn);
+    const int m0 = pm * TM, n0 = pn * TW;
+    const int live = min(M, __ldg(n_rows));
+    if (m0 >= live) return;
+    const int KS = K / PCK;
+
+    if (tid < TM) sal[tid] = a_s[(int64_t)min(m0 + tid, M - 1) * as_sm];
+    for (int t = tid; t < TW; t += 256) {
+        const int n = min(n0 + t, N - 1);
+        swl[t] = WS16 ? f16_to_f32(static_cast<const uint16_t*>(w_s)[n]) : static_cast<const float*>(w_s)[n];
+    }
+
+    // activations: lane L of copy i holds row 16 (DIA wv + i) + L / 4, 16-byte chunk (L % 4) ^ swz of the stage's 64
+    // inputs, stored at LDS byte (DIA wv + i) 1024 + 16 L
+    const __amdgpu_buffer_rsrc_t ra = buf_rsrc(a + (int64_t)m0 * K);
+    uint32_t ao[DIA];
 #pragma unroll
-    for (int t = 0; t < 4; t++) {
-        const int ml = 128 * wm + 32 * t + r;
-        const int m = m0 + ml;
-        if (m >= live) continue;
-        const float sa = sal[ml];
+    for (int i = 0; i < DIA; i++) {
+        const int row = 16 * (DIA * wv + i) + (lane >> 2);
+        ao[i] = (uint32_t)(min(row, M - 1 - m0) * K + 16 * ((lane & 3) ^ pc_swz(row)));
+    }
+    const int r = lane & 31, h = lane >> 5;
+    const int nt0 = n0 >> 4;
+    const __amdgpu_buffer_rsrc_t rw = buf_rsrc(w + (int64_t)nt0 * KS * 1024);
+    uint32_t wo[2][TN];
+#pragma unroll
+    for (int u = 0; u < TN; u++) {
+        const int t = min(nt0 + 2 * TN * wv + 2 * u + (r >> 4), N / 16 - 1) - nt0;
+#pragma unroll
+        for (int s = 0; s < 2; s++) wo[s][u] = (uint32_t)(t * KS * 1024 + (16 * (2 * s + h) + (r & 15)) * 16);
+    }
+    v4i xr[2][DIA], wr[3][2][TN];
+    auto load = [&](int st, v4i (&x)[DIA], v4i (&f)[2][TN]) {       // activations first, then weights
+#pragma unroll
+        for (int i = 0; i < DIA; i++) x[i] = buf_load16(ra, ao[i], (uint32_t)st * PCK);
+        __builtin_amdgcn_sched_barrier(0);         // kept in this order: the waits count the weight loads last
+#pragma unroll
+        for (int s = 0; s < 2; s++)
+#pragma unroll
+            for (int u = 0; u < TN; u++) f[s][u] = buf_load16(rw, wo[s][u], (uint32_t)st * 1024);
+    };
+    auto stage_store = [&](int st, const v4i (&x)[DIA]) {
+#pragma unroll
+        for (int i = 0; i < DIA; i++)
+            *reinterpret_cast<v4i*>(lds + (st & 1) * AOPER + (DIA * wv + i) * 1024 + 16 * lane) = x[i];
+    };
+    int aoff[2][4];
+#pragma unroll
+    for (int s = 0; s < 2; s++)
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const int ra_ = 32 * t + r;
+            aoff[s][t] = ra_ * PCK + 16 * ((2 * s + h) ^ pc_swz(ra_));
+        }
+
+    v16i acc[4][TN];
+#pragma unroll
+    for (int t = 0; t < 4; t++)
 #pragma unroll
         for (int u = 0; u < TN; u++)
 #pragma unroll
-            for (int g = 0; g < 4; g++) {
-                const int nl = CW * wn + 32 * u + 8 * g + 4 * h;
-                const int n = n0 + nl;
-                if (n >= N) continue;
-                float y[4];
+            for (int e = 0; e < 16; e++) acc[t][u][e] = 0;
+
+    // Stage indices past the last are clamped to it (redundant loads into slots never read), so every step issues
+    // the same DIA + WL loads and the waits are fixed counts.  Step st: wait for stage st + 1's activations and
+    // stage st's weights (only stage st + 1's WL weight loads were issued after the former); store those
+    // activations into the free LDS buffer; read stage st's fragments; request stage st + 2; barrier; MFMAs.
+    load(0, xr[0], wr[0]);
+    load(min(1, KS - 1), xr[1], wr[1]);
+    vm_wait_tracked<DIA + 2 * WL>();
+    stage_store(0, xr[0]);
+    lds_barrier();
+    auto step = [&](int st, int j) {                 // j = st mod 6: register slots st mod 2 and st mod 3
+        vm_wait_tracked<WL>();
+        stage_store(st + 1, xr[(j + 1) % 2]);       // past the end: into the free buffer, never read
+        const uint8_t* b = lds + (st & 1) * AOPER;
+        v4i fa[2][4];
 #pragma unroll
-                for (int e = 0; e < 4; e++) y[e] = mul_rn(mul_rn((float)acc[t][u][4 * g + e], sa), swl[nl + e]);
-                if (EPI == 0) {
-                    uint16_t* o = static_cast<uint16_t*>(out) + (int64_t)m * ldo + n;
-                    *reinterpret_cast<v2u*>(o) = v2u{f32_to_bf16(y[0]) | (f32_to_bf16(y[1]) << 16),
-                                                     f32_to_bf16(y[2]) | (f32_to_bf16(y[3]) << 16)};
-                } else {
-                    float4* o = reinterpret_cast<float4*>(static_cast<float*>(out) + (int64_t)m * ldo + n);
-                    const float4 p = *o;
-                    *o = make_float4(add_rn(p.x, y[0]), add_rn(p.y, y[1]), add_rn(p.z, y[2]), add_rn(p.w, y[3]));
-                }
-            }
+        for (int s = 0; s < 2; s++)
+#pragma unroll
+            for (int t = 0; t < 4; t++) fa[s][t] = *reinterpret_cast<const v4i*>(b + aoff[s][t]);
+        load(min(st + 2, KS - 1), xr[j % 2], wr[(j + 2) % 3]);
+        lds_barrier();
+#pragma unroll
+        for (int s = 0; s < 2; s++)
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+#pragma unroll
+                for (int u = 0; u < TN; u++)
+                    acc[t][u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wr[j % 3][s][u], fa[s][t], acc[t][u], 0, 0, 0);
+    };
+    int st = 0;
+    for (; st + U <= KS; st += U) {
+#pragma unroll
+        for (int j = 0; j < U; j++) step(st + j, j);
     }
+#pragma unroll
+    for (int j = 0; j < U - 1; j++)
+        if (st + j < KS) step(st + j, j);
+    pc_store<EPI, TN>(acc, sal, swl, 0, 32 * TN * wv, lane, m0, n0, live, N, out, ldo);
 }
 
 // ---------------------------------------------------------------------------------------------- decode
@@ -327,6 +465,27 @@ int launch_w8a8_pc(int kernel, bool wpack, const int8_t* a, const float* a_s, in
 #undef PDL_G
 #undef PDL_MT
 #undef PDL
+        PRISM_LAUNCH_CHECK();
+        return PRISM_OK;
+    }
+#ifndef PC_WD
+#define PC_WD 1                                   // packed weights: the direct-weight tile kernel, 128 x 256 TN
+                                                  // (1: TN 2, 2: TN 4; 0: the LDS tile kernel)
+#endif
+    if (PC_WD && wpack && (int64_t)N * K < (1LL << 31)) {
+#define PWL(W16, E, TN)                                                                                            \
+    hipLaunchKernelGGL((w8a8_pc_wd_kernel<W16, E, TN>), dim3(tiles_m * tiles_n), dim3(256), 0, st, a, a_s, as_sm, w,\
+                       w_s, out, ldo, n_rows, M, N, K, tiles_m, tiles_n)
+#define PWL_T(TN)                                                                                                  \
+    do {                                                                                                           \
+        const int tiles_m = (M + 127) / 128, tiles_n = (N + 128 * TN - 1) / (128 * TN);                           \
+        if (ws16) { if (epi == 0) PWL(true, 0, TN); else PWL(true, 1, TN); }                                       \
+        else { if (epi == 0) PWL(false, 0, TN); else PWL(false, 1, TN); }                                          \
+    } while (0)
+        if (PC_WD == 2) PWL_T(4);
+        else PWL_T(2);
+#undef PWL_T
+#undef PWL
         PRISM_LAUNCH_CHECK();
         return PRISM_OK;
     }

@@ -64,6 +64,42 @@ def test_config1_q8_0_prefill_full_size(dev):
     assert np.array_equal(_bits(o16), _bits(out)[sub])
 
 
+def test_config1_per_channel_prefill_full_size(dev):
+    """The per-channel projection (weight_from_q8(q8, K), the engine's production operand) at config 1's shape, the
+    per-channel prefill line of the bench: sampled rows bit-exact against the oracle, and the 16-row decode kernel
+    on the same rows gives the same bits."""
+    from prism_amd import gguf_formats as GF
+    from prism_amd import quant as KQ
+    from prism_amd import w8a8 as KW
+    M, K, N = 8192, 5120, 27648
+    g = torch.Generator(device=dev)
+    g.manual_seed(103)
+    q8 = GF.quantize_q8_0(torch.randn(N, K, generator=g, device=dev) * 0.02)
+    pw, _ = KW.weight_from_q8(q8, K)
+    del q8
+    x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+    q = torch.empty(M, K, dtype=torch.int8, device=dev)
+    s = torch.empty(M, dtype=torch.float32, device=dev)
+    n = torch.tensor([M], dtype=torch.int32, device=dev)
+    KQ.rows_q8(x, None, q, s, n, M)
+    out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    KW.gemm(q, s, pw, None, out, n, K, kernel="tile")
+    torch.cuda.synchronize()
+    rows = _rows(M, 3)
+    # the packed chunks back to rows: qt[t, c, l, b] is row 16 t + l % 16, input 64 c + 16 (l / 16) + b
+    w = pw.qt.view(N // 16, K // 64, 4, 16, 16).permute(0, 3, 1, 2, 4).reshape(N, K).cpu().numpy()
+    sw = pw.ws.float().cpu().numpy().reshape(N, 1)
+    qa, sa = q.cpu().numpy()[rows], s.cpu().numpy()[rows]
+    want = O.w8a8_gemm(qa, sa, w, sw, K, epi=0, nthreads=16)
+    assert np.array_equal(_bits(out)[rows], want)
+    sub = rows[:16]
+    o16 = torch.empty(16, N, dtype=torch.bfloat16, device=dev)
+    KW.gemm(_t(qa[:16], dev), _t(sa[:16], dev), pw, None, o16, torch.tensor([16], dtype=torch.int32, device=dev),
+            K, kernel="decode")
+    torch.cuda.synchronize()
+    assert np.array_equal(_bits(o16), _bits(out)[sub])
+
+
 def test_config3_q4k_prefill_full_size(dev):
     """Config 3: M = 2048, K = 5120, N = 13824, Q4_K W4A8, one activation scale per token."""
     from prism_amd import gguf_formats as GF

@@ -192,6 +192,32 @@ def test_per_channel_gk_equals_k(dev, M, N, K, live):
         assert np.array_equal(o1.cpu().numpy(), want1), ("packed", kernel)
 
 
+@pytest.mark.parametrize("K", [64, 192, 320, 384, 448, 832])
+def test_per_channel_packed_stage_counts(dev, K):
+    """The packed per-channel tile kernel walks K in 64-input stages, unrolled by six with the register rings indexed
+    by stage mod 6 and the loads two stages ahead clamped at the end: stage counts 1, 3, 5, 6, 7 and 13, with ragged
+    rows and columns (528 = 2 x 256 + 16) and live rows, both epilogues, bit-exact against the oracle."""
+    from prism_amd import w8a8 as KW
+    M, N, live = 150, 528, 140
+    g = rng(K + 77)
+    a = g.integers(-127, 128, (M, K), dtype=np.int8)
+    w = g.integers(-127, 128, (N, K), dtype=np.int8)
+    sa = (g.random(M) * 1e-2).astype(np.float32)
+    sw = (g.random((N, 1)) * 1e-3).astype(np.float32)
+    base = g.standard_normal((M, N)).astype(np.float32)
+    want = O.w8a8_gemm(a, sa, w, sw, K, epi=0, live=live)
+    want1 = O.w8a8_gemm(a, sa, w, sw, K, epi=1, out=base.copy(), live=live)
+    pw = KW.pack_i8(_t(w, dev), _t(sw, dev))
+    out = torch.full((M, N), 7, dtype=torch.int16, device=dev).view(torch.bfloat16)
+    KW.gemm(_t(a, dev), _t(sa, dev), pw, None, out, _live(live, dev), K, epi=0, kernel="tile")
+    o1 = _t(base, dev).clone()
+    KW.gemm(_t(a, dev), _t(sa, dev), pw, None, o1, _live(live, dev), K, epi=1, kernel="tile")
+    torch.cuda.synchronize()
+    got = out.view(torch.int16).cpu().numpy().view(np.uint16)
+    assert np.array_equal(got[:live], want[:live]) and (got[live:] == 7).all()
+    assert np.array_equal(o1.cpu().numpy(), want1)
+
+
 def test_pack_i8_layout(dev):
     """prism_i8_pack: lane slot l of chunk (t, j) holds row 16 t + l % 16, inputs 64 j + 16 q .. + 15 (q = l / 16),
     checked over the whole tensor against a numpy reshape."""
