@@ -64,8 +64,8 @@ def pack_q8(qs, d):
 class PackedPC(NamedTuple):
     """Per-channel (gk = K) int8 weights [n, k] in 1 KB chunks of 16 rows x 64 inputs (qt int8 [n/16, k/64, 64,
     16], lane slot l: row l % 16, inputs 16 (l / 16) .. + 15), with their per-channel scales ws (fp32 [n, 1]).  Made
-    once at load by pack_i8 / weight_from_q8(q8, K); the decode kernels stream it as 1 KB chunks, the tile kernel
-    copies the chunks to LDS."""
+    once at load by pack_i8 / weight_from_q8(q8, K); the decode kernels stream it as 1 KB chunks, and the prefill
+    tile kernel loads each wave's MFMA fragments straight from them (a lane's 16 bytes are its operand)."""
     qt: torch.Tensor
     ws: torch.Tensor
     n: int
