@@ -216,6 +216,10 @@ def test_per_channel_packed_stage_counts(dev, K):
     got = out.view(torch.int16).cpu().numpy().view(np.uint16)
     assert np.array_equal(got[:live], want[:live]) and (got[live:] == 7).all()
     assert np.array_equal(o1.cpu().numpy(), want1)
+    # row-major int8 weights (prism_w8a8_gemm, the LDS tile kernel) at the same stage counts
+    got = _gemm(dev, a, sa, w, sw, K, 0, "tile", live=live).view(torch.int16).cpu().numpy().view(np.uint16)
+    assert np.array_equal(got[:live], want[:live]) and (got[live:] == 7).all()
+    assert np.array_equal(_gemm(dev, a, sa, w, sw, K, 1, "tile", live=live, out0=base).cpu().numpy(), want1)
 
 
 def test_pack_i8_layout(dev):
