@@ -483,7 +483,7 @@ def measure_peaks(dev):
     out = {}
     wgs, iters = 256 * 8, 256
     for kind, name in ((0, "int8_tops"), (1, "fp8_tflops"), (2, "fp4_tflops"), (3, "bf16_tflops"),
-                       (4, "int8_random_operands_tops")):
+                       (4, "int8_random_operands_tops"), (5, "fp4xfp8_random_operands_tflops")):
         best = 1e30
         for _ in range(4):
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -582,6 +582,9 @@ def main():
         for row in (configs or {}).get(key, []):
             if row.get("bound") == "mfma" and "TOPS" in row:
                 row["frac_of_measured_random_operands"] = round(row["TOPS"] / peaks["int8_random_operands_tops"], 4)
+    for row in (configs or {}).get("c4", []):                     # MXFP4: fp4 operands on the f8f6f4 MFMA
+        if row.get("bound") == "mfma" and "TOPS" in row:
+            row["frac_of_measured_random_operands"] = round(row["TOPS"] / peaks["fp4xfp8_random_operands_tflops"], 4)
     line = {
         "metric": "W8A8/W4A8 GEMM TOPS and GB/s vs MI355X roofline, prefill M=8192 and decode M=1..64",
         "value": round(res["value"], 2),

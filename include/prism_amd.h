@@ -338,7 +338,7 @@ PRISM_API int prism_mxfp4_gemm(const uint8_t* aq, const uint8_t* as, int a_fmt, 
  * each wave issuing `iters` x 4 independent MFMAs of one kind on register operands: 0 int8
  * (v_mfma_i32_32x32x32_i8), 1 fp8 e4m3 and 2 fp4 e2m1 (v_mfma_scale_f32_16x16x128_f8f6f4, unit scales), 3 bf16
  * (v_mfma_f32_32x32x16_bf16), 4 int8 with pseudo-random operands changing from one MFMA to the next (what a GEMM's
- * operands draw under the power limit); prism_probe_mfma_ops gives one instruction's operations (2 M N K).  prism_probe_read
+ * operands draw under the power limit), 5 e2m1 x e4m3 likewise; prism_probe_mfma_ops gives one instruction's operations (2 M N K).  prism_probe_read
  * streams `bytes` of `buf` (16-byte aligned) with `workgroups` workgroups of 512 threads, each a contiguous slice, 8
  * nontemporal 16-byte loads per lane in flight.  `sink` (device, >= workgroups elements) is written only on a value
  * the probes never produce.

@@ -4,7 +4,7 @@
 //         wave so an instruction never waits on the one before it; one kind per launch: int8
 //         (v_mfma_i32_32x32x32_i8, 65536 ops), fp8 and fp4 (v_mfma_scale_f32_16x16x128_f8f6f4 with unit e8m0 scales,
 //         65536 flops), bf16 (v_mfma_f32_32x32x16_bf16, 32768 flops) and int8 again with pseudo-random operands that
-//         change from one MFMA to the next (the power a GEMM's operands draw; kind 4).  The same idea as the reference's
+//         change from one MFMA to the next (the power a GEMM's operands draw; kind 4), and e2m1 x e4m3 likewise (kind 5).  The same idea as the reference's
 //         bench/csrc/mma_peak.cu:14-70 (mma.sync chains per warp), written for CDNA4's MFMA.
 //   HBM:  each workgroup streams a contiguous slice of a buffer with 16-byte nontemporal loads, U per lane in flight
 //         (the reference's bench/csrc/l2_bw.cu:8 reader, at the sizes the decode GEMMs stream).
@@ -46,12 +46,49 @@ __global__ __launch_bounds__(256) void mfma_peak_kernel(int iters, float* __rest
                 a[q][e] = (int)x;
             }
         v16i c[kChains] = {};
-        for (int i = 0; i < iters; i++)
+        // two phases with different operand pairs, every register index fixed (iters MFMAs per chain in all)
+        for (int i = 0; i + 1 < iters; i += 2) {
 #pragma unroll
-            for (int j = 0; j < kChains; j++)
-                c[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[j & 3], a[(j + 1 + (i & 1)) & 3], c[j], 0, 0, 0);
+            for (int j = 0; j < kChains; j++) c[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[j & 3], a[(j + 1) & 3], c[j], 0, 0, 0);
+#pragma unroll
+            for (int j = 0; j < kChains; j++) c[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[j & 3], a[(j + 2) & 3], c[j], 0, 0, 0);
+        }
+        if (iters & 1)
+#pragma unroll
+            for (int j = 0; j < kChains; j++) c[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[j & 3], a[(j + 1) & 3], c[j], 0, 0, 0);
 #pragma unroll
         for (int j = 0; j < kChains; j++) s += (float)c[j][0];
+    } else if (KIND == 5) {
+        // e2m1 x e4m3 (the MXFP4 GEMM's weight x activation formats) with changing pseudo-random operands, as kind 4
+        // for int8 (the e4m3 bytes keep their exponent's low bit clear, so none is a NaN)
+        v8i a[4];
+        uint32_t x = 0x9e3779b9u * (uint32_t)(t + 1) ^ (uint32_t)blockIdx.x * 0x85ebca6bu;
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                x ^= x << 13; x ^= x >> 17; x ^= x << 5;
+                a[q][e] = (int)x;
+            }
+        v8i b[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) b[q] = a[(q + 1) & 3] & 0xf7f7f7f7;
+        v4f c[kChains] = {};
+        for (int i = 0; i + 1 < iters; i += 2) {
+#pragma unroll
+            for (int j = 0; j < kChains; j++)
+                c[j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a[j & 3], b[j & 3], c[j], 4, 0, 0, 127, 0, 127);
+#pragma unroll
+            for (int j = 0; j < kChains; j++)
+                c[j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a[j & 3], b[(j + 1) & 3], c[j], 4, 0, 0, 127, 0,
+                                                                        127);
+        }
+        if (iters & 1)
+#pragma unroll
+            for (int j = 0; j < kChains; j++)
+                c[j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a[j & 3], b[j & 3], c[j], 4, 0, 0, 127, 0, 127);
+#pragma unroll
+        for (int j = 0; j < kChains; j++) s += c[j][0];
     } else if (KIND == 1 || KIND == 2) {
         const v8i a = {0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x22222222, 0x22222222, 0x22222222,
                        0x22222222};
@@ -109,6 +146,7 @@ extern "C" int prism_probe_mfma(int kind, int64_t workgroups, int64_t iters, flo
         case 2: hipLaunchKernelGGL(mfma_peak_kernel<2>, g, b, 0, st, (int)iters, sink); break;
         case 3: hipLaunchKernelGGL(mfma_peak_kernel<3>, g, b, 0, st, (int)iters, sink); break;
         case 4: hipLaunchKernelGGL(mfma_peak_kernel<4>, g, b, 0, st, (int)iters, sink); break;
+        case 5: hipLaunchKernelGGL(mfma_peak_kernel<5>, g, b, 0, st, (int)iters, sink); break;
         default: return PRISM_ERR_ARG;
     }
     PRISM_LAUNCH_CHECK();
@@ -117,7 +155,7 @@ extern "C" int prism_probe_mfma(int kind, int64_t workgroups, int64_t iters, flo
 
 extern "C" int64_t prism_probe_mfma_ops(int kind) {
     switch (kind) {
-        case 0: case 1: case 2: case 4: return 65536;
+        case 0: case 1: case 2: case 4: case 5: return 65536;
         case 3: return 32768;
         default: return 0;
     }
