@@ -486,6 +486,157 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN <= 4 ? 2 : 1) void mx_tile_ke
 }
 
 
+// Direct-weight tile kernel: the 64 x 256 tile of mx_tile_kernel's default (4 waves of 64 x 64, WM = 1), with each
+// wave's weight fragments and scale bytes loaded straight into registers by buffer loads (a lane's 16 bytes of the
+// 1 KB chunk and its scale byte are its MFMA operands as they lie), two steps ahead in a register ring; only the
+// activation rows and their scales, which all four waves read, pass through LDS.  That takes the weights' LDS
+// writes and fragment reads (about half the tile kernel's LDS traffic) off the LDS.  The activations are staged
+// through registers with buffer loads and ds_write rather than LDS-DMA, so every request is a plain load and one
+// counted wait covers both operands (an LDS-DMA and later buffer loads complete out of order).  Same MFMAs in the
+// same order per output as mx_tile_kernel, the same segment folds: identical results.
+template <int AF, int EPI>
+__global__ __launch_bounds__(256, 2) void mx_tile_wd_kernel(const uint8_t* __restrict__ aq,
+                                                            const uint8_t* __restrict__ as,
+                                                            const uint8_t* __restrict__ wq,
+                                                            const uint8_t* __restrict__ ws, void* __restrict__ out,
+                                                            int64_t ldo, const int32_t* __restrict__ n_rows, int M,
+                                                            int N, int K, int tiles_m, int tiles_n) {
+    constexpr int AR = 4, TA = 4;                          // activation tiles of 16 rows (one per wave to stage)
+    constexpr int AT = AF == 0 ? 2048 : 1024;              // activation bytes per tile and step
+    constexpr int ABUF = TA * AT + TA * 256;               // one LDS buffer: the tiles, then their scale dwords
+    constexpr int AP = AF == 0 ? 2 : 1;                    // 16-byte activation loads per lane and step
+    constexpr int WL = 8;                                  // weight loads per step (4 fragments, 4 scale bytes)
+    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * ABUF];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    int pm, pn;
+    xcd_tile_coords(blockIdx.x, tiles_m, tiles_n, pm, pn);
+    const int m0 = pm * 64, n0 = pn * 256;
+    const int live = n_rows ? min(M, __ldg(n_rows)) : M;
+    if (m0 >= live) return;
+    const int KS = K / kMxStep, NT = N / 16;
+    const int p = lane >> 4, r = lane & 15;
+    const int abytes = AF == 0 ? K : K / 2;
+
+    // wave w stages activation tile w: row m0 + 16 w + r, 16-byte piece p of each 64-byte half (e4m3: two halves)
+    const int mr = min(m0 + 16 * w + r, M - 1) - m0;
+    const __amdgpu_buffer_rsrc_t ra = buf_rsrc(aq + (int64_t)m0 * abytes);
+    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(as + (int64_t)m0 * (K / 32));
+    const uint32_t ao = (uint32_t)(mr * abytes + 16 * p), so = (uint32_t)(mr * (K / 32) + p);
+    // weights: tile 4 w + a of the workgroup's 16 (clamped), lane slot l of its chunk, scale byte l
+    const int nt0 = n0 / 16;
+    const __amdgpu_buffer_rsrc_t rw = buf_rsrc(wq + (int64_t)nt0 * KS * 1024);
+    const __amdgpu_buffer_rsrc_t rws = buf_rsrc(ws + (int64_t)nt0 * KS * 64);
+    uint32_t wo[4], wso[4];
+#pragma unroll
+    for (int a = 0; a < 4; a++) {
+        const int t = min(nt0 + 4 * w + a, NT - 1) - nt0;
+        wo[a] = (uint32_t)(t * KS * 1024 + lane * 16);
+        wso[a] = (uint32_t)(t * KS * 64 + lane);
+    }
+    struct Act { v4i q[AP]; uint32_t s; };
+    struct Wt { v4i f[4]; uint32_t s[4]; };
+    Act xr[2];
+    Wt wr[2];
+    auto load_a = [&](int st, Act& x) {
+#pragma unroll
+        for (int h = 0; h < AP; h++) x.q[h] = buf_load16(ra, ao + 64 * h, (uint32_t)st * (AF == 0 ? 128 : 64));
+        x.s = buf_load1(rs, so, (uint32_t)st * 4);
+    };
+    auto load_w = [&](int st, Wt& f) {
+#pragma unroll
+        for (int a = 0; a < 4; a++) f.f[a] = buf_load16(rw, wo[a], (uint32_t)st * 1024);
+#pragma unroll
+        for (int a = 0; a < 4; a++) f.s[a] = buf_load1(rws, wso[a], (uint32_t)st * 64);
+    };
+    auto stage_store = [&](int st, const Act& x) {         // the LDS image mx_tile_kernel's DMA copies make
+        uint8_t* b = lds + (st & 1) * ABUF;
+#pragma unroll
+        for (int h = 0; h < AP; h++) *reinterpret_cast<v4i*>(b + w * AT + h * 1024 + lane * 16) = x.q[h];
+        *reinterpret_cast<uint32_t*>(b + TA * AT + w * 256 + lane * 4) = x.s;
+    };
+
+    v4f acc[4][AR], tot[4][AR];
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int c = 0; c < AR; c++) acc[a][c] = tot[a][c] = v4f{0.f, 0.f, 0.f, 0.f};
+    auto fold = [&](bool first) {                          // segment sum into the running total, left to right
+#pragma unroll
+        for (int a = 0; a < 4; a++)
+#pragma unroll
+            for (int c = 0; c < AR; c++) {
+                const v4f z = acc[a][c];
+                tot[a][c] = first ? z
+                                  : v4f{add_rn(tot[a][c].x, z.x), add_rn(tot[a][c].y, z.y), add_rn(tot[a][c].z, z.z),
+                                        add_rn(tot[a][c].w, z.w)};
+                acc[a][c] = v4f{0.f, 0.f, 0.f, 0.f};
+            }
+    };
+
+    // Both operands two steps ahead in two-slot register rings: step st requests stage st + 2's activations before
+    // its MFMAs and its weights after them (into the slot those MFMAs free).  Stage indices past the last are
+    // clamped (redundant loads into slots never read), so every step issues the same loads and at step st's wait only
+    // stage st + 1's WL weight loads follow stage st + 1's activations.
+    load_a(0, xr[0]);
+    load_w(0, wr[0]);
+    load_a(min(1, KS - 1), xr[1]);
+    load_w(min(1, KS - 1), wr[1]);
+    vm_wait_tracked<2 * WL + AP + 1>();
+    stage_store(0, xr[0]);
+    lds_barrier();
+    auto step = [&](int st, int j) {                       // j = st mod 2: the register slot
+        vm_wait_tracked<WL>();
+        stage_store(st + 1, xr[j ^ 1]);                    // past the end: into the free buffer, never read
+        const uint8_t* b = lds + (st & 1) * ABUF;
+        v8i af[AR];
+        uint32_t asf[AR];
+#pragma unroll
+        for (int c = 0; c < AR; c++) {
+            if (AF == 0) {
+                const v4i lo = *reinterpret_cast<const v4i*>(b + c * AT + lane * 16);
+                const v4i hi = *reinterpret_cast<const v4i*>(b + c * AT + 1024 + lane * 16);
+                af[c] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+            } else {
+                const v4i lo = *reinterpret_cast<const v4i*>(b + c * AT + lane * 16);
+                af[c] = v8i{lo.x, lo.y, lo.z, lo.w, 0, 0, 0, 0};
+            }
+            asf[c] = *reinterpret_cast<const uint32_t*>(b + TA * AT + c * 256 + lane * 4);
+        }
+        load_a(min(st + 2, KS - 1), xr[j]);
+        lds_barrier();
+#pragma unroll
+        for (int a = 0; a < 4; a++)
+#pragma unroll
+            for (int c = 0; c < AR; c++) acc[a][c] = mx_mfma<AF>(wr[j].f[a], af[c], acc[a][c], wr[j].s[a], asf[c]);
+        load_w(min(st + 2, KS - 1), wr[j]);
+    };
+    // segments of kMxSegSteps (8) steps, unrolled, the fold after each; the last segment may be shorter
+    static_assert(kMxSegSteps == 8, "segment unroll");
+    int st = 0;
+    for (; st + kMxSegSteps <= KS; st += kMxSegSteps) {
+#pragma unroll
+        for (int j = 0; j < kMxSegSteps; j++) step(st + j, j & 1);
+        fold(st == 0);
+    }
+    if (st < KS) {
+#pragma unroll
+        for (int j = 0; j < kMxSegSteps - 1; j++)
+            if (st + j < KS) step(st + j, j & 1);
+        fold(st == 0);
+    }
+
+#pragma unroll
+    for (int c = 0; c < AR; c++) {
+        const int m = m0 + 16 * c + r;
+        if (m >= live) continue;
+#pragma unroll
+        for (int a = 0; a < 4; a++) {
+            const int n = n0 + 16 * (4 * w + a) + 4 * p;
+            if (n < N) mx_store<EPI>(out, ldo, m, n, tot[a][c]);
+        }
+    }
+}
+
 // ------------------------------------------------------------------------------ decode kernel, staged activations
 // e4m3 activations, M <= 16.  One workgroup per NTG 16-row weight tiles; waves w = (tile w % NTG, segment lane
 // w / NTG), SL segment lanes, segments taken in rounds of SL.  Per round every wave loads its segment's weights
@@ -709,6 +860,20 @@ extern "C" int prism_mxfp4_gemm(const uint8_t* aq, const uint8_t* as, int a_fmt,
 #undef MXT_
         const int tiles_m = (int)((M + 16 * kAR * kWM - 1) / (16 * kAR * kWM)), tiles_n = (int)((N + 64 * kWN - 1) / (64 * kWN));
         dim3 grid((unsigned)(tiles_m * tiles_n));
+#ifndef MX_WD
+#define MX_WD 1
+#endif
+        if (MX_WD && N * K / 2 < (1LL << 31)) {            // the direct-weight form of the 64 x 256 tile
+            const int tm = (int)((M + 63) / 64), tn = (int)((N + 255) / 256);
+#define TWD(AF, E)                                                                                                   \
+    hipLaunchKernelGGL((mx_tile_wd_kernel<AF, E>), dim3((unsigned)(tm * tn)), dim3(256), 0, st, aq, as, wq, ws, out, \
+                       ldo, n_rows, (int)M, (int)N, (int)K, tm, tn)
+            if (a_fmt == PRISM_MX_E4M3) { if (epi) TWD(0, 1); else TWD(0, 0); }
+            else { if (epi) TWD(4, 1); else TWD(4, 0); }
+#undef TWD
+            PRISM_LAUNCH_CHECK();
+            return PRISM_OK;
+        }
 #define TILE(AF, E)                                                                                                  \
     do {                                                                                                             \
         const size_t lds = (size_t)kNS * MxStage<AF, kWM, kWN, kAR>::BYTES;                                          \
