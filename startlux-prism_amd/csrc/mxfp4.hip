@@ -494,8 +494,8 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN <= 4 ? 2 : 1) void mx_tile_ke
 // through registers with buffer loads and ds_write rather than LDS-DMA, so every request is a plain load and one
 // counted wait covers both operands (an LDS-DMA and later buffer loads complete out of order).  Same MFMAs in the
 // same order per output as mx_tile_kernel, the same segment folds: identical results.
-template <int AF, int EPI>
-__global__ __launch_bounds__(256, 2) void mx_tile_wd_kernel(const uint8_t* __restrict__ aq,
+template <int AF, int EPI, int WT>
+__global__ __launch_bounds__(256, WT == 4 ? 2 : 1) void mx_tile_wd_kernel(const uint8_t* __restrict__ aq,
                                                             const uint8_t* __restrict__ as,
                                                             const uint8_t* __restrict__ wq,
                                                             const uint8_t* __restrict__ ws, void* __restrict__ out,
@@ -505,12 +505,12 @@ __global__ __launch_bounds__(256, 2) void mx_tile_wd_kernel(const uint8_t* __res
     constexpr int AT = AF == 0 ? 2048 : 1024;              // activation bytes per tile and step
     constexpr int ABUF = TA * AT + TA * 256;               // one LDS buffer: the tiles, then their scale dwords
     constexpr int AP = AF == 0 ? 2 : 1;                    // 16-byte activation loads per lane and step
-    constexpr int WL = 8;                                  // weight loads per step (4 fragments, 4 scale bytes)
+    constexpr int WL = 2 * WT;                             // weight loads per step (WT fragments, WT scale bytes)
     __shared__ __attribute__((aligned(16))) uint8_t lds[2 * ABUF];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     int pm, pn;
     xcd_tile_coords(blockIdx.x, tiles_m, tiles_n, pm, pn);
-    const int m0 = pm * 64, n0 = pn * 256;
+    const int m0 = pm * 64, n0 = pn * 64 * WT;
     const int live = n_rows ? min(M, __ldg(n_rows)) : M;
     if (m0 >= live) return;
     const int KS = K / kMxStep, NT = N / 16;
@@ -526,15 +526,15 @@ __global__ __launch_bounds__(256, 2) void mx_tile_wd_kernel(const uint8_t* __res
     const int nt0 = n0 / 16;
     const __amdgpu_buffer_rsrc_t rw = buf_rsrc(wq + (int64_t)nt0 * KS * 1024);
     const __amdgpu_buffer_rsrc_t rws = buf_rsrc(ws + (int64_t)nt0 * KS * 64);
-    uint32_t wo[4], wso[4];
+    uint32_t wo[WT], wso[WT];
 #pragma unroll
-    for (int a = 0; a < 4; a++) {
-        const int t = min(nt0 + 4 * w + a, NT - 1) - nt0;
+    for (int a = 0; a < WT; a++) {
+        const int t = min(nt0 + WT * w + a, NT - 1) - nt0;
         wo[a] = (uint32_t)(t * KS * 1024 + lane * 16);
         wso[a] = (uint32_t)(t * KS * 64 + lane);
     }
     struct Act { v4i q[AP]; uint32_t s; };
-    struct Wt { v4i f[4]; uint32_t s[4]; };
+    struct Wt { v4i f[WT]; uint32_t s[WT]; };
     Act xr[2];
     Wt wr[2];
     auto load_a = [&](int st, Act& x) {
@@ -544,9 +544,9 @@ __global__ __launch_bounds__(256, 2) void mx_tile_wd_kernel(const uint8_t* __res
     };
     auto load_w = [&](int st, Wt& f) {
 #pragma unroll
-        for (int a = 0; a < 4; a++) f.f[a] = buf_load16(rw, wo[a], (uint32_t)st * 1024);
+        for (int a = 0; a < WT; a++) f.f[a] = buf_load16(rw, wo[a], (uint32_t)st * 1024);
 #pragma unroll
-        for (int a = 0; a < 4; a++) f.s[a] = buf_load1(rws, wso[a], (uint32_t)st * 64);
+        for (int a = 0; a < WT; a++) f.s[a] = buf_load1(rws, wso[a], (uint32_t)st * 64);
     };
     auto stage_store = [&](int st, const Act& x) {         // the LDS image mx_tile_kernel's DMA copies make
         uint8_t* b = lds + (st & 1) * ABUF;
@@ -555,14 +555,14 @@ __global__ __launch_bounds__(256, 2) void mx_tile_wd_kernel(const uint8_t* __res
         *reinterpret_cast<uint32_t*>(b + TA * AT + w * 256 + lane * 4) = x.s;
     };
 
-    v4f acc[4][AR], tot[4][AR];
+    v4f acc[WT][AR], tot[WT][AR];
 #pragma unroll
-    for (int a = 0; a < 4; a++)
+    for (int a = 0; a < WT; a++)
 #pragma unroll
         for (int c = 0; c < AR; c++) acc[a][c] = tot[a][c] = v4f{0.f, 0.f, 0.f, 0.f};
     auto fold = [&](bool first) {                          // segment sum into the running total, left to right
 #pragma unroll
-        for (int a = 0; a < 4; a++)
+        for (int a = 0; a < WT; a++)
 #pragma unroll
             for (int c = 0; c < AR; c++) {
                 const v4f z = acc[a][c];
@@ -605,7 +605,7 @@ __global__ __launch_bounds__(256, 2) void mx_tile_wd_kernel(const uint8_t* __res
         load_a(min(st + 2, KS - 1), xr[j]);
         lds_barrier();
 #pragma unroll
-        for (int a = 0; a < 4; a++)
+        for (int a = 0; a < WT; a++)
 #pragma unroll
             for (int c = 0; c < AR; c++) acc[a][c] = mx_mfma<AF>(wr[j].f[a], af[c], acc[a][c], wr[j].s[a], asf[c]);
         load_w(min(st + 2, KS - 1), wr[j]);
@@ -630,8 +630,8 @@ __global__ __launch_bounds__(256, 2) void mx_tile_wd_kernel(const uint8_t* __res
         const int m = m0 + 16 * c + r;
         if (m >= live) continue;
 #pragma unroll
-        for (int a = 0; a < 4; a++) {
-            const int n = n0 + 16 * (4 * w + a) + 4 * p;
+        for (int a = 0; a < WT; a++) {
+            const int n = n0 + 16 * (WT * w + a) + 4 * p;
             if (n < N) mx_store<EPI>(out, ldo, m, n, tot[a][c]);
         }
     }
@@ -864,10 +864,11 @@ extern "C" int prism_mxfp4_gemm(const uint8_t* aq, const uint8_t* as, int a_fmt,
 #define MX_WD 1
 #endif
         if (MX_WD && N * K / 2 < (1LL << 31)) {            // the direct-weight form of the 64 x 256 tile
-            const int tm = (int)((M + 63) / 64), tn = (int)((N + 255) / 256);
+            constexpr int WT = MX_WD == 2 ? 8 : 4;           // weight tiles per wave
+            const int tm = (int)((M + 63) / 64), tn = (int)((N + 64 * WT - 1) / (64 * WT));
 #define TWD(AF, E)                                                                                                   \
-    hipLaunchKernelGGL((mx_tile_wd_kernel<AF, E>), dim3((unsigned)(tm * tn)), dim3(256), 0, st, aq, as, wq, ws, out, \
-                       ldo, n_rows, (int)M, (int)N, (int)K, tm, tn)
+    hipLaunchKernelGGL((mx_tile_wd_kernel<AF, E, WT>), dim3((unsigned)(tm * tn)), dim3(256), 0, st, aq, as, wq, ws,  \
+                       out, ldo, n_rows, (int)M, (int)N, (int)K, tm, tn)
             if (a_fmt == PRISM_MX_E4M3) { if (epi) TWD(0, 1); else TWD(0, 0); }
             else { if (epi) TWD(4, 1); else TWD(4, 0); }
 #undef TWD
