@@ -148,7 +148,7 @@ PRISM_API int prism_w8a8_pc_packed_gemm_split(const int8_t* a, const int8_t* qt,
  * workspace: device memory of at least prism_w8a8_q8_0_packed_workspace_bytes(N, K) bytes, zeroed once before its
  * first use (every launch leaves it zeroed), or NULL (kernel 4 is then unavailable).  Launches that share a
  * workspace must not run concurrently.  This argument is the reference schema's `workspace`
- * (csrc/w8a8_gemm.cu:794-797), which its engine allocates once per device (kernels/cuda_ext.py:432-437).
+ * (csrc/w8a8_gemm.cu:794-797), which its engine allocates once per device (kernels/cuda_ext.py:138-143).
  * Needs K % 128 == 0.
  */
 PRISM_API int prism_w8a8_q8_0_packed_gemm(const int8_t* a, const float* a_s, int64_t as_sm, const int8_t* qt,
@@ -162,11 +162,12 @@ PRISM_API int64_t prism_w8a8_q8_0_packed_workspace_bytes(int64_t N, int64_t K);
 /*
  * prism_w8a8_q8_0_packed_gemm without a workspace argument and without any allocation: the same kernels and bits,
  * with kernel 4's handoff words in a 512 KB array of device memory that the library holds, one per GPU, for the life
- * of the process (found with hipGetSymbolAddress, and cleared by a fill kernel on `stream`, at the first call on a
- * device).  This entry point has no counterpart in the reference; it is for callers that cannot allocate (code
+ * of the process (zero when the library loads; found with hipGetSymbolAddress at the first call on a device, which,
+ * outside graph capture, also clears it with a fill kernel on `stream` and waits for that clear; a first call under
+ * capture records no clear into the graph).  This entry point has no counterpart in the reference; it is for callers that cannot allocate (code
  * under graph capture, tight serving loops, harnesses that forbid hipMalloc).  Calls on one GPU share the array:
  * calls that overlap in time on one GPU (two streams) race; calls in sequence are safe, since every launch leaves
- * the array zeroed.  Workspace needs above 512 KB are rejected with PRISM_ERR_SHAPE (none arises: the balanced
+ * the array zeroed (and a launch's handoff words carry its own tag, so a word another launch left is never taken).  Workspace needs above 512 KB are rejected with PRISM_ERR_SHAPE (none arises: the balanced
  * kernel runs at most 256 workgroups, 2 KB each).  PRISM_ERR_LAUNCH if the array's address cannot be found.
  */
 PRISM_API int prism_w8a8_q8_0_packed_gemm_noalloc(const int8_t* a, const float* a_s, int64_t as_sm, const int8_t* qt,

@@ -69,7 +69,7 @@ __device__ __forceinline__ float mul_f16_rn(float x, uint32_t word) {
 
 // Every listed kernel argument in scalar registers at this point, with one wait: the compiler otherwise loads each
 // argument where it is first used, one scalar memory round trip after another, and a decode-size kernel's first
-// weight request then waits behind several of them.  Up to 14 arguments (all wave-uniform values).
+// weight request then waits behind several of them.  Up to 16 arguments (all wave-uniform values).
 #define PRISM_S_(x) "s"(x)
 #define PRISM_MAP1(f, x) f(x)
 #define PRISM_MAP2(f, x, ...) f(x), PRISM_MAP1(f, __VA_ARGS__)
@@ -85,8 +85,10 @@ __device__ __forceinline__ float mul_f16_rn(float x, uint32_t word) {
 #define PRISM_MAP12(f, x, ...) f(x), PRISM_MAP11(f, __VA_ARGS__)
 #define PRISM_MAP13(f, x, ...) f(x), PRISM_MAP12(f, __VA_ARGS__)
 #define PRISM_MAP14(f, x, ...) f(x), PRISM_MAP13(f, __VA_ARGS__)
-#define PRISM_NARG_(_1, _2, _3, _4, _5, _6, _7, _8, _9, _10, _11, _12, _13, _14, N, ...) N
-#define PRISM_NARG(...) PRISM_NARG_(__VA_ARGS__, 14, 13, 12, 11, 10, 9, 8, 7, 6, 5, 4, 3, 2, 1)
+#define PRISM_MAP15(f, x, ...) f(x), PRISM_MAP14(f, __VA_ARGS__)
+#define PRISM_MAP16(f, x, ...) f(x), PRISM_MAP15(f, __VA_ARGS__)
+#define PRISM_NARG_(_1, _2, _3, _4, _5, _6, _7, _8, _9, _10, _11, _12, _13, _14, _15, _16, N, ...) N
+#define PRISM_NARG(...) PRISM_NARG_(__VA_ARGS__, 16, 15, 14, 13, 12, 11, 10, 9, 8, 7, 6, 5, 4, 3, 2, 1)
 #define PRISM_CAT_(a, b) a##b
 #define PRISM_CAT(a, b) PRISM_CAT_(a, b)
 #define kernel_args_now(...) \

@@ -10,19 +10,32 @@
 // first (its running sums handed on as soon as they are complete), whole tiles in between, the tail last (by when
 // the previous workgroup has long published its head).  A round is up to RP units of one tile.
 //
-// Handoff protocol (per output word, never leaves a word set after a launch): the producer writes (1 << 32) | bits
-// with a compare-and-swap from 0 (whose result it checks only at its end); the consumer takes the bits, normally read
-// one round ahead, else by polling, and clears the word.  A consumer that polls past its bound (a predecessor that
-// never ran: not expected, every predecessor is dispatched first and publishes before it waits on anything) swaps in
-// an "abandoned" tag and takes its value if the producer had just finished, or yields NaN outputs (loud, never
-// silently wrong); a producer that finds "abandoned" clears the word.
+// Handoff protocol (per output word, never leaves a word set after a launch that completes): each launch carries a
+// tag (hand_next_tag: 1 .. 2^32 - 2, a different one per launch made by the library); the producer writes
+// tag << 32 | bits with a compare-and-swap from 0 (whose result it checks at its end); the consumer takes the bits
+// only under its own launch's tag, normally read one round ahead, else by polling, and clears the word.  A consumer
+// that polls past its bound (a predecessor that never ran: not expected, every predecessor is dispatched first and
+// publishes before it waits on anything) swaps in the "abandoned" tag and takes its value if the producer had just
+// finished, or yields NaN outputs (loud, never silently wrong); a producer that finds "abandoned" clears the word.  A
+// word left set by an earlier launch that did not complete (killed, or two streams overlapping on one workspace)
+// carries another tag: the consumer never takes it, and the producer whose compare-and-swap it defeated replaces it
+// with its own value at its end.  What is not detected: a stale word under the same tag, which only a captured
+// graph replayed after a replay of it was killed can leave (a captured launch keeps the tag it was recorded with).
 #pragma once
+
+#include <atomic>
 
 #include "common.h"
 
 namespace prism {
 
-constexpr unsigned long long kTagValid = 1ull << 32, kTagAbandoned = 2ull << 32;
+constexpr unsigned kTagAbandoned = 0xffffffffu;
+
+// The next launch's tag (host side): never 0 (an empty word) nor kTagAbandoned.
+inline unsigned hand_next_tag() {
+    static std::atomic<unsigned> counter{0};
+    return counter.fetch_add(1, std::memory_order_relaxed) % 0xfffffffeu + 1u;
+}
 
 __device__ __forceinline__ unsigned long long hand_load(unsigned long long* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -31,30 +44,52 @@ __device__ __forceinline__ void hand_store(unsigned long long* p, unsigned long 
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Takes the previous workgroup's y (bounded wait).
-__device__ __forceinline__ float hand_take(unsigned long long* p) {
+// Takes the previous workgroup's y published under `tag` (bounded wait).
+__device__ __forceinline__ float hand_take(unsigned long long* p, unsigned tag) {
     for (int it = 0; it < (1 << 22); it++) {
         const unsigned long long v = hand_load(p);
-        if ((v >> 32) == 1) {
+        if ((v >> 32) == tag) {
             hand_store(p, 0);
             return __uint_as_float((uint32_t)v);
         }
         __builtin_amdgcn_s_sleep(2);
     }
-    const unsigned long long old = __hip_atomic_exchange(p, kTagAbandoned, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if ((old >> 32) == 1) {
+    const unsigned long long old =
+        __hip_atomic_exchange(p, (unsigned long long)kTagAbandoned << 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if ((old >> 32) == tag) {
         hand_store(p, 0);
         return __uint_as_float((uint32_t)old);
     }
     return __uint_as_float(0x7fc00000u);
 }
 
-// Publishes y without waiting for the compare-and-swap's result (returned, for the check at the end).
-__device__ __forceinline__ unsigned long long hand_publish(unsigned long long* p, float y) {
+__device__ __forceinline__ unsigned long long hand_word(float y, unsigned tag) {
+    return (unsigned long long)tag << 32 | __float_as_uint(y);
+}
+
+// Publishes `word` without waiting for the compare-and-swap's result (returned, for hand_settle at the end).
+__device__ __forceinline__ unsigned long long hand_publish(unsigned long long* p, unsigned long long word) {
     unsigned long long expect = 0;
-    __hip_atomic_compare_exchange_strong(p, &expect, kTagValid | __float_as_uint(y), __ATOMIC_RELAXED,
-                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_compare_exchange_strong(p, &expect, word, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
     return expect;
+}
+
+// The producer's check at its end, `old` being hand_publish's result: 0, the publish stood; "abandoned", the
+// consumer gave up (clear the word); anything else is a stale word of another launch that the publish did not
+// replace: replace it now (the consumer polls for this launch's tag meanwhile, or abandons it).
+__device__ __forceinline__ void hand_settle(unsigned long long* p, unsigned long long old, unsigned long long word) {
+    for (int it = 0; it < 4 && old != 0; it++) {
+        if ((old >> 32) == kTagAbandoned) {
+            hand_store(p, 0);
+            return;
+        }
+        unsigned long long expect = old;
+        if (__hip_atomic_compare_exchange_strong(p, &expect, word, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT))
+            return;
+        old = expect;
+    }
 }
 
 // Bounded wait on an LDS counter (workgroup scope): every wave of the workgroup is resident, so the counter's

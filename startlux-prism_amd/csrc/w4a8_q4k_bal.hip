@@ -23,13 +23,13 @@ template <int NW, int MX, int RD, int EPI>
 __global__ __launch_bounds__((NW + (MX * 16 + 63) / 64) * 64) void w4a8_q4k_bal_kernel(
     const int8_t* __restrict__ xq, const float* __restrict__ a, int64_t a_sb, const int8_t* __restrict__ xs,
     const uint8_t* __restrict__ qv, const uint8_t* __restrict__ meta, void* __restrict__ out, int64_t ldo,
-    const int32_t* __restrict__ n_rows, int M, int N, int K, unsigned long long* __restrict__ hand) {
+    const int32_t* __restrict__ n_rows, int M, int N, int K, unsigned long long* __restrict__ hand, unsigned tag) {
     constexpr int FW = (MX * 16 + 63) / 64;
     constexpr int NT = NW * 64;                    // compute threads; NT .. NT + 64 FW - 1 fold
     constexpr int RP = NW;                         // super-blocks per round, one per compute wave
     static_assert(MX <= 16, "one 16-row activation tile");
     const int W = gridDim.x, v = blockIdx.x;
-    kernel_args_now(xq, a, a_sb, xs, qv, meta, out, ldo, n_rows, M, N, K, hand, W);
+    kernel_args_now(xq, a, a_sb, xs, qv, meta, out, ldo, n_rows, M, N, K, hand, tag, W);
     const int NB = K / 256;
     const int LDX = K + 32;                        // activation image row (bytes)
     extern __shared__ __attribute__((aligned(16))) int8_t dsm[];
@@ -141,7 +141,7 @@ __global__ __launch_bounds__((NW + (MX * 16 + 63) / 64) * 64) void w4a8_q4k_bal_
         float y = 0.f;
         __syncthreads();
         const int live = min(M, __ldg(n_rows));
-        unsigned long long pre = 0, pub_old = 0;
+        unsigned long long pre = 0, pub_old = 0, pub_word = 0;
         unsigned long long* pub = nullptr;
         for (int r = 0; r < NR; r++) {
             const Round d = walk.round(r);
@@ -155,11 +155,11 @@ __global__ __launch_bounds__((NW + (MX * 16 + 63) / 64) * 64) void w4a8_q4k_bal_
                 if (d.first) {
                     if (d.ps == 0) {
                         y = 0.f;
-                    } else if ((pre >> 32) == 1) {
+                    } else if ((pre >> 32) == tag) {
                         hand_store(hand + (int64_t)(v - 1) * (MX * 16) + fo, 0);
                         y = __uint_as_float((uint32_t)pre);
                     } else {
-                        y = hand_take(hand + (int64_t)(v - 1) * (MX * 16) + fo);
+                        y = hand_take(hand + (int64_t)(v - 1) * (MX * 16) + fo, tag);
                     }
                 }
                 const float* tp = terms + slot * tstride + fo;
@@ -170,7 +170,8 @@ __global__ __launch_bounds__((NW + (MX * 16 + 63) / 64) * 64) void w4a8_q4k_bal_
                 if (d.last) {
                     if (d.pe < NB) {
                         pub = hand + (int64_t)v * (MX * 16) + fo;
-                        pub_old = hand_publish(pub, y);
+                        pub_word = hand_word(y, tag);
+                        pub_old = hand_publish(pub, pub_word);
                     } else if (mo < live) {
                         const int n = 16 * d.nt + (fo & 15);
                         if (EPI == 0) {
@@ -185,8 +186,8 @@ __global__ __launch_bounds__((NW + (MX * 16 + 63) / 64) * 64) void w4a8_q4k_bal_
             // the wave's reads of the slot are complete before it is counted released
             if (lane == 0) __hip_atomic_fetch_add(&fdone[slot], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
-        // a consumer that gave up on this word (never expected) left it tagged abandoned: clear it
-        if (pub && pub_old == kTagAbandoned) hand_store(pub, 0);
+        // a consumer that gave up on the word (never expected) or a stale word of another launch: settle it
+        if (pub) hand_settle(pub, pub_old, pub_word);
     }
 }
 
@@ -212,10 +213,11 @@ static void q4k_bal_run(const int8_t* xq, const float* a, int64_t a_sb, const in
                         const uint8_t* meta, void* out, int64_t ldo, const int32_t* n_rows, int M, int N, int K,
                         unsigned long long* hand, hipStream_t st) {
     auto fn = w4a8_q4k_bal_kernel<kQ4BalNW, MX, kQ4BalRD, EPI>;
+    const unsigned tag = hand_next_tag();
     const size_t lds = q4k_bal_lds(M, K);
     allow_lds(fn, lds);
     hipLaunchKernelGGL(fn, dim3(q4k_bal_workgroups(N)), dim3((kQ4BalNW + (MX * 16 + 63) / 64) * 64), lds, st, xq, a,
-                       a_sb, xs, qv, meta, out, ldo, n_rows, M, N, K, hand);
+                       a_sb, xs, qv, meta, out, ldo, n_rows, M, N, K, hand, tag);
 }
 
 int q4k_bal_launch(const int8_t* xq, const float* a, int64_t a_sb, const int8_t* xs, const uint8_t* qv,

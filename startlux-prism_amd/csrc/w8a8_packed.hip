@@ -674,8 +674,11 @@ extern "C" int64_t prism_w8a8_q8_0_packed_workspace_bytes(int64_t N, int64_t K) 
 // ---------------------------------------------------------------------------------------------- no-allocation form
 // For callers that cannot allocate (code under graph capture, serving loops, harnesses that forbid hipMalloc): the
 // balanced decode kernel's workspace is this file-scope device array instead of a caller's buffer.  Each GPU holds
-// its own copy (zero-initialised when the code object loads, cleared once more by a fill kernel at the first call
-// on the device, and left zeroed by every launch: each handoff word is reset by the workgroup that consumes it).
+// its own copy, zero-initialised when the code object loads; the first call on a device that is not being captured
+// clears it once more with a fill kernel and waits for that clear before the address is kept.  A first call under
+// graph capture records no clear into the caller's graph: it relies on the load-time zero, and the address is kept
+// only once a clear has run.  Every launch leaves the array zeroed (each handoff word is reset by the workgroup that
+// consumes it, and words of a launch that did not complete carry another launch's tag, never taken).
 // In host code the array's name is not a device address; its per-device address comes from hipGetSymbolAddress.
 constexpr int64_t kScratchBytes = 512 * 1024;
 static __device__ __align__(256) unsigned long long scratch[kScratchBytes / 8];
@@ -690,20 +693,22 @@ constexpr int kMaxDevices = 64;
 static void* g_scratch[kMaxDevices];
 static std::mutex g_scratch_mu;
 
-// The device's scratch address (looked up, and cleared on `st`, at the first call on the device), or nullptr.
+// The device's scratch address, or nullptr.  At the first call on the device outside capture: looked up, cleared on
+// `st` and waited for, then kept.  Under capture: looked up and returned, not kept, nothing recorded.
 static void* device_scratch(hipStream_t st) {
     int dev = -1;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
     std::lock_guard<std::mutex> lock(g_scratch_mu);
-    if (!g_scratch[dev]) {
-        void* ptr = nullptr;
-        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
-        hipLaunchKernelGGL(scratch_clear_kernel, dim3(64), dim3(256), 0, st, (unsigned long long*)ptr,
-                           kScratchBytes / 8);
-        if (hipGetLastError() != hipSuccess) return nullptr;
-        g_scratch[dev] = ptr;
-    }
-    return g_scratch[dev];
+    if (g_scratch[dev]) return g_scratch[dev];
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess) return nullptr;
+    if (cs != hipStreamCaptureStatusNone) return ptr;
+    hipLaunchKernelGGL(scratch_clear_kernel, dim3(64), dim3(256), 0, st, (unsigned long long*)ptr, kScratchBytes / 8);
+    if (hipGetLastError() != hipSuccess || hipStreamSynchronize(st) != hipSuccess) return nullptr;
+    g_scratch[dev] = ptr;
+    return ptr;
 }
 
 extern "C" int prism_w8a8_q8_0_packed_gemm_noalloc(const int8_t* a, const float* a_s, int64_t as_sm, const int8_t* qt,

@@ -8,7 +8,7 @@
 // workgroup finishes (a "head").  Every output's fp32 sum over blocks runs in block order (kernels/w8a8.py:74-76), so a
 // tail's fold has to start from the head's running sums.  The workgroup walks its tiles last to first: the head comes
 // first and its running sums are handed to the next workgroup through the workspace (one 64-bit word per output:
-// a "valid" tag and the fp32 bits), and the tail comes last, by when the previous workgroup has long published its
+// the launch's tag and the fp32 bits), and the tail comes last, by when the previous workgroup has long published its
 // head.  Whole tiles in between fold from zero and store their outputs.
 //
 // Inside a workgroup: NW compute waves take the round's block pairs (CP each); per block one MFMA with the activation
@@ -35,7 +35,7 @@ template <int NW, int R, int MX, int D, int RD, int EPI, bool XL>
 __global__ __launch_bounds__((NW + (MX * 16 + 63) / 64) * 64) void w8a8_q8_stream_kernel(
     const int8_t* __restrict__ a, const float* __restrict__ a_s, int64_t as_sm, const int8_t* __restrict__ qt,
     const uint16_t* __restrict__ dt, void* __restrict__ out, int64_t ldo, const int32_t* __restrict__ n_rows, int M,
-    int N, int K, unsigned long long* __restrict__ hand) {
+    int N, int K, unsigned long long* __restrict__ hand, unsigned tag) {
     constexpr int FW = (MX * 16 + 63) / 64;
     constexpr int NT = NW * 64;                    // compute threads; NT .. NT + 64 FW - 1 fold
     constexpr int RP = R / 2;                      // block pairs per round
@@ -59,7 +59,7 @@ __global__ __launch_bounds__((NW + (MX * 16 + 63) / 64) * 64) void w8a8_q8_strea
     // round trip after another before the first weight request
     const int W = gridDim.x, v = blockIdx.x;
     asm volatile("" ::"s"(a), "s"(a_s), "s"(as_sm), "s"(qt), "s"(dt), "s"(out), "s"(ldo), "s"(n_rows), "s"(M), "s"(N),
-                 "s"(K), "s"(hand), "s"(W));
+                 "s"(K), "s"(hand), "s"(tag), "s"(W));
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int KP = K / 64;
     const int lm = lane & 15, q = lane >> 4;
@@ -215,7 +215,7 @@ __global__ __launch_bounds__((NW + (MX * 16 + 63) / 64) * 64) void w8a8_q8_strea
         unsigned long long pre = 0;
         // the running sums handed on: the compare-and-swap's result is checked once, at the end
         unsigned long long* pub = nullptr;
-        unsigned long long pub_old = 0;
+        unsigned long long pub_old = 0, pub_word = 0;
         for (int r = 0; r < NR; r++) {
             const Round d = round_of(r);
             const int slot = r % RD;
@@ -228,11 +228,11 @@ __global__ __launch_bounds__((NW + (MX * 16 + 63) / 64) * 64) void w8a8_q8_strea
                 if (d.first) {
                     if (d.ps == 0) {
                         y = 0.f;
-                    } else if ((pre >> 32) == 1) {
+                    } else if ((pre >> 32) == tag) {
                         hand_store(hand + (int64_t)(v - 1) * (MX * 16) + fo, 0);
                         y = __uint_as_float((uint32_t)pre);
                     } else {
-                        y = hand_take(hand + (int64_t)(v - 1) * (MX * 16) + fo);
+                        y = hand_take(hand + (int64_t)(v - 1) * (MX * 16) + fo, tag);
                     }
                 }
                 const float* tp = terms + slot * tstride + fo * TL;
@@ -253,7 +253,8 @@ __global__ __launch_bounds__((NW + (MX * 16 + 63) / 64) * 64) void w8a8_q8_strea
                 if (d.last) {
                     if (d.pe < KP) {
                         pub = hand + (int64_t)v * (MX * 16) + fo;
-                        pub_old = hand_publish(pub, y);
+                        pub_word = hand_word(y, tag);
+                        pub_old = hand_publish(pub, pub_word);
                     } else {
                         const int m = fo >> 4, n = 16 * d.nt + (fo & 15);
                         if (m < live) {
@@ -270,8 +271,8 @@ __global__ __launch_bounds__((NW + (MX * 16 + 63) / 64) * 64) void w8a8_q8_strea
             // the wave's reads of the slot are complete before it is counted released
             if (lane == 0) __hip_atomic_fetch_add(&fdone[slot], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
-        // a consumer that gave up on this word (never expected) left it tagged abandoned: clear it
-        if (pub && pub_old == kTagAbandoned) hand_store(pub, 0);
+        // a consumer that gave up on the word (never expected) or a stale word of another launch: settle it
+        if (pub) hand_settle(pub, pub_old, pub_word);
     }
 }
 
@@ -291,6 +292,7 @@ template <int EPI>
 static void launch(const int8_t* a, const float* a_s, int64_t as_sm, const int8_t* qt, const uint16_t* dt, void* out,
                    int64_t ldo, const int32_t* n_rows, int M, int N, int K, unsigned long long* hand, int W,
                    hipStream_t st) {
+    const unsigned tag = hand_next_tag();
 #define QS(NW, R, MX, D, RD)                                                                                        \
     do {                                                                                                            \
         constexpr int NTH = (NW + (MX * 16 + 63) / 64) * 64;                                                        \
@@ -298,12 +300,12 @@ static void launch(const int8_t* a, const float* a_s, int64_t as_sm, const int8_
             auto fn = w8a8_q8_stream_kernel<NW, R, MX, D, RD, EPI, true>;                                           \
             allow_lds(fn, stream_lds(R, RD, M, K, true));                                                           \
             hipLaunchKernelGGL(fn, dim3(W), dim3(NTH), stream_lds(R, RD, M, K, true), st, a, a_s, as_sm, qt, dt,    \
-                               out, ldo, n_rows, M, N, K, hand);                                                    \
+                               out, ldo, n_rows, M, N, K, hand, tag);                                               \
         } else {                                                                                                    \
             auto fn = w8a8_q8_stream_kernel<NW, R, MX, D, RD, EPI, false>;                                          \
             allow_lds(fn, stream_lds(R, RD, M, K, false));                                                          \
             hipLaunchKernelGGL(fn, dim3(W), dim3(NTH), stream_lds(R, RD, M, K, false), st, a, a_s, as_sm, qt, dt,   \
-                               out, ldo, n_rows, M, N, K, hand);                                                    \
+                               out, ldo, n_rows, M, N, K, hand, tag);                                               \
         }                                                                                                           \
     } while (0)
 #ifndef Q8S_XL

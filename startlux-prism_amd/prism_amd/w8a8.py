@@ -172,7 +172,7 @@ _WS = {}
 
 def workspace(dev):
     """The per-device workspace of the packed Q8_0 "stream" kernel (the reference schema's `workspace`, allocated once
-    per device as kernels/cuda_ext.py:432-437 does): zeroed once, left zeroed by every launch.  None while a graph is
+    per device as kernels/cuda_ext.py:138-143 does): zeroed once, left zeroed by every launch.  None while a graph is
     being captured on a device that has none yet (its zero fill would be a graph node): "auto" then picks another
     kernel and "stream" raises."""
     idx = dev.index if dev.index is not None else torch.cuda.current_device()
