@@ -21,6 +21,7 @@
 #include "common.h"
 #include "w4a8_bal.h"
 #include "w4a8_common.h"
+#include "w4a8_tile.h"
 
 #ifndef Q4S_TG2_ROWS
 #define Q4S_TG2_ROWS 5
@@ -913,7 +914,11 @@ extern "C" int prism_w4a8_q4k_gemm(const int8_t* xq, const float* a, int64_t a_s
         else { if (epi == 0) W4S_TG(4, 0); else W4S_TG(4, 1); }
 #undef W4S_TG
 #undef W4S
+    } else if ((int64_t)(N / 16) * (K / 256) * 2048 < ((int64_t)1 << 31) && M * K < ((int64_t)1 << 31)) {
+        // the 128 x 128 tile kernel (w4a8_q4k_tile.hip), whose stage offsets are 32-bit
+        q4k_tile_launch(xq, a, a_sb, xs, qv, meta, out, ldo, n_rows, Mi, Ni, Ki, epi, st);
     } else {
+        // operands of 2 GB or more: the 128 x 64 tile kernel above
         const int tiles_m = (Mi + QBM - 1) / QBM, tiles_n = (Ni + QBN - 1) / QBN;
         if (epi == 0)
             hipLaunchKernelGGL((w4a8_tile_kernel<0>), dim3(tiles_m * tiles_n), dim3(256), 0, st, xq, a, a_sb, xs, qv,
