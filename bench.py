@@ -164,7 +164,7 @@ def _copies(wbytes, M):
 def _row(M, K, N, us, wbytes, bound, peak=None):
     gbs = wbytes / (us * 1e-6) / 1e9
     tops = 2 * M * N * K / (us * 1e-6) / 1e12
-    r = dict(M=M, K=K, N=N, us=round(us, 2), GBps=round(gbs, 1), TOPS=round(tops, 2), bound=bound)
+    r = dict(M=M, K=K, N=N, us=round(us, 2), GBps=round(gbs, 1), TOPS=round(tops, 2), bound=bound, bytes=wbytes)
     r["frac"] = round(gbs / PEAK_HBM_GBS, 3) if bound == "hbm" else round(tops / peak, 4)
     return r
 
@@ -471,6 +471,49 @@ def cpu_reference_path(sample, rows_max=M1, budget_s=5.0):
                        f"{dt:.2f} s")
 
 
+def read_probe(dev, sizes):
+    """The attainable HBM read time of each byte size in `sizes`: the library's read probe (prism_probe_read, 16-byte
+    loads over the whole buffer) graph-replayed back to back with copies rotated past the MALL, exactly as the decode
+    lines are timed.  Returns {nbytes: (us, GB/s)}."""
+    import ctypes
+    import torch
+    from prism_amd import _lib as L
+    st = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)   # noqa: E731
+    sink = torch.zeros(1 << 16, dtype=torch.float32, device=dev)
+    out = {}
+    sizes = sorted(set(int(n) for n in sizes))
+    if not sizes:
+        return out
+    buf = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    buf.fill_(1)
+    for nbytes in sizes:
+        copies = _copies(nbytes, 1)
+        views = [buf[i * nbytes:(i + 1) * nbytes] for i in range(min(copies, (1 << 30) // nbytes))]
+        us = _graph_us(lambda i: L.call("prism_probe_read", L.ptr(views[i]), nbytes, 256, L.ptr(sink), st()),
+                       len(views), 40)
+        out[nbytes] = (us, nbytes / us / 1e3)
+    del buf
+    torch.cuda.empty_cache()
+    return out
+
+
+def annotate_hbm_rows(configs, probes):
+    """Every HBM-bound line also against the read probe of its own byte size (the rate a pure read of those bytes
+    attains here), besides `frac` against the published 8 TB/s."""
+    for rows in configs.values():
+        for row in rows if isinstance(rows, list) else []:
+            if row.get("bound") == "hbm" and row.get("bytes") in probes:
+                us, gbs = probes[row["bytes"]]
+                row["read_probe_us"] = round(us, 2)
+                row["read_probe_GBps"] = round(gbs, 1)
+                row["frac_of_measured"] = round(row["GBps"] / gbs, 3)
+
+
+def hbm_sizes(configs):
+    return [r["bytes"] for rows in configs.values() if isinstance(rows, list) for r in rows
+            if r.get("bound") == "hbm" and "bytes" in r]
+
+
 def measure_peaks(dev):
     """The roofline denominators measured on this GPU with the library's probes: dense MFMA rates (int8, fp8, fp4,
     bf16; independent MFMA chains in registers) and the HBM read rate (a 1 GiB stream, and the decode GEMMs' sizes
@@ -565,11 +608,17 @@ def main():
         print(json.dumps({"copy_bytes_read": src.numel() * 4, "copy_bytes_written": dst.numel() * 4}))
         return
     if a.only:
-        print(json.dumps({"configs": bench_configs(dev, a.only.split(","))}), flush=True)
+        configs = bench_configs(dev, a.only.split(","))
+        annotate_hbm_rows(configs, read_probe(dev, hbm_sizes(configs)))
+        print(json.dumps({"configs": configs}), flush=True)
         return
     res, sample = bench_prefill(a.steps, a.warmup, dev)
     configs = None if a.no_sweep else bench_configs(dev)
     peaks = measure_peaks(dev)
+    if configs:
+        probes = read_probe(dev, hbm_sizes(configs))
+        annotate_hbm_rows(configs, probes)
+        peaks["read_probe_us_by_bytes"] = {str(k): round(v[0], 2) for k, v in probes.items()}
     cpu = None
     if not a.no_cpu:
         cpu = cpu_baseline(sample, a.cpu_rows)
