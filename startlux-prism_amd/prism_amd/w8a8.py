@@ -75,9 +75,24 @@ class PackedPC(NamedTuple):
     def shape(self):
         return (self.n, self.k)
 
+    def __getitem__(self, key):
+        """w[r0:r1]: the rows r0 .. r1 - 1 as a PackedPC view (no copy; r0 and r1 multiples of 16, whole 16-row
+        chunks), the engine's row slice of a fused projection (engine/model.py:848-850: lw["qkv_q"][qn:]).  An integer
+        index is the tuple's field."""
+        if not isinstance(key, slice):
+            return tuple.__getitem__(self, key)
+        r0, r1, step = key.indices(self.n)
+        if step != 1 or r0 % 16 or r1 % 16 or r1 <= r0:
+            raise ValueError(f"PackedPC rows [{key.start}:{key.stop}]: whole 16-row chunks only")
+        return PackedPC(self.qt[r0 // 16:r1 // 16], self.ws[r0:r1], r1 - r0, self.k)
+
 
 def pack_i8(w, ws):
-    """int8 [n, k] and scales [n] / [n, 1] (on the GPU) -> PackedPC (n % 16 == 0, k % 64 == 0)."""
+    """int8 [n, k] and scales [n] / [n, 1] (on the GPU) -> PackedPC (n % 16 == 0, k % 64 == 0).  The load-time step
+    for the engine's smooth_quant output (engine/model.py:72-82): `wq, ws, extra = smooth_quant(...)` followed by
+    `wq = pack_i8(wq, ws)` gives the operand the packed per-channel kernels read; the engine's calls
+    `KW.gemm(xq, as_, wq, ws, ...)` and its row slices `wq[qn:]` then work unchanged (`ws` is then ignored: the
+    scales travel in the PackedPC)."""
     n, k = w.shape
     if w.dtype != torch.int8 or not w.is_contiguous():
         raise ValueError("pack_i8: w must be contiguous int8 [n, k]")

@@ -59,8 +59,11 @@ def test_engine_kquant_segments(dev):
     assert np.array_equal(part.view(torch.int16).cpu().numpy().view(np.uint16), want[:, 64:])
 
 
-def test_engine_per_channel_plain_weights(dev):
-    """KW.gemm(xq, as_, lw["qkv_q"][qn:], lw["qkv_s"][qn:], proj[:, qn:], tok, hidden) with int8 [N, K] and fp32 [N]."""
+@pytest.mark.parametrize("form", ["plain", "packed_at_load"])
+def test_engine_per_channel_plain_weights(dev, form):
+    """KW.gemm(xq, as_, lw["qkv_q"][qn:], lw["qkv_s"][qn:], proj[:, qn:], tok, hidden) with smooth_quant's int8 [N, K]
+    and fp32 [N] as they are (plain), or after the one load-time line `wq = KW.pack_i8(wq, ws)` (packed_at_load: the
+    engine's calls and row slices unchanged, the packed per-channel kernels)."""
     from prism_amd import w8a8 as KW
     M, K, N, qn = 21, 2048, 384, 128
     g = rng(520)
@@ -70,6 +73,9 @@ def test_engine_per_channel_plain_weights(dev):
     a, sa = O.quant_rows_i8(acts_bf16(M, K, seed=522))
     want = O.w8a8_gemm(a, sa, wq.numpy(), ws.numpy().reshape(N, 1), K, epi=0)
     wd, wsd = wq.to(dev), ws.to(dev)
+    if form == "packed_at_load":
+        wd = KW.pack_i8(wd, wsd)
+        assert wd.shape == (N, K) and wd[qn:].shape == (N - qn, K)
     ad, sad = _t(a, dev), _t(sa, dev)
     n = torch.tensor([M], dtype=torch.int32, device=dev)
     proj = torch.full((M, N), 7, dtype=torch.int16, device=dev).view(torch.bfloat16)
