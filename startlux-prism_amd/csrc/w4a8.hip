@@ -21,7 +21,7 @@
 #include "common.h"
 #include "w4a8_bal.h"
 #include "w4a8_common.h"
-#include "w4a8_tile.h"
+#include "w4a8_prefill.h"
 
 #ifndef Q4S_TG2_ROWS
 #define Q4S_TG2_ROWS 5
@@ -915,7 +915,7 @@ extern "C" int prism_w4a8_q4k_gemm(const int8_t* xq, const float* a, int64_t a_s
 #undef W4S_TG
 #undef W4S
     } else if ((int64_t)(N / 16) * (K / 256) * 2048 < ((int64_t)1 << 31) && M * K < ((int64_t)1 << 31)) {
-        // the 128 x 128 tile kernel (w4a8_q4k_tile.hip), whose stage offsets are 32-bit
+        // the 128 x 128 tile kernel (w4a8_prefill.hip), whose stage offsets are 32-bit
         q4k_tile_launch(xq, a, a_sb, xs, qv, meta, out, ldo, n_rows, Mi, Ni, Ki, epi, st);
     } else {
         // operands of 2 GB or more: the 128 x 64 tile kernel above
@@ -997,7 +997,11 @@ extern "C" int prism_w4a8_q6k_gemm(const int8_t* xq, const float* a, int64_t a_s
         }
 #undef Q6DEC_
 #undef Q6DEC
+    } else if ((int64_t)(N / 16) * (K / 256) * 4096 < ((int64_t)1 << 31) && M * K < ((int64_t)1 << 31)) {
+        // the 128 x 128 two-plane tile kernel (w4a8_prefill.hip), whose stage offsets are 32-bit
+        q6k_tile_launch(xq, a, a_sb, qv, meta, out, ldo, n_rows, Mi, Ni, Ki, epi, st);
     } else {
+        // operands of 2 GB or more: the 32 x 32 x 16 tile kernel above
         const int tiles_m = (Mi + QBM - 1) / QBM, tiles_n = (Ni + Q6BN - 1) / Q6BN;
         if (epi == 0)
             hipLaunchKernelGGL((w4a8_q6k_tile32_kernel<0>), dim3(tiles_m * tiles_n), dim3(256), 0, st, xq, a, a_sb,

@@ -24,7 +24,7 @@
 // delays the next MFMA.
 #include "common.h"
 #include "w4a8_common.h"
-#include "w4a8_tile.h"
+#include "w4a8_prefill.h"
 
 namespace prism {
 
@@ -270,6 +270,235 @@ __global__ __launch_bounds__(512, 1) void w4a8_q4k_tile_kernel(const int8_t* __r
             }
         }
     }
+}
+
+// ---------------------------------------------------------------------------------------------- Q6_K prefill
+// Q6_K (prism_q6k_pack: values q - 32 as int8, 16 int8 scales per row and super-block, one per 16 inputs) on the same
+// 128 x 128 tile, eight waves, two LDS stages and block schedule as the Q4_K kernel above.  Per super-block
+// (kernels/w4a8.py:19-20, 193-197): acc = sum_h sc_h P_h over the sixteen 16-input sub-blocks, exact in int32;
+// y = fma(a[b, m], RN(d float(acc)), y) in super-block order.  The scales go into the MFMA weight operand as two
+// int8 planes: a lane's 16 inputs of an operand are one sub-block, w = sc v (|w| <= 4096) is split as
+// w = (w & 63) + 64 (w >> 6), both parts int8, and two MFMA chains give acc = lo + 64 hi over the whole super-block
+// (the form of the reference's own CUDA kernel, csrc/w4a8_wgmma.cu:9-10): nothing per output until the super-block
+// ends (the 32 x 32 x 16 kernel it replaces does one v_mad per output and 16-input sub-block).
+// A lane's operand for inputs 64 p + 16 q .. + 15 is two 8-byte pieces of the packed chunk p: lane slots
+// 32 (q & 1) + lm and 32 (q & 1) + 16 + lm, bytes 8 (q >> 1) .. + 7 of each.
+
+// Four signed weights (bytes of v) times the scale pair sc16 (sc in both 16-bit halves) as the two plane dwords
+// (w & 63, w >> 6) in byte order.
+__device__ __forceinline__ void q6_planes(uint32_t v, uint32_t sc16, uint32_t& lo, uint32_t& hi) {
+    typedef short s2 __attribute__((ext_vector_type(2)));
+    const s2 ev = __builtin_bit_cast(s2, v << 8) >> (s2){8, 8};       // bytes 0, 2 sign-extended
+    const s2 od = __builtin_bit_cast(s2, v) >> (s2){8, 8};            // bytes 1, 3
+    const s2 sc = __builtin_bit_cast(s2, sc16);
+    const s2 we = ev * sc, wo = od * sc;                              // |w| <= 4096: exact in 16 bits
+    const uint32_t le = __builtin_bit_cast(uint32_t, we) & 0x003f003fu, lo_ = __builtin_bit_cast(uint32_t, wo) & 0x003f003fu;
+    const uint32_t he = __builtin_bit_cast(uint32_t, (s2)(we >> (s2){6, 6}));
+    const uint32_t ho = __builtin_bit_cast(uint32_t, (s2)(wo >> (s2){6, 6}));
+    lo = __builtin_amdgcn_perm(lo_, le, 0x06020400u);                  // bytes e0 o0 e1 o1
+    hi = __builtin_amdgcn_perm(ho, he, 0x06020400u);
+}
+
+template <int EPI>
+__global__ __launch_bounds__(512, 1) void w4a8_q6k_tile_kernel(const int8_t* __restrict__ xq,
+                                                                const float* __restrict__ a, int64_t a_sb,
+                                                                const uint8_t* __restrict__ qv,
+                                                                const uint8_t* __restrict__ meta,
+                                                                void* __restrict__ out, int64_t ldo,
+                                                                const int32_t* __restrict__ n_rows, int M, int N,
+                                                                int K, int tiles_m, int tiles_n) {
+    // stage buffers as separate objects: 8 weight tiles x 4 KB as packed; the activation rows, chunk c of row r at
+    // 16-byte slot c ^ (r & 15)
+    __shared__ __attribute__((aligned(16))) uint8_t Bs0[8 * 4096];
+    __shared__ __attribute__((aligned(16))) uint8_t Bs1[8 * 4096];
+    __shared__ __attribute__((aligned(16))) int8_t As0[T8M * 256];
+    __shared__ __attribute__((aligned(16))) int8_t As1[T8M * 256];
+    __shared__ __attribute__((aligned(16))) v4u scl[2][T8N];           // per weight row: its 16 int8 scales
+    __shared__ __attribute__((aligned(16))) float dl[2][T8N];
+    __shared__ float al[2][T8M];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lm = lane & 15, q = lane >> 4;
+    int pm, pn;
+    xcd_tile_coords(blockIdx.x, tiles_m, tiles_n, pm, pn);
+    const int m0 = pm * T8M, n0 = pn * T8N;
+    const int live = min(M, __ldg(n_rows));
+    if (m0 >= live) return;
+    const int NB = K / 256, ntiles = N / 16;
+
+    // DMA: per stage 2048 weight chunks and 2048 activation chunks of 16 bytes, four of each per thread
+    uint32_t woff[4], xoff[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int c = tid + 512 * i;
+        woff[i] = (uint32_t)((min(n0 / 16 + (c >> 8), ntiles - 1) * NB * 256 + (c & 255)) * 16);
+        const int r = c >> 4;
+        xoff[i] = (uint32_t)(min(m0 + r, M - 1) * K + (((c & 15) ^ (r & 15)) * 16));
+    }
+    auto dma = [&](int b, uint8_t* Bd, int8_t* Ad) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) dma16(qv + (woff[i] + (uint32_t)b * 4096u), &Bd[(512 * i + 64 * wv) * 16]);
+#pragma unroll
+        for (int i = 0; i < 4; i++) dma16(xq + (xoff[i] + (uint32_t)b * 256u), &Ad[(512 * i + 64 * wv) * 16]);
+    };
+    // meta: thread t loads weight row t % 128's 16 scale bytes and d, and activation row t % 128's scale, every
+    // thread unconditionally (no branch, so the loaded values need no merge); waves 0-1 store the scales, 2-3 d,
+    // 4-5 the activation scales
+    const int hrow = tid & 127;
+    const uint8_t* msrc = meta + (int64_t)min(n0 / 16 + (hrow >> 4), ntiles - 1) * NB * Q6_META;
+    const int srow = min(m0 + hrow, M - 1);
+    v4u rm;
+    uint32_t rd;
+    float ra;
+    auto gmeta = [&](int b) {
+        const uint8_t* mp = msrc + (int64_t)b * Q6_META;
+        rm = reinterpret_cast<const v4u*>(mp)[hrow & 15];
+        rd = reinterpret_cast<const uint16_t*>(mp + 256)[hrow & 15];
+        ra = a[(int64_t)b * a_sb + srow];
+    };
+    auto smeta = [&](int buf) {
+        if (wv < 2) scl[buf][hrow] = rm;
+        else if (wv < 4) dl[buf][hrow] = f16_to_f32(rd);
+        else if (wv < 6) al[buf][hrow] = ra;
+    };
+
+    float y[8][4];
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) y[j][e] = 0.f;
+    const int wrow = 16 * wv + lm;
+    // this lane's two lane slots of a chunk and the byte half (see the comment above)
+    const int bs0 = (wv * 4 * 64 + 32 * (q & 1) + lm) * 16 + 8 * (q >> 1);
+
+    gmeta(0);
+    dma(0, Bs0, As0);
+    vm_wait<0>();
+    smeta(0);
+    lds_barrier();
+    // two super-blocks per trip, each stage's buffers distinct LDS objects (see the Q4_K kernel)
+    auto step = [&](const int b, const int cb, const uint8_t* __restrict__ Bc, const int8_t* __restrict__ Ac,
+                    uint8_t* __restrict__ Bn, int8_t* __restrict__ An) __attribute__((always_inline)) {
+        {
+            const int bn = min(b + 1, NB - 1);
+            gmeta(bn);
+            dma(bn, Bn, An);
+        }
+        // this lane's sub-block scales (sub-block 4 p + q: byte q of scale dword p) as 16-bit pairs
+        const v4u sv = scl[cb][wrow];
+        uint32_t sc16[4];
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const uint32_t sc = (uint32_t)__builtin_amdgcn_sbfe((int)sv[p], 8 * q, 8) & 0xffffu;
+            sc16[p] = sc | (sc << 16);
+        }
+        const v4f dd = *reinterpret_cast<const v4f*>(&dl[cb][16 * wv + 4 * q]);
+        v4i wl[4], wh[4];
+        auto planes = [&](int p) {
+            const v2u x0 = *reinterpret_cast<const v2u*>(&Bc[bs0 + p * 1024]);
+            const v2u x1 = *reinterpret_cast<const v2u*>(&Bc[bs0 + p * 1024 + 256]);
+            uint32_t l[4], h[4];
+            q6_planes(x0[0], sc16[p], l[0], h[0]);
+            q6_planes(x0[1], sc16[p], l[1], h[1]);
+            q6_planes(x1[0], sc16[p], l[2], h[2]);
+            q6_planes(x1[1], sc16[p], l[3], h[3]);
+            wl[p] = v4i{(int)l[0], (int)l[1], (int)l[2], (int)l[3]};
+            wh[p] = v4i{(int)h[0], (int)h[1], (int)h[2], (int)h[3]};
+        };
+        auto epilogue = [&](int j, v4i lo, v4i hi, float am) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) y[j][e] = fmaf(am, mul_rn(dd[e], (float)(lo[e] + 64 * hi[e])), y[j][e]);
+            asm volatile("" : "+v"(y[j][0]), "+v"(y[j][1]), "+v"(y[j][2]), "+v"(y[j][3]));
+        };
+        v4i af[8][4], los[8], his[8];
+        float amv[8];
+        auto acts = [&](int j) {
+#pragma unroll
+            for (int p = 0; p < 4; p++)
+                af[j][p] = *reinterpret_cast<const v4i*>(&Ac[(16 * j + lm) * 256 + (((4 * p + q) ^ lm) * 16)]);
+            amv[j] = al[cb][16 * j + lm];
+        };
+        // blocks 0..3 pair by pair, then blocks 4..7 one by one with the epilogue of block j - 4 between the MFMAs
+        // of block j (the Q4_K kernel's schedule)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acts(j);
+        {
+            v4i lo4[4], hi4[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) lo4[j] = hi4[j] = v4i{0, 0, 0, 0};
+#pragma unroll
+            for (int p = 0; p < 4; p++) {
+                planes(p);
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    lo4[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wl[p], af[j][p], lo4[j], 0, 0, 0);
+                    hi4[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wh[p], af[j][p], hi4[j], 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) los[j] = lo4[j], his[j] = hi4[j];
+            acts(4);
+            acts(5);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 4; j < 8; j++) {
+            v4i lo = {0, 0, 0, 0}, hi = {0, 0, 0, 0};
+#pragma unroll
+            for (int p = 0; p < 4; p++) {
+                lo = __builtin_amdgcn_mfma_i32_16x16x64_i8(wl[p], af[j][p], lo, 0, 0, 0);
+                hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(wh[p], af[j][p], hi, 0, 0, 0);
+            }
+            los[j] = lo, his[j] = hi;
+            epilogue(j - 4, los[j - 4], his[j - 4], amv[j - 4]);
+            if (j + 2 < 8) acts(j + 2);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int j = 4; j < 8; j++) epilogue(j, los[j], his[j], amv[j]);
+        vm_wait<0>();
+        smeta(cb ^ 1);
+        lds_barrier();
+    };
+    for (int b = 0; b < NB; b += 2) {
+        step(b, 0, Bs0, As0, Bs1, As1);
+        if (b + 1 < NB) step(b + 1, 1, Bs1, As1, Bs0, As0);
+    }
+    // D element (j, e): n = n0 + 16 wv + 4 q + e, m = m0 + 16 j + lm
+    const int nb = n0 + 16 * wv + 4 * q;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const int m = m0 + 16 * j + lm;
+        if (m < live && nb < N) {
+            if (EPI == 0) {
+                const uint32_t lo = f32_to_bf16(y[j][0]) | (f32_to_bf16(y[j][1]) << 16);
+                const uint32_t hi = f32_to_bf16(y[j][2]) | (f32_to_bf16(y[j][3]) << 16);
+                uint16_t* o = reinterpret_cast<uint16_t*>(out) + (int64_t)m * ldo + nb;
+                if ((((uintptr_t)o) & 7) == 0) {
+                    *reinterpret_cast<v2u*>(o) = v2u{lo, hi};
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; e++) o[e] = (uint16_t)f32_to_bf16(y[j][e]);
+                }
+            } else {
+                float* o = reinterpret_cast<float*>(out) + (int64_t)m * ldo + nb;
+#pragma unroll
+                for (int e = 0; e < 4; e++) o[e] = add_rn(o[e], y[j][e]);
+            }
+        }
+    }
+}
+
+void q6k_tile_launch(const int8_t* xq, const float* a, int64_t a_sb, const uint8_t* qv, const uint8_t* meta,
+                     void* out, int64_t ldo, const int32_t* n_rows, int M, int N, int K, int epi, hipStream_t st) {
+    const int tm = (M + T8M - 1) / T8M, tn = (N + T8N - 1) / T8N;
+    if (epi == 0)
+        hipLaunchKernelGGL((w4a8_q6k_tile_kernel<0>), dim3(tm * tn), dim3(512), 0, st, xq, a, a_sb, qv, meta, out, ldo,
+                           n_rows, M, N, K, tm, tn);
+    else
+        hipLaunchKernelGGL((w4a8_q6k_tile_kernel<1>), dim3(tm * tn), dim3(512), 0, st, xq, a, a_sb, qv, meta, out, ldo,
+                           n_rows, M, N, K, tm, tn);
 }
 
 void q4k_tile_launch(const int8_t* xq, const float* a, int64_t a_sb, const int8_t* xs, const uint8_t* qv,
