@@ -115,6 +115,11 @@ __device__ __forceinline__ void dma1(const void* g, void* lds) {
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, 0x00020000);
 }
+// The same with the record count set to `bytes` from the base: a load past it returns zeros instead of reading beyond
+// the caller's buffer (the check is per dword).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc_n(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
 constexpr int kBufNT = 2;                 // the cache-policy bit of a non-temporal (streaming) load
 template <int AUX = 0>
 __device__ __forceinline__ v4i buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {

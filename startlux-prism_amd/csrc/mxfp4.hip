@@ -520,8 +520,11 @@ __global__ __launch_bounds__(256, WT == 4 ? 2 : 1) void mx_tile_wd_kernel(const 
     // wave w stages activation tile w: row m0 + 16 w + r, 16-byte piece p of each 64-byte half (e4m3: two halves)
     const int mr = min(m0 + 16 * w + r, M - 1) - m0;
     const __amdgpu_buffer_rsrc_t ra = buf_rsrc(aq + (int64_t)m0 * abytes);
-    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(as + (int64_t)m0 * (K / 32));
-    const uint32_t ao = (uint32_t)(mr * abytes + 16 * p), so = (uint32_t)(mr * (K / 32) + p);
+    // (bounded: the last group of four steps' scales may reach past the last row when K / 128 is not a multiple of 4)
+    const __amdgpu_buffer_rsrc_t rs = buf_rsrc_n(as + (int64_t)m0 * (K / 32), (uint32_t)((M - m0) * (K / 32)));
+    // activation scales: one 16-byte load per lane every fourth step, row mr's bytes of four steps (the lane's own is
+    // byte 4 (st % 4) + p); single-byte loads every step measured 10% of the kernel's time at C4
+    const uint32_t ao = (uint32_t)(mr * abytes + 16 * p), so = (uint32_t)(mr * (K / 32));
     // weights: tile 4 w + a of the workgroup's 16 (clamped), lane slot l of its chunk, scale byte l
     const int nt0 = n0 / 16;
     const __amdgpu_buffer_rsrc_t rw = buf_rsrc(wq + (int64_t)nt0 * KS * 1024);
@@ -533,14 +536,19 @@ __global__ __launch_bounds__(256, WT == 4 ? 2 : 1) void mx_tile_wd_kernel(const 
         wo[a] = (uint32_t)(t * KS * 1024 + lane * 16);
         wso[a] = (uint32_t)(t * KS * 64 + lane);
     }
-    struct Act { v4i q[AP]; uint32_t s; };
+    struct Act { v4i q[AP]; };
+    v4u sgrp[2];                                           // scale bytes of steps 4 g .. 4 g + 3, slot g % 2
     struct Wt { v4i f[WT]; uint32_t s[WT]; };
     Act xr[2];
     Wt wr[2];
-    auto load_a = [&](int st, Act& x) {
+    // st: the stage (clamped to the last for the addresses); sj: its position in the eight-step segment, known at
+    // compile time, which picks the scale group's register slot (st is a multiple of 8 plus sj)
+    auto load_a = [&](int st, int sj, Act& x) {
+        const uint32_t sc = (uint32_t)min(st, KS - 1);
+        // (issued before the step's activations: the waits below count the loads that follow those)
+        if ((sj & 3) == 0) sgrp[(sj >> 2) & 1] = __builtin_bit_cast(v4u, buf_load16(rs, so, (sc & ~3u) * 4));
 #pragma unroll
-        for (int h = 0; h < AP; h++) x.q[h] = buf_load16(ra, ao + 64 * h, (uint32_t)st * (AF == 0 ? 128 : 64));
-        x.s = buf_load1(rs, so, (uint32_t)st * 4);
+        for (int h = 0; h < AP; h++) x.q[h] = buf_load16(ra, ao + 64 * h, sc * (AF == 0 ? 128 : 64));
     };
     auto load_w = [&](int st, Wt& f) {
 #pragma unroll
@@ -548,11 +556,12 @@ __global__ __launch_bounds__(256, WT == 4 ? 2 : 1) void mx_tile_wd_kernel(const 
 #pragma unroll
         for (int a = 0; a < WT; a++) f.s[a] = buf_load1(rws, wso[a], (uint32_t)st * 64);
     };
-    auto stage_store = [&](int st, const Act& x) {         // the LDS image mx_tile_kernel's DMA copies make
-        uint8_t* b = lds + (st & 1) * ABUF;
+    auto stage_store = [&](int sj, const Act& x) {         // the LDS image mx_tile_kernel's DMA copies make
+        uint8_t* b = lds + (sj & 1) * ABUF;
 #pragma unroll
         for (int h = 0; h < AP; h++) *reinterpret_cast<v4i*>(b + w * AT + h * 1024 + lane * 16) = x.q[h];
-        *reinterpret_cast<uint32_t*>(b + TA * AT + w * 256 + lane * 4) = x.s;
+        *reinterpret_cast<uint32_t*>(b + TA * AT + w * 256 + lane * 4) =
+            __builtin_amdgcn_ubfe(sgrp[(sj >> 2) & 1][sj & 3], 8 * p, 8);
     };
 
     v4f acc[WT][AR], tot[WT][AR];
@@ -575,19 +584,20 @@ __global__ __launch_bounds__(256, WT == 4 ? 2 : 1) void mx_tile_wd_kernel(const 
 
     // Both operands two steps ahead in two-slot register rings: step st requests stage st + 2's activations before
     // its MFMAs and its weights after them (into the slot those MFMAs free).  Stage indices past the last are
-    // clamped (redundant loads into slots never read), so every step issues the same loads and at step st's wait only
-    // stage st + 1's WL weight loads follow stage st + 1's activations.
-    load_a(0, xr[0]);
+    // clamped (redundant loads into slots never read), so at step st's wait only stage st + 1's WL weight loads follow
+    // stage st + 1's activations (a step whose activation scales start a group of four loads them first).
+    load_a(0, 0, xr[0]);
     load_w(0, wr[0]);
-    load_a(min(1, KS - 1), xr[1]);
+    load_a(1, 1, xr[1]);
     load_w(min(1, KS - 1), wr[1]);
-    vm_wait_tracked<2 * WL + AP + 1>();
+    vm_wait_tracked<2 * WL + AP>();                       // stage 0's scales and activations (stage 1 loads none)
     stage_store(0, xr[0]);
     lds_barrier();
-    auto step = [&](int st, int j) {                       // j = st mod 2: the register slot
+    auto step = [&](int st, int sj) {                      // sj = st mod 8, known at compile time
+        const int j = sj & 1;                              // the register slot
         vm_wait_tracked<WL>();
-        stage_store(st + 1, xr[j ^ 1]);                    // past the end: into the free buffer, never read
-        const uint8_t* b = lds + (st & 1) * ABUF;
+        stage_store(sj + 1, xr[j ^ 1]);                    // past the end: into the free buffer, never read
+        const uint8_t* b = lds + j * ABUF;
         v8i af[AR];
         uint32_t asf[AR];
 #pragma unroll
@@ -602,7 +612,7 @@ __global__ __launch_bounds__(256, WT == 4 ? 2 : 1) void mx_tile_wd_kernel(const 
             }
             asf[c] = *reinterpret_cast<const uint32_t*>(b + TA * AT + c * 256 + lane * 4);
         }
-        load_a(min(st + 2, KS - 1), xr[j]);
+        load_a(st + 2, sj + 2, xr[j]);
         lds_barrier();
 #pragma unroll
         for (int a = 0; a < WT; a++)
@@ -615,13 +625,13 @@ __global__ __launch_bounds__(256, WT == 4 ? 2 : 1) void mx_tile_wd_kernel(const 
     int st = 0;
     for (; st + kMxSegSteps <= KS; st += kMxSegSteps) {
 #pragma unroll
-        for (int j = 0; j < kMxSegSteps; j++) step(st + j, j & 1);
+        for (int j = 0; j < kMxSegSteps; j++) step(st + j, j);
         fold(st == 0);
     }
     if (st < KS) {
 #pragma unroll
         for (int j = 0; j < kMxSegSteps - 1; j++)
-            if (st + j < KS) step(st + j, j & 1);
+            if (st + j < KS) step(st + j, j);
         fold(st == 0);
     }
 
