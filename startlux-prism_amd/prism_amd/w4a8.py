@@ -51,6 +51,30 @@ class W4(NamedTuple):
     def nbytes(self):
         return self.qv.numel() + self.meta.numel()
 
+    # The reference W4's field names (kernels/w4a8.py:44-54), so its op call `w4a8_gemm(xq, a, xs, w.q, w.sc, w.mn,
+    # w.d, w.dm, ...)` (kernels/w4a8.py:365) passes this layout through torch_ops unchanged: q the values, sc the
+    # per-row meta bytes (scales, mins, d, dmin); mn and dm are not separate here (None), and d, which the schema
+    # requires as a tensor, is the meta tensor again (not read).
+    @property
+    def q(self):
+        return self.qv
+
+    @property
+    def sc(self):
+        return self.meta
+
+    @property
+    def d(self):
+        return self.meta
+
+    @property
+    def mn(self):
+        return None
+
+    @property
+    def dm(self):
+        return None
+
 
 def _is_kquant(kq):
     """Duck type of a k-quant matrix: this build's gguf_formats.KQuant or the reference engine's own
