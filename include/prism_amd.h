@@ -132,6 +132,23 @@ PRISM_API int prism_w8a8_pc_packed_gemm_split(const int8_t* a, const int8_t* qt,
                                               int split, void* stream);
 
 /*
+ * The per-channel GEMM on packed weights with the split decode (kernel 2), the CUDA kernel's split-K of the
+ * per-channel product (csrc/w8a8_gemm.cu:624-671, :737-766, its workspace kernels/cuda_ext.py:138-143): K in three
+ * parts, each part's int32 sums into a slot of `ws`, then a second kernel adds the slots (exact in any order) and
+ * applies the epilogue; bits equal the unsplit kernels'.  Arguments as prism_w8a8_pc_packed_gemm, plus ws (256-byte
+ * aligned, ws_bytes of it; no initial contents needed).  kernel: -1 the split where ws holds it and it measured faster
+ * (16 - 64 rows at K >= 12288, 48 - 64 rows up to N = 5120)
+ * (prism_w8a8_pc_split_workspace_bytes), else as prism_w8a8_pc_packed_gemm; 0 / 1 as there; 2 the split (an error
+ * when ws cannot hold it).  Calls that overlap on one GPU must not share ws.
+ */
+PRISM_API int prism_w8a8_pc_packed_gemm_ws(const int8_t* a, const float* a_s, int64_t as_sm, const int8_t* qt,
+                                           const void* w_s, int ws_fp16, void* out, int64_t ldo,
+                                           const int32_t* n_rows, int64_t M, int64_t N, int64_t K, int epi,
+                                           int kernel, void* ws, int64_t ws_bytes, void* stream);
+/* Bytes of ws the split decode needs at M rows (1..64) and N columns; 0 for shapes it does not take. */
+PRISM_API int64_t prism_w8a8_pc_split_workspace_bytes(int64_t M, int64_t N);
+
+/*
  * Q8_0 W8A8 GEMM (gk = 32, one activation scale per token) on packed weights: the arithmetic and bits of
  * prism_w8a8_gemm with gk = 32 (kernels/w8a8.py:64-85), the engine entry kernels/w8a8.py:183-231.
  * a int8 [M, K]; a_s fp32, row m at a_s[m * as_sm]; qt / dt from prism_q8_0_pack; out as prism_w8a8_gemm.

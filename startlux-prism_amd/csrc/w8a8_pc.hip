@@ -516,9 +516,120 @@ int launch_w8a8_pc(int kernel, bool wpack, const int8_t* a, const float* a_s, in
     return PRISM_OK;
 }
 
+// The split decode on packed weights (kernel 2): four 16-row weight tiles per workgroup (two where N is not a
+// multiple of 64) and K in three parts, each part's int32 sums into its slot of the workspace (the decode kernel's
+// epilogue 2), then pc_fold_kernel adds the three slots (exact in any order) and applies the epilogue.  Every
+// workgroup reads all activation rows over its K range, so with four tiles per workgroup the activation rows are read
+// half as often per weight byte as with the unsplit kernel's two, while 3 N / 64 workgroups still cover the CUs:
+// at 64 rows, 5120 x 17408 -> 5120, 46.8 -> 25.9 us for the sums.  Two or four parts lost most of that gain.  The
+// parts meet at the launch boundary rather than through counters and a last-arriving part: the partial sums would
+// then have to be written and read device-coherently (agent scope), past the XCDs' separate L2s, which measured
+// 38 us for the same product.
+constexpr int kPcSplit = 3;
+
+int64_t pc_split_workspace_bytes(int64_t M, int64_t N) { return (int64_t)kPcSplit * M * N * 4; }
+
+// out rows m < n_rows: y = RN(RN(float(sum_z slots[z][m][n]) sa) sw), stored as bf16 (EPI 0) or added (EPI 1).
+template <bool WS16, int EPI>
+__global__ __launch_bounds__(256) void pc_fold_kernel(const int32_t* __restrict__ slots, int64_t zstride, int S,
+                                                      const float* __restrict__ a_s, int64_t as_sm,
+                                                      const void* __restrict__ w_s, void* __restrict__ out,
+                                                      int64_t ldo, const int32_t* __restrict__ n_rows, int M, int N) {
+    const int m = blockIdx.y, n = 4 * (blockIdx.x * 256 + threadIdx.x);
+    if (n >= N || m >= min(M, __ldg(n_rows))) return;
+    v4i P = v4i{0, 0, 0, 0};
+    for (int z = 0; z < S; z++) {
+        const v4i u = *reinterpret_cast<const v4i*>(slots + z * zstride + (int64_t)m * N + n);
+        P = v4i{P.x + u.x, P.y + u.y, P.z + u.z, P.w + u.w};
+    }
+    const float sa = a_s[(int64_t)m * as_sm];
+    float y[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const float sw = WS16 ? f16_to_f32(static_cast<const uint16_t*>(w_s)[n + e]) : static_cast<const float*>(w_s)[n + e];
+        y[e] = mul_rn(mul_rn((float)P[e], sa), sw);
+    }
+    if (EPI == 0) {
+        uint16_t* o = static_cast<uint16_t*>(out) + (int64_t)m * ldo + n;
+        *reinterpret_cast<v2u*>(o) = v2u{f32_to_bf16(y[0]) | (f32_to_bf16(y[1]) << 16),
+                                         f32_to_bf16(y[2]) | (f32_to_bf16(y[3]) << 16)};
+    } else {
+        float4* o = reinterpret_cast<float4*>(static_cast<float*>(out) + (int64_t)m * ldo + n);
+        const float4 p = *o;
+        *o = make_float4(add_rn(p.x, y[0]), add_rn(p.y, y[1]), add_rn(p.z, y[2]), add_rn(p.w, y[3]));
+    }
+}
+
+int launch_w8a8_pc_split(const int8_t* a, const float* a_s, int64_t as_sm, const int8_t* w, const void* w_s,
+                         bool ws16, void* out, int64_t ldo, const int32_t* n_rows, int M, int N, int K, int epi,
+                         void* ws, hipStream_t st) {
+    const int MT = min(4, (M + 15) / 16);
+    const int G = N % 64 == 0 ? 4 : (N % 32 == 0 ? 2 : 1);
+    const int KP = K / 64 / kPcSplit;
+    const int nw = min(8, max(1, KP / 4));
+    const size_t lds = (size_t)nw * G * MT * 64 * sizeof(v4i);
+    int32_t* slots = static_cast<int32_t*>(ws);
+    const int64_t zstride = (int64_t)M * N;
+    dim3 grid((unsigned)(N / (16 * G)), (unsigned)((M + 16 * MT - 1) / (16 * MT)), (unsigned)kPcSplit);
+#define PSL(GV, MTV)                                                                                               \
+    hipLaunchKernelGGL((w8a8_pc_decode_kernel<GV, MTV, true, false, 2>), grid, dim3(64 * nw), lds, st, a, a_s, as_sm, \
+                       w, w_s, slots, (int64_t)N, n_rows, M, N, K, zstride)
+#define PSL_MT(GV)                                                                                                 \
+    do {                                                                                                           \
+        if (MT == 1) PSL(GV, 1); else if (MT == 2) PSL(GV, 2); else if (MT == 3) PSL(GV, 3); else PSL(GV, 4);      \
+    } while (0)
+    if (G == 4) PSL_MT(4); else if (G == 2) PSL_MT(2); else PSL_MT(1);
+#undef PSL_MT
+#undef PSL
+    PRISM_LAUNCH_CHECK();
+    dim3 fgrid((unsigned)((N / 4 + 255) / 256), (unsigned)M);
+#define PFL(W16, E) hipLaunchKernelGGL((pc_fold_kernel<W16, E>), fgrid, dim3(256), 0, st, slots, zstride, kPcSplit, a_s, \
+                                       as_sm, w_s, out, ldo, n_rows, M, N)
+    if (ws16) { if (epi == 0) PFL(true, 0); else PFL(true, 1); }
+    else { if (epi == 0) PFL(false, 0); else PFL(false, 1); }
+#undef PFL
+    PRISM_LAUNCH_CHECK();
+    return PRISM_OK;
+}
+
 }  // namespace prism
 
 using namespace prism;
+
+extern "C" int prism_w8a8_pc_packed_gemm(const int8_t* a, const float* a_s, int64_t as_sm, const int8_t* qt,
+                                         const void* w_s, int ws_fp16, void* out, int64_t ldo, const int32_t* n_rows,
+                                         int64_t M, int64_t N, int64_t K, int epi, int kernel, void* stream);
+
+extern "C" int64_t prism_w8a8_pc_split_workspace_bytes(int64_t M, int64_t N) {
+    if (M <= 0 || N <= 0 || M > 64 || N % 16) return 0;
+    return pc_split_workspace_bytes(M, N);
+}
+
+// prism_w8a8_pc_packed_gemm with the workspace of the split decode (kernel 2).  kernel -1 with a workspace that holds
+// the split takes it where it measured faster (below), else picks as prism_w8a8_pc_packed_gemm; 0 / 1 as there.
+extern "C" int prism_w8a8_pc_packed_gemm_ws(const int8_t* a, const float* a_s, int64_t as_sm, const int8_t* qt,
+                                            const void* w_s, int ws_fp16, void* out, int64_t ldo,
+                                            const int32_t* n_rows, int64_t M, int64_t N, int64_t K, int epi,
+                                            int kernel, void* ws, int64_t ws_bytes, void* stream) {
+    if (kernel < -1 || kernel > 2) return PRISM_ERR_ARG;
+    const bool fits = ws && M >= 1 && M <= 64 && N % 16 == 0 && K / 64 >= 4 * kPcSplit &&
+                      ws_bytes >= pc_split_workspace_bytes(M, N) && PRISM_ALIGNED(ws, 256);
+    if (kernel == 2 && !fits) return ws ? PRISM_ERR_SHAPE : PRISM_ERR_ARG;
+    // without a table entry: the split where it measured faster (long K from 16 rows: 5120 x 17408 -> 5120 at 16 /
+    // 32 / 64 rows 24.7 / 34.0 / 46.9 -> 21.9 / 24.2 / 29.8 us; up to N = 5120 at 48 - 64 rows: 5120^2 at 64 rows
+    // 17.9 -> 16.5 us); below 16 rows and on wide projections the unsplit kernels stay ahead
+    if (kernel == -1 && fits && M >= 16 && (K >= 12288 || (M >= 48 && N <= 5120))) kernel = 2;
+    if (kernel != 2)
+        return prism_w8a8_pc_packed_gemm(a, a_s, as_sm, qt, w_s, ws_fp16, out, ldo, n_rows, M, N, K, epi, kernel,
+                                         stream);
+    if (!a || !a_s || !qt || !w_s || !out || !n_rows) return PRISM_ERR_ARG;
+    if (epi != 0 && epi != 1) return PRISM_ERR_ARG;
+    if (N <= 0 || K <= 0 || K % 64 || ldo < N || K > (1 << 17)) return PRISM_ERR_SHAPE;
+    if (!PRISM_ALIGNED(a, 16) || !PRISM_ALIGNED(qt, 16) || ldo % 4 || !PRISM_ALIGNED(out, epi ? 16 : 8))
+        return PRISM_ERR_ALIGN;
+    return launch_w8a8_pc_split(a, a_s, as_sm, qt, w_s, ws_fp16 != 0, out, ldo, n_rows, (int)M, (int)N, (int)K,
+                                epi, ws, (hipStream_t)stream);
+}
 
 extern "C" int prism_w8a8_pc_packed_gemm(const int8_t* a, const float* a_s, int64_t as_sm, const int8_t* qt,
                                          const void* w_s, int ws_fp16, void* out, int64_t ldo, const int32_t* n_rows,

@@ -35,6 +35,9 @@ _SIGS = {
     "prism_i8_pack": (_int, [_p, _p, _i64, _i64, _p]),
     "prism_w8a8_pc_packed_gemm": (_int, [_p, _p, _i64, _p, _p, _int, _p, _i64, _p, _i64, _i64, _i64, _int, _int, _p]),
     "prism_w8a8_pc_packed_gemm_split": (_int, [_p, _p, _p, _i64, _i64, _p, _i64, _i64, _i64, _int, _p]),
+    "prism_w8a8_pc_packed_gemm_ws": (_int, [_p, _p, _i64, _p, _p, _int, _p, _i64, _p, _i64, _i64, _i64, _int, _int,
+                                            _p, _i64, _p]),
+    "prism_w8a8_pc_split_workspace_bytes": (_i64, [_i64, _i64]),
     "prism_norm_quant": (_int, [_p, _i64, _p, _p, _p, _p, _p, _p, _i64, _i64, ctypes.c_float, _int, _p]),
     "prism_norm_quant_fold": (_int, [_p, _i64, _p, _p, _p, _p, _p, _i64, _i64, ctypes.c_float, _int, _p, _i64, _i64,
                                      _int, _p, _i64, _p, _int, _p]),

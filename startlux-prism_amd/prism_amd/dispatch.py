@@ -8,7 +8,8 @@ Tables (JSON next to this module, written by prism_amd.tune on the GPU they desc
                           The reference serves gk = 32 with one Triton rule and no table.
   w4a8_table_<tag>.json   W4A8: "kind,N,K" (kind q4k or q6k) -> {M: [kernel]}, looked up at the smallest measured M
                           >= the request, else the largest (kernels/w4a8.py:309-316).
-<tag> is "mi355x" on gfx950.  A kernel is a name of the op's KERNELS ("tile", "decode", "mid", "stream").  STARTLUX_PRISM_GEMM_TABLE,
+<tag> is "mi355x" on gfx950.  A kernel is a name of the op's KERNELS ("tile", "decode", "mid", "stream", and "split" for the per-channel
+split decode).  STARTLUX_PRISM_GEMM_TABLE,
 STARTLUX_PRISM_Q8_TABLE and STARTLUX_PRISM_W4A8_TABLE name other files, or "off"; without a table (or for a shape it does not
 hold) the library's own rule picks (kernel "auto").  Every kernel computes the same bits, so a table changes speed
 only.

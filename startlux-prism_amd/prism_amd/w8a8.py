@@ -164,6 +164,8 @@ def gemm(a, a_s, w, w_s, out, n_rows, gk, epi=0, outs=None, cfg=None, slots=None
         raise ValueError("n_rows must be int32")
     if gk == K:
         kernel = _tabled(kernel, N, K, M, gk)     # per channel on int8 planes: the same table as PackedPC
+        if kernel == "split":
+            kernel = "decode"                     # the split decode reads the packed chunks only
     L.call("prism_w8a8_gemm", L.ptr(a), L.ptr(a_s), as_sm, as_sg, L.ptr(w), L.ptr(w_s),
            int(w_s.dtype == torch.float16), L.ptr(out), out.stride(0), L.ptr(n_rows), M, N, K, gk, epi,
            KERNELS[kernel], L.stream_of(a))
@@ -178,7 +180,7 @@ def _tabled(kernel, N, K, M, gk, packed_q8=False):
         return kernel
     c = dispatch.w8a8_kernel(N, K, M, gk)
     ok = c == "tile" or (c == "decode" and (M <= 64 or gk == K)) or (c == "mid" and gk == 32) or \
-        (c == "stream" and packed_q8 and 1 <= M <= 16)
+        (c == "stream" and packed_q8 and 1 <= M <= 16) or (c == "split" and gk == K and not packed_q8 and M <= 64)
     return c if ok else "auto"
 
 
@@ -227,8 +229,30 @@ def _gemm_packed(a, a_s, w, out, n_rows, gk, epi, kernel):
     return None
 
 
+_PCWS = {}
+PC_WS_BYTES = 96 << 20        # as the reference's workspace (kernels/cuda_ext.py:20): the split decode's slots
+
+
+def pc_workspace(dev):
+    """The per-device workspace of the per-channel split decode (kernel "split"): the K parts' int32 slots, rewritten
+    by every launch.  None while a graph is being captured on a device that has none yet: "auto" then picks another
+    kernel and "split" raises."""
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    ws = _PCWS.get(idx)
+    if ws is None:
+        if torch.cuda.is_current_stream_capturing():
+            return None
+        ws = torch.empty(PC_WS_BYTES, dtype=torch.uint8, device=torch.device("cuda", idx))
+        _PCWS[idx] = ws
+    return ws
+
+
+_PC_KERNELS = {"auto": -1, "tile": 0, "decode": 1, "split": 2}
+
+
 def _gemm_pc_packed(a, a_s, w, out, n_rows, gk, epi, kernel):
     M, K = a.shape
+    asked = kernel
     kernel = _tabled(kernel, w.n, K, M, gk)
     if gk != K or w.k != K:
         raise ValueError("packed per-channel weights: gk must equal K and K must match")
@@ -239,11 +263,17 @@ def _gemm_pc_packed(a, a_s, w, out, n_rows, gk, epi, kernel):
     want = torch.bfloat16 if epi == 0 else torch.float32
     if out.dtype != want or out.shape[0] < M or out.shape[1] < w.n or out.stride(1) != 1:
         raise ValueError(f"out must be {want} [>= {M}, >= {w.n}] with unit column stride")
-    if kernel not in ("auto", "tile", "decode"):
-        raise ValueError(f"packed per-channel kernels: auto, tile or decode, not {kernel}")
-    L.call("prism_w8a8_pc_packed_gemm", L.ptr(a), L.ptr(a_s), a_s.stride(0), L.ptr(w.qt), L.ptr(w.ws),
+    if kernel not in _PC_KERNELS:
+        raise ValueError(f"packed per-channel kernels: auto, tile, decode or split, not {kernel}")
+    ws = pc_workspace(a.device) if kernel in ("auto", "split") and M <= 64 else None
+    if kernel == "split" and ws is None and asked == "auto":
+        kernel = "auto"             # the table's pick needs the workspace; the library then picks without it
+    if kernel == "split" and ws is None:
+        raise L.PrismError('kernel "split" needs the device workspace, made outside graph capture: run one eager '
+                           'call first')
+    L.call("prism_w8a8_pc_packed_gemm_ws", L.ptr(a), L.ptr(a_s), a_s.stride(0), L.ptr(w.qt), L.ptr(w.ws),
            int(w.ws.dtype == torch.float16), L.ptr(out), out.stride(0), L.ptr(n_rows), M, w.n, K, epi,
-           KERNELS[kernel], L.stream_of(a))
+           _PC_KERNELS[kernel], L.ptr(ws), 0 if ws is None else ws.numel(), L.stream_of(a))
     return None
 
 
