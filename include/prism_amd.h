@@ -137,7 +137,7 @@ PRISM_API int prism_w8a8_pc_packed_gemm_split(const int8_t* a, const int8_t* qt,
  * parts, each part's int32 sums into a slot of `ws`, then a second kernel adds the slots (exact in any order) and
  * applies the epilogue; bits equal the unsplit kernels'.  Arguments as prism_w8a8_pc_packed_gemm, plus ws (256-byte
  * aligned, ws_bytes of it; no initial contents needed).  kernel: -1 the split where ws holds it and it measured faster
- * (16 - 64 rows at K >= 12288, 48 - 64 rows up to N = 5120)
+ * (16 - 64 rows at K >= 12288, 48 - 64 rows up to N = 5120, 65 - 256 rows at K >= 12288 up to N = 8192)
  * (prism_w8a8_pc_split_workspace_bytes), else as prism_w8a8_pc_packed_gemm; 0 / 1 as there; 2 the split (an error
  * when ws cannot hold it).  Calls that overlap on one GPU must not share ws.
  */
@@ -145,7 +145,7 @@ PRISM_API int prism_w8a8_pc_packed_gemm_ws(const int8_t* a, const float* a_s, in
                                            const void* w_s, int ws_fp16, void* out, int64_t ldo,
                                            const int32_t* n_rows, int64_t M, int64_t N, int64_t K, int epi,
                                            int kernel, void* ws, int64_t ws_bytes, void* stream);
-/* Bytes of ws the split decode needs at M rows (1..64) and N columns; 0 for shapes it does not take. */
+/* Bytes of ws the split decode needs at M rows (1..512) and N columns; 0 for shapes it does not take. */
 PRISM_API int64_t prism_w8a8_pc_split_workspace_bytes(int64_t M, int64_t N);
 
 /*

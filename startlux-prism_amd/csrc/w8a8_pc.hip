@@ -526,6 +526,7 @@ int launch_w8a8_pc(int kernel, bool wpack, const int8_t* a, const float* a_s, in
 // then have to be written and read device-coherently (agent scope), past the XCDs' separate L2s, which measured
 // 38 us for the same product.
 constexpr int kPcSplit = 3;
+constexpr int kPcSplitRows = 512;     // rows the split takes (grid rows of 64 beyond 64)
 
 int64_t pc_split_workspace_bytes(int64_t M, int64_t N) { return (int64_t)kPcSplit * M * N * 4; }
 
@@ -601,7 +602,7 @@ extern "C" int prism_w8a8_pc_packed_gemm(const int8_t* a, const float* a_s, int6
                                          int64_t M, int64_t N, int64_t K, int epi, int kernel, void* stream);
 
 extern "C" int64_t prism_w8a8_pc_split_workspace_bytes(int64_t M, int64_t N) {
-    if (M <= 0 || N <= 0 || M > 64 || N % 16) return 0;
+    if (M <= 0 || N <= 0 || M > kPcSplitRows || N % 16) return 0;
     return pc_split_workspace_bytes(M, N);
 }
 
@@ -612,13 +613,15 @@ extern "C" int prism_w8a8_pc_packed_gemm_ws(const int8_t* a, const float* a_s, i
                                             const int32_t* n_rows, int64_t M, int64_t N, int64_t K, int epi,
                                             int kernel, void* ws, int64_t ws_bytes, void* stream) {
     if (kernel < -1 || kernel > 2) return PRISM_ERR_ARG;
-    const bool fits = ws && M >= 1 && M <= 64 && N % 16 == 0 && K / 64 >= 4 * kPcSplit &&
+    const bool fits = ws && M >= 1 && M <= kPcSplitRows && N % 16 == 0 && K / 64 >= 4 * kPcSplit &&
                       ws_bytes >= pc_split_workspace_bytes(M, N) && PRISM_ALIGNED(ws, 256);
     if (kernel == 2 && !fits) return ws ? PRISM_ERR_SHAPE : PRISM_ERR_ARG;
     // without a table entry: the split where it measured faster (long K from 16 rows: 5120 x 17408 -> 5120 at 16 /
     // 32 / 64 rows 24.7 / 34.0 / 46.9 -> 21.9 / 24.2 / 29.8 us; up to N = 5120 at 48 - 64 rows: 5120^2 at 64 rows
     // 17.9 -> 16.5 us); below 16 rows and on wide projections the unsplit kernels stay ahead
-    if (kernel == -1 && fits && M >= 16 && (K >= 12288 || (M >= 48 && N <= 5120))) kernel = 2;
+    if (kernel == -1 && fits && M >= 16 &&
+        ((M <= 64 && (K >= 12288 || (M >= 48 && N <= 5120))) || (M <= 256 && K >= 12288 && N <= 8192)))
+        kernel = 2;
     if (kernel != 2)
         return prism_w8a8_pc_packed_gemm(a, a_s, as_sm, qt, w_s, ws_fp16, out, ldo, n_rows, M, N, K, epi, kernel,
                                          stream);

@@ -105,7 +105,7 @@ def tune_w8(kind, shapes, Ms, dev, log):
                 # "decode" hands 17..64 rows to the "mid" kernel, so it is a candidate up to 16 rows only
                 cands = ["decode", "stream", "mid", "tile"] if M <= 16 else ["mid", "tile"]
             else:
-                cands = ["decode", "split", "tile"] if M <= 64 else ["decode", "tile"]
+                cands = ["decode", "split", "tile"] if M <= 512 else ["decode", "tile"]
             best, us = _pick(cands, lambda c: (lambda i: KW.gemm(a, s, ws[i], None, out, n, gk, kernel=c)),
                              len(ws), M)
             row[str(M)] = [best]

@@ -180,7 +180,7 @@ def _tabled(kernel, N, K, M, gk, packed_q8=False):
         return kernel
     c = dispatch.w8a8_kernel(N, K, M, gk)
     ok = c == "tile" or (c == "decode" and (M <= 64 or gk == K)) or (c == "mid" and gk == 32) or \
-        (c == "stream" and packed_q8 and 1 <= M <= 16) or (c == "split" and gk == K and not packed_q8 and M <= 64)
+        (c == "stream" and packed_q8 and 1 <= M <= 16) or (c == "split" and gk == K and not packed_q8 and M <= 512)
     return c if ok else "auto"
 
 
@@ -265,7 +265,7 @@ def _gemm_pc_packed(a, a_s, w, out, n_rows, gk, epi, kernel):
         raise ValueError(f"out must be {want} [>= {M}, >= {w.n}] with unit column stride")
     if kernel not in _PC_KERNELS:
         raise ValueError(f"packed per-channel kernels: auto, tile, decode or split, not {kernel}")
-    ws = pc_workspace(a.device) if kernel in ("auto", "split") and M <= 64 else None
+    ws = pc_workspace(a.device) if kernel in ("auto", "split") and M <= 512 else None
     if kernel == "split" and ws is None and asked == "auto":
         kernel = "auto"             # the table's pick needs the workspace; the library then picks without it
     if kernel == "split" and ws is None:

@@ -49,7 +49,7 @@ def test_off(tables, monkeypatch):
     assert dispatch.w4a8_kernel("q4k", 13824, 5120, 1) == "auto"
 
 
-LIMITS = {"gemm_table": {"decode": 1 << 20, "split": 64, "tile": 1 << 30}, "q8_table": {"decode": 64, "stream": 16, "mid": 1 << 20,
+LIMITS = {"gemm_table": {"decode": 1 << 20, "split": 512, "tile": 1 << 30}, "q8_table": {"decode": 64, "stream": 16, "mid": 1 << 20,
                                                                                    "tile": 1 << 30},
           "w4a8_table": {"decode": 16, "stream": 16, "tile": 1 << 30}}
 

@@ -33,7 +33,8 @@ def _bits(t):
 
 @pytest.mark.parametrize("M,N,K,live", [(16, 5120, 5120, 16), (64, 5120, 17408, 64), (64, 5120, 17408, 41),
                                         (33, 2080, 4096, 33), (50, 1040, 1536, 29), (20, 256, 768, 20),
-                                        (1, 512, 3072, 1), (4, 3072, 5120, 3)])
+                                        (1, 512, 3072, 1), (4, 3072, 5120, 3), (200, 1024, 17408, 200),
+                                        (512, 512, 4096, 300)])
 def test_split_bit_exact(dev, M, N, K, live):
     from prism_amd import w8a8 as KW
     a, sa, wq, ws, pw = _case(M, N, K, 700 + M + N % 997, dev)
@@ -85,11 +86,11 @@ def test_split_graph_replay(dev):
         assert np.array_equal(_bits(out), O.w8a8_gemm(a2, sa2, wq, ws, K, epi=0, nthreads=16)), r
 
 
-def test_split_needs_workspace_shape(dev):
-    """Beyond 64 rows the split is refused; "auto" there takes the unsplit kernels."""
+def test_split_refuses_large_m(dev):
+    """Beyond 512 rows the split is refused; "auto" there takes the unsplit kernels."""
     from prism_amd import _lib as L
     from prism_amd import w8a8 as KW
-    M, N, K = 80, 512, 1024
+    M, N, K = 528, 512, 1024
     a, sa, wq, ws, pw = _case(M, N, K, 780, dev)
     out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
     n = torch.tensor([M], dtype=torch.int32, device=dev)
