@@ -4,6 +4,13 @@ import numpy as np
 
 import oracle as O
 
+# MXFP4 GEMM tolerance for the fp32 result, relative to sum |terms| (the float64 value's absolute terms).  The scaled
+# MFMA adds its 128 products and the accumulator with a limited alignment window, not as a chain of rounded fp32
+# adds: on operands whose block scales span 2^20 (products over about 2^48) one v_mfma_scale_f32_16x16x128_f8f6f4
+# was measured up to 205 u sum|terms| off (u = 2^-24), a 2048-input chain 284 u; Gaussian operands of one scale 13 u.
+# The bound is 1024 u, four times the worst measured.
+MX_ACC_REL = 2.0 ** -14
+
 
 def rng(seed):
     return np.random.default_rng(seed)

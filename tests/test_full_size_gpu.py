@@ -8,7 +8,7 @@ import pytest
 import torch
 
 import oracle as O
-from _inputs import acts_bf16, rng, weights_f32
+from _inputs import MX_ACC_REL, acts_bf16, rng, weights_f32
 
 pytestmark = pytest.mark.gpu
 
@@ -199,7 +199,7 @@ def test_config4_mxfp4_prefill_full_size(dev):
     wq, ws = (t.cpu().numpy() for t in MX.to_rows(mw))
     y64, yabs = O.mx_gemm(aq.cpu().numpy(), asc.cpu().numpy(), wq, ws, nthreads=16)      # every row
     got = out.float().cpu().numpy().astype(np.float64)
-    assert (np.abs(got - y64) <= 2.0 ** -8 * np.abs(y64) + 2.0 ** -16 * yabs + 1e-30).all()
+    assert (np.abs(got - y64) <= 2.0 ** -8 * np.abs(y64) + MX_ACC_REL * yabs + 1e-30).all()
     sub = rows[:16]
     o16 = torch.empty(16, N, dtype=torch.bfloat16, device=dev)
     MX.gemm(aq[_t(sub, dev)].contiguous(), asc[_t(sub, dev)].contiguous(), mw, o16, 16, kernel="decode")

@@ -8,7 +8,7 @@ import pytest
 import torch
 
 import oracle as O
-from _inputs import acts_bf16, q8_weights, rng, weights_f32
+from _inputs import MX_ACC_REL, acts_bf16, q8_weights, rng, weights_f32
 
 pytestmark = pytest.mark.gpu
 
@@ -156,7 +156,7 @@ def test_mxfp4(dev):
     wq, ws = (t.cpu().numpy() for t in MX.to_rows(mw))
     y64, yabs = O.mx_gemm(aq.cpu().numpy(), asc.cpu().numpy(), wq, ws)
     got = O.bf16_to_f32(want).astype(np.float64)
-    assert (np.abs(got - y64) <= 2.0 ** -8 * np.abs(y64) + 2.0 ** -16 * yabs + 1e-30).all()
+    assert (np.abs(got - y64) <= 2.0 ** -8 * np.abs(y64) + MX_ACC_REL * yabs + 1e-30).all()
     n = torch.tensor([M], dtype=torch.int32, device=dev)
     for kernel in ("auto", "decode", "tile"):
         rows = 16 if kernel == "decode" else M

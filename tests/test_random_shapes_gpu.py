@@ -7,7 +7,7 @@ import pytest
 import torch
 
 import oracle as O
-from _inputs import acts_bf16, q6k_random_blocks, rng, weights_f32
+from _inputs import MX_ACC_REL, acts_bf16, q6k_random_blocks, rng, weights_f32
 
 pytestmark = pytest.mark.gpu
 
@@ -136,5 +136,5 @@ def test_mxfp4_random(dev, case):
     wq, ws = (t.cpu().numpy() for t in MX.to_rows(mw))
     y64, yabs = O.mx_gemm(aq.cpu().numpy()[:live], asc.cpu().numpy()[:live], wq, ws)
     got = out.float().cpu().numpy()[:live].astype(np.float64)
-    assert (np.abs(got - y64) <= 2.0 ** -8 * np.abs(y64) + 2.0 ** -16 * yabs + 1e-30).all()
+    assert (np.abs(got - y64) <= 2.0 ** -8 * np.abs(y64) + MX_ACC_REL * yabs + 1e-30).all()
     assert (out.view(torch.int16).cpu().numpy()[live:] == 7).all()
