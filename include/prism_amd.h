@@ -305,8 +305,12 @@ PRISM_API int prism_gated_norm_quant(const float* o, int64_t ldo, const void* z,
                                      void* stream);
 
 /* ------------------------------------------------------------------------------------------------ MXFP4 */
-/* Element formats of MX operands (the MFMA format codes): e4m3 (OCP float8_e4m3fn) and e2m1 (fp4). */
-enum { PRISM_MX_E4M3 = 0, PRISM_MX_E2M1 = 4 };
+/* Element formats of MX operands (the MFMA format codes): e4m3 (OCP float8_e4m3fn) and e2m1 (fp4).
+ * PRISM_MX_E4M3_PANELS: e4m3 activations in the panel layout (no counterpart in the reference, whose activations
+ * are e2m1 row-major; the e4m3 activations are the C4 workload's): 16-row blocks of K / 128 chunks of 2 KB, byte
+ * 1024 h + 16 (16 p + r) + i of chunk st of block b holding row 16 b + r, input 128 st + 64 h + 16 p + i.  The
+ * buffer holds ceil(M / 16) blocks (16 K bytes each); the prefill tile kernel reads each 16-row step in one piece. */
+enum { PRISM_MX_E4M3 = 0, PRISM_MX_E4M3_PANELS = 1, PRISM_MX_E2M1 = 4 };
 
 /*
  * Quantize fp32 weights w [N, K] (row stride ldw) to MXFP4 in the device layout the GEMM reads: 32-input blocks,
@@ -331,7 +335,8 @@ PRISM_API int prism_mxfp4_repack(const uint8_t* q_rows, const uint8_t* s_rows, u
  * inv [K] first.  fmt PRISM_MX_E2M1: replaces kernels/mxfp4.py:181-185 (quantize_act) and :173-178
  * (quantize_act_scaled): e = clip(ceil(log2(max(amax, 1e-30) / 6)), +-127), q uint8 [M, K/2].  fmt PRISM_MX_E4M3:
  * tests/quant_sim.py:75-81 (mxfp8, the C4 activations): e = floor(log2(max(amax, 1e-30))) - 8,
- * q = e4m3(clamp(x / 2^e, +-448)) nearest even, q uint8 [M, K].  s uint8 [M, K/32] = e + 127.
+ * q = e4m3(clamp(x / 2^e, +-448)) nearest even, q uint8 [M, K]; fmt PRISM_MX_E4M3_PANELS: the same codes in the
+ * panel layout (K % 128 == 0, q of ceil(M / 16) 16 K bytes).  s uint8 [M, K/32] = e + 127 (row-major always).
  * Rows >= *n_rows (when n_rows is not null) are not written.
  */
 PRISM_API int prism_mxfp4_quant_act(const void* x, int x_f32, int64_t ldx, const float* inv, uint8_t* q, uint8_t* s,
@@ -345,6 +350,8 @@ PRISM_API int prism_mxfp4_quant_act(const void* x, int x_f32, int64_t ldx, const
  * null (all M rows live).  Every kernel sums in the same order (128-input MFMA steps chained within 1024-input
  * segments, segment sums added left to right), so results do not depend on M or on the kernel.
  * kernel: -1 picks by M; 0 the tile kernel; 1 the decode kernel (M <= 64).  Needs N % 16 == 0, K % 128 == 0.
+ * a_fmt PRISM_MX_E4M3_PANELS (activations from prism_mxfp4_quant_act in that format): the tile kernel only (kernel
+ * -1 or 0; N K / 2 < 2^31), bits equal to the row-major e4m3 call's.
  */
 PRISM_API int prism_mxfp4_gemm(const uint8_t* aq, const uint8_t* as, int a_fmt, const uint8_t* wq, const uint8_t* ws,
                                void* out, int64_t ldo, const int32_t* n_rows, int64_t M, int64_t N, int64_t K,

@@ -140,11 +140,21 @@ __global__ __launch_bounds__(64) void mx_repack_kernel(const uint8_t* __restrict
 }
 
 // ------------------------------------------------------------------------------------------ activation quantizer
+// Panel layout of e4m3 activations (PRISM_MX_E4M3_PANELS): 16-row blocks, each a run of K / 128 chunks of 2 KB, one
+// per 128-input step, holding the step's 16 rows as the tile kernel's lanes load them: byte h 1024 + (16 p + r) 16 + i
+// is row 16 b + r, input 128 st + 64 h + 16 p + i.  A wave's activation load for a step is then 2 KB in one piece
+// instead of 16 rows' 128 bytes K apart.  Block b starts at byte 16 b K, as row 16 b does in the row-major layout.
+__host__ __device__ __forceinline__ int64_t mx_act_panel_offset(int64_t row, int64_t k, int64_t K) {
+    const int64_t st = k >> 7, h = (k >> 6) & 1, p = (k >> 4) & 3;
+    return (row >> 4) * 16 * K + st * 2048 + h * 1024 + (16 * p + (row & 15)) * 16 + (k & 15);
+}
+
 // One thread per (row, 32-input block).  AF 4: kernels/mxfp4.py:124-146 (_quant_kernel; with inv, :149-170
 // _quant_scaled_kernel): e = clip(ceil(log2(max(amax, 1e-30) / 6)), +-127), strict-threshold codes, the sign bit
 // set for every negative input.  AF 0: tests/quant_sim.py:75-81 (mxfp8): e = floor(log2(max(amax, 1e-30))) - 8,
 // codes e4m3(clamp(x / 2^e, +-448)) nearest even.  XF32: fp32 input, else bf16.  Rows >= n_rows are skipped.
-template <int AF, bool XF32>
+// PAN (e4m3 only): q in the panel layout mx_act_panel_offset defines instead of row-major.
+template <int AF, bool XF32, bool PAN = false>
 __global__ __launch_bounds__(256) void mx_quant_act_kernel(const void* __restrict__ x, int64_t ldx,
                                                            const float* __restrict__ inv, uint8_t* __restrict__ q,
                                                            uint8_t* __restrict__ s,
@@ -197,9 +207,15 @@ __global__ __launch_bounds__(256) void mx_quant_act_kernel(const void* __restric
             const float a = fminf(fmaxf(v[i] * r, -448.f), 448.f);
             words[i >> 2] |= e4m3_code(a) << (8 * (i & 3));
         }
-        v4u* dst = reinterpret_cast<v4u*>(q + (int64_t)row * K + 32 * blk);
-        dst[0] = v4u{words[0], words[1], words[2], words[3]};
-        dst[1] = v4u{words[4], words[5], words[6], words[7]};
+        if (PAN) {                                         // the block's two 16-byte pieces p = 2 (blk % 2) + 0, 1
+            uint8_t* d = q + mx_act_panel_offset(row, 32 * blk, K);
+            *reinterpret_cast<v4u*>(d) = v4u{words[0], words[1], words[2], words[3]};
+            *reinterpret_cast<v4u*>(d + 256) = v4u{words[4], words[5], words[6], words[7]};
+        } else {
+            v4u* dst = reinterpret_cast<v4u*>(q + (int64_t)row * K + 32 * blk);
+            dst[0] = v4u{words[0], words[1], words[2], words[3]};
+            dst[1] = v4u{words[4], words[5], words[6], words[7]};
+        }
     } else {
         e = min(127, max(-127, ilog2_ceil(div_rn(fmaxf(amax, 1e-30f), 6.0f))));
         const float r = pow2i(-e);
@@ -493,8 +509,9 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN <= 4 ? 2 : 1) void mx_tile_ke
 // writes and fragment reads (about half the tile kernel's LDS traffic) off the LDS.  The activations are staged
 // through registers with buffer loads and ds_write rather than LDS-DMA, so every request is a plain load and one
 // counted wait covers both operands (an LDS-DMA and later buffer loads complete out of order).  Same MFMAs in the
-// same order per output as mx_tile_kernel, the same segment folds: identical results.
-template <int AF, int EPI, int WT>
+// same order per output as mx_tile_kernel, the same segment folds: identical results.  PAN (e4m3): the activations
+// in the panel layout, so each wave's load of a step is one 2 KB piece (C4: 131-138 -> 119-121 us).
+template <int AF, int EPI, int WT, bool PAN = false>
 __global__ __launch_bounds__(256, WT == 4 ? 2 : 1) void mx_tile_wd_kernel(const uint8_t* __restrict__ aq,
                                                             const uint8_t* __restrict__ as,
                                                             const uint8_t* __restrict__ wq,
@@ -524,7 +541,10 @@ __global__ __launch_bounds__(256, WT == 4 ? 2 : 1) void mx_tile_wd_kernel(const 
     const __amdgpu_buffer_rsrc_t rs = buf_rsrc_n(as + (int64_t)m0 * (K / 32), (uint32_t)((M - m0) * (K / 32)));
     // activation scales: one 16-byte load per lane every fourth step, row mr's bytes of four steps (the lane's own is
     // byte 4 (st % 4) + p); single-byte loads every step measured 10% of the kernel's time at C4
-    const uint32_t ao = (uint32_t)(mr * abytes + 16 * p), so = (uint32_t)(mr * (K / 32));
+    // panels: block m0 / 16 + w (clamped to the last), the lane's 16 bytes of each 1 KB half
+    const uint32_t ao = PAN ? (uint32_t)((min(m0 / 16 + w, (M - 1) / 16) - m0 / 16) * 16 * K + 16 * lane)
+                            : (uint32_t)(mr * abytes + 16 * p);
+    const uint32_t so = (uint32_t)(mr * (K / 32));
     // weights: tile 4 w + a of the workgroup's 16 (clamped), lane slot l of its chunk, scale byte l
     const int nt0 = n0 / 16;
     const __amdgpu_buffer_rsrc_t rw = buf_rsrc(wq + (int64_t)nt0 * KS * 1024);
@@ -548,7 +568,8 @@ __global__ __launch_bounds__(256, WT == 4 ? 2 : 1) void mx_tile_wd_kernel(const 
         // (issued before the step's activations: the waits below count the loads that follow those)
         if ((sj & 3) == 0) sgrp[(sj >> 2) & 1] = __builtin_bit_cast(v4u, buf_load16(rs, so, (sc & ~3u) * 4));
 #pragma unroll
-        for (int h = 0; h < AP; h++) x.q[h] = buf_load16(ra, ao + 64 * h, sc * (AF == 0 ? 128 : 64));
+        for (int h = 0; h < AP; h++)
+            x.q[h] = PAN ? buf_load16(ra, ao + 1024 * h, sc * 2048) : buf_load16(ra, ao + 64 * h, sc * (AF == 0 ? 128 : 64));
     };
     auto load_w = [&](int st, Wt& f) {
 #pragma unroll
@@ -790,8 +811,9 @@ extern "C" int prism_mxfp4_repack(const uint8_t* q_rows, const uint8_t* s_rows, 
 extern "C" int prism_mxfp4_quant_act(const void* x, int x_f32, int64_t ldx, const float* inv, uint8_t* q, uint8_t* s,
                                      const int32_t* n_rows, int64_t M, int64_t K, int fmt, void* stream) {
     if (!x || !q || !s) return PRISM_ERR_ARG;
-    if (fmt != PRISM_MX_E4M3 && fmt != PRISM_MX_E2M1) return PRISM_ERR_ARG;
+    if (fmt != PRISM_MX_E4M3 && fmt != PRISM_MX_E2M1 && fmt != PRISM_MX_E4M3_PANELS) return PRISM_ERR_ARG;
     if (M < 0 || K <= 0 || K % 32 || ldx < K || M > 65535) return PRISM_ERR_SHAPE;
+    if (fmt == PRISM_MX_E4M3_PANELS && K % kMxStep) return PRISM_ERR_SHAPE;
     if ((x_f32 ? ldx % 4 : ldx % 8) || !PRISM_ALIGNED(x, 16) || !PRISM_ALIGNED(q, 16) ||
         (inv && !PRISM_ALIGNED(inv, 16)))
         return PRISM_ERR_ALIGN;
@@ -800,7 +822,12 @@ extern "C" int prism_mxfp4_quant_act(const void* x, int x_f32, int64_t ldx, cons
     hipStream_t st = (hipStream_t)stream;
 #define QA(AF, F) hipLaunchKernelGGL((mx_quant_act_kernel<AF, F>), grid, dim3(256), 0, st, x, ldx, inv, q, s, n_rows, \
                                      (int)M, (int)K)
-    if (fmt == PRISM_MX_E4M3) { if (x_f32) QA(0, true); else QA(0, false); }
+    if (fmt == PRISM_MX_E4M3_PANELS) {
+        if (x_f32) hipLaunchKernelGGL((mx_quant_act_kernel<0, true, true>), grid, dim3(256), 0, st, x, ldx, inv, q, s,
+                                      n_rows, (int)M, (int)K);
+        else hipLaunchKernelGGL((mx_quant_act_kernel<0, false, true>), grid, dim3(256), 0, st, x, ldx, inv, q, s,
+                                n_rows, (int)M, (int)K);
+    } else if (fmt == PRISM_MX_E4M3) { if (x_f32) QA(0, true); else QA(0, false); }
     else { if (x_f32) QA(4, true); else QA(4, false); }
 #undef QA
     PRISM_LAUNCH_CHECK();
@@ -811,7 +838,7 @@ extern "C" int prism_mxfp4_gemm(const uint8_t* aq, const uint8_t* as, int a_fmt,
                                 const uint8_t* ws, void* out, int64_t ldo, const int32_t* n_rows, int64_t M,
                                 int64_t N, int64_t K, int epi, int kernel, void* stream) {
     if (!aq || !as || !wq || !ws || !out) return PRISM_ERR_ARG;
-    if (a_fmt != PRISM_MX_E4M3 && a_fmt != PRISM_MX_E2M1) return PRISM_ERR_ARG;
+    if (a_fmt != PRISM_MX_E4M3 && a_fmt != PRISM_MX_E2M1 && a_fmt != PRISM_MX_E4M3_PANELS) return PRISM_ERR_ARG;
     if (epi != 0 && epi != 1) return PRISM_ERR_ARG;
     if (M < 0 || N <= 0 || K <= 0 || N % 16 || K % kMxStep || ldo < N || M > (1 << 24) || N / 16 > (1 << 24))
         return PRISM_ERR_SHAPE;
@@ -820,6 +847,10 @@ extern "C" int prism_mxfp4_gemm(const uint8_t* aq, const uint8_t* as, int a_fmt,
     if (M == 0) return PRISM_OK;
     hipStream_t st = (hipStream_t)stream;
     const int MT = (int)((M + 15) / 16);
+    if (a_fmt == PRISM_MX_E4M3_PANELS) {                 // the direct-weight tile kernel only
+        if (kernel == 1 || (int64_t)N * K / 2 >= (1LL << 31)) return PRISM_ERR_SHAPE;
+        kernel = 0;
+    }
     if (kernel < 0) kernel = (MT <= 4 && mx_decode_lds(MT, (int)K) <= 64 * 1024) ? 1 : 0;
     if (kernel == 1 && MT == 1 && a_fmt == PRISM_MX_E4M3) {
         const int nseg = (int)((K / kMxStep + kMxSegSteps - 1) / kMxSegSteps);
@@ -876,11 +907,12 @@ extern "C" int prism_mxfp4_gemm(const uint8_t* aq, const uint8_t* as, int a_fmt,
         if (MX_WD && N * K / 2 < (1LL << 31)) {            // the direct-weight form of the 64 x 256 tile
             constexpr int WT = MX_WD == 2 ? 8 : 4;           // weight tiles per wave
             const int tm = (int)((M + 63) / 64), tn = (int)((N + 64 * WT - 1) / (64 * WT));
-#define TWD(AF, E)                                                                                                   \
-    hipLaunchKernelGGL((mx_tile_wd_kernel<AF, E, WT>), dim3((unsigned)(tm * tn)), dim3(256), 0, st, aq, as, wq, ws,  \
-                       out, ldo, n_rows, (int)M, (int)N, (int)K, tm, tn)
-            if (a_fmt == PRISM_MX_E4M3) { if (epi) TWD(0, 1); else TWD(0, 0); }
-            else { if (epi) TWD(4, 1); else TWD(4, 0); }
+#define TWD(AF, E, PN)                                                                                               \
+    hipLaunchKernelGGL((mx_tile_wd_kernel<AF, E, WT, PN>), dim3((unsigned)(tm * tn)), dim3(256), 0, st, aq, as, wq,  \
+                       ws, out, ldo, n_rows, (int)M, (int)N, (int)K, tm, tn)
+            if (a_fmt == PRISM_MX_E4M3_PANELS) { if (epi) TWD(0, 1, true); else TWD(0, 0, true); }
+            else if (a_fmt == PRISM_MX_E4M3) { if (epi) TWD(0, 1, false); else TWD(0, 0, false); }
+            else { if (epi) TWD(4, 1, false); else TWD(4, 0, false); }
 #undef TWD
             PRISM_LAUNCH_CHECK();
             return PRISM_OK;

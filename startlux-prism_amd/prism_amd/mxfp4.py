@@ -21,7 +21,7 @@ import torch
 from . import _lib as L
 
 QK = 32
-E4M3, E2M1 = 0, 4
+E4M3, E4M3_PANELS, E2M1 = 0, 1, 4
 MODES = {"max": 0, "mse": 1, "ocp": 2}
 KERNELS = {"auto": -1, "tile": 0, "decode": 1}
 
@@ -110,8 +110,13 @@ def _quant(x, inv, q, s, fmt, n_rows=None):
     n, k = x.shape
     if x.dtype not in (torch.bfloat16, torch.float32) or x.stride(1) != 1:
         raise ValueError("mxfp4 quantize: x bf16 or fp32 with unit inner stride")
-    want = (n, k) if fmt == E4M3 else (n, k // 2)
-    if q.dtype != torch.uint8 or s.dtype != torch.uint8 or tuple(q.shape[-2:]) != want or s.shape[-1] != k // QK:
+    if fmt == E4M3 and q.dim() == 3:
+        fmt, want, got = E4M3_PANELS, _panel_shape(n, k), tuple(q.shape)
+        if not q.is_contiguous():
+            raise ValueError("mxfp4 quantize: panel buffer must be contiguous (act_panels)")
+    else:
+        want, got = ((n, k) if fmt == E4M3 else (n, k // 2)), tuple(q.shape[-2:])
+    if q.dtype != torch.uint8 or s.dtype != torch.uint8 or got != want or s.shape[-1] != k // QK:
         raise ValueError(f"mxfp4 quantize: q uint8 {want}, s uint8 [{n}, {k // QK}]")
     if inv is not None:
         inv = inv.to(torch.float32).contiguous()
@@ -131,26 +136,53 @@ def quantize_act_scaled(x: torch.Tensor, inv: torch.Tensor, q: torch.Tensor, s: 
 
 
 def quantize_act_fp8(x: torch.Tensor, q: torch.Tensor, s: torch.Tensor, n_rows=None) -> None:
-    """x [n, k] bf16/fp32 -> q uint8 [n, k] (e4m3), s uint8 [n, k/32] (the MXFP8 activations of the C4 workload)."""
+    """x [n, k] bf16/fp32 -> q uint8 [n, k] (e4m3), s uint8 [n, k/32] (the MXFP8 activations of the C4 workload).
+    q may instead be a panel buffer from act_panels(n, k): the same codes in the layout the prefill kernel reads."""
     _quant(x, None, q, s, E4M3, n_rows)
 
 
+def _panel_shape(n, k):
+    return ((n + 15) // 16, k // 128, 2048)
+
+
+def act_panels(n: int, k: int, device) -> torch.Tensor:
+    """A buffer for n e4m3 activation rows of k inputs in the panel layout (PRISM_MX_E4M3_PANELS): uint8
+    [ceil(n / 16), k / 128, 2048], chunk [b, st] holding rows 16 b .. 16 b + 15, inputs 128 st .. + 127 in the order
+    the tile kernel's lanes load them.  gemm() takes it for a_q; only the prefill tile kernel reads it."""
+    if k % 128:
+        raise ValueError("act_panels: k must be a multiple of 128")
+    return torch.empty(_panel_shape(n, k), dtype=torch.uint8, device=device)
+
+
+def panels_to_rows(q: torch.Tensor, n: int) -> torch.Tensor:
+    """The row-major e4m3 codes [n, k] of a panel buffer (a byte permutation, for checks)."""
+    b, ks, _ = q.shape
+    t = q.view(b, ks, 2, 4, 16, 16).permute(0, 4, 1, 2, 3, 5).reshape(b * 16, ks * 128)
+    return t[:n]
+
+
 def gemm(a_q, a_s, w: MX4, out, n_rows, epi=0, out_stride=None, kernel="auto"):
-    """a_q uint8 [n_rows, k/2] (e2m1) or [n_rows, k] (e4m3), a_s uint8 [n_rows, k/32]; w MX4 [N, k].  epi=0 writes
-    bf16 into `out`; epi=1 adds into the fp32 residual `out`.  n_rows: int, or a device int32 [1] of live rows
-    (then the launch covers a_q.shape[0] rows)."""
+    """a_q uint8 [n_rows, k/2] (e2m1) or [n_rows, k] (e4m3), or an e4m3 panel buffer (act_panels; the tile kernel
+    reads it, same bits); a_s uint8 [n_rows, k/32]; w MX4 [N, k].  epi=0 writes bf16 into `out`; epi=1 adds into the
+    fp32 residual `out`.  n_rows: int, or a device int32 [1] of live rows (then the launch covers a_s.shape[0] rows)."""
     K, N = w.k, w.n
     if isinstance(n_rows, torch.Tensor):
-        M, live = a_q.shape[0], n_rows
+        M, live = (a_s.shape[0] if a_q.dim() == 3 else a_q.shape[0]), n_rows
     else:
         M, live = int(n_rows), None
-    if a_q.shape[1] == K:
+    if a_q.dim() == 3:
+        if tuple(a_q.shape) != _panel_shape(M, K) or not a_q.is_contiguous():
+            raise ValueError(f"mxfp4.gemm: panel activations must be act_panels({M}, {K})")
+        if kernel not in ("auto", "tile"):
+            raise ValueError("mxfp4.gemm: panel activations are read by the tile kernel only")
+        fmt = E4M3_PANELS
+    elif a_q.shape[1] == K:
         fmt = E4M3
     elif a_q.shape[1] * 2 == K:
         fmt = E2M1
     else:
         raise ValueError(f"mxfp4.gemm: a_q width {a_q.shape[1]} matches neither e4m3 ({K}) nor e2m1 ({K // 2})")
-    if a_q.stride(1) != 1 or a_q.stride(0) != a_q.shape[1] or a_s.stride(0) != K // QK:
+    if fmt != E4M3_PANELS and (a_q.stride(1) != 1 or a_q.stride(0) != a_q.shape[1]) or a_s.stride(0) != K // QK:
         raise ValueError("mxfp4.gemm: a_q and a_s must be row-major with packed rows")
     if epi == 0 and out.dtype != torch.bfloat16 or epi == 1 and out.dtype != torch.float32:
         raise ValueError("mxfp4.gemm: epi 0 writes bf16, epi 1 adds into fp32")

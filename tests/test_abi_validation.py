@@ -70,14 +70,23 @@ def test_w4a8_q4k_gemm_checks(lib):
 def test_mxfp4_gemm_checks(lib):
     f = lib.prism_mxfp4_gemm
 
-    def call(aq=P, fmt=0, M=16, N=64, K=256, epi=0, out=P):
-        return f(aq, P, fmt, P, P, out, N, P, M, N, K, epi, -1, None)
+    def call(aq=P, fmt=0, M=16, N=64, K=256, epi=0, out=P, kernel=-1):
+        return f(aq, P, fmt, P, P, out, N, P, M, N, K, epi, kernel, None)
     assert call(aq=None) == ARG
-    assert call(fmt=1) == ARG                    # neither e4m3 (0) nor e2m1 (4)
+    assert call(fmt=2) == ARG                    # neither e4m3 (0), e4m3 panels (1) nor e2m1 (4)
+    assert call(fmt=1, kernel=1) == SHAPE        # panel activations: the tile kernel only
+    assert call(fmt=1, M=0) == OK
     assert call(K=192) == SHAPE                  # K % 128
     assert call(aq=U) == ALIGN
     assert call(epi=1, out=P + 8) == ALIGN       # the fp32 residual needs 16-byte rows
     assert call(M=0) == OK
+
+
+def test_mxfp4_quant_act_checks(lib):
+    f = lib.prism_mxfp4_quant_act
+    assert f(P, 0, 256, None, P, P, None, 16, 256, 2, None) == ARG            # fmt
+    assert f(P, 0, 160, None, P, P, None, 16, 160, 1, None) == SHAPE          # panels: K % 128
+    assert f(P, 0, 256, None, P, P, None, 0, 256, 1, None) == OK
 
 
 def test_quant_and_split_checks(lib):

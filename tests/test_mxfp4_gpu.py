@@ -255,3 +255,50 @@ def test_one_order_on_order_sensitive_data(dev, M, N, K, live):
     assert torch.equal(got["tile"][:live], got["decode"][:live])
     g = got["tile"][:live].cpu().numpy()
     assert (g != y[:live].astype(np.float32)).any(), "operands too tame: every fp32 sum was exact"
+
+
+@pytest.mark.parametrize("M,K,live", [(1, 128, 1), (17, 1152, 17), (130, 5120, 100)])
+def test_quant_act_panels(dev, M, K, live):
+    """The panel layout holds the row-major quantizer's codes, permuted as act_panels documents; scales unchanged."""
+    from prism_amd import mxfp4 as MX
+    xb = acts_bf16(M, K, seed=M + K + 5)
+    x = torch.from_numpy(xb.view(np.int16)).to(dev).view(torch.bfloat16)
+    n = torch.tensor([live], dtype=torch.int32, device=dev)
+    q, s = torch.zeros(M, K, dtype=torch.uint8, device=dev), torch.zeros(M, K // 32, dtype=torch.uint8, device=dev)
+    MX.quantize_act_fp8(x, q, s, n)
+    qp, sp = MX.act_panels(M, K, dev).zero_(), torch.zeros(M, K // 32, dtype=torch.uint8, device=dev)
+    MX.quantize_act_fp8(x, qp, sp, n)
+    torch.cuda.synchronize()
+    assert torch.equal(MX.panels_to_rows(qp, M)[:live], q[:live]) and torch.equal(sp, s)
+    # the permutation itself, element by element at a few places
+    qn, rn = qp.cpu().numpy(), q.cpu().numpy()
+    for (r, k) in [(0, 0), (live - 1, K - 1), (live // 2, 77), (min(15, live - 1), 64 + 16 + 3)]:
+        b, st, h, p, i = r // 16, k // 128, (k // 64) % 2, (k // 16) % 4, k % 16
+        assert qn[b, st, 1024 * h + 16 * (16 * p + r % 16) + i] == rn[r, k]
+
+
+@pytest.mark.parametrize("M,N,K,live", [(17, 256, 1152, 17), (64, 512, 5120, 50), (130, 272, 1152, 130),
+                                        (300, 1024, 2048, 257)])
+def test_gemm_panels_equal_rows(dev, M, N, K, live):
+    """The tile kernel on panel activations gives the row-major call's bits, both epilogues, with live rows."""
+    from prism_amd import mxfp4 as MX
+    xb = acts_bf16(M, K, seed=M + N)
+    x = torch.from_numpy(xb.view(np.int16)).to(dev).view(torch.bfloat16)
+    m = _mx(dev, weights_f32(N, K, seed=N + 9))
+    q, s = _acts(dev, xb, "e4m3")
+    qp = MX.act_panels(M, K, dev)
+    sp = torch.zeros(M, K // 32, dtype=torch.uint8, device=dev)
+    MX.quantize_act_fp8(x, qp, sp)
+    n = torch.tensor([live], dtype=torch.int32, device=dev)
+    base = rng(M + 1).standard_normal((M, N)).astype(np.float32)
+    for epi in (0, 1):
+        outs = []
+        for a_q, a_s in ((q, s), (qp, sp)):
+            out = (torch.full((M, N), 7, dtype=torch.int16, device=dev).view(torch.bfloat16) if epi == 0
+                   else torch.from_numpy(base).to(dev).clone())
+            MX.gemm(a_q, a_s, m, out, n, epi=epi, kernel="tile")
+            outs.append(out)
+        torch.cuda.synchronize()
+        assert torch.equal(outs[0].view(torch.int32 if epi else torch.int16), outs[1].view(torch.int32 if epi else torch.int16))
+    with pytest.raises(ValueError):
+        MX.gemm(qp, sp, m, outs[1], n, epi=1, kernel="decode")
