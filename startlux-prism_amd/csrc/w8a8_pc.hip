@@ -191,8 +191,10 @@ __global__ __launch_bounds__(64 * NWV, TM == 128 ? 2 : 1) void w8a8_pc_tile_kern
 // activation rows are staged through registers (buffer loads two stages ahead, then one ds_write per 16 bytes)
 // rather than by LDS-DMA: every request is then a plain load, and those complete in order, so one counted wait
 // covers both operands (an LDS-DMA and later buffer loads were measured to complete out of order).  The rings are
-// indexed by stage mod 6 in a loop unrolled by six, so every slot is a fixed register.
-template <bool WS16, int EPI, int TN>
+// indexed by stage mod 6 in a loop unrolled by six, so every slot is a fixed register.  PAN: `a` is the panel image
+// of pc_act_panel_kernel, so a wave's activation load for a stage is one 1 KB piece (C1 shape 1.20 -> 1.10 ms for the
+// tile kernel; the row-major form reads 16 rows' 64 bytes K apart per load).
+template <bool WS16, int EPI, int TN, bool PAN = false>
 __global__ __launch_bounds__(256, TN == 2 ? 2 : 1) void w8a8_pc_wd_kernel(const int8_t* __restrict__ a, const float* __restrict__ a_s,
                                                             int64_t as_sm, const int8_t* __restrict__ w,
                                                             const void* __restrict__ w_s, void* __restrict__ out,
@@ -224,7 +226,8 @@ __global__ __launch_bounds__(256, TN == 2 ? 2 : 1) void w8a8_pc_wd_kernel(const 
 #pragma unroll
     for (int i = 0; i < DIA; i++) {
         const int row = 16 * (DIA * wv + i) + (lane >> 2);
-        ao[i] = (uint32_t)(min(row, M - 1 - m0) * K + 16 * ((lane & 3) ^ pc_swz(row)));
+        ao[i] = PAN ? (uint32_t)((min(m0 / 16 + DIA * wv + i, (M - 1) / 16) - m0 / 16) * KS * 1024 + 16 * lane)
+                    : (uint32_t)(min(row, M - 1 - m0) * K + 16 * ((lane & 3) ^ pc_swz(row)));
     }
     const int r = lane & 31, h = lane >> 5;
     const int nt0 = n0 >> 4;
@@ -239,7 +242,7 @@ __global__ __launch_bounds__(256, TN == 2 ? 2 : 1) void w8a8_pc_wd_kernel(const 
     v4i xr[2][DIA], wr[3][2][TN];
     auto load = [&](int st, v4i (&x)[DIA], v4i (&f)[2][TN]) {       // activations first, then weights
 #pragma unroll
-        for (int i = 0; i < DIA; i++) x[i] = buf_load16(ra, ao[i], (uint32_t)st * PCK);
+        for (int i = 0; i < DIA; i++) x[i] = buf_load16(ra, ao[i], (uint32_t)st * (PAN ? 1024 : PCK));
         __builtin_amdgcn_sched_barrier(0);         // kept in this order: the waits count the weight loads last
 #pragma unroll
         for (int s = 0; s < 2; s++)
@@ -305,6 +308,49 @@ __global__ __launch_bounds__(256, TN == 2 ? 2 : 1) void w8a8_pc_wd_kernel(const 
     for (int j = 0; j < U - 1; j++)
         if (st + j < KS) step(st + j, j);
     pc_store<EPI, TN>(acc, sal, swl, 0, 32 * TN * wv, lane, m0, n0, live, N, out, ldo);
+}
+
+// Panel image of the activations for w8a8_pc_wd_kernel<.., true>: 16-row blocks of K / 64 chunks of 1 KB, block b
+// starting at byte 16 b K; chunk st holds what the kernel's lane L stores at LDS byte 16 L for the block's stage st:
+// row 16 b + L / 4 (clamped to M - 1), inputs 64 st + 16 ((L % 4) ^ pc_swz(L / 4)) .. + 15.  One workgroup per
+// (block, 1024 inputs); each row's 1 KB is read in one piece.
+__global__ __launch_bounds__(256) void pc_act_panel_kernel(const int8_t* __restrict__ a, int8_t* __restrict__ pan,
+                                                           int M, int K) {
+    const int rb = blockIdx.y, KS = K / PCK;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int piece = threadIdx.x + 256 * j, r = piece >> 6;
+        const int k = 1024 * blockIdx.x + 16 * (piece & 63);
+        if (k >= K) continue;
+        const v4i v = *reinterpret_cast<const v4i*>(a + (int64_t)min(16 * rb + r, M - 1) * K + k);
+        const int L = 4 * r + (((k >> 4) & 3) ^ pc_swz(r));
+        *reinterpret_cast<v4i*>(pan + ((int64_t)rb * KS + (k >> 6)) * 1024 + 16 * L) = v;
+    }
+}
+
+constexpr int kPcPanelRows = 256;                // the panel pass pays from here (a copy of M K bytes first)
+
+int64_t pc_panel_bytes(int64_t M, int64_t K) { return (M + 15) / 16 * 16 * K; }
+
+// The tile kernel on the panel image of `a` built in ws first.  The caller has checked the shapes, the alignment,
+// packed weights with N K < 2^31 and ws of pc_panel_bytes.
+int launch_w8a8_pc_panels(const int8_t* a, const float* a_s, int64_t as_sm, const int8_t* w, const void* w_s,
+                          bool ws16, void* out, int64_t ldo, const int32_t* n_rows, int M, int N, int K, int epi,
+                          void* ws, hipStream_t st) {
+    int8_t* pan = static_cast<int8_t*>(ws);
+    hipLaunchKernelGGL(pc_act_panel_kernel, dim3((unsigned)((K + 1023) / 1024), (unsigned)((M + 15) / 16)), dim3(256),
+                       0, st, a, pan, M, K);
+    PRISM_LAUNCH_CHECK();
+    constexpr int TN = 2;
+    const int tiles_m = (M + 127) / 128, tiles_n = (N + 128 * TN - 1) / (128 * TN);
+#define PPL(W16, E)                                                                                                \
+    hipLaunchKernelGGL((w8a8_pc_wd_kernel<W16, E, TN, true>), dim3(tiles_m * tiles_n), dim3(256), 0, st, pan, a_s, \
+                       as_sm, w, w_s, out, ldo, n_rows, M, N, K, tiles_m, tiles_n)
+    if (ws16) { if (epi == 0) PPL(true, 0); else PPL(true, 1); }
+    else { if (epi == 0) PPL(false, 0); else PPL(false, 1); }
+#undef PPL
+    PRISM_LAUNCH_CHECK();
+    return PRISM_OK;
 }
 
 // ---------------------------------------------------------------------------------------------- decode
@@ -623,6 +669,19 @@ extern "C" int prism_w8a8_pc_packed_gemm_ws(const int8_t* a, const float* a_s, i
     if (kernel == -1 && fits && M >= 16 &&
         ((M <= 64 && (K >= 12288 || (M >= 48 && N <= 5120))) || (M <= 256 && K >= 12288 && N <= 8192)))
         kernel = 2;
+    // the tile kernel on panel activations where ws holds them (from kPcPanelRows rows: below, the copy costs more
+    // than it saves); the table's "tile" choice and kernel 0 take it too
+    if ((kernel == 0 || (kernel == -1 && M > 64)) && M >= kPcPanelRows && ws && ws_bytes >= pc_panel_bytes(M, K) &&
+        PRISM_ALIGNED(ws, 256) && N * K < (1LL << 31) && M <= 65535 * 16 && N % 16 == 0 && K % 64 == 0 &&
+        K <= (1 << 17)) {
+        if (!a || !a_s || !qt || !w_s || !out || !n_rows) return PRISM_ERR_ARG;
+        if (epi != 0 && epi != 1) return PRISM_ERR_ARG;
+        if (ldo < N) return PRISM_ERR_SHAPE;
+        if (!PRISM_ALIGNED(a, 16) || !PRISM_ALIGNED(qt, 16) || ldo % 4 || !PRISM_ALIGNED(out, epi ? 16 : 8))
+            return PRISM_ERR_ALIGN;
+        return launch_w8a8_pc_panels(a, a_s, as_sm, qt, w_s, ws_fp16 != 0, out, ldo, n_rows, (int)M, (int)N, (int)K,
+                                     epi, ws, (hipStream_t)stream);
+    }
     if (kernel != 2)
         return prism_w8a8_pc_packed_gemm(a, a_s, as_sm, qt, w_s, ws_fp16, out, ldo, n_rows, M, N, K, epi, kernel,
                                          stream);

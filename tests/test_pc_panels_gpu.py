@@ -1,0 +1,70 @@
+"""The per-channel tile kernel on the panel copy of the activations (from 256 rows, where the per-channel GEMM's
+workspace holds ceil(M / 16) 16 K bytes): bit-exact against the oracle and equal to the row-major tile kernel
+(the same call without a workspace), both epilogues, M not a multiple of 16 or of the 128-row tile, live rows
+below M, N not a multiple of the 256-column tile, calls back to back, and replays of a captured graph."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from _inputs import rng
+from test_pc_split_gpu import _bits, _case, _t
+
+pytestmark = pytest.mark.gpu
+
+
+def _call(a, sa, pw, out, n, epi, ws):
+    from prism_amd import _lib as L
+    M, K = a.shape
+    L.call("prism_w8a8_pc_packed_gemm_ws", L.ptr(a), L.ptr(sa), sa.stride(0), L.ptr(pw.qt), L.ptr(pw.ws),
+           int(pw.ws.dtype == torch.float16), L.ptr(out), out.stride(0), L.ptr(n), M, pw.n, K, epi, 0, L.ptr(ws),
+           0 if ws is None else ws.numel(), L.stream_of(a))
+
+
+@pytest.mark.parametrize("M,N,K,live", [(256, 512, 1024, 256), (300, 784, 2048, 300), (1000, 1040, 5120, 777),
+                                        (2049, 2560, 1536, 2049)])
+def test_panels_bit_exact(dev, M, N, K, live):
+    from prism_amd import w8a8 as KW
+    a, sa, wq, ws, pw = _case(M, N, K, 900 + M, dev)
+    want0 = O.w8a8_gemm(a, sa, wq, ws, K, epi=0, live=live, nthreads=16)
+    base = rng(M + 3).standard_normal((M, N)).astype(np.float32)
+    want1 = O.w8a8_gemm(a, sa, wq, ws, K, epi=1, out=base.copy(), live=live, nthreads=16)
+    ad, sad = _t(a, dev), _t(sa, dev)
+    n = torch.tensor([live], dtype=torch.int32, device=dev)
+    wsp = KW.pc_workspace(dev)
+    for w in (wsp, wsp, None):                        # panels twice back to back, then the row-major kernel
+        out = torch.full((M, N), 7, dtype=torch.int16, device=dev).view(torch.bfloat16)
+        _call(ad, sad, pw, out, n, 0, w)
+        h = _t(base, dev)
+        _call(ad, sad, pw, h, n, 1, w)
+        torch.cuda.synchronize()
+        got = _bits(out)
+        assert np.array_equal(got[:live], want0[:live]) and (got[live:] == 7).all()
+        assert np.array_equal(h.cpu().numpy(), want1)
+
+
+def test_panels_graph_replay(dev):
+    """KW.gemm's "auto" path at 512 rows takes the panel copy; in a captured graph with new activations between
+    replays every replay equals the oracle."""
+    from prism_amd import w8a8 as KW
+    M, N, K = 512, 1024, 2048
+    _, _, wq, ws, pw = _case(M, N, K, 31, dev)
+    KW.pc_workspace(dev)
+    ad = torch.empty(M, K, dtype=torch.int8, device=dev)
+    sad = torch.empty(M, dtype=torch.float32, device=dev)
+    out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    n = torch.tensor([M], dtype=torch.int32, device=dev)
+    KW.gemm(ad, sad, pw, None, out, n, K, epi=0)       # warm-up outside capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        KW.gemm(ad, sad, pw, None, out, n, K, epi=0)
+    for rep in range(3):
+        a, sa = O.quant_rows_i8(O.bf16_bits(rng(50 + rep).standard_normal((M, K)).astype(np.float32)))
+        ad.copy_(_t(a, dev))
+        sad.copy_(_t(sa.reshape(-1), dev))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        want = O.w8a8_gemm(a, sa, wq, ws, K, epi=0, nthreads=16)
+        assert np.array_equal(_bits(out), want), rep
