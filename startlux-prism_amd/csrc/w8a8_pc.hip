@@ -192,8 +192,8 @@ __global__ __launch_bounds__(64 * NWV, TM == 128 ? 2 : 1) void w8a8_pc_tile_kern
 // rather than by LDS-DMA: every request is then a plain load, and those complete in order, so one counted wait
 // covers both operands (an LDS-DMA and later buffer loads were measured to complete out of order).  The rings are
 // indexed by stage mod 6 in a loop unrolled by six, so every slot is a fixed register.  PAN: `a` is the panel image
-// of pc_act_panel_kernel, so a wave's activation load for a stage is one 1 KB piece (C1 shape 1.20 -> 1.10 ms for the
-// tile kernel; the row-major form reads 16 rows' 64 bytes K apart per load).
+// of pc_act_panel_kernel, so a wave's activation load for a stage is one 1 KB piece (C1 shape 1.20 -> 1.11 ms with
+// the copy; the row-major form reads 16 rows' 64 bytes K apart per load).
 template <bool WS16, int EPI, int TN, bool PAN = false>
 __global__ __launch_bounds__(256, TN == 2 ? 2 : 1) void w8a8_pc_wd_kernel(const int8_t* __restrict__ a, const float* __restrict__ a_s,
                                                             int64_t as_sm, const int8_t* __restrict__ w,
@@ -328,7 +328,9 @@ __global__ __launch_bounds__(256) void pc_act_panel_kernel(const int8_t* __restr
     }
 }
 
-constexpr int kPcPanelRows = 256;                // the panel pass pays from here (a copy of M K bytes first)
+// The panel copy (2 M K bytes of traffic first) pays where many column tiles read each activation panel: measured
+// at 27648 x 5120, 2048 / 4096 rows 281 / 597 -> 271 / 555 us; at N = 1024 - 5120 it cost 0-15%.
+constexpr int kPcPanelRows = 1024, kPcPanelCols = 16384;
 
 int64_t pc_panel_bytes(int64_t M, int64_t K) { return (M + 15) / 16 * 16 * K; }
 
@@ -669,9 +671,10 @@ extern "C" int prism_w8a8_pc_packed_gemm_ws(const int8_t* a, const float* a_s, i
     if (kernel == -1 && fits && M >= 16 &&
         ((M <= 64 && (K >= 12288 || (M >= 48 && N <= 5120))) || (M <= 256 && K >= 12288 && N <= 8192)))
         kernel = 2;
-    // the tile kernel on panel activations where ws holds them (from kPcPanelRows rows: below, the copy costs more
-    // than it saves); the table's "tile" choice and kernel 0 take it too
-    if ((kernel == 0 || (kernel == -1 && M > 64)) && M >= kPcPanelRows && ws && ws_bytes >= pc_panel_bytes(M, K) &&
+    // the tile kernel on panel activations where ws holds them and the shape is wide enough to repay the copy; the
+    // table's "tile" choice and kernel 0 take it too
+    if ((kernel == 0 || (kernel == -1 && M > 64)) && M >= kPcPanelRows && N >= kPcPanelCols && ws &&
+        ws_bytes >= pc_panel_bytes(M, K) &&
         PRISM_ALIGNED(ws, 256) && N * K < (1LL << 31) && M <= 65535 * 16 && N % 16 == 0 && K % 64 == 0 &&
         K <= (1 << 17)) {
         if (!a || !a_s || !qt || !w_s || !out || !n_rows) return PRISM_ERR_ARG;

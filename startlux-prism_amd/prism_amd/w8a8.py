@@ -236,7 +236,7 @@ PC_WS_BYTES = 96 << 20        # as the reference's workspace (kernels/cuda_ext.p
 
 def pc_workspace(dev):
     """The per-device workspace of the per-channel GEMM: the split decode's int32 slots (kernel "split") or the tile
-    kernel's panel copy of the activations (from 256 rows), rewritten by every launch.  None while a graph is being captured on a device that has none yet: "auto" then picks another
+    kernel's panel copy of the activations (wide projections from 1024 rows), rewritten by every launch.  None while a graph is being captured on a device that has none yet: "auto" then picks another
     kernel and "split" raises."""
     idx = dev.index if dev.index is not None else torch.cuda.current_device()
     ws = _PCWS.get(idx)
@@ -266,8 +266,8 @@ def _gemm_pc_packed(a, a_s, w, out, n_rows, gk, epi, kernel):
         raise ValueError(f"out must be {want} [>= {M}, >= {w.n}] with unit column stride")
     if kernel not in _PC_KERNELS:
         raise ValueError(f"packed per-channel kernels: auto, tile, decode or split, not {kernel}")
-    # the workspace: the split decode's slots (up to 512 rows), or from 256 rows the tile kernel's panel copy of the
-    # activations (ceil(M / 16) 16 K bytes) where it fits
+    # the workspace: the split decode's slots (up to 512 rows), or the tile kernel's panel copy of the activations
+    # (ceil(M / 16) 16 K bytes; the library takes it from 1024 rows on projections at least 16384 wide) where it fits
     use_ws = kernel == "split" or (kernel in ("auto", "tile") and
                                    (M <= 512 or (M + 15) // 16 * 16 * K <= PC_WS_BYTES))
     ws = pc_workspace(a.device) if use_ws else None

@@ -1,5 +1,5 @@
-"""The per-channel tile kernel on the panel copy of the activations (from 256 rows, where the per-channel GEMM's
-workspace holds ceil(M / 16) 16 K bytes): bit-exact against the oracle and equal to the row-major tile kernel
+"""The per-channel tile kernel on the panel copy of the activations (from 1024 rows on projections at least 16384
+wide, where the per-channel GEMM's workspace holds ceil(M / 16) 16 K bytes): bit-exact against the oracle and equal to the row-major tile kernel
 (the same call without a workspace), both epilogues, M not a multiple of 16 or of the 128-row tile, live rows
 below M, N not a multiple of the 256-column tile, calls back to back, and replays of a captured graph."""
 import numpy as np
@@ -21,8 +21,8 @@ def _call(a, sa, pw, out, n, epi, ws):
            0 if ws is None else ws.numel(), L.stream_of(a))
 
 
-@pytest.mark.parametrize("M,N,K,live", [(256, 512, 1024, 256), (300, 784, 2048, 300), (1000, 1040, 5120, 777),
-                                        (2049, 2560, 1536, 2049)])
+@pytest.mark.parametrize("M,N,K,live", [(1024, 16384, 512, 1024), (1100, 16400, 1024, 999),
+                                        (2049, 16640, 1536, 2049)])
 def test_panels_bit_exact(dev, M, N, K, live):
     from prism_amd import w8a8 as KW
     a, sa, wq, ws, pw = _case(M, N, K, 900 + M, dev)
@@ -44,10 +44,10 @@ def test_panels_bit_exact(dev, M, N, K, live):
 
 
 def test_panels_graph_replay(dev):
-    """KW.gemm's "auto" path at 512 rows takes the panel copy; in a captured graph with new activations between
-    replays every replay equals the oracle."""
+    """KW.gemm's "auto" path at 1024 rows and N = 16384 takes the panel copy; in a captured graph with new activations
+    between replays every replay equals the oracle."""
     from prism_amd import w8a8 as KW
-    M, N, K = 512, 1024, 2048
+    M, N, K = 1024, 16384, 1024
     _, _, wq, ws, pw = _case(M, N, K, 31, dev)
     KW.pc_workspace(dev)
     ad = torch.empty(M, K, dtype=torch.int8, device=dev)
