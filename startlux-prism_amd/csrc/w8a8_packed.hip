@@ -248,7 +248,9 @@ constexpr int PLDB = 2048 + 64;         // one 16-row tile's two chunks, padded
 
 // RA: the reassociated order (one activation scale per token, factored out of the block sum): per block
 // y = fma(float(P), sw, y), then y = RN(y sa) once; 2 VALU operations per output and block instead of 4.
-template <int EPI, bool RA>
+// PAN: `a` is the panel copy of q8_act_panel_kernel, so a wave's activation load for a stage is one 1 KB piece
+// (8 rows x 128 bytes of the tile's 16 KB stage chunk) instead of 8 rows' 128 bytes K apart.
+template <int EPI, bool RA, bool PAN = false>
 __global__ __launch_bounds__(256, 2) void w8a8_packed_tile_kernel(const int8_t* __restrict__ a,
                                                                   const float* __restrict__ a_s, int64_t as_sm,
                                                                   const int8_t* __restrict__ qt,
@@ -274,7 +276,13 @@ __global__ __launch_bounds__(256, 2) void w8a8_packed_tile_kernel(const int8_t* 
     const int lr = tid >> 3, lc = (tid & 7) * 16;
     const int8_t* ap[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) ap[i] = a + (int64_t)min(m0 + lr + 32 * i, M - 1) * K + lc;
+    for (int i = 0; i < 4; i++) {
+        if (PAN) {                                   // the tile's panel: row lr + 32 i of each 16 KB stage chunk
+            ap[i] = a + (int64_t)m0 * K + (lr + 32 * i) * 128 + lc;
+        } else {
+            ap[i] = a + (int64_t)min(m0 + lr + 32 * i, M - 1) * K + lc;
+        }
+    }
     // weight loader: chunk c = tid + 256 i -> tile c / 128 (clamped in range), 16 bytes (c % 128) of its 2 KB run
     const v4i* bp[4];
 #pragma unroll
@@ -292,7 +300,7 @@ __global__ __launch_bounds__(256, 2) void w8a8_packed_tile_kernel(const int8_t* 
     auto gload = [&](int kb) {                       // kb: first block of the stage (a multiple of 4)
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            ra[i] = *reinterpret_cast<const v4i*>(ap[i] + kb * 32);
+            ra[i] = *reinterpret_cast<const v4i*>(ap[i] + (PAN ? (int64_t)(kb / 4) * 16384 : (int64_t)kb * 32));
             rb[i] = __builtin_nontemporal_load(bp[i] + (int64_t)(kb / 2) * 64);
         }
         rs = sp[(int64_t)(kb / 2) * 4];
@@ -544,10 +552,30 @@ static size_t packed_decode_lds(int R, int M) {
     return 2 * (size_t)R * M * 16 * 4 + 2 * (size_t)R * 16 * 4 + 2 * (size_t)M * (R * 32 + 16);
 }
 
+// Panel copy of the activations for w8a8_packed_tile_kernel<.., true>: 128-row tiles of K / 128 chunks of 16 KB, tile
+// t starting at byte 128 t K, chunk st holding rows 128 t .. + 127 (clamped to M - 1), inputs 128 st .. + 127,
+// row-major inside the chunk, so a tile's stage is one 16 KB piece.  One workgroup per (16 rows, 1024 inputs); each
+// row's 1 KB is read in one piece.
+__global__ __launch_bounds__(256) void q8_act_panel_kernel(const int8_t* __restrict__ a, int8_t* __restrict__ pan,
+                                                           int M, int K) {
+    const int rb = blockIdx.y;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int piece = threadIdx.x + 256 * j, r = piece >> 6;
+        const int k = 1024 * blockIdx.x + 16 * (piece & 63);
+        if (k >= K) continue;
+        const v4i v = *reinterpret_cast<const v4i*>(a + (int64_t)min(16 * rb + r, M - 1) * K + k);
+        const int row = 16 * rb + r;
+        *reinterpret_cast<v4i*>(pan + (int64_t)(row >> 7) * 128 * K + (int64_t)(k >> 7) * 16384 + (row & 127) * 128 +
+                                (k & 127)) = v;
+    }
+}
+
+// pan: the panel buffer for the tile kernels (kernels 0 and 3), or null for row-major activations
 template <int EPI>
 static void launch_packed(int kernel, const int8_t* a, const float* a_s, int64_t as_sm, const int8_t* qt,
                           const uint16_t* dt, void* out, int64_t ldo, const int32_t* n_rows, int M, int N, int K,
-                          hipStream_t st) {
+                          hipStream_t st, int8_t* pan) {
     if (kernel == 1) {
         dim3 grid(N / 16);
 #define PDEC(NW, R, MX, D)                                                                                         \
@@ -586,7 +614,16 @@ static void launch_packed(int kernel, const int8_t* a, const float* a_s, int64_t
                                a, a_s, as_sm, qt, dt, out, ldo, n_rows, M, N, K);
     } else if (kernel == 0 || kernel == 3) {
         const int tiles_m = (M + PBM - 1) / PBM, tiles_n = (N + PBN - 1) / PBN;
-        if (kernel == 0)
+        if (pan) {                                   // the panel copy first, then the tile kernel reads it
+            hipLaunchKernelGGL(q8_act_panel_kernel, dim3((unsigned)((K + 1023) / 1024), (unsigned)((M + 127) / 128 * 8)),
+                               dim3(256), 0, st, a, pan, M, K);
+            if (kernel == 0)
+                hipLaunchKernelGGL((w8a8_packed_tile_kernel<EPI, false, true>), dim3(tiles_m * tiles_n), dim3(256), 0,
+                                   st, pan, a_s, as_sm, qt, dt, out, ldo, n_rows, M, N, K, tiles_m, tiles_n);
+            else
+                hipLaunchKernelGGL((w8a8_packed_tile_kernel<EPI, true, true>), dim3(tiles_m * tiles_n), dim3(256), 0,
+                                   st, pan, a_s, as_sm, qt, dt, out, ldo, n_rows, M, N, K, tiles_m, tiles_n);
+        } else if (kernel == 0)
             hipLaunchKernelGGL((w8a8_packed_tile_kernel<EPI, false>), dim3(tiles_m * tiles_n), dim3(256), 0, st, a,
                                a_s, as_sm, qt, dt, out, ldo, n_rows, M, N, K, tiles_m, tiles_n);
         else
@@ -623,6 +660,11 @@ extern "C" int prism_i8_pack(const int8_t* w, int8_t* qt, int64_t N, int64_t K, 
     return PRISM_OK;
 }
 
+// The workspace's first kQ8PanelOffset bytes hold the balanced decode kernel's handoff words (zero between launches,
+// at most kQ8StreamMaxWG x 2 KB for any shape); the prefill's panel copy goes after them.
+constexpr int64_t kQ8PanelOffset = 512 * 1024;
+static_assert(kQ8StreamMaxWG * 16 * 16 * 8 <= kQ8PanelOffset, "the handoff words end before the panel copy");
+
 static int packed_gemm(const int8_t* a, const float* a_s, int64_t as_sm, const int8_t* qt, const uint16_t* dt,
                        void* out, int64_t ldo, const int32_t* n_rows, int64_t M, int64_t N, int64_t K, int epi,
                        int kernel, void* workspace, int64_t workspace_bytes, void* stream) {
@@ -650,10 +692,16 @@ static int packed_gemm(const int8_t* a, const float* a_s, int64_t as_sm, const i
         PRISM_LAUNCH_CHECK();
         return PRISM_OK;
     }
+    // the tile kernels on a panel copy of the activations where the workspace holds it past the handoff words and the
+    // shape repays the copy (2 M K bytes of traffic): from 1024 rows on projections at least 16384 wide
+    int8_t* pan = nullptr;
+    if ((kernel == 0 || kernel == 3) && M >= 1024 && N >= 16384 && M <= 65535 * 16 && workspace &&
+        PRISM_ALIGNED(workspace, 256) && workspace_bytes >= kQ8PanelOffset + (M + 127) / 128 * 128 * K)
+        pan = static_cast<int8_t*>(workspace) + kQ8PanelOffset;
     if (epi == 0)
-        launch_packed<0>(kernel, a, a_s, as_sm, qt, dt, out, ldo, n_rows, (int)M, (int)N, (int)K, st);
+        launch_packed<0>(kernel, a, a_s, as_sm, qt, dt, out, ldo, n_rows, (int)M, (int)N, (int)K, st, pan);
     else
-        launch_packed<1>(kernel, a, a_s, as_sm, qt, dt, out, ldo, n_rows, (int)M, (int)N, (int)K, st);
+        launch_packed<1>(kernel, a, a_s, as_sm, qt, dt, out, ldo, n_rows, (int)M, (int)N, (int)K, st, pan);
     PRISM_LAUNCH_CHECK();
     return PRISM_OK;
 }

@@ -185,11 +185,17 @@ def _tabled(kernel, N, K, M, gk, packed_q8=False):
 
 
 _WS = {}
+# the handoff words (the first 512 KB, the most any shape needs) and the prefill tile kernels' panel copy of the
+# activations after them (ceil(M / 128) 128 K bytes; the library takes it from 1024 rows on projections at least
+# 16384 wide)
+Q8_HANDOFF_BYTES = 512 << 10
+Q8_WS_BYTES = Q8_HANDOFF_BYTES + (96 << 20)
 
 
 def workspace(dev):
-    """The per-device workspace of the packed Q8_0 "stream" kernel (the reference schema's `workspace`, allocated once
-    per device as kernels/cuda_ext.py:138-143 does): zeroed once, left zeroed by every launch.  None while a graph is
+    """The per-device workspace of the packed Q8_0 GEMM (the reference schema's `workspace`, allocated once per device
+    as kernels/cuda_ext.py:138-143 does): the "stream" kernel's handoff words, zeroed once and left zeroed by every
+    launch, then the prefill's panel copy of the activations.  None while a graph is
     being captured on a device that has none yet (its zero fill would be a graph node): "auto" then picks another
     kernel and "stream" raises."""
     idx = dev.index if dev.index is not None else torch.cuda.current_device()
@@ -197,8 +203,7 @@ def workspace(dev):
     if ws is None:
         if torch.cuda.is_current_stream_capturing():
             return None
-        nbytes = int(L.lib().prism_w8a8_q8_0_packed_workspace_bytes(1 << 20, 128))   # the most any shape needs
-        ws = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=torch.device("cuda", idx))
+        ws = torch.zeros(Q8_WS_BYTES, dtype=torch.uint8, device=torch.device("cuda", idx))
         torch.cuda.current_stream(idx).synchronize()
         _WS[idx] = ws
     return ws
@@ -217,7 +222,9 @@ def _gemm_packed(a, a_s, w, out, n_rows, gk, epi, kernel):
     want = torch.bfloat16 if epi == 0 else torch.float32
     if out.dtype != want or out.shape[0] < M or out.shape[1] < w.n or out.stride(1) != 1:
         raise ValueError(f"out must be {want} [>= {M}, >= {w.n}] with unit column stride")
-    ws = workspace(a.device) if M <= 16 and kernel in ("auto", "decode", "stream") else None
+    pan = M >= 1024 and w.n >= 16384 and kernel in ("auto", "tile", "reassoc") and \
+        Q8_HANDOFF_BYTES + (M + 127) // 128 * 128 * K <= Q8_WS_BYTES
+    ws = workspace(a.device) if (M <= 16 and kernel in ("auto", "decode", "stream")) or pan else None
     if kernel == "stream" and ws is None and asked == "auto":
         kernel = "auto"             # the table's pick needs the workspace; the library then picks without it
     if kernel == "stream" and ws is None:

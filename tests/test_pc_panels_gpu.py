@@ -1,7 +1,8 @@
-"""The per-channel tile kernel on the panel copy of the activations (from 1024 rows on projections at least 16384
-wide, where the per-channel GEMM's workspace holds ceil(M / 16) 16 K bytes): bit-exact against the oracle and equal to the row-major tile kernel
-(the same call without a workspace), both epilogues, M not a multiple of 16 or of the 128-row tile, live rows
-below M, N not a multiple of the 256-column tile, calls back to back, and replays of a captured graph."""
+"""The per-channel and packed Q8_0 tile kernels on the panel copy of the activations (from 1024 rows on projections
+at least 16384 wide, where the GEMM's workspace holds ceil(M / 16) 16 K bytes): bit-exact against the oracle and
+equal to the row-major tile kernel (the same call without a workspace), both epilogues, M not a multiple of 16 or
+of the 128-row tile, live rows below M, N not a multiple of the column tile, calls back to back, and replays of a
+captured graph."""
 import numpy as np
 import pytest
 import torch
@@ -68,3 +69,41 @@ def test_panels_graph_replay(dev):
         torch.cuda.synchronize()
         want = O.w8a8_gemm(a, sa, wq, ws, K, epi=0, nthreads=16)
         assert np.array_equal(_bits(out), want), rep
+
+
+def _q8_call(a, s, pw, out, n, epi, kernel, ws):
+    from prism_amd import _lib as L
+    M, K = a.shape
+    L.call("prism_w8a8_q8_0_packed_gemm", L.ptr(a), L.ptr(s), s.stride(0), L.ptr(pw.qt), L.ptr(pw.dt), L.ptr(out),
+           out.stride(0), L.ptr(n), M, pw.n, K, epi, kernel, L.ptr(ws), 0 if ws is None else ws.numel(),
+           L.stream_of(a))
+
+
+@pytest.mark.parametrize("M,N,K,live", [(1024, 16384, 256, 1024), (1100, 16400, 1024, 999)])
+def test_q8_panels_bit_exact(dev, M, N, K, live):
+    """The packed Q8_0 tile kernels (exact and reassociated) on the panel copy past the handoff words (128-row tiles): the oracle's
+    bits (exact kernel), the row-major call's bits (both), both epilogues; the handoff words stay zero."""
+    from _inputs import acts_bf16, q8_weights
+    from prism_amd import w8a8 as KW
+    qs, d = q8_weights(N, K, seed=M + 1)
+    a, s = O.quant_rows_i8(acts_bf16(M, K, seed=M + 2))
+    pw = KW.pack_q8(_t(qs, dev), _t(d, dev).view(torch.float16))
+    ad, sd = _t(a, dev), _t(s, dev)
+    n = torch.tensor([live], dtype=torch.int32, device=dev)
+    want0 = O.w8a8_gemm(a, s, qs, d, 32, epi=0, live=live, nthreads=16)
+    base = rng(M).standard_normal((M, N)).astype(np.float32)
+    wsq = KW.workspace(dev)
+    for kernel in (0, 3):
+        outs = []
+        for w in (wsq, None):
+            out = torch.full((M, N), 7, dtype=torch.int16, device=dev).view(torch.bfloat16)
+            _q8_call(ad, sd, pw, out, n, 0, kernel, w)
+            h = _t(base, dev)
+            _q8_call(ad, sd, pw, h, n, 1, kernel, w)
+            torch.cuda.synchronize()
+            outs.append((_bits(out), h.cpu().numpy()))
+        assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1]), kernel
+        assert (outs[0][0][live:] == 7).all()
+        if kernel == 0:
+            assert np.array_equal(outs[0][0][:live], want0[:live])
+    assert not wsq[:KW.Q8_HANDOFF_BYTES].any()
