@@ -169,6 +169,9 @@ PRISM_API int64_t prism_w8a8_pc_split_workspace_bytes(int64_t M, int64_t N);
  * first use (every launch leaves it zeroed), or NULL (kernel 4 is then unavailable).  Launches that share a
  * workspace must not run concurrently.  This argument is the reference schema's `workspace`
  * (csrc/w8a8_gemm.cu:794-797), which its engine allocates once per device (kernels/cuda_ext.py:138-143).
+ * Bytes past the first 512 KB (the most any shape's handoff words take) are scratch for the tile kernels (0, 3):
+ * from M >= 1024 on N >= 16384, where they hold ceil(M / 128) 128 K bytes, the activations are first copied there as
+ * 128-row panels (each 128-input stage of a tile in one 16 KB piece); same bits, about 1% faster at config 1.
  * Needs K % 128 == 0.
  */
 PRISM_API int prism_w8a8_q8_0_packed_gemm(const int8_t* a, const float* a_s, int64_t as_sm, const int8_t* qt,
