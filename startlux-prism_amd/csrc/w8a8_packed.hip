@@ -695,7 +695,7 @@ static int packed_gemm(const int8_t* a, const float* a_s, int64_t as_sm, const i
     // the tile kernels on a panel copy of the activations where the workspace holds it past the handoff words and the
     // shape repays the copy (2 M K bytes of traffic): from 1024 rows on projections at least 16384 wide
     int8_t* pan = nullptr;
-    if ((kernel == 0 || kernel == 3) && M >= 1024 && N >= 16384 && M <= 65535 * 16 && workspace &&
+    if ((kernel == 0 || kernel == 3) && M >= 1024 && N >= 16384 && M <= 8191 * 128 && workspace &&
         PRISM_ALIGNED(workspace, 256) && workspace_bytes >= kQ8PanelOffset + (M + 127) / 128 * 128 * K)
         pan = static_cast<int8_t*>(workspace) + kQ8PanelOffset;
     if (epi == 0)
