@@ -331,6 +331,8 @@ __global__ __launch_bounds__(256) void pc_act_panel_kernel(const int8_t* __restr
 // The panel copy (2 M K bytes of traffic first) pays where many column tiles read each activation panel: measured
 // at 27648 x 5120, 2048 / 4096 rows 281 / 597 -> 271 / 555 us; at N = 1024 - 5120 it cost 0-15%.
 constexpr int kPcPanelRows = 1024, kPcPanelCols = 16384;
+// The split decode reads a panel copy too from 48 rows on K >= 8192 (the copy is a launch and 2 M K bytes).
+constexpr int kPcDecodePanelRows = 48, kPcDecodePanelK = 8192;
 
 int64_t pc_panel_bytes(int64_t M, int64_t K) { return (M + 15) / 16 * 16 * K; }
 
@@ -364,7 +366,9 @@ int launch_w8a8_pc_panels(const int8_t* a, const float* a_s, int64_t as_sm, cons
 // instruction) and the same 16 inputs of its activation row per m-tile, reused across the G tiles; one
 // v_mfma_i32_16x16x64_i8 per (tile, m-tile) accumulates into int32.  The waves' sums meet in LDS, and the epilogue
 // applies the two roundings.
-template <int G, int MT, bool WPACK, bool WS16, int EPI>
+// PAN: `a` is the panel copy of pc_act_panel_kernel (lane (lm, q)'s 16 bytes of a chunk at 16 (4 lm + (q ^
+// pc_swz(lm))) of the block's 1 KB), so each activation load is one 1 KB piece.
+template <int G, int MT, bool WPACK, bool WS16, int EPI, bool PAN = false>
 __global__ __launch_bounds__(512) void w8a8_pc_decode_kernel(const int8_t* __restrict__ a,
                                                               const float* __restrict__ a_s, int64_t as_sm,
                                                               const int8_t* __restrict__ w,
@@ -393,7 +397,9 @@ __global__ __launch_bounds__(512) void w8a8_pc_decode_kernel(const int8_t* __res
     }
     const int8_t* ab[MT];
 #pragma unroll
-    for (int u = 0; u < MT; u++) ab[u] = a + (int64_t)min(r0 + 16 * u + lm, M - 1) * K + 16 * q;
+    for (int u = 0; u < MT; u++)
+        ab[u] = PAN ? a + (int64_t)min((r0 + 16 * u) / 16, (M - 1) / 16) * 16 * K + 16 * (4 * lm + (q ^ pc_swz(lm)))
+                    : a + (int64_t)min(r0 + 16 * u + lm, M - 1) * K + 16 * q;
 
     // both layouts give lane (lm, q) the 16 inputs 64 j + 16 q .. + 15 of its weight row and of its activation row:
     // one v_mfma_i32_16x16x64_i8 per (tile, m-tile) and chunk
@@ -406,7 +412,7 @@ __global__ __launch_bounds__(512) void w8a8_pc_decode_kernel(const int8_t* __res
 #pragma unroll
         for (int g = 0; g < G; g++) c.w[g] = *reinterpret_cast<const v4i*>(wb[g] + (int64_t)jj * (WPACK ? 1024 : 64));
 #pragma unroll
-        for (int u = 0; u < MT; u++) c.x[u] = *reinterpret_cast<const v4i*>(ab[u] + (int64_t)jj * 64);
+        for (int u = 0; u < MT; u++) c.x[u] = *reinterpret_cast<const v4i*>(ab[u] + (int64_t)jj * (PAN ? 1024 : 64));
     };
     v4i acc[G][MT];
 #pragma unroll
@@ -609,9 +615,10 @@ __global__ __launch_bounds__(256) void pc_fold_kernel(const int32_t* __restrict_
     }
 }
 
+// pan: null, or room for the panel copy of `a` (pc_panel_bytes) that the decode kernel then reads
 int launch_w8a8_pc_split(const int8_t* a, const float* a_s, int64_t as_sm, const int8_t* w, const void* w_s,
                          bool ws16, void* out, int64_t ldo, const int32_t* n_rows, int M, int N, int K, int epi,
-                         void* ws, hipStream_t st) {
+                         void* ws, hipStream_t st, int8_t* pan) {
     const int MT = min(4, (M + 15) / 16);
     const int G = N % 64 == 0 ? 4 : (N % 32 == 0 ? 2 : 1);
     const int KP = K / 64 / kPcSplit;
@@ -620,9 +627,20 @@ int launch_w8a8_pc_split(const int8_t* a, const float* a_s, int64_t as_sm, const
     int32_t* slots = static_cast<int32_t*>(ws);
     const int64_t zstride = (int64_t)M * N;
     dim3 grid((unsigned)(N / (16 * G)), (unsigned)((M + 16 * MT - 1) / (16 * MT)), (unsigned)kPcSplit);
+    if (pan) {
+        hipLaunchKernelGGL(pc_act_panel_kernel, dim3((unsigned)((K + 1023) / 1024), (unsigned)((M + 15) / 16)),
+                           dim3(256), 0, st, a, pan, M, K);
+        PRISM_LAUNCH_CHECK();
+    }
 #define PSL(GV, MTV)                                                                                               \
-    hipLaunchKernelGGL((w8a8_pc_decode_kernel<GV, MTV, true, false, 2>), grid, dim3(64 * nw), lds, st, a, a_s, as_sm, \
-                       w, w_s, slots, (int64_t)N, n_rows, M, N, K, zstride)
+    do {                                                                                                           \
+        if (pan)                                                                                                   \
+            hipLaunchKernelGGL((w8a8_pc_decode_kernel<GV, MTV, true, false, 2, true>), grid, dim3(64 * nw), lds, st, \
+                               pan, a_s, as_sm, w, w_s, slots, (int64_t)N, n_rows, M, N, K, zstride);              \
+        else                                                                                                       \
+            hipLaunchKernelGGL((w8a8_pc_decode_kernel<GV, MTV, true, false, 2>), grid, dim3(64 * nw), lds, st, a,  \
+                               a_s, as_sm, w, w_s, slots, (int64_t)N, n_rows, M, N, K, zstride);                   \
+    } while (0)
 #define PSL_MT(GV)                                                                                                 \
     do {                                                                                                           \
         if (MT == 1) PSL(GV, 1); else if (MT == 2) PSL(GV, 2); else if (MT == 3) PSL(GV, 3); else PSL(GV, 4);      \
@@ -693,8 +711,14 @@ extern "C" int prism_w8a8_pc_packed_gemm_ws(const int8_t* a, const float* a_s, i
     if (N <= 0 || K <= 0 || K % 64 || ldo < N || K > (1 << 17)) return PRISM_ERR_SHAPE;
     if (!PRISM_ALIGNED(a, 16) || !PRISM_ALIGNED(qt, 16) || ldo % 4 || !PRISM_ALIGNED(out, epi ? 16 : 8))
         return PRISM_ERR_ALIGN;
+    // the decode kernel on a panel copy of the activations, after the slots, from 48 rows on long K (5120 x 17408 at
+    // 64 rows: 31.7 -> 28.x us with the copy)
+    int8_t* pan = nullptr;
+    const int64_t slot_bytes = (pc_split_workspace_bytes(M, N) + 255) / 256 * 256;
+    if (M >= kPcDecodePanelRows && K >= kPcDecodePanelK && ws_bytes >= slot_bytes + pc_panel_bytes(M, K))
+        pan = static_cast<int8_t*>(ws) + slot_bytes;
     return launch_w8a8_pc_split(a, a_s, as_sm, qt, w_s, ws_fp16 != 0, out, ldo, n_rows, (int)M, (int)N, (int)K,
-                                epi, ws, (hipStream_t)stream);
+                                epi, ws, (hipStream_t)stream, pan);
 }
 
 extern "C" int prism_w8a8_pc_packed_gemm(const int8_t* a, const float* a_s, int64_t as_sm, const int8_t* qt,
