@@ -683,11 +683,12 @@ extern "C" int prism_w8a8_pc_packed_gemm_ws(const int8_t* a, const float* a_s, i
                       ws_bytes >= pc_split_workspace_bytes(M, N) && PRISM_ALIGNED(ws, 256);
     if (kernel == 2 && !fits) return ws ? PRISM_ERR_SHAPE : PRISM_ERR_ARG;
     // without a table entry: the split where it measured faster (long K from 16 rows: 5120 x 17408 -> 5120 at 16 /
-    // 32 / 64 rows 24.7 / 34.0 / 46.9 -> 21.9 / 24.2 / 29.8 us, at 128 / 256 rows 80.1 / 118.3 -> 48.5 / 84.9 us; up
-    // to N = 5120 at 48 - 64 rows: 5120^2 at 64 rows 17.9 -> 16.5 us); below 16 rows, on wide projections and from
-    // 384 rows on (the tile kernel) the unsplit kernels stay ahead
+    // 32 / 64 rows 24.5 / 34.0 / 46.5 -> 21.8 / 24.0 / 29.7 us, at 128 / 256 / 384 rows 80.4 / 117.4 / 151.5 ->
+    // 43.5 / 70.4 / 87.1 us with the panel copy, against 107.7 us for the tile kernel at 384; up to N = 5120 at 48 - 64
+    // rows: 5120^2 at 64 rows 17.9 -> 16.5 us); below 16 rows, on wide projections and from 512 rows on (the tile
+    // kernel) the unsplit kernels stay ahead
     if (kernel == -1 && fits && M >= 16 &&
-        ((M <= 64 && (K >= 12288 || (M >= 48 && N <= 5120))) || (M <= 256 && K >= 12288 && N <= 8192)))
+        ((M <= 64 && (K >= 12288 || (M >= 48 && N <= 5120))) || (M <= 384 && K >= 12288 && N <= 8192)))
         kernel = 2;
     // the tile kernel on panel activations where ws holds them and the shape is wide enough to repay the copy; the
     // table's "tile" choice and kernel 0 take it too
