@@ -329,7 +329,8 @@ __global__ __launch_bounds__(256) void pc_act_panel_kernel(const int8_t* __restr
 }
 
 // The panel copy (2 M K bytes of traffic first) pays where many column tiles read each activation panel: measured
-// at 27648 x 5120, 2048 / 4096 rows 281 / 597 -> 271 / 555 us; at N = 1024 - 5120 it cost 0-15%.
+// at 27648 x 5120, 2048 / 4096 rows 281 / 597 -> 271 / 555 us; at N = 1024 - 5120 it cost 0-15%, at 17408 x 5120
+// and 1024 rows 1% (M N below 2^25).
 constexpr int kPcPanelRows = 1024, kPcPanelCols = 16384;
 // The split decode reads a panel copy too from 48 rows on K >= 8192 (the copy is a launch and 2 M K bytes).
 constexpr int kPcDecodePanelRows = 48, kPcDecodePanelK = 8192;
@@ -692,7 +693,8 @@ extern "C" int prism_w8a8_pc_packed_gemm_ws(const int8_t* a, const float* a_s, i
         kernel = 2;
     // the tile kernel on panel activations where ws holds them and the shape is wide enough to repay the copy; the
     // table's "tile" choice and kernel 0 take it too
-    if ((kernel == 0 || (kernel == -1 && M > 64)) && M >= kPcPanelRows && N >= kPcPanelCols && ws &&
+    if ((kernel == 0 || (kernel == -1 && M > 64)) && M >= kPcPanelRows && N >= kPcPanelCols &&
+        M * N >= (1LL << 25) && ws &&
         ws_bytes >= pc_panel_bytes(M, K) &&
         PRISM_ALIGNED(ws, 256) && N * K < (1LL << 31) && M <= 65535 * 16 && N % 16 == 0 && K % 64 == 0 &&
         K <= (1 << 17)) {
