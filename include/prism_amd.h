@@ -140,7 +140,7 @@ PRISM_API int prism_w8a8_pc_packed_gemm_split(const int8_t* a, const int8_t* qt,
  * (16 - 64 rows at K >= 12288, 48 - 64 rows up to N = 5120, 65 - 384 rows at K >= 12288 up to N = 8192)
  * (prism_w8a8_pc_split_workspace_bytes), else as prism_w8a8_pc_packed_gemm; 0 / 1 as there; 2 the split (an error
  * when ws cannot hold it; from 48 rows on K >= 8192 it reads a panel copy of the activations placed after the slots
- * when ws holds both).  With kernel -1 (M > 64) or 0, M >= 1024, N >= 16384 and ws of at least
+ * when ws holds both).  With kernel -1 (M > 64) or 0, M >= 1024, N >= 16384, M N >= 2^25 and ws of at least
  * ceil(M / 16) 16 K bytes, the tile kernel first copies the activations into ws as panels (each 16-row, 64-input
  * stage in one 1 KB piece, the order the kernel's lanes store to LDS): same bits, 8% faster at config 1's shape.
  * Calls that overlap on one GPU must not share ws.

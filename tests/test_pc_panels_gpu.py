@@ -1,5 +1,5 @@
 """The per-channel and packed Q8_0 tile kernels on the panel copy of the activations (from 1024 rows on projections
-at least 16384 wide, where the GEMM's workspace holds ceil(M / 16) 16 K bytes): bit-exact against the oracle and
+at least 16384 wide, per channel also M N >= 2^25, where the GEMM's workspace holds the copy): bit-exact against the oracle and
 equal to the row-major tile kernel (the same call without a workspace), both epilogues, M not a multiple of 16 or
 of the 128-row tile, live rows below M, N not a multiple of the column tile, calls back to back, and replays of a
 captured graph."""
@@ -22,7 +22,7 @@ def _call(a, sa, pw, out, n, epi, ws):
            0 if ws is None else ws.numel(), L.stream_of(a))
 
 
-@pytest.mark.parametrize("M,N,K,live", [(1024, 16384, 512, 1024), (1100, 16400, 1024, 999),
+@pytest.mark.parametrize("M,N,K,live", [(2048, 16384, 512, 2048), (2100, 16400, 1024, 1999),
                                         (2049, 16640, 1536, 2049)])
 def test_panels_bit_exact(dev, M, N, K, live):
     from prism_amd import w8a8 as KW
@@ -45,10 +45,10 @@ def test_panels_bit_exact(dev, M, N, K, live):
 
 
 def test_panels_graph_replay(dev):
-    """KW.gemm's "auto" path at 1024 rows and N = 16384 takes the panel copy; in a captured graph with new activations
+    """KW.gemm's "auto" path at 2048 rows and N = 16384 takes the panel copy; in a captured graph with new activations
     between replays every replay equals the oracle."""
     from prism_amd import w8a8 as KW
-    M, N, K = 1024, 16384, 1024
+    M, N, K = 2048, 16384, 512
     _, _, wq, ws, pw = _case(M, N, K, 31, dev)
     KW.pc_workspace(dev)
     ad = torch.empty(M, K, dtype=torch.int8, device=dev)
