@@ -13,8 +13,11 @@ Differences from the reference, by design of this single-GPU MI355X build:
   * The deferred split-K residual add (kernels/w8a8.py:200-204) is produced for per-channel packed weights only
     (PackedPC, epilogue 1, up to 64 rows, the decode kernel's domain, where K split over more workgroups feeds
     every CU): its int32 parts go to `slots` and gemm returns a Deferred for quant.norm_q8 / quant.fold, which give
-    the residual the unsplit product's bits.  cfg / outs / pdl are accepted and ignored.  Epilogues 2 (fused
-    SwiGLU) and 3 (raw int32, tensor parallel) are not provided.
+    the residual the unsplit product's bits.  cfg / pdl are accepted and ignored.
+  * Epilogue 2 (SwiGLU into int8, kernels/w8a8.py:86-98) runs as the product in fp32 (epilogue 1 into a zeroed
+    buffer, so y exactly) followed by the SwiGLU quantizer over each tile's gate and up halves: the values of a fused
+    epilogue, with the library's exact silu (quant.swiglu_q8), at the cost of one fp32 round trip of the product.
+    Epilogue 3 (raw int32, tensor parallel) is gemm_i32.
 """
 from typing import NamedTuple
 
@@ -131,8 +134,11 @@ def gemm(a, a_s, w, w_s, out, n_rows, gk, epi=0, outs=None, cfg=None, slots=None
     (epi 0: bf16 [M, >=N] row stride out.stride(0); epi 1: fp32, out += y).  n_rows: device int32 [1], rows >=
     n_rows[0] untouched.  Returns None, or a Deferred when an epi 1 per-channel product split K into `slots` (int32
     [S, >= M, N]): then `out` is untouched and the residual add is finished by quant.norm_q8 / quant.fold."""
+    if epi == 2:
+        return _gemm_swiglu(a, a_s, w, w_s, out, outs, n_rows, gk, kernel)
     if epi not in (0, 1):
-        raise NotImplementedError(f"epilogue {epi}: only 0 (bf16 store) and 1 (fp32 residual add) are provided")
+        raise NotImplementedError(f"epilogue {epi}: 0 (bf16 store), 1 (fp32 residual add), 2 (SwiGLU to int8); "
+                                  "the raw int32 sums are gemm_i32")
     if isinstance(w, PackedQ8):
         return _gemm_packed(a, a_s, w, out, n_rows, gk, epi, kernel)
     if isinstance(w, PackedPC):
@@ -317,6 +323,50 @@ def _gemm_pc_deferred(a, a_s, w, slots, n_rows, kernel):
     L.call("prism_w8a8_pc_packed_gemm_split", L.ptr(a), L.ptr(w.qt), L.ptr(slots), slots.stride(0), slots.stride(1),
            L.ptr(n_rows), M, w.n, K, split, L.stream_of(a))
     return Deferred(split, a_s, w.ws, slots)
+
+
+def swiglu_tile(M, N, K):
+    """The tile width BN of epilogue 2 for an M x N x K product: each BN-wide column tile holds BN / 2 gate columns
+    then the matching up columns, and its SwiGLU output is quantized with one scale per row and tile.  The value the
+    reference's tile choice gives epilogue 2 (kernels/w8a8.py:122-141, pick(M, N, K, 2)[1]), since the output format
+    depends on it."""
+    if N >= 8192:
+        return 64 if M <= 64 else 128
+    return 64 if K <= 4096 else 128
+
+
+def interleave_gate_up(gate, up, bn):
+    """Rows of gate [FF, K] and up [FF, K] -> [2 FF, K] in tiles of bn rows: bn / 2 gate rows, then the same up rows
+    (kernels/w8a8.py:289-294), the weight order epilogue 2 reads."""
+    FF, K = gate.shape
+    h = bn // 2
+    if FF % h or up.shape != gate.shape:
+        raise ValueError("interleave_gate_up: gate and up [FF, K] with FF a multiple of bn / 2")
+    return torch.stack([gate.reshape(FF // h, h, K), up.reshape(FF // h, h, K)], 1).reshape(2 * FF, K).contiguous()
+
+
+def _gemm_swiglu(a, a_s, w, w_s, out, outs, n_rows, gk, kernel):
+    """Epilogue 2 (kernels/w8a8.py:86-98): for every BN-wide tile t of the product y (BN = swiglu_tile(M, N, K)),
+    act = silu(y[:, t BN + j]) * y[:, t BN + BN/2 + j], j < BN / 2, quantized per row and tile: outs[m, t] =
+    RN(max(amax, 1e-10) / 127), out[m, t BN/2 + j] = rint(act / outs[m, t]).  out int8 [M, N / 2] contiguous, outs
+    fp32 [M, N / BN] contiguous; rows >= n_rows untouched."""
+    from . import quant as KQ
+    M, K = a.shape
+    N = w.n if isinstance(w, (PackedQ8, PackedPC)) else w.shape[0]
+    BN = swiglu_tile(M, N, K)
+    HB, nt = BN // 2, N // BN
+    if N % BN:
+        raise ValueError(f"epilogue 2: N ({N}) must be a multiple of the tile width {BN} (interleave_gate_up)")
+    if out.dtype != torch.int8 or tuple(out.shape) != (M, N // 2) or not out.is_contiguous():
+        raise ValueError(f"epilogue 2: out must be contiguous int8 [{M}, {N // 2}]")
+    if outs is None or outs.dtype != torch.float32 or outs.numel() != M * nt or not outs.is_contiguous():
+        raise ValueError(f"epilogue 2: outs must be contiguous fp32 [{M}, {nt}] (one scale per row and tile)")
+    y = torch.empty(M, N, dtype=torch.float32, device=a.device).zero_()
+    d = gemm(a, a_s, w, w_s, y, n_rows, gk, epi=1, kernel=kernel)
+    assert d is None
+    live = (n_rows * nt).to(torch.int32)
+    KQ.swiglu_q8(y.view(M * nt, BN), None, out.view(M * nt, HB), outs.view(M * nt), live, M * nt)
+    return None
 
 
 def gemm_i32(a, a_s, w, w_s, slots, n_rows, max_split=4, pdl=False):
