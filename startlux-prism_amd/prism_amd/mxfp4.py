@@ -166,6 +166,11 @@ def gemm(a_q, a_s, w: MX4, out, n_rows, epi=0, out_stride=None, kernel="auto"):
     reads it, same bits); a_s uint8 [n_rows, k/32]; w MX4 [N, k].  epi=0 writes bf16 into `out`; epi=1 adds into the
     fp32 residual `out`.  n_rows: int, or a device int32 [1] of live rows (then the launch covers a_s.shape[0] rows)."""
     K, N = w.k, w.n
+    if w.q.dim() != 4 or tuple(w.q.shape) != (N // 16, K // 128, 64, 16) or tuple(w.s.shape) != (N // 16, K // 128, 64):
+        if w.q.dim() == 2:
+            raise ValueError("mxfp4.gemm: w holds row-major bytes (q [n, k/2], as pack() of the reference or a side "
+                             "file gives them); convert once at load with mxfp4.from_rows(q, s)")
+        raise ValueError(f"mxfp4.gemm: w must be in the device layout (q uint8 [{N // 16}, {K // 128}, 64, 16])")
     if isinstance(n_rows, torch.Tensor):
         M, live = (a_s.shape[0] if a_q.dim() == 3 else a_q.shape[0]), n_rows
     else:
@@ -189,3 +194,14 @@ def gemm(a_q, a_s, w: MX4, out, n_rows, epi=0, out_stride=None, kernel="auto"):
     ldo = out.stride(0) if out_stride is None else out_stride
     L.call("prism_mxfp4_gemm", L.ptr(a_q), L.ptr(a_s), fmt, L.ptr(w.q), L.ptr(w.s), L.ptr(out), ldo, L.ptr(live), M,
            N, K, epi, KERNELS[kernel], L.stream_of(a_q))
+
+
+def cutlass_enabled():
+    """kernels/mxfp4.py:227-228: the reference's SM120 CUTLASS path; there is none on MI355X (one kernel family
+    serves every M), so False and the engine's load_mlp keeps its MX4 objects as they are."""
+    return False
+
+
+def cutlass_prepare(w):
+    """kernels/mxfp4.py:231-242: the CUTLASS scale copy; nothing to prepare here, w is returned as it is."""
+    return w

@@ -1,6 +1,7 @@
-"""Host logic of the MXFP4 e4m3 panel layout (no GPU): `mxfp4.panels_to_rows` undoes the layout the header and
+"""Host logic of the MXFP4 module (no GPU): `mxfp4.panels_to_rows` undoes the e4m3 panel layout the header and
 mx_act_panel_offset document (byte 1024 h + 16 (16 p + r) + i of chunk st of block b holds row 16 b + r, input
-128 st + 64 h + 16 p + i), for row counts that are and are not multiples of 16."""
+128 st + 64 h + 16 p + i), for row counts that are and are not multiples of 16; gemm refuses row-major weights;
+the engine's CUTLASS hooks are inert."""
 import numpy as np
 import pytest
 import torch
@@ -32,3 +33,22 @@ def test_act_panels_shape_and_k_rule():
     assert tuple(MX.act_panels(33, 256, "cpu").shape) == (3, 2, 2048)
     with pytest.raises(ValueError):
         MX.act_panels(16, 192, "cpu")
+
+
+def test_mxfp4_gemm_refuses_row_major_weights():
+    """A row-major MX4 (the reference pack's or a side file's bytes) is refused with the conversion to use, never
+    read as the device layout."""
+    n, k = 32, 256
+    w = MX.MX4(torch.zeros(n, k // 2, dtype=torch.uint8), torch.zeros(n, k // 32, dtype=torch.uint8), n, k)
+    a = torch.zeros(4, k, dtype=torch.uint8)
+    s = torch.zeros(4, k // 32, dtype=torch.uint8)
+    out = torch.zeros(4, n, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="from_rows"):
+        MX.gemm(a, s, w, out, 4)
+
+
+def test_cutlass_hooks_are_inert():
+    """The engine's load_mlp asks cutlass_enabled() and may call cutlass_prepare (engine/mxfp4.py:77-81)."""
+    assert MX.cutlass_enabled() is False
+    w = MX.MX4(torch.zeros(1), torch.zeros(1), 16, 128)
+    assert MX.cutlass_prepare(w) is w
