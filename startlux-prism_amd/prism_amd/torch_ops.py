@@ -106,3 +106,10 @@ def load():
             lib.impl(schema.split("(", 1)[0], fn, "CUDA")
         _lib = lib
     return torch.ops.startlux_prism
+
+
+def l2_prefetch(tensors, ctas=32):
+    """kernels/cuda_ext.py:171-173 (the engine's optional weight prefetch on a side stream, engine/model.py:785-791):
+    an L2 residency hint for the next layer's weights.  On MI355X each XCD's L2 is 4 MB and the 256 MB MALL behind it
+    already keeps recently streamed weights, so this is a no-op; it exists so an engine with the option on runs."""
+    return None
