@@ -252,6 +252,9 @@ def test_bad_arguments_raise(dev):
                 device=dev), _live(4, dev), 48)
     with pytest.raises(NotImplementedError):
         KW.gemm(a, torch.ones(4, device=dev), w, torch.ones(16, 1, device=dev), torch.empty(4, 16, dtype=torch.bfloat16,
+                device=dev), _live(4, dev), 48, epi=3)
+    with pytest.raises(ValueError):            # epilogue 2 needs int8 out [M, N / 2] and the per-tile scales
+        KW.gemm(a, torch.ones(4, device=dev), w, torch.ones(16, 1, device=dev), torch.empty(4, 16, dtype=torch.bfloat16,
                 device=dev), _live(4, dev), 48, epi=2)
 
 
