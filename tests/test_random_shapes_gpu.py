@@ -1,7 +1,9 @@
 """A seeded sweep of random shapes through every GEMM kernel and weight format, bit for bit against the CPU oracle
 (MXFP4: within its fp32 bound): rows, live rows, N, K, the epilogue and the kernel are drawn per case, so shape edges
 (a single row, a partial tile, live < M, K at the smallest step) meet every kernel rather than only the hand-picked
-cases of the per-format tests."""
+cases of the per-format tests.  PRISM_SWEEP_BASE=<n> draws another set of cases (the default set is n = 0)."""
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -10,6 +12,7 @@ import oracle as O
 from _inputs import MX_ACC_REL, acts_bf16, q6k_random_blocks, rng, weights_f32
 
 pytestmark = pytest.mark.gpu
+BASE = 100000 * int(os.environ.get("PRISM_SWEEP_BASE", "0"))
 
 
 def _t(x, dev):
@@ -46,11 +49,11 @@ def _check(out, want, live, epi):
 def test_w8a8_q8_0_random(dev, case):
     from prism_amd import gguf_formats as GF
     from prism_amd import w8a8 as KW
-    g = rng(1000 + case)
+    g = rng(1000 + case + BASE)
     M, live, N, K, epi = _draw(g, 128, 4096)
     kernel = str(g.choice(["tile", "mid"] + (["decode"] if M <= 64 else [])))
-    qs, d = O.q8_0_quantize(weights_f32(N, K, seed=case))
-    a, s = O.quant_rows_i8(acts_bf16(M, K, seed=case + 1))
+    qs, d = O.q8_0_quantize(weights_f32(N, K, seed=case + BASE))
+    a, s = O.quant_rows_i8(acts_bf16(M, K, seed=case + 1 + BASE))
     base = g.standard_normal((M, N)).astype(np.float32)
     want = O.w8a8_gemm(a, s, qs, d, 32, epi=epi, out=None if epi == 0 else base.copy(), live=live)
     pw = KW.pack_q8(_t(qs, dev), _t(d.view(np.int16), dev).view(torch.float16))
@@ -63,9 +66,9 @@ def test_w8a8_q8_0_random(dev, case):
 @pytest.mark.parametrize("case", range(10))
 def test_w8a8_per_channel_random(dev, case):
     from prism_amd import w8a8 as KW
-    g = rng(2000 + case)
+    g = rng(2000 + case + BASE)
     M, live, N, K, epi = _draw(g, 64, 6144)
-    kernel = str(g.choice(["tile", "decode"]))
+    kernel = str(g.choice(["tile", "decode"] + (["split"] if K >= 768 else [])))
     w = g.integers(-127, 128, (N, K)).astype(np.int8)
     a = g.integers(-127, 128, (M, K)).astype(np.int8)
     sa = (g.random(M) * 0.02).astype(np.float32)
@@ -83,12 +86,12 @@ def test_w8a8_per_channel_random(dev, case):
 def test_w4a8_q4k_random(dev, case):
     from prism_amd import gguf_formats as GF
     from prism_amd import w4a8 as KW4
-    g = rng(3000 + case)
+    g = rng(3000 + case + BASE)
     M, live, N, K, epi = _draw(g, 256, 6144)
     kernel = str(g.choice(["tile"] + (["decode", "stream"] if M <= 16 else [])))
     group = int(g.choice([256, K]))
-    blocks = O.q4k_quantize(weights_f32(N, K, seed=case + 7))
-    xq, a, xs = O.quant_rows_g(O.bf16_to_f32(acts_bf16(M, K, seed=case + 8)), group)
+    blocks = O.q4k_quantize(weights_f32(N, K, seed=case + 7 + BASE))
+    xq, a, xs = O.quant_rows_g(O.bf16_to_f32(acts_bf16(M, K, seed=case + 8 + BASE)), group)
     ao = a if group == 256 else a[0].copy()
     base = g.standard_normal((M, N)).astype(np.float32)
     want = O.w4a8_gemm(xq, ao, xs, O.q4k_repack(blocks), epi=epi, out=None if epi == 0 else base.copy(), live=live)
@@ -103,11 +106,11 @@ def test_w4a8_q4k_random(dev, case):
 def test_w4a8_q6k_random(dev, case):
     from prism_amd import gguf_formats as GF
     from prism_amd import w4a8 as KW4
-    g = rng(4000 + case)
+    g = rng(4000 + case + BASE)
     M, live, N, K, epi = _draw(g, 256, 6144)
     kernel = str(g.choice(["tile"] + (["decode", "stream"] if M <= 16 else [])))
-    blocks = q6k_random_blocks(N, K // 256, seed=case + 9)
-    xq, a, _ = O.quant_rows_g(O.bf16_to_f32(acts_bf16(M, K, seed=case + 10)), 256)
+    blocks = q6k_random_blocks(N, K // 256, seed=case + 9 + BASE)
+    xq, a, _ = O.quant_rows_g(O.bf16_to_f32(acts_bf16(M, K, seed=case + 10 + BASE)), 256)
     base = g.standard_normal((M, N)).astype(np.float32)
     want = O.w4a8_gemm_q6k(xq, a, O.q6k_repack(blocks), epi=epi, out=None if epi == 0 else base.copy(), live=live)
     w = KW4.repack(GF.KQuant(_t(blocks, dev), GF.GGML_Q6_K, K))
@@ -121,11 +124,11 @@ def test_w4a8_q6k_random(dev, case):
 @pytest.mark.parametrize("case", range(8))
 def test_mxfp4_random(dev, case):
     from prism_amd import mxfp4 as MX
-    g = rng(5000 + case)
+    g = rng(5000 + case + BASE)
     M, live, N, K, _ = _draw(g, 128, 4096)
     kernel = str(g.choice(["tile"] + (["decode"] if M <= 64 else [])))
-    w = weights_f32(N, K, seed=case + 11)
-    x = acts_bf16(M, K, seed=case + 12)
+    w = weights_f32(N, K, seed=case + 11 + BASE)
+    x = acts_bf16(M, K, seed=case + 12 + BASE)
     mw = MX.pack(_t(w, dev), "ocp")
     aq = torch.empty(M, K, dtype=torch.uint8, device=dev)
     asc = torch.empty(M, K // 32, dtype=torch.uint8, device=dev)
