@@ -28,6 +28,16 @@ constexpr int PC_STAGE = 2 * PC_OPER;
 // ((r / 2) % 4, conflict-free over 8 rows only, cost 4 conflict cycles per read, measured).
 __device__ __forceinline__ int pc_swz(int row) { return (row >> 2) & 3; }
 
+// Staged activations of the decode kernel (STG): bytes per LDS row for `bytes` of a row (whole 1 KB pieces, plus 16 so
+// the 16 rows' fragment reads spread over the banks).  Taken from kPcStageRows rows while the image fits kPcStageLds
+// and the grid fits the CUs at once (one workgroup per CU then): 5120^2 / 5120 x 6144 / 3072 x 5120 at 16 rows 9.5 /
+// 12.4 / 9.6 -> 8.5 / 10.2 / 8.4 us.  With more workgroups than CUs (17408 or 27648 x 5120) every round waits for its
+// copy and it measured 20-25% slower; below 8 rows it does not pay.
+__host__ __device__ constexpr int pc_stage_row_bytes(int bytes) { return (bytes + 1023) / 1024 * 1024 + 16; }
+constexpr int kPcStageRows = 8;
+constexpr size_t kPcStageLds = 150 * 1024;
+constexpr int64_t kPcStageGrid = 256;
+
 
 // Epilogue of a wave's 128 x 32 TN outputs at tile rows ml0 .. + 127, columns nl0 .. + 32 TN - 1: y = RN(RN(float(P) sa)
 // sw), stored as bf16 (EPI 0) or added to the fp32 output (EPI 1).  acc[t][u] lane l: row 32 t + l % 32, columns
@@ -369,7 +379,10 @@ int launch_w8a8_pc_panels(const int8_t* a, const float* a_s, int64_t as_sm, cons
 // applies the two roundings.
 // PAN: `a` is the panel copy of pc_act_panel_kernel (lane (lm, q)'s 16 bytes of a chunk at 16 (4 lm + (q ^
 // pc_swz(lm))) of the block's 1 KB), so each activation load is one 1 KB piece.
-template <int G, int MT, bool WPACK, bool WS16, int EPI, bool PAN = false>
+// STG (MT == 1): the workgroup first copies its 16 activation rows over its K range into LDS by LDS-DMA, one 1 KB
+// row piece per instruction (rows pc_stage_row_bytes apart), and the MFMA operands come from there instead of 16
+// rows' 64 bytes per load.
+template <int G, int MT, bool WPACK, bool WS16, int EPI, bool PAN = false, bool STG = false>
 __global__ __launch_bounds__(512) void w8a8_pc_decode_kernel(const int8_t* __restrict__ a,
                                                               const float* __restrict__ a_s, int64_t as_sm,
                                                               const int8_t* __restrict__ w,
@@ -412,15 +425,32 @@ __global__ __launch_bounds__(512) void w8a8_pc_decode_kernel(const int8_t* __res
         const int jj = kc0 + min(j, KC - 1);
 #pragma unroll
         for (int g = 0; g < G; g++) c.w[g] = *reinterpret_cast<const v4i*>(wb[g] + (int64_t)jj * (WPACK ? 1024 : 64));
+        if (!STG) {
 #pragma unroll
-        for (int u = 0; u < MT; u++) c.x[u] = *reinterpret_cast<const v4i*>(ab[u] + (int64_t)jj * (PAN ? 1024 : 64));
+            for (int u = 0; u < MT; u++) c.x[u] = *reinterpret_cast<const v4i*>(ab[u] + (int64_t)jj * (PAN ? 1024 : 64));
+        }
     };
+    const int rowb = STG ? (KC * 64 + 1023) / 1024 * 1024 + 16 : 0;
+    const int8_t* img = reinterpret_cast<const int8_t*>(red + NW * G * MT * 64);
+    if (STG) {
+        static_assert(!STG || MT == 1, "staged activations: one 16-row block");
+        const int pieces = (KC * 64 + 1023) / 1024;
+        for (int row = wv; row < 16; row += NW) {
+            const int8_t* src = a + (int64_t)min(r0 + row, M - 1) * K + (int64_t)kc0 * 64;
+            for (int pc = 0; pc < pieces; pc++)
+                // lanes past the range re-read its last 16 bytes into the row's padding (never read)
+                __builtin_amdgcn_global_load_lds(
+                    src + min(1024 * pc + 16 * lane, KC * 64 - 16),
+                    (__attribute__((address_space(3))) void*)(img + row * rowb + 1024 * pc), 16, 0, 0);
+        }
+    }
     v4i acc[G][MT];
 #pragma unroll
     for (int g = 0; g < G; g++)
 #pragma unroll
         for (int u = 0; u < MT; u++) acc[g][u] = v4i{0, 0, 0, 0};
-    auto mma = [&](const Chunk& c) {
+    auto mma = [&](Chunk& c, int j) {
+        if (STG) c.x[0] = *reinterpret_cast<const v4i*>(img + lm * rowb + min(j, KC - 1) * 64 + 16 * q);
 #pragma unroll
         for (int g = 0; g < G; g++)
 #pragma unroll
@@ -431,11 +461,15 @@ __global__ __launch_bounds__(512) void w8a8_pc_decode_kernel(const int8_t* __res
     Chunk ring[PD];
 #pragma unroll
     for (int d = 0; d < PD; d++) load(wv + NW * d, ring[d]);
+    if (STG) {                                       // the image complete before the first fragment read
+        vm_wait_tracked<0>();
+        __syncthreads();
+    }
     const int full = cnt / PD * PD;
     for (int i0 = 0; i0 < full; i0 += PD) {
 #pragma unroll
         for (int d = 0; d < PD; d++) {
-            mma(ring[d]);
+            mma(ring[d], wv + NW * (i0 + d));
             load(wv + NW * (i0 + d + PD), ring[d]);
             // keep each chunk's MFMAs in place: hoisted across chunks, they would wait for the whole ring
             __builtin_amdgcn_sched_barrier(0);
@@ -443,7 +477,7 @@ __global__ __launch_bounds__(512) void w8a8_pc_decode_kernel(const int8_t* __res
     }
 #pragma unroll
     for (int d = 0; d < PD; d++)
-        if (full + d < cnt) mma(ring[d]);
+        if (full + d < cnt) mma(ring[d], wv + NW * (full + d));
 
 #pragma unroll
     for (int g = 0; g < G; g++)
@@ -503,6 +537,26 @@ int launch_w8a8_pc(int kernel, bool wpack, const int8_t* a, const float* a_s, in
         int nw = min(8, max(1, KP / 4));  // 8 waves (the launch bound), 4 chunks each in flight (16 waves measured slower)
         const size_t lds = (size_t)nw * G * MT * 64 * sizeof(v4i);
         dim3 grid((unsigned)(N / (16 * G)), (unsigned)((M + 16 * MT - 1) / (16 * MT)), (unsigned)split);
+#ifndef PC_STG
+#define PC_STG 1
+#endif
+        const size_t stg = lds + 16 * (size_t)pc_stage_row_bytes((KP + 1) * 64);
+        if (PC_STG && MT == 1 && wpack && epi != 2 && M >= kPcStageRows && stg <= kPcStageLds &&
+            (int64_t)grid.x * grid.y * grid.z <= kPcStageGrid) {
+#define PDS(GV, W16, E)                                                                                            \
+    do {                                                                                                           \
+        allow_lds(w8a8_pc_decode_kernel<GV, 1, true, W16, E, false, true>, stg);                                   \
+        hipLaunchKernelGGL((w8a8_pc_decode_kernel<GV, 1, true, W16, E, false, true>), grid, dim3(64 * nw), stg, st, a, \
+                           a_s, as_sm, w, w_s, out, ldo, n_rows, M, N, K, zstride);                                \
+    } while (0)
+#define PDS_G(W16, E) do { if (G == 2) PDS(2, W16, E); else PDS(1, W16, E); } while (0)
+            if (ws16) { if (epi == 0) PDS_G(true, 0); else PDS_G(true, 1); }
+            else { if (epi == 0) PDS_G(false, 0); else PDS_G(false, 1); }
+#undef PDS_G
+#undef PDS
+            PRISM_LAUNCH_CHECK();
+            return PRISM_OK;
+        }
 #define PDL(GV, MTV, WP, W16, E)                                                                                   \
     hipLaunchKernelGGL((w8a8_pc_decode_kernel<GV, MTV, WP, W16, E>), grid, dim3(64 * nw), lds, st, a, a_s, as_sm, w, \
                        w_s, out, ldo, n_rows, M, N, K, zstride)
@@ -633,6 +687,18 @@ int launch_w8a8_pc_split(const int8_t* a, const float* a_s, int64_t as_sm, const
                            dim3(256), 0, st, a, pan, M, K);
         PRISM_LAUNCH_CHECK();
     }
+    const size_t stg = lds + 16 * (size_t)pc_stage_row_bytes((KP + 1) * 64);
+    if (PC_STG && MT == 1 && !pan && M >= kPcStageRows && stg <= kPcStageLds &&
+        (int64_t)grid.x * grid.y * grid.z <= kPcStageGrid) {
+#define PSS(GV)                                                                                                    \
+    do {                                                                                                           \
+        allow_lds(w8a8_pc_decode_kernel<GV, 1, true, false, 2, false, true>, stg);                                 \
+        hipLaunchKernelGGL((w8a8_pc_decode_kernel<GV, 1, true, false, 2, false, true>), grid, dim3(64 * nw), stg, st, \
+                           a, a_s, as_sm, w, w_s, slots, (int64_t)N, n_rows, M, N, K, zstride);                    \
+    } while (0)
+        if (G == 4) PSS(4); else if (G == 2) PSS(2); else PSS(1);
+#undef PSS
+    } else {
 #define PSL(GV, MTV)                                                                                               \
     do {                                                                                                           \
         if (pan)                                                                                                   \
@@ -649,6 +715,7 @@ int launch_w8a8_pc_split(const int8_t* a, const float* a_s, int64_t as_sm, const
     if (G == 4) PSL_MT(4); else if (G == 2) PSL_MT(2); else PSL_MT(1);
 #undef PSL_MT
 #undef PSL
+    }
     PRISM_LAUNCH_CHECK();
     dim3 fgrid((unsigned)((N / 4 + 255) / 256), (unsigned)M);
 #define PFL(W16, E) hipLaunchKernelGGL((pc_fold_kernel<W16, E>), fgrid, dim3(256), 0, st, slots, zstride, kPcSplit, a_s, \

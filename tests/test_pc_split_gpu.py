@@ -99,3 +99,26 @@ def test_split_refuses_large_m(dev):
     KW.gemm(_t(a, dev), _t(sa, dev), pw, None, out, n, K, epi=0)
     torch.cuda.synchronize()
     assert np.array_equal(_bits(out), O.w8a8_gemm(a, sa, wq, ws, K, epi=0, nthreads=16))
+
+
+@pytest.mark.parametrize("M,N,K,live,kernel", [(16, 5120, 5120, 16, "decode"), (8, 3072, 9216, 8, "decode"),
+                                               (12, 5120, 17408, 9, "split"), (16, 1040, 1600, 16, "decode"),
+                                               (7, 512, 4096, 7, "decode"), (16, 5120, 6144, 13, "split")])
+def test_staged_decode_bit_exact(dev, M, N, K, live, kernel):
+    """The decode kernel with its activation rows staged in LDS (8-16 rows, a grid within the CUs; K not a multiple
+    of the 1 KB row piece included), unsplit and split, against the oracle; 7 rows take the unstaged form."""
+    from prism_amd import w8a8 as KW
+    a, sa, wq, ws, pw = _case(M, N, K, 900 + M + N % 991, dev)
+    want0 = O.w8a8_gemm(a, sa, wq, ws, K, epi=0, live=live, nthreads=16)
+    base = rng(M + N).standard_normal((M, N)).astype(np.float32)
+    want1 = O.w8a8_gemm(a, sa, wq, ws, K, epi=1, out=base.copy(), live=live, nthreads=16)
+    ad, sad = _t(a, dev), _t(sa, dev)
+    n = torch.tensor([live], dtype=torch.int32, device=dev)
+    out = torch.full((M, N), 7, dtype=torch.int16, device=dev).view(torch.bfloat16)
+    KW.gemm(ad, sad, pw, None, out, n, K, epi=0, kernel=kernel)
+    h = _t(base, dev)
+    KW.gemm(ad, sad, pw, None, h, n, K, epi=1, kernel=kernel)
+    torch.cuda.synchronize()
+    got = _bits(out)
+    assert np.array_equal(got[:live], want0[:live]) and (got[live:] == 7).all()
+    assert np.array_equal(h.cpu().numpy(), want1)
