@@ -363,6 +363,21 @@ PRISM_API int prism_mxfp4_quant_act(const void* x, int x_f32, int64_t ldx, const
 PRISM_API int prism_mxfp4_gemm(const uint8_t* aq, const uint8_t* as, int a_fmt, const uint8_t* wq, const uint8_t* ws,
                                void* out, int64_t ldo, const int32_t* n_rows, int64_t M, int64_t N, int64_t K,
                                int epi, int kernel, void* stream);
+/*
+ * prism_mxfp4_gemm with a workspace (the same arguments and bits; no counterpart in the reference, whose gemm is one
+ * Triton launch): kernel 2, the split decode (M <= 16, a_fmt PRISM_MX_E4M3), spreads the projection's (1024-input
+ * segment, 16-row weight tile) units over up to 256 workgroups in segment-major order, so each workgroup copies only
+ * one or two segments of the activation rows; the segment sums go to `work` and a second launch on the stream adds
+ * each tile's sums left to right, as every kernel does.  kernel -1 takes it where it measured faster than the staged
+ * decode and `work` is given.  work: device memory of at least prism_mxfp4_split_workspace_bytes(N, K) bytes,
+ * 16-byte aligned, rewritten by every launch, or NULL.  Calls that overlap on one GPU must not share work.
+ */
+PRISM_API int prism_mxfp4_gemm_ws(const uint8_t* aq, const uint8_t* as, int a_fmt, const uint8_t* wq,
+                                  const uint8_t* ws, void* out, int64_t ldo, const int32_t* n_rows, int64_t M,
+                                  int64_t N, int64_t K, int epi, int kernel, void* work, int64_t work_bytes,
+                                  void* stream);
+/* Bytes of work the split decode needs for an N x K projection; 0 for shapes it does not take. */
+PRISM_API int64_t prism_mxfp4_split_workspace_bytes(int64_t N, int64_t K);
 
 /*
  * Peak probes (measurement tooling: the reference's bench/csrc/mma_peak.cu:14-70 and bench/csrc/l2_bw.cu:8 for

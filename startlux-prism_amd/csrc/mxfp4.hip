@@ -772,6 +772,124 @@ __global__ __launch_bounds__(1024) void mx_decode_staged_kernel(const uint8_t* _
     if (w < NTG && r < live) mx_store<EPI>(out, ldo, r, 16 * (blockIdx.x * NTG + w) + 4 * p, y);
 }
 
+// ---------------------------------------------------------------------------- decode kernel, segments split
+// e4m3 activations, M <= 16, over a balanced grid.  The projection's work is its (1024-input segment s, 16-row
+// weight tile t) units, u = s T + t (segment-major); W workgroups take equal contiguous ranges, so a workgroup's
+// units mostly share one segment (at most two when a range is no longer than T), and it copies only those segments'
+// 16 activation rows into LDS (1 KB row DMAs) where the tile-major staged kernel copies all of K per pair of tiles.
+// One wave per unit: the segment's weights into registers, the same MFMA chain from zero as every kernel, its fp32
+// segment sums to the workspace `part` [nseg][T][64] (v4f per lane); mx_split_fold_kernel, launched next on the
+// stream, adds each tile's segment sums left to right, as every kernel does, and stores.  (The sums handed between
+// workgroups inside one launch measured slower: they must pass the XCDs' L2s, through write-through stores or a
+// cache write-back per hand-over.)  With one segment (K <= 1024) the split kernel stores the outputs itself.
+constexpr int kMxSplitWG = 256;                  // workgroups (CUs)
+constexpr int kMxSplitWaves = 16;                // waves per workgroup at most (more units loop)
+
+template <int EPI>
+__global__ __launch_bounds__(1024) void mx_decode_split_kernel(const uint8_t* __restrict__ aq,
+                                                               const uint8_t* __restrict__ as,
+                                                               const uint8_t* __restrict__ wq,
+                                                               const uint8_t* __restrict__ ws,
+                                                               void* __restrict__ out, int64_t ldo,
+                                                               const int32_t* __restrict__ n_rows, int M, int K,
+                                                               int T, v4f* __restrict__ part) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    uint8_t* act = lds;                                  // [2][16][kDecRow]
+    uint8_t* asl = lds + 2 * kDecActSlot;                // [2][16][32]
+    kernel_args_now(aq, as, wq, ws, out, ldo, n_rows, M, K, T, part);
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, NWV = blockDim.x >> 6;
+    const int W = gridDim.x, v = blockIdx.x;
+    const int KS = K / kMxStep, nseg = (KS + kMxSegSteps - 1) / kMxSegSteps;
+    const int64_t U = (int64_t)nseg * T;
+    const int u0 = (int)(U * v / W), u1 = (int)(U * (v + 1) / W);
+    const int sA = u0 / T, nsl = (u1 - 1) / T - sA + 1;  // segments of the range (1 or 2: ranges of at most T units)
+    const int p = lane >> 4, r = lane & 15;
+
+    v4u wr[kMxSegSteps];
+    uint32_t wsc[kMxSegSteps];
+    auto load = [&](int u) {
+        const int s = u / T, t = u - s * T;
+        const int s0 = s * kMxSegSteps;
+#pragma unroll
+        for (int j = 0; j < kMxSegSteps; j++) {
+            const int st = min(s0 + j, KS - 1);
+            wr[j] = reinterpret_cast<const v4u*>(wq)[((int64_t)t * KS + st) * 64 + lane];
+            wsc[j] = ws[((int64_t)t * KS + st) * 64 + lane];
+        }
+    };
+    int u = u0 + wv;
+    if (u < u1) load(u);                               // the weight requests first
+    // the range's activation segments: 16 rows x 1 KB each (one DMA per row), their scale bytes (16 rows x 32)
+    for (int c = wv; c < 16 * nsl; c += NWV) {
+        const int sl = c >> 4, row = c & 15;
+        const int s0 = (sA + sl) * kMxSegSteps, ns = min(kMxSegSteps, KS - s0);
+        // a short last segment: lanes past its end re-read its last 16 bytes (never used)
+        const uint8_t* src = aq + (int64_t)min(row, M - 1) * K + (int64_t)s0 * kMxStep + min(16 * lane, ns * kMxStep - 16);
+        __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(act + sl * kDecActSlot + row * kDecRow),
+                                         16, 0, 0);
+    }
+    for (int c = wv; c < 2 * nsl; c += NWV) {          // lane L covers row 8 h + L / 8, bytes 4 (L % 8) .. + 3
+        const int sl = c >> 1, h = c & 1;
+        const int s0 = (sA + sl) * kMxSegSteps, ns = min(kMxSegSteps, KS - s0);
+        const int row = 8 * h + (lane >> 3);
+        const uint8_t* src = as + (int64_t)min(row, M - 1) * (K / 32) + s0 * 4 + min(4 * (lane & 7), 4 * ns - 4);
+        __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(asl + sl * kDecScaleSlot + h * 256),
+                                         4, 0, 0);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    lds_barrier();
+    for (; u < u1; u += NWV) {
+        const int s = u / T, t = u - s * T;
+        const int sl = s - sA, ns = min(kMxSegSteps, KS - s * kMxSegSteps);
+        const uint8_t* slot = act + sl * kDecActSlot + r * kDecRow + 16 * p;
+        const uint8_t* sslot = asl + sl * kDecScaleSlot + r * 32 + p;
+        v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < kMxSegSteps; j++) {
+            if (j < ns) {
+                const v4i lo = *reinterpret_cast<const v4i*>(slot + 128 * j);
+                const v4i hi = *reinterpret_cast<const v4i*>(slot + 128 * j + 64);
+                const uint32_t sc = sslot[4 * j];
+                const v4i wi = {(int)wr[j].x, (int)wr[j].y, (int)wr[j].z, (int)wr[j].w};
+                acc = mx_mfma<0>(wi, v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w}, acc, wsc[j], sc);
+            }
+        }
+        if (u + NWV < u1) load(u + NWV);
+        if (nseg > 1) {
+            part[((int64_t)s * T + t) * 64 + lane] = acc;
+        } else {
+            const int live = n_rows ? min(M, __ldg(n_rows)) : M;
+            if (r < live) mx_store<EPI>(out, ldo, r, 16 * t + 4 * p, acc);
+        }
+    }
+}
+
+// The split decode's second launch: one wave per 16-row tile adds its nseg segment sums left to right and stores.
+template <int EPI>
+__global__ __launch_bounds__(256) void mx_split_fold_kernel(const v4f* __restrict__ part, void* __restrict__ out,
+                                                           int64_t ldo, const int32_t* __restrict__ n_rows, int M,
+                                                           int T, int nseg) {
+    const int lane = threadIdx.x & 63, t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= T) return;
+    v4f y = part[(int64_t)t * 64 + lane];
+    for (int i0 = 1; i0 < nseg; i0 += 4) {
+        v4f z[4];                                        // four segments' sums in flight at once
+#pragma unroll
+        for (int i = 0; i < 4; i++) z[i] = part[((int64_t)min(i0 + i, nseg - 1) * T + t) * 64 + lane];
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if (i0 + i < nseg) y = v4f{add_rn(y.x, z[i].x), add_rn(y.y, z[i].y), add_rn(y.z, z[i].z), add_rn(y.w, z[i].w)};
+    }
+    const int live = n_rows ? min(M, __ldg(n_rows)) : M;
+    const int p = lane >> 4, r = lane & 15;
+    if (r < live) mx_store<EPI>(out, ldo, r, 16 * t + 4 * p, y);
+}
+
+int64_t mx_split_workspace_bytes(int64_t N, int64_t K) {     // 1 KB of segment sums per unit
+    const int64_t T = N / 16, nseg = (K / kMxStep + kMxSegSteps - 1) / kMxSegSteps;
+    return nseg > 1 ? nseg * T * 1024 : 16;
+}
+
 static size_t mx_decode_lds(int MT, int K) {
     const int nseg = (K / kMxStep + kMxSegSteps - 1) / kMxSegSteps;
     return (size_t)nseg * MT * 64 * sizeof(v4f);
@@ -834,9 +952,10 @@ extern "C" int prism_mxfp4_quant_act(const void* x, int x_f32, int64_t ldx, cons
     return PRISM_OK;
 }
 
-extern "C" int prism_mxfp4_gemm(const uint8_t* aq, const uint8_t* as, int a_fmt, const uint8_t* wq,
-                                const uint8_t* ws, void* out, int64_t ldo, const int32_t* n_rows, int64_t M,
-                                int64_t N, int64_t K, int epi, int kernel, void* stream) {
+extern "C" int prism_mxfp4_gemm_ws(const uint8_t* aq, const uint8_t* as, int a_fmt, const uint8_t* wq,
+                                   const uint8_t* ws, void* out, int64_t ldo, const int32_t* n_rows, int64_t M,
+                                   int64_t N, int64_t K, int epi, int kernel, void* work, int64_t work_bytes,
+                                   void* stream) {
     if (!aq || !as || !wq || !ws || !out) return PRISM_ERR_ARG;
     if (a_fmt != PRISM_MX_E4M3 && a_fmt != PRISM_MX_E2M1 && a_fmt != PRISM_MX_E4M3_PANELS) return PRISM_ERR_ARG;
     if (epi != 0 && epi != 1) return PRISM_ERR_ARG;
@@ -848,11 +967,36 @@ extern "C" int prism_mxfp4_gemm(const uint8_t* aq, const uint8_t* as, int a_fmt,
     hipStream_t st = (hipStream_t)stream;
     const int MT = (int)((M + 15) / 16);
     if (a_fmt == PRISM_MX_E4M3_PANELS) {                 // the direct-weight tile kernel only
-        if (kernel == 1 || (int64_t)N * K / 2 >= (1LL << 31)) return PRISM_ERR_SHAPE;
+        if (kernel == 1 || kernel == 2 || (int64_t)N * K / 2 >= (1LL << 31)) return PRISM_ERR_SHAPE;
         kernel = 0;
     }
+    // the split decode: one 16-row block of e4m3 rows, its workspace, ranges of at most T units (two segments)
+    const int64_t T = N / 16, nseg = (K / kMxStep + kMxSegSteps - 1) / kMxSegSteps, U = nseg * T;
+    const int64_t need = mx_split_workspace_bytes(N, K);
+    const bool split_ok = MT == 1 && a_fmt == PRISM_MX_E4M3 && work && need > 0 && work_bytes >= need &&
+                          PRISM_ALIGNED(work, 16) && (U + kMxSplitWG - 1) / kMxSplitWG <= T && U < (1 << 30);
+    if (kernel == 2 && !split_ok) return !work ? PRISM_ERR_ARG : !PRISM_ALIGNED(work, 16) ? PRISM_ERR_ALIGN : PRISM_ERR_SHAPE;
+    // measured against the staged decode at 1-16 rows: 15.8-16.0 against 17.3-18.8 us at 17408 x 5120, 16.9
+    // against 18.2-20.6 at 5120 x 17408, 21.5-21.7 against 23.5-25.6 at 27648 x 5120; slower below about 80 M weights
+    // (its second launch costs about 2.5 us: 8.5 against 6.7-7.3 us at 5120^2, 14.0 against 11.4 at 8192^2)
+    if (kernel < 0 && split_ok && N * K >= (80LL << 20)) kernel = 2;
     if (kernel < 0) kernel = (MT <= 4 && mx_decode_lds(MT, (int)K) <= 64 * 1024) ? 1 : 0;
-    if (kernel == 1 && MT == 1 && a_fmt == PRISM_MX_E4M3) {
+    if (kernel == 2) {
+        const int W = (int)std::min<int64_t>(kMxSplitWG, U);
+        const int nw = (int)std::min<int64_t>(kMxSplitWaves, (U + W - 1) / W);
+        const size_t lds = 2 * (size_t)(kDecActSlot + kDecScaleSlot);
+        auto* part = static_cast<v4f*>(work);
+#define DSP(E)                                                                                                       \
+    do {                                                                                                             \
+        hipLaunchKernelGGL((mx_decode_split_kernel<E>), dim3(W), dim3(64 * nw), lds, st, aq, as, wq, ws, out, ldo,   \
+                           n_rows, (int)M, (int)K, (int)T, part);                                                    \
+        if (nseg > 1)                                                                                                \
+            hipLaunchKernelGGL((mx_split_fold_kernel<E>), dim3((unsigned)((T + 3) / 4)), dim3(256), 0, st, part, out, \
+                               ldo, n_rows, (int)M, (int)T, (int)nseg);                                              \
+    } while (0)
+        if (epi) DSP(1); else DSP(0);
+#undef DSP
+    } else if (kernel == 1 && MT == 1 && a_fmt == PRISM_MX_E4M3) {
         const int nseg = (int)((K / kMxStep + kMxSegSteps - 1) / kMxSegSteps);
         const int ntg = (N % 32 == 0) ? 2 : 1;     // two weight tiles share each staged activation copy
         const int sl = min(nseg, 8);        // 8 segment lanes: 154 KB of LDS at NTG 2
@@ -930,4 +1074,15 @@ extern "C" int prism_mxfp4_gemm(const uint8_t* aq, const uint8_t* as, int a_fmt,
     }
     PRISM_LAUNCH_CHECK();
     return PRISM_OK;
+}
+
+extern "C" int prism_mxfp4_gemm(const uint8_t* aq, const uint8_t* as, int a_fmt, const uint8_t* wq,
+                                const uint8_t* ws, void* out, int64_t ldo, const int32_t* n_rows, int64_t M,
+                                int64_t N, int64_t K, int epi, int kernel, void* stream) {
+    return prism_mxfp4_gemm_ws(aq, as, a_fmt, wq, ws, out, ldo, n_rows, M, N, K, epi, kernel, nullptr, 0, stream);
+}
+
+extern "C" int64_t prism_mxfp4_split_workspace_bytes(int64_t N, int64_t K) {
+    if (N <= 0 || K <= 0 || N % 16 || K % kMxStep) return 0;
+    return mx_split_workspace_bytes(N, K);
 }

@@ -52,6 +52,8 @@ _SIGS = {
     "prism_probe_mfma_ops": (_i64, [_int]),
     "prism_probe_read": (_int, [_p, _i64, _i64, _p, _p]),
     "prism_mxfp4_gemm": (_int, [_p, _p, _int, _p, _p, _p, _i64, _p, _i64, _i64, _i64, _int, _int, _p]),
+    "prism_mxfp4_gemm_ws": (_int, [_p, _p, _int, _p, _p, _p, _i64, _p, _i64, _i64, _i64, _int, _int, _p, _i64, _p]),
+    "prism_mxfp4_split_workspace_bytes": (_i64, [_i64, _i64]),
 }
 
 _lib = None

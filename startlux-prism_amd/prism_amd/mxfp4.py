@@ -23,7 +23,23 @@ from . import _lib as L
 QK = 32
 E4M3, E4M3_PANELS, E2M1 = 0, 1, 4
 MODES = {"max": 0, "mse": 1, "ocp": 2}
-KERNELS = {"auto": -1, "tile": 0, "decode": 1}
+KERNELS = {"auto": -1, "tile": 0, "decode": 1, "split": 2}
+SPLIT_WS_BYTES = 32 << 20     # the split decode's segment sums: 1 KB per (1024-input segment, 16-row tile)
+_WS = {}
+
+
+def split_workspace(dev):
+    """The per-device workspace of the split decode (kernel "split"): its segment sums, rewritten by every launch.
+    None while a graph is being captured on a device that has none yet: "auto" then picks another kernel and
+    "split" raises."""
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    ws = _WS.get(idx)
+    if ws is None:
+        if torch.cuda.is_current_stream_capturing():
+            return None
+        ws = torch.empty(SPLIT_WS_BYTES, dtype=torch.uint8, device=torch.device("cuda", idx))
+        _WS[idx] = ws
+    return ws
 
 
 class MX4(NamedTuple):
@@ -192,8 +208,12 @@ def gemm(a_q, a_s, w: MX4, out, n_rows, epi=0, out_stride=None, kernel="auto"):
     if epi == 0 and out.dtype != torch.bfloat16 or epi == 1 and out.dtype != torch.float32:
         raise ValueError("mxfp4.gemm: epi 0 writes bf16, epi 1 adds into fp32")
     ldo = out.stride(0) if out_stride is None else out_stride
-    L.call("prism_mxfp4_gemm", L.ptr(a_q), L.ptr(a_s), fmt, L.ptr(w.q), L.ptr(w.s), L.ptr(out), ldo, L.ptr(live), M,
-           N, K, epi, KERNELS[kernel], L.stream_of(a_q))
+    ws = split_workspace(a_q.device) if fmt == E4M3 and M <= 16 and kernel in ("auto", "split") else None
+    if kernel == "split" and ws is None:
+        raise L.PrismError('kernel "split" needs the device workspace, made outside graph capture: run one eager call '
+                           'first')
+    L.call("prism_mxfp4_gemm_ws", L.ptr(a_q), L.ptr(a_s), fmt, L.ptr(w.q), L.ptr(w.s), L.ptr(out), ldo, L.ptr(live),
+           M, N, K, epi, KERNELS[kernel], L.ptr(ws), 0 if ws is None else ws.numel(), L.stream_of(a_q))
 
 
 def cutlass_enabled():

@@ -82,6 +82,22 @@ def test_mxfp4_gemm_checks(lib):
     assert call(M=0) == OK
 
 
+def test_mxfp4_split_checks(lib):
+    f = lib.prism_mxfp4_gemm_ws
+
+    def call(fmt=0, M=16, N=64, K=2048, kernel=2, work=P, work_bytes=1 << 20):
+        return f(P, P, fmt, P, P, P, N, P, M, N, K, 0, kernel, work, work_bytes, None)
+    assert call(work=None, work_bytes=0) == ARG     # the split decode needs its workspace
+    assert call(work_bytes=1024) == SHAPE           # 2 segments x 4 tiles x 1 KB
+    assert call(M=17) == SHAPE                      # one 16-row block
+    assert call(fmt=4) == SHAPE                     # e4m3 row-major activations only
+    assert call(fmt=1) == SHAPE                     # panels: the tile kernel only
+    assert call(work=U) == ALIGN                    # 16-byte aligned segment sums
+    assert call(M=0) == OK
+    b = lib.prism_mxfp4_split_workspace_bytes
+    assert b(5120, 5120) == 5 * 320 * 1024 and b(64, 1024) == 16 and b(60, 128) == 0 and b(64, 192) == 0
+
+
 def test_mxfp4_quant_act_checks(lib):
     f = lib.prism_mxfp4_quant_act
     assert f(P, 0, 256, None, P, P, None, 16, 256, 2, None) == ARG            # fmt

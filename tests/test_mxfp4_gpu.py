@@ -249,10 +249,11 @@ def test_one_order_on_order_sensitive_data(dev, M, N, K, live):
     wq, ws = (t.cpu().numpy() for t in MX.to_rows(m))
     y, ya = O.mx_gemm(q.cpu().numpy(), s.cpu().numpy(), wq, ws)
     zero = np.zeros((M, N), dtype=np.float32)
-    got = {k: _run(dev, q, s, m, M, N, 1, k, live=live, out0=zero) for k in ("tile", "decode")}
+    kernels = ("tile", "decode", "split") if M <= 16 else ("tile", "decode")
+    got = {k: _run(dev, q, s, m, M, N, 1, k, live=live, out0=zero) for k in kernels}
     for k in got:
         _check(got[k], y, ya, live, 1, zero)
-    assert torch.equal(got["tile"][:live], got["decode"][:live])
+        assert torch.equal(got["tile"][:live], got[k][:live]), k
     g = got["tile"][:live].cpu().numpy()
     assert (g != y[:live].astype(np.float32)).any(), "operands too tame: every fp32 sum was exact"
 
@@ -302,3 +303,49 @@ def test_gemm_panels_equal_rows(dev, M, N, K, live):
         assert torch.equal(outs[0].view(torch.int32 if epi else torch.int16), outs[1].view(torch.int32 if epi else torch.int16))
     with pytest.raises(ValueError):
         MX.gemm(qp, sp, m, outs[1], n, epi=1, kernel="decode")
+
+
+@pytest.mark.parametrize("M,N,K,live", [(16, 512, 17408, 11), (5, 256, 1152, 4), (1, 64, 128, 1),
+                                        (16, 48, 4224, 16), (13, 1024, 9216, 13), (16, 4096, 1024, 16),
+                                        (2, 17408, 5120, 2)])
+def test_split_decode_equals_tile(dev, M, N, K, live):
+    """The split decode (segment-major units over the grid, the segment sums added by a second launch) gives the
+    tile kernel's bits, both epilogues, with live rows: one segment (K <= 1024, no second launch), a short last
+    segment (K 4224), ranges spanning two segments, and more units than 16 waves per workgroup take (17408 x 5120:
+    5440 units on 256 workgroups, the shape "auto" sends to it)."""
+    from prism_amd import mxfp4 as MX
+    m = _mx(dev, weights_f32(N, K, seed=N + K))
+    q, s = _acts(dev, acts_bf16(M, K, seed=M + K), "e4m3")
+    n = torch.tensor([live], dtype=torch.int32, device=dev)
+    base = rng(M + 2).standard_normal((M, N)).astype(np.float32)
+    for epi in (0, 1):
+        outs = []
+        for kern in ("tile", "split", "split", "auto"):     # twice: the workspace is rewritten, not accumulated
+            out = (torch.full((M, N), 7, dtype=torch.int16, device=dev).view(torch.bfloat16) if epi == 0
+                   else torch.from_numpy(base).to(dev).clone())
+            MX.gemm(q, s, m, out, n, epi=epi, kernel=kern)
+            outs.append(out)
+        torch.cuda.synchronize()
+        for o in outs[1:]:
+            assert torch.equal(o, outs[0])
+
+
+def test_split_decode_graph_replay(dev):
+    """The split decode's two launches captured in a graph: every replay, with eager work between, equals eager."""
+    from prism_amd import mxfp4 as MX
+    M, N, K = 16, 1024, 5120
+    m = _mx(dev, weights_f32(N, K, seed=11))
+    q, s = _acts(dev, acts_bf16(M, K, seed=12), "e4m3")
+    ref = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    MX.gemm(q, s, m, ref, M, kernel="split")          # eager first: the workspace exists before capture
+    out = torch.empty_like(ref)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        MX.gemm(q, s, m, out, M, kernel="split")
+    other = torch.empty_like(ref)
+    for _ in range(3):
+        out.fill_(0)
+        g.replay()
+        MX.gemm(q, s, m, other, M, kernel="tile")
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref) and torch.equal(other, ref)
