@@ -335,25 +335,19 @@ __global__ __launch_bounds__(NW * 64) void w4a8_q4k_stream_kernel(const int8_t* 
         const int64_t shi = q == 0 ? ((int64_t)(uint32_t)c.s[2] | ((int64_t)(uint32_t)c.s[3] << 32)) : 0;
 #pragma unroll
         for (int g = 0; g < TG; g++) {
-            float d, dm;
-            int sc[8], mn[8];
-            row_meta(c.mt[g], d, dm, sc, mn);             // this lane's weight row lm of tile g
+            // this lane's weight row lm of tile g: d, dmin and its four sub-blocks' split scales
+            const float d = f16_to_f32(c.mt[g][0] & 0xffffu), dm = f16_to_f32(c.mt[g][0] >> 16);
+            uint32_t sp[4];
+            q4k_lane_splits(c.mt[g], q >> 1, sp);
             v4i alo = {0, 0, 0, 0}, ahi = {0, 0, 0, 0};
 #pragma unroll
             for (int p = 0; p < 4; p++) {
                 v4i wl, wh;
-                const int j2 = 2 * p + (q >> 1);
-                int scg = sc[0];
-#pragma unroll
-                for (int j = 1; j < 8; j++) scg = j2 == j ? sc[j] : scg;
-                two_plane(c.w[g][p >> 1][2 * (p & 1)], c.w[g][p >> 1][2 * (p & 1) + 1], split_scale(scg), wl, wh);
+                two_plane(c.w[g][p >> 1][2 * (p & 1)], c.w[g][p >> 1][2 * (p & 1) + 1], sp[p], wl, wh);
                 alo = __builtin_amdgcn_mfma_i32_16x16x64_i8(wl, c.x[p], alo, 0, 0, 0);
                 ahi = __builtin_amdgcn_mfma_i32_16x16x64_i8(wh, c.x[p], ahi, 0, 0, 0);
             }
-            const int64_t mn8 =
-                q == 0 ? (int64_t)(uint32_t)(mn[0] | (mn[1] << 8) | (mn[2] << 16) | (mn[3] << 24)) |
-                             ((int64_t)(uint32_t)(mn[4] | (mn[5] << 8) | (mn[6] << 16) | (mn[7] << 24)) << 32)
-                       : 0;
+            const int64_t mn8 = q == 0 ? q4k_mins8(c.mt[g]) : 0;
             const v4i mins = mins_mfma(mn8, slo, shi);
             v4f t;
 #pragma unroll
@@ -873,12 +867,12 @@ extern "C" int prism_w4a8_q4k_gemm(const int8_t* xq, const float* a, int64_t a_s
         return PRISM_ERR_ALIGN;
     if (kernel < -1 || kernel > 2) return PRISM_ERR_ARG;
     const bool can_bal = q4k_bal_fits(M, N, K) && workspace && workspace_bytes >= q4k_bal_workspace_bytes(N);
-    // by default up to 4 rows: the balanced kernel for projections of fewer than two 16-row tiles per CU (where a
-    // tile per workgroup leaves CUs with one tile more than others: 5120 x 17408 at 1 row 15.96 us against
-    // 18.73 us), given its workspace; the per-tile kernel otherwise (13824 x 5120: 12.9 us against 16.0 us) and from
-    // 5 rows, where it takes two tiles per workgroup (5120^2 at 16 rows 8.9 against 9.9 us); the tile kernel beyond 16
-    // rows.  The MI355X table overrides this per shape.
-    if (kernel == -1) kernel = M >= 1 && M <= 16 ? (can_bal && N / 16 < 512 && M <= 4 ? 2 : 1) : 0;
+    // by default up to 4 rows: the balanced kernel for long projections of fewer than two 16-row tiles per CU (where
+    // a tile per workgroup leaves CUs with one tile more than others: 5120 x 17408 at 1 row 15.1 us against 18.4 us),
+    // given its workspace; the per-tile kernel otherwise (13824 x 5120: 11.4 against 15.4 us; 5120^2 at 1-4 rows
+    // 7.5-8.0 against 8.2-8.8 us) and from 5 rows, where it takes two tiles per workgroup (5120^2 at 16 rows 8.9
+    // against 9.9 us); the tile kernel beyond 16 rows.  The MI355X table overrides this per shape.
+    if (kernel == -1) kernel = M >= 1 && M <= 16 ? (can_bal && N / 16 < 512 && K >= 8192 && M <= 4 ? 2 : 1) : 0;
     if (kernel == 1 && M > 16) return PRISM_ERR_ARG;
     if (kernel == 2 && !can_bal) return M > 16 || !q4k_bal_fits(M, N, K) ? PRISM_ERR_SHAPE : PRISM_ERR_ARG;
     if (M == 0) return PRISM_OK;

@@ -55,6 +55,26 @@ __device__ __forceinline__ void row_meta(v4u m, float& d, float& dm, int* sc, in
     }
 }
 
+// The split scales (split_scale) of the four sub-blocks a lane's MFMA operands take, 2 p + h for p = 0..3 (h, the
+// lane's 32-input half of each 64-input piece), read straight from the row's GGUF packing (get_scale_min_k4 as in
+// row_meta: sub-block j < 4 is bits 8 j .. 8 j + 5 of m[1]; j >= 4 is bits 8 (j - 4) .. + 3 of m[3] with bits
+// 8 (j - 4) + 6 .. + 7 of m[1] above them), with no unpacking of the other twelve values and no per-lane select.
+__device__ __forceinline__ void q4k_lane_splits(v4u m, int h, uint32_t* sp) {
+    const uint32_t s = m[1] >> (8 * h), c = m[3] >> (8 * h);
+    sp[0] = (s & 7) | (((s >> 3) & 7) << 16);
+    sp[1] = ((s >> 16) & 7) | (((s >> 19) & 7) << 16);
+    sp[2] = (c & 7) | ((((c >> 3) & 1) | (((s >> 6) & 3) << 1)) << 16);
+    sp[3] = ((c >> 16) & 7) | ((((c >> 19) & 1) | (((s >> 22) & 3) << 1)) << 16);
+}
+
+// The row's eight mins as the bytes of the mins MFMA operand (mins_mfma), from the same packing: mins 0..3 are the
+// low six bits of m[2]'s bytes, mins 4..7 the high nibbles of m[3]'s bytes with m[2]'s top two bits above them.
+__device__ __forceinline__ int64_t q4k_mins8(v4u m) {
+    const uint32_t lo = m[2] & 0x3f3f3f3fu;
+    const uint32_t hi = ((m[3] >> 4) & 0x0f0f0f0fu) | ((m[2] >> 2) & 0x30303030u);
+    return (int64_t)lo | ((int64_t)hi << 32);
+}
+
 // t = RN(d float(acc)); t = fma(-dm, float(mins), t)   (kernels/w4a8.py:191)
 __device__ __forceinline__ float q4k_term(float d, float dm, int acc, int mins) {
     return fmaf(-dm, (float)mins, mul_rn(d, (float)acc));

@@ -93,27 +93,20 @@ __global__ __launch_bounds__((NW + (MX * 16 + 63) / 64) * 64) void w4a8_q4k_bal_
                     const Round rd = walk.round(rho);
                     const Unit& u = ring[d];
                     const int b = min(rd.p0 + wv, NB - 1);
-                    float dd, dm;
-                    int sc[8], mn[8];
-                    row_meta(u.mt, dd, dm, sc, mn);
+                    const float dd = f16_to_f32(u.mt[0] & 0xffffu), dm = f16_to_f32(u.mt[0] >> 16);
+                    uint32_t sp[4];
+                    q4k_lane_splits(u.mt, q >> 1, sp);
                     v4i alo = {0, 0, 0, 0}, ahi = {0, 0, 0, 0};
 #pragma unroll
                     for (int p = 0; p < 4; p++) {
                         v4i wl, wh;
-                        const int g = 2 * p + (q >> 1);
-                        int scg = sc[0];
-#pragma unroll
-                        for (int j = 1; j < 8; j++) scg = g == j ? sc[j] : scg;
-                        two_plane(u.w[p >> 1][2 * (p & 1)], u.w[p >> 1][2 * (p & 1) + 1], split_scale(scg), wl, wh);
+                        two_plane(u.w[p >> 1][2 * (p & 1)], u.w[p >> 1][2 * (p & 1) + 1], sp[p], wl, wh);
                         const v4i x = *reinterpret_cast<const v4i*>(xrow + b * 256 + 64 * p);
                         alo = __builtin_amdgcn_mfma_i32_16x16x64_i8(wl, x, alo, 0, 0, 0);
                         ahi = __builtin_amdgcn_mfma_i32_16x16x64_i8(wh, x, ahi, 0, 0, 0);
                     }
                     const v4i s = *reinterpret_cast<const v4i*>(sl + (b * M + m) * 16);
-                    const int64_t mn8 =
-                        q == 0 ? (int64_t)(uint32_t)(mn[0] | (mn[1] << 8) | (mn[2] << 16) | (mn[3] << 24)) |
-                                     ((int64_t)(uint32_t)(mn[4] | (mn[5] << 8) | (mn[6] << 16) | (mn[7] << 24)) << 32)
-                               : 0;
+                    const int64_t mn8 = q == 0 ? q4k_mins8(u.mt) : 0;
                     const int64_t slo = q == 0 ? ((int64_t)(uint32_t)s[0] | ((int64_t)(uint32_t)s[1] << 32)) : 0;
                     const int64_t shi = q == 0 ? ((int64_t)(uint32_t)s[2] | ((int64_t)(uint32_t)s[3] << 32)) : 0;
                     const v4i mins = mins_mfma(mn8, slo, shi);
