@@ -126,7 +126,7 @@ def test_mxfp4_random(dev, case):
     from prism_amd import mxfp4 as MX
     g = rng(5000 + case + BASE)
     M, live, N, K, _ = _draw(g, 128, 4096)
-    kernel = str(g.choice(["tile"] + (["decode"] if M <= 64 else [])))
+    kernel = str(g.choice(["tile"] + (["decode"] if M <= 64 else []) + (["split"] if M <= 16 else [])))
     w = weights_f32(N, K, seed=case + 11 + BASE)
     x = acts_bf16(M, K, seed=case + 12 + BASE)
     mw = MX.pack(_t(w, dev), "ocp")
