@@ -431,11 +431,12 @@ __global__ __launch_bounds__(512) void w8a8_pc_decode_kernel(const int8_t* __res
         }
     };
     const int rowb = STG ? (KC * 64 + 1023) / 1024 * 1024 + 16 : 0;
-    const int8_t* img = reinterpret_cast<const int8_t*>(red + NW * G * MT * 64);
+    // one 16-row block: the image after the reduction buffer; more: the image where the reduction buffer goes (a
+    // barrier separates the last image read from the first reduction write)
+    const int8_t* img = reinterpret_cast<const int8_t*>(MT == 1 ? red + NW * G * MT * 64 : red);
     if (STG) {
-        static_assert(!STG || MT == 1, "staged activations: one 16-row block");
         const int pieces = (KC * 64 + 1023) / 1024;
-        for (int row = wv; row < 16; row += NW) {
+        for (int row = wv; row < 16 * MT; row += NW) {
             const int8_t* src = a + (int64_t)min(r0 + row, M - 1) * K + (int64_t)kc0 * 64;
             for (int pc = 0; pc < pieces; pc++)
                 // lanes past the range re-read its last 16 bytes into the row's padding (never read)
@@ -450,7 +451,11 @@ __global__ __launch_bounds__(512) void w8a8_pc_decode_kernel(const int8_t* __res
 #pragma unroll
         for (int u = 0; u < MT; u++) acc[g][u] = v4i{0, 0, 0, 0};
     auto mma = [&](Chunk& c, int j) {
-        if (STG) c.x[0] = *reinterpret_cast<const v4i*>(img + lm * rowb + min(j, KC - 1) * 64 + 16 * q);
+        if (STG) {
+#pragma unroll
+            for (int u = 0; u < MT; u++)
+                c.x[u] = *reinterpret_cast<const v4i*>(img + (16 * u + lm) * rowb + min(j, KC - 1) * 64 + 16 * q);
+        }
 #pragma unroll
         for (int g = 0; g < G; g++)
 #pragma unroll
@@ -479,6 +484,7 @@ __global__ __launch_bounds__(512) void w8a8_pc_decode_kernel(const int8_t* __res
     for (int d = 0; d < PD; d++)
         if (full + d < cnt) mma(ring[d], wv + NW * (full + d));
 
+    if (STG && MT > 1) __syncthreads();              // every wave's image reads done: the sums overwrite it
 #pragma unroll
     for (int g = 0; g < G; g++)
 #pragma unroll
@@ -687,16 +693,26 @@ int launch_w8a8_pc_split(const int8_t* a, const float* a_s, int64_t as_sm, const
                            dim3(256), 0, st, a, pan, M, K);
         PRISM_LAUNCH_CHECK();
     }
-    const size_t stg = lds + 16 * (size_t)pc_stage_row_bytes((KP + 1) * 64);
-    if (PC_STG && MT == 1 && !pan && M >= kPcStageRows && stg <= kPcStageLds &&
+    // staged activations: one 16-row block (image after the sums), or up to four (image in the sums' place)
+    const size_t img = 16 * (size_t)MT * pc_stage_row_bytes((KP + 1) * 64);
+    const size_t stg = MT == 1 ? lds + img : std::max(lds, img);
+#ifndef PC_STG_MT
+#define PC_STG_MT 4
+#endif
+    if (PC_STG && MT <= PC_STG_MT && !pan && M >= kPcStageRows && stg <= kPcStageLds &&
         (int64_t)grid.x * grid.y * grid.z <= kPcStageGrid) {
-#define PSS(GV)                                                                                                    \
+#define PSS(GV, MTV)                                                                                               \
     do {                                                                                                           \
-        allow_lds(w8a8_pc_decode_kernel<GV, 1, true, false, 2, false, true>, stg);                                 \
-        hipLaunchKernelGGL((w8a8_pc_decode_kernel<GV, 1, true, false, 2, false, true>), grid, dim3(64 * nw), stg, st, \
-                           a, a_s, as_sm, w, w_s, slots, (int64_t)N, n_rows, M, N, K, zstride);                    \
+        allow_lds(w8a8_pc_decode_kernel<GV, MTV, true, false, 2, false, true>, stg);                               \
+        hipLaunchKernelGGL((w8a8_pc_decode_kernel<GV, MTV, true, false, 2, false, true>), grid, dim3(64 * nw), stg, \
+                           st, a, a_s, as_sm, w, w_s, slots, (int64_t)N, n_rows, M, N, K, zstride);                \
     } while (0)
-        if (G == 4) PSS(4); else if (G == 2) PSS(2); else PSS(1);
+#define PSS_MT(GV)                                                                                                 \
+    do {                                                                                                           \
+        if (MT == 1) PSS(GV, 1); else if (MT == 2) PSS(GV, 2); else if (MT == 3) PSS(GV, 3); else PSS(GV, 4);      \
+    } while (0)
+        if (G == 4) PSS_MT(4); else if (G == 2) PSS_MT(2); else PSS_MT(1);
+#undef PSS_MT
 #undef PSS
     } else {
 #define PSL(GV, MTV)                                                                                               \
