@@ -29,9 +29,9 @@ _WS = {}
 
 
 def split_workspace(dev):
-    """The per-device workspace of the split decode (kernel "split"): its segment sums, rewritten by every launch.
-    None while a graph is being captured on a device that has none yet: "auto" then picks another kernel and
-    "split" raises."""
+    """The per-device workspace of the split decode (kernel "split"): its segment sums, rewritten by every launch, so
+    calls that overlap in time on one GPU (on different streams) must not both take the split.  None while a graph
+    is being captured on a device that has none yet: "auto" then picks another kernel and "split" raises."""
     idx = dev.index if dev.index is not None else torch.cuda.current_device()
     ws = _WS.get(idx)
     if ws is None:
