@@ -356,7 +356,8 @@ PRISM_API int prism_mxfp4_quant_act(const void* x, int x_f32, int64_t ldx, const
  * prism_mxfp4_pack / _repack.  epi 0: bf16 out; epi 1: out (fp32) = out + y.  Output row stride ldo.  n_rows may be
  * null (all M rows live).  Every kernel sums in the same order (128-input MFMA steps chained within 1024-input
  * segments, segment sums added left to right), so results do not depend on M or on the kernel.
- * kernel: -1 picks by M; 0 the tile kernel; 1 the decode kernel (M <= 64).  Needs N % 16 == 0, K % 128 == 0.
+ * kernel: -1 picks by M; 0 the tile kernel; 1 the decode kernel (M <= 64); 2 the split decode, which needs the
+ * workspace of prism_mxfp4_gemm_ws (here: PRISM_ERR_ARG).  Needs N % 16 == 0, K % 128 == 0.
  * a_fmt PRISM_MX_E4M3_PANELS (activations from prism_mxfp4_quant_act in that format): the tile kernel only (kernel
  * -1 or 0; N K / 2 < 2^31), bits equal to the row-major e4m3 call's.
  */
